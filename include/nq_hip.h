@@ -1,0 +1,138 @@
+/*
+ * nq_hip.h - C ABI of the MI355X (gfx950) NanoQuant inference kernels.
+ *
+ * Plain pointers and sizes only: every pointer is device memory on the current
+ * HIP device of the calling thread, every call is enqueued on `stream` (a
+ * hipStream_t passed as void*, NULL = the null stream) and never synchronises.
+ * No entry point allocates: scratch comes from caller buffers whose sizes the
+ * *_workspace_bytes queries give. Calls are thread-safe except that two calls
+ * sharing one workspace must not overlap.
+ *
+ * Every entry point returns an nq_status; nq_status_string() names it and
+ * nq_last_error_message() gives the detail of the last failure on this thread.
+ *
+ * Bit layouts (identical to the reference's packers):
+ *   NQ_PACK_LSB_FIRST  element j of a 32-column block -> bit j
+ *   NQ_PACK_HALF2      element j of a 32-column block -> bit 15 - j/2 + 16*(j%2)
+ *   Marlin             element (o,k) of a [O,K] weight -> word (k/16, 32*(o/64) + 4*(o%8) + (k%8)/2),
+ *                      bit 15 - 2*((o%16)/8) - (k%16)/8 + 16*(k%2) - 4*((o%64)/16)
+ * A set bit means -1, a clear bit +1.
+ */
+#ifndef NQ_HIP_H
+#define NQ_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* nq_stream_t;
+
+typedef enum {
+    NQ_OK = 0,
+    NQ_ERR_INVALID_ARGUMENT = 1, /* null pointer, negative size, unknown enum */
+    NQ_ERR_SHAPE = 2,            /* sizes inconsistent with each other or with the layout */
+    NQ_ERR_DTYPE = 3,            /* unsupported element type */
+    NQ_ERR_ALIGNMENT = 4,        /* a pointer is not aligned as the layout needs */
+    NQ_ERR_WORKSPACE = 5,        /* workspace smaller than the matching *_workspace_bytes */
+    NQ_ERR_HIP = 6,              /* the HIP runtime reported an error (launch or device) */
+    NQ_ERR_UNSUPPORTED = 7       /* valid request this build does not handle */
+} nq_status;
+
+typedef enum { NQ_F16 = 0, NQ_BF16 = 1 } nq_dtype;
+
+typedef enum { NQ_PACK_LSB_FIRST = 0, NQ_PACK_HALF2 = 1 } nq_pack_method;
+
+const char* nq_status_string(int status);
+const char* nq_last_error_message(void);
+/* Library version as 10000*major + 100*minor + patch. */
+int nq_version(void);
+
+/* ---------------------------------------------------------------- packing */
+
+/* int8 {-1,+1} [rows, cols] (row-major) -> uint32 [rows, ceil(cols/32)].
+ * Columns past `cols` in the last word are packed as +1 (bit 0). A value v is
+ * packed as -1 iff v < 0.
+ * Replaces pack_binary_gemv (src/nanoquant/kernel/utils.py:51-113). */
+int nq_pack_signs(const int8_t* src, uint32_t* dst, int64_t rows, int64_t cols, int method,
+                  nq_stream_t stream);
+
+/* uint32 [rows, ceil(cols/32)] -> int8 {-1,+1} [rows, cols]; padding bits are ignored.
+ * Replaces unpack_binary_gemv (src/nanoquant/kernel/utils.py:116-183). */
+int nq_unpack_signs(const uint32_t* src, int8_t* dst, int64_t rows, int64_t cols, int method,
+                    nq_stream_t stream);
+
+/* Re-order the bits of packed words from one method to the other without
+ * expanding them (on-disk lsb_first checkpoint words -> half2 kernel words).
+ * Padding bits must be clear in `src` (as the packers leave them) and stay clear.
+ * No reference counterpart as one call: replaces binary_unpacker (kernel/utils.py:116-183,
+ * called at load time by utils/load_utils.py:392) followed by binary_packer(..., "half2")
+ * (modules/linear.py:205-206). */
+int nq_repack_signs(const uint32_t* src, uint32_t* dst, int64_t rows, int64_t cols, int src_method,
+                    int dst_method, nq_stream_t stream);
+
+/* int8 {-1,+1} weight [O, K] -> Marlin words uint32 [K/16, O/2]; O % 64 == 0, K % 16 == 0.
+ * Replaces the weight part of pack_binary_marlin (src/nanoquant/kernel/utils.py:191-205). */
+int nq_pack_marlin(const int8_t* weight, uint32_t* dst, int64_t O, int64_t K, nq_stream_t stream);
+
+/* Marlin words [K/16, O/2] -> int8 {-1,+1} [O, K] (inverse of nq_pack_marlin; no reference
+ * counterpart, used to check and to read packed GEMM weights back). */
+int nq_unpack_marlin(const uint32_t* words, int8_t* weight, int64_t O, int64_t K, nq_stream_t stream);
+
+/* Scale permutations of pack_binary_marlin (src/nanoquant/kernel/utils.py:206-209), on
+ * 16-bit elements: in  [K] -> out [K], natural 16c+8a+2b+d -> 16c+4b+2a+d (K % 16 == 0);
+ *                  out [O] -> out [O], natural 32c+8a+2b+d -> 32c+8b+2a+d (O % 32 == 0).
+ * Either pair of pointers may be NULL to skip that vector. */
+int nq_permute_marlin_scales(const uint16_t* scale_in, uint16_t* scale_in_out, int64_t K,
+                             const uint16_t* scale_out, uint16_t* scale_out_out, int64_t O,
+                             nq_stream_t stream);
+
+/* ---------------------------------------------------------------- decode GEMV */
+
+/* Bytes of workspace nq_gemv needs (fp32 intermediate plus grid-barrier words). */
+size_t nq_gemv_workspace_bytes(int64_t batch, int64_t n, int64_t r, int64_t m);
+
+/* y[b, :] = sat(s_out * (U * ((V * (s_in * x[b, :])) * s_mid)))  for b < batch.
+ *   x      dtype [batch, n]           s_in  dtype [n]
+ *   v_bits uint32 [r, ceil(n/32)]     half2 words of V (+-1 [r, n])
+ *   s_mid  dtype [r] or NULL
+ *   u_bits uint32 [m, ceil(r/32)]     half2 words of U (+-1 [m, r])
+ *   s_out  dtype [m]                  y     dtype [batch, m]
+ * Accumulates in fp32; the intermediate stays fp32; fp16 outputs saturate at
+ * +-64504 as the reference GEMV does. `workspace` must hold
+ * nq_gemv_workspace_bytes(batch, n, r, m) bytes, 256-byte aligned, and be zero-filled
+ * once before its first use; it is left ready for the next call.
+ * Replaces nanoquant_dyn_forward (src/nanoquant/kernel/cuda/gemv_kernel.cu:308-429;
+ * declared at gemv.h:6-16, registered at pybind.cpp:85-90,110). */
+int nq_gemv(int dtype, const void* x, const void* s_in, const uint32_t* v_bits, const void* s_mid,
+            const uint32_t* u_bits, const void* s_out, void* y, int64_t batch, int64_t n, int64_t r,
+            int64_t m, void* workspace, size_t workspace_bytes, nq_stream_t stream);
+
+/* ---------------------------------------------------------------- prefill GEMM */
+
+/* C[M, N] = sat((A[M, K] * W) * s_out) with W[k, o] = sign(k, o) * s_in[k]:
+ *   A  dtype [M, K] row-major       w_bits uint32 Marlin words [K/16, N/2]
+ *   s_in, s_out: permuted as pack_binary_marlin returns them, or NULL (= ones)
+ *   C  dtype [M, N]
+ * K % 16 == 0, N % 64 == 0. fp32 accumulation; fp16 outputs saturate at +-65504.
+ * Replaces marlin_onebit_forward (src/nanoquant/kernel/cuda/gemm.cpp:59-98,
+ * registered at pybind.cpp:93-98,113). */
+int nq_gemm_onebit(int dtype, const void* A, const uint32_t* w_bits, const void* s_in, const void* s_out,
+                   void* C, int64_t M, int64_t K, int64_t N, nq_stream_t stream);
+
+/* Both stages: imm = A * (V_bits, s_g, s_l) [M, r_pad], then C = imm * (U_bits, s_h) [M, m].
+ *   v_bits [n/16, r_pad/2], u_bits [r_pad/16, m/2], s_g [n], s_l [r_pad] or NULL, s_h [m] or NULL
+ *   (all permuted as pack_binary_marlin_fused returns them); imm dtype [M, r_pad] is caller memory.
+ * Replaces marlin_nanoquant_forward (src/nanoquant/kernel/cuda/gemm.cpp:112-122,
+ * registered at pybind.cpp:99-104,114). */
+int nq_gemm_nanoquant(int dtype, const void* A, const uint32_t* v_bits, const uint32_t* u_bits,
+                      const void* s_g, const void* s_l, const void* s_h, void* imm, void* C, int64_t M,
+                      int64_t n, int64_t r_pad, int64_t m, nq_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NQ_HIP_H */

@@ -1,0 +1,83 @@
+// Shared device and host helpers of the gfx950 NanoQuant kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include <string>
+
+#include "../../include/nq_hip.h"
+
+namespace nq {
+
+// ----------------------------------------------------------------------------- host side
+
+// Records the detail of the last failure on this thread; returns `status`.
+int fail(int status, const char* fmt, ...);
+// Checks the launch that was just enqueued.
+int check_launch(const char* what);
+
+inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+inline hipStream_t as_stream(nq_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ----------------------------------------------------------------------------- element types
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Storage of both 16-bit float formats is uint16_t; the tag selects the arithmetic.
+struct F16 {
+    static constexpr uint32_t ONE_PAIR = 0x3C003C00u;  // (+1.0, +1.0)
+    static constexpr float SAT = 64504.0f;              // GEMV saturation of the reference (cuda_utils.cuh:84-86)
+    static constexpr float SAT_GEMM = 65504.0f;         // GEMM saturation of the reference (gemm_kernel.cu:124-126)
+    __device__ static inline float to_float(uint16_t v) {
+        return static_cast<float>(__builtin_bit_cast(_Float16, v));
+    }
+    __device__ static inline uint16_t from_float(float f) {
+        return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+    }
+    // a.lo*b.lo + a.hi*b.hi + c, products exact, fp32 sum.
+    __device__ static inline float dot2(uint32_t a, uint32_t b, float c) {
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c, false);
+    }
+};
+
+struct BF16 {
+    static constexpr uint32_t ONE_PAIR = 0x3F803F80u;
+    static constexpr float SAT = 3.3895313892515355e+38f;  // largest finite bf16
+    static constexpr float SAT_GEMM = 3.3895313892515355e+38f;
+    __device__ static inline float to_float(uint16_t v) {
+        return __builtin_bit_cast(float, static_cast<uint32_t>(v) << 16);
+    }
+    __device__ static inline uint16_t from_float(float f) {
+        return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+    }
+    __device__ static inline float dot2(uint32_t a, uint32_t b, float c) {
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c,
+                                               false);
+    }
+};
+
+template <typename T>
+__device__ inline uint16_t saturate_to(float v, float sat) {
+    v = fminf(fmaxf(v, -sat), sat);  // as the reference's clamp: a NaN input becomes -sat
+    return T::from_float(v);
+}
+
+// ----------------------------------------------------------------------------- wave helpers
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+}  // namespace nq

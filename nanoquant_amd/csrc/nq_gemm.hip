@@ -1,0 +1,235 @@
+// Prefill GEMM on the Marlin sign layout: C[M, N] = sat((A[M, K] * W) * s_out) with
+// W[k, o] = sign(k, o) * s_in[k], on gfx950 MFMA (v_mfma_f32_16x16x32_{f16,bf16}).
+//
+// Marlin word (tr, col) of the [K/16, N/2] array holds o = 64*(col/32) + 16*o16 + 8*o8 + o1
+// (o1 = (col%32)/4) by k = 16*tr + 8*r8 + 2*r2 + r1 (r2 = col%4), element at bit
+// 15 - (2*o8 + r8) + 16*r1 - 4*o16. Shifting a word left by 2*o8 + r8 + 4*o16 puts the
+// signs of (k, k+1) at bits 15 and 31: exactly the sign bits of a packed 16-bit pair.
+// The B fragment of one MFMA lane is therefore two adjacent words (r2 = 2g', 2g'+1 of
+// its column o) turned into four (+-s_in[k], +-s_in[k+1]) pairs with one shift, one
+// and, one xor each; no +-1 matrix is ever materialised.
+//
+// K-slot order: the 32 k of one MFMA step are split over the 4 lane groups g = 2t + g'
+// (t = tile_red of the step, g' = pair of r2 values) and inside a lane over dwords
+// d = (r8 = d>>1, r2 = 2g' + (d&1)). A and B use the same order, so the product is the
+// plain sum over k. The A fragment of a lane is then k = 16t + 4g' + {0..3} and
+// 16t + 8 + 4g' + {0..3}: two 8-byte LDS reads.
+//
+// Block tile 128 x 128, 4 waves (2 x 2), wave tile 64 x 64 = 4 x 4 MFMA tiles, K step 32.
+#include "nq_common.h"
+
+namespace nq {
+namespace {
+
+constexpr int BM = 128;
+constexpr int BN = 128;
+constexpr int BK = 32;
+constexpr int LDA = BK + 8;  // LDS row stride in 16-bit elements (80 bytes)
+constexpr int kThreads = 256;
+
+template <typename T>
+struct Mfma;
+
+template <>
+struct Mfma<F16> {
+    __device__ static inline f32x4 run(u32x4 a, u32x4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                      0, 0, 0);
+    }
+};
+
+template <>
+struct Mfma<BF16> {
+    __device__ static inline f32x4 run(u32x4 a, u32x4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                       c, 0, 0, 0);
+    }
+};
+
+// Position of natural output index o in the permuted output-scale vector.
+__device__ inline int perm_out(int o) {
+    return 32 * (o >> 5) + 8 * ((o & 7) >> 1) + 2 * ((o & 31) >> 3) + (o & 1);
+}
+
+template <typename T, bool kSin, bool kSout>
+__global__ __launch_bounds__(kThreads) void gemm_onebit_kernel(const uint16_t* __restrict__ A,
+                                                               const uint32_t* __restrict__ W,
+                                                               const uint16_t* __restrict__ s_in,
+                                                               const uint16_t* __restrict__ s_out,
+                                                               uint16_t* __restrict__ C, int M, int K, int N) {
+    __shared__ __attribute__((aligned(16))) uint16_t As[BM * LDA];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave >> 1;
+    const int wn = wave & 1;
+    const int m0 = blockIdx.y * BM;
+    const int n0 = blockIdx.x * BN;
+    const int c = lane & 15;
+    const int g = lane >> 4;
+    const int t = g >> 1;
+    const int gp = g & 1;
+    const int half_n = N >> 1;
+    const int k_tiles = K >> 4;
+
+    const int o_wave = n0 + wn * 64;  // first output column of this wave (multiple of 64)
+    const bool n_valid = o_wave < N;
+    // word column of (o, r2 = 2g') for this lane; o%8 = c%8 for every ni
+    const int wcol = 32 * (o_wave >> 6) + 4 * (c & 7) + 2 * gp;
+
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int ld_row = tid >> 1;
+    const int ld_col = (tid & 1) * 16;
+
+    for (int k0 = 0; k0 < K; k0 += BK) {
+        // ---- A tile -> LDS
+        u32x4 v0 = u32x4{0, 0, 0, 0}, v1 = u32x4{0, 0, 0, 0};
+        {
+            const int gm = m0 + ld_row;
+            const int gk = k0 + ld_col;
+            if (gm < M && gk < K) {
+                const uint16_t* p = A + static_cast<size_t>(gm) * K + gk;
+                v0 = *reinterpret_cast<const u32x4*>(p);
+                v1 = *reinterpret_cast<const u32x4*>(p + 8);
+            }
+        }
+        // ---- B words and input scales for this lane
+        const int tr = (k0 >> 4) + t;
+        const bool k_valid = tr < k_tiles;
+        uint32_t wlo = 0, whi = 0;
+        if (n_valid && k_valid) {
+            const uint2 w2 = *reinterpret_cast<const uint2*>(W + static_cast<size_t>(tr) * half_n + wcol);
+            wlo = w2.x;
+            whi = w2.y;
+        }
+        uint32_t sp[4];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            if (kSin) {
+                sp[d] = k_valid ? *reinterpret_cast<const uint32_t*>(s_in + k0 + 16 * t + 4 * (2 * gp + (d & 1)) +
+                                                                     2 * (d >> 1))
+                                : 0u;
+            } else {
+                sp[d] = T::ONE_PAIR;
+            }
+        }
+
+        __syncthreads();
+        *reinterpret_cast<u32x4*>(&As[ld_row * LDA + ld_col]) = v0;
+        *reinterpret_cast<u32x4*>(&As[ld_row * LDA + ld_col + 8]) = v1;
+        __syncthreads();
+
+        if (n_valid) {
+            u32x4 bfrag[4];
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) {
+                const int sh0 = 2 * (c >> 3) + 4 * ni;
+                bfrag[ni].x = sp[0] ^ ((wlo << sh0) & 0x80008000u);
+                bfrag[ni].y = sp[1] ^ ((whi << sh0) & 0x80008000u);
+                bfrag[ni].z = sp[2] ^ ((wlo << (sh0 + 1)) & 0x80008000u);
+                bfrag[ni].w = sp[3] ^ ((whi << (sh0 + 1)) & 0x80008000u);
+            }
+            const int kb = 16 * t + 4 * gp;
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi) {
+                const int row = wm * 64 + mi * 16 + c;
+                const uint2 a01 = *reinterpret_cast<const uint2*>(&As[row * LDA + kb]);
+                const uint2 a23 = *reinterpret_cast<const uint2*>(&As[row * LDA + kb + 8]);
+                const u32x4 afrag = u32x4{a01.x, a01.y, a23.x, a23.y};
+#pragma unroll
+                for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = Mfma<T>::run(afrag, bfrag[ni], acc[mi][ni]);
+            }
+        }
+    }
+
+    if (!n_valid) return;
+    // ---- epilogue: acc[mi][ni][i] is C[m0 + wm*64 + mi*16 + 4g + i][o_wave + ni*16 + c]
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) {
+        const int o = o_wave + ni * 16 + c;
+        const float so = kSout ? T::to_float(s_out[perm_out(o)]) : 1.0f;
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = m0 + wm * 64 + mi * 16 + 4 * g + i;
+                if (row < M) C[static_cast<size_t>(row) * N + o] = saturate_to<T>(acc[mi][ni][i] * so, T::SAT_GEMM);
+            }
+        }
+    }
+}
+
+template <typename T>
+int launch_onebit(const void* A, const uint32_t* W, const void* s_in, const void* s_out, void* C, int64_t M, int64_t K,
+                  int64_t N, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(ceil_div(N, BN)), static_cast<unsigned>(ceil_div(M, BM)));
+    const auto* a = static_cast<const uint16_t*>(A);
+    const auto* si = static_cast<const uint16_t*>(s_in);
+    const auto* so = static_cast<const uint16_t*>(s_out);
+    auto* c = static_cast<uint16_t*>(C);
+    if (s_in && s_out)
+        gemm_onebit_kernel<T, true, true><<<grid, kThreads, 0, stream>>>(a, W, si, so, c, (int)M, (int)K, (int)N);
+    else if (s_in)
+        gemm_onebit_kernel<T, true, false><<<grid, kThreads, 0, stream>>>(a, W, si, so, c, (int)M, (int)K, (int)N);
+    else if (s_out)
+        gemm_onebit_kernel<T, false, true><<<grid, kThreads, 0, stream>>>(a, W, si, so, c, (int)M, (int)K, (int)N);
+    else
+        gemm_onebit_kernel<T, false, false><<<grid, kThreads, 0, stream>>>(a, W, si, so, c, (int)M, (int)K, (int)N);
+    return check_launch("nq_gemm_onebit");
+}
+
+int check_onebit(const char* name, int dtype, const void* A, const uint32_t* W, const void* s_in, const void* s_out,
+                 const void* C, int64_t M, int64_t K, int64_t N) {
+    if (dtype != NQ_F16 && dtype != NQ_BF16) return fail(NQ_ERR_DTYPE, "%s: unsupported dtype %d", name, dtype);
+    if (M < 0 || K < 0 || N < 0) return fail(NQ_ERR_INVALID_ARGUMENT, "%s: negative size", name);
+    if (K % 16 || N % 64)
+        return fail(NQ_ERR_SHAPE, "%s: need K %% 16 == 0 and N %% 64 == 0, got K=%lld N=%lld", name, (long long)K,
+                    (long long)N);
+    if (M > INT32_MAX / 2 || K > INT32_MAX / 2 || N > INT32_MAX / 2 || M * K > (int64_t)1 << 40)
+        return fail(NQ_ERR_UNSUPPORTED, "%s: sizes too large", name);
+    if (M == 0 || N == 0) return NQ_OK;
+    if (!A || !W || !C) return fail(NQ_ERR_INVALID_ARGUMENT, "%s: null pointer", name);
+    if (!aligned(A, 16) || !aligned(W, 8) || !aligned(C, 2) || (s_in && !aligned(s_in, 4)) ||
+        (s_out && !aligned(s_out, 2)))
+        return fail(NQ_ERR_ALIGNMENT, "%s: misaligned operand (A needs 16 bytes, weights 8)", name);
+    return NQ_OK;
+}
+
+}  // namespace
+}  // namespace nq
+
+using namespace nq;
+
+extern "C" {
+
+int nq_gemm_onebit(int dtype, const void* A, const uint32_t* w_bits, const void* s_in, const void* s_out, void* C,
+                   int64_t M, int64_t K, int64_t N, nq_stream_t stream) {
+    if (int s = check_onebit("nq_gemm_onebit", dtype, A, w_bits, s_in, s_out, C, M, K, N)) return s;
+    if (M == 0 || N == 0) return NQ_OK;
+    if (dtype == NQ_F16) return launch_onebit<F16>(A, w_bits, s_in, s_out, C, M, K, N, as_stream(stream));
+    return launch_onebit<BF16>(A, w_bits, s_in, s_out, C, M, K, N, as_stream(stream));
+}
+
+int nq_gemm_nanoquant(int dtype, const void* A, const uint32_t* v_bits, const uint32_t* u_bits, const void* s_g,
+                      const void* s_l, const void* s_h, void* imm, void* C, int64_t M, int64_t n, int64_t r_pad,
+                      int64_t m, nq_stream_t stream) {
+    if (int s = check_onebit("nq_gemm_nanoquant stage 1", dtype, A, v_bits, s_g, s_l, imm, M, n, r_pad)) return s;
+    if (int s = check_onebit("nq_gemm_nanoquant stage 2", dtype, imm, u_bits, nullptr, s_h, C, M, r_pad, m)) return s;
+    if (M == 0 || m == 0) return NQ_OK;
+    hipStream_t st = as_stream(stream);
+    if (r_pad > 0) {
+        const int s1 = dtype == NQ_F16 ? launch_onebit<F16>(A, v_bits, s_g, s_l, imm, M, n, r_pad, st)
+                                       : launch_onebit<BF16>(A, v_bits, s_g, s_l, imm, M, n, r_pad, st);
+        if (s1) return s1;
+    }
+    return dtype == NQ_F16 ? launch_onebit<F16>(imm, u_bits, nullptr, s_h, C, M, r_pad, m, st)
+                           : launch_onebit<BF16>(imm, u_bits, nullptr, s_h, C, M, r_pad, m, st);
+}
+
+}  // extern "C"

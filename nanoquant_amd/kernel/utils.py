@@ -1,0 +1,215 @@
+"""Packers and op lookup with the signatures of the reference's ``kernel/utils.py``.
+
+Each function keeps the reference's name, arguments, return values, layouts and
+errors (``src/nanoquant/kernel/utils.py:33-284,503-507``); the bit work runs in the
+gfx950 HIP library. Tensors that live on the CPU are packed on the current GPU and
+the result is returned on the caller's device; without a GPU these functions raise.
+"""
+from __future__ import annotations
+
+from typing import Tuple
+
+import torch
+
+from .. import _lib
+
+MARLIN_MIN_MAX_PAR = 32
+
+_METHODS = {"lsb_first": _lib.NQ_PACK_LSB_FIRST, "half2": _lib.NQ_PACK_HALF2}
+
+
+def get_kernel_function(namespace: str, dtype: torch.dtype, kernel_type: str):
+    """Resolve ``torch.ops.binary_kernels.<namespace>[_dyn]_forward`` (kernel/utils.py:33-48)."""
+    try:
+        from .. import binary_kernels
+        binary_kernels.ensure_loaded()
+    except Exception as exc:
+        raise ImportError("Could not import `binary_kernels`. Did you build the extension?\n"
+                          f"Original error: {exc}") from exc
+
+    mid = "_dyn" if kernel_type != "fixed" else ""
+    op_name = f"{namespace}{mid}_forward"
+
+    try:
+        return getattr(torch.ops.binary_kernels, op_name)
+    except AttributeError as exc:
+        have = dir(torch.ops.binary_kernels) if hasattr(torch.ops, "binary_kernels") else []
+        raise AttributeError(f"Dispatcher op `{namespace}::{op_name}` not found. "
+                             f"Available in torch.ops.binary_kernels: {have}") from exc
+
+
+def _method_code(method: str) -> int:
+    try:
+        return _METHODS[method]
+    except KeyError:
+        raise ValueError(f"Unsupported method: '{method}'. Supported methods are 'lsb_first', 'half2'.") from None
+
+
+def _on_gpu(t: torch.Tensor) -> torch.Tensor:
+    if t.is_cuda:
+        return t.contiguous()
+    if not torch.cuda.is_available():
+        raise RuntimeError("nanoquant_amd packs signs with HIP kernels and needs a GPU; no GPU is available")
+    return t.to(device=torch.device("cuda", torch.cuda.current_device())).contiguous()
+
+
+def pack_binary_gemv(tensor: torch.Tensor, method: str = "lsb_first") -> torch.Tensor:
+    """Pack a {-1,+1} int8 matrix [R, C] into int32 words [R, ceil(C/32)] (kernel/utils.py:51-113).
+
+    TypeError for a non-int8 input; ValueError for an unknown ``method``. Columns are
+    padded with +1 (bit 0); a set bit means -1. ``method`` 'lsb_first' puts column j of a
+    32-column block at bit j, 'half2' at bit 15 - j//2 + 16*(j%2).
+    """
+    if tensor.dtype != torch.int8:
+        raise TypeError("Input tensor must be int8.")
+    n_rows, n_cols = tensor.shape
+    code = _method_code(method)
+    words = (n_cols + 31) // 32
+    src = _on_gpu(tensor)
+    out = torch.empty((n_rows, words), dtype=torch.int32, device=src.device)
+    if out.numel():
+        lib = _lib.load()
+        with torch.cuda.device(src.device):
+            status = lib.nq_pack_signs(src.data_ptr(), out.data_ptr(), n_rows, n_cols, code,
+                                       _lib.stream_of(src.device))
+        _lib.check(status, "pack_binary_gemv")
+    return out if tensor.is_cuda else out.to(tensor.device)
+
+
+def unpack_binary_gemv(packed_tensor: torch.Tensor, original_shape: Tuple[int, int],
+                       method: str = "lsb_first") -> torch.Tensor:
+    """Inverse of :func:`pack_binary_gemv` (kernel/utils.py:116-183): int8 {-1,+1} of
+    ``original_shape``. ValueError for a non-2D input, a shape that is not
+    (rows, ceil(cols/32)), or an unknown ``method``."""
+    if packed_tensor.dim() != 2:
+        raise ValueError(f"Unsupported packed tensor format. Expected 2D tensor, got {packed_tensor.dim()} dimensions.")
+    n_rows, n_cols = (int(s) for s in original_shape)
+    words_per_row = (n_cols + 31) // 32
+    if tuple(packed_tensor.shape) != (n_rows, words_per_row):
+        raise ValueError(
+            f"Unsupported packed tensor shape. Expected ({n_rows}, {words_per_row}), got {packed_tensor.shape}.")
+    code = _method_code(method)
+    if packed_tensor.dtype not in (torch.int32, torch.uint32):
+        raise TypeError(f"packed words must be int32, got {packed_tensor.dtype}")
+    src = _on_gpu(packed_tensor)
+    out = torch.empty((n_rows, n_cols), dtype=torch.int8, device=src.device)
+    if out.numel():
+        lib = _lib.load()
+        with torch.cuda.device(src.device):
+            status = lib.nq_unpack_signs(src.data_ptr(), out.data_ptr(), n_rows, n_cols, code,
+                                         _lib.stream_of(src.device))
+        _lib.check(status, "unpack_binary_gemv")
+    return out if packed_tensor.is_cuda else out.to(packed_tensor.device)
+
+
+def repack_binary_gemv(packed_tensor: torch.Tensor, original_shape: Tuple[int, int], src_method: str = "lsb_first",
+                       dst_method: str = "half2") -> torch.Tensor:
+    """Re-order packed words between bit orders without expanding them.
+
+    Equivalent to ``pack_binary_gemv(unpack_binary_gemv(p, shape, src), dst)``, the
+    route a checkpoint's lsb_first words take to the GEMV's half2 words
+    (load_utils.py:392 then linear.py:205-206), in one pass over the words.
+    """
+    if packed_tensor.dim() != 2:
+        raise ValueError(f"Unsupported packed tensor format. Expected 2D tensor, got {packed_tensor.dim()} dimensions.")
+    n_rows, n_cols = (int(s) for s in original_shape)
+    if tuple(packed_tensor.shape) != (n_rows, (n_cols + 31) // 32):
+        raise ValueError(f"Unsupported packed tensor shape. Expected ({n_rows}, {(n_cols + 31) // 32}), "
+                         f"got {packed_tensor.shape}.")
+    if packed_tensor.dtype not in (torch.int32, torch.uint32):
+        raise TypeError(f"packed words must be int32, got {packed_tensor.dtype}")
+    s_code, d_code = _method_code(src_method), _method_code(dst_method)
+    src = _on_gpu(packed_tensor)
+    out = torch.empty(src.shape, dtype=torch.int32, device=src.device)
+    if out.numel():
+        lib = _lib.load()
+        with torch.cuda.device(src.device):
+            status = lib.nq_repack_signs(src.data_ptr(), out.data_ptr(), n_rows, n_cols, s_code, d_code,
+                                         _lib.stream_of(src.device))
+        _lib.check(status, "repack_binary_gemv")
+    return out if packed_tensor.is_cuda else out.to(packed_tensor.device)
+
+
+def _permute_scales(scale_in, scale_out):
+    s_in = _on_gpu(scale_in.reshape(-1))
+    s_out = _on_gpu(scale_out.reshape(-1))
+    for name, s in (("scale_in", s_in), ("scale_out", s_out)):
+        if s.element_size() != 2:
+            raise TypeError(f"{name} must be a 16-bit float tensor, got {s.dtype}")
+    if s_in.numel() % 16:
+        raise RuntimeError(f"shape '[{s_in.numel() // 16}, 2, 4, 2]' is invalid for input of size {s_in.numel()}")
+    if s_out.numel() % 32:
+        raise RuntimeError(f"shape '[{s_out.numel() // 32}, 4, 4, 2]' is invalid for input of size {s_out.numel()}")
+    p_in = torch.empty_like(s_in)
+    p_out = torch.empty_like(s_out)
+    lib = _lib.load()
+    with torch.cuda.device(s_in.device):
+        status = lib.nq_permute_marlin_scales(s_in.data_ptr(), p_in.data_ptr(), s_in.numel(), s_out.data_ptr(),
+                                              p_out.data_ptr(), s_out.numel(), _lib.stream_of(s_in.device))
+    _lib.check(status, "pack_binary_marlin scales")
+    return p_in, p_out
+
+
+def pack_binary_marlin(weight: torch.Tensor, scale_in: torch.Tensor,
+                       scale_out: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, int]:
+    """Pack a {-1,+1} weight [O, K] for the binary GEMM (kernel/utils.py:186-214).
+
+    Returns (int32 words [K/16, O/2], permuted scale_in, permuted scale_out,
+    workspace_size). O must be a multiple of 64 and K of 16 (RuntimeError otherwise,
+    as the reference's reshape raises).
+    """
+    O, K = weight.shape
+    if O % 64 or K % 16:
+        raise RuntimeError(f"shape '[{O // 64}, 4, 2, 8, {K // 16}, 2, 4, 2]' is invalid for input of size {O * K}")
+    w = _on_gpu(weight if weight.dtype == torch.int8 else weight.to(torch.int8))
+    words = torch.empty((K // 16, O // 2), dtype=torch.int32, device=w.device)
+    if words.numel():
+        lib = _lib.load()
+        with torch.cuda.device(w.device):
+            status = lib.nq_pack_marlin(w.data_ptr(), words.data_ptr(), O, K, _lib.stream_of(w.device))
+        _lib.check(status, "pack_binary_marlin")
+    s_in, s_out = _permute_scales(scale_in, scale_out)
+    workspace_size = s_out.numel() // 128 * MARLIN_MIN_MAX_PAR
+    if not weight.is_cuda:
+        words, s_in, s_out = words.to(weight.device), s_in.to(weight.device), s_out.to(weight.device)
+    return words, s_in, s_out, workspace_size
+
+
+def pack_binary_marlin_fused(V_sign: torch.Tensor, U_sign: torch.Tensor, scale_g: torch.Tensor,
+                             scale_l: torch.Tensor, scale_h: torch.Tensor):
+    """Pack both binary factors for ``marlin_nanoquant_forward`` (kernel/utils.py:217-284).
+
+    V_sign [N, R] and U_sign [R, M] in {-1,+1}; R is padded to a multiple of 256 with +1
+    signs and zero ``scale_l``. Returns (V_bits, U_bits, scale_g', scale_l', scale_h',
+    workspace) with an int32 zero workspace. ``scale_l`` is required (the reference
+    fails without it; NanoQuantLinear passes ones when the layer has no mid scale).
+    """
+    if scale_l is None:
+        raise ValueError("pack_binary_marlin_fused needs scale_l (use ones when the layer has none)")
+    dev = V_sign.device
+    N = scale_g.shape[0]
+    R = scale_l.shape[0]
+    M = scale_h.shape[0]
+    p = 32
+    if R % p != 0:
+        R = ((R // p) + 1) * p
+    rank_p = 256
+    rank_marlin = (R + rank_p - 1) // rank_p * rank_p
+    if rank_marlin > R:
+        pad_amount = rank_marlin - R
+        V_sign = torch.cat([V_sign, torch.ones(N, pad_amount, device=dev, dtype=torch.int8)], dim=1)
+        U_sign = torch.cat([U_sign, torch.ones(pad_amount, M, device=dev, dtype=torch.int8)], dim=0)
+        scale_l = torch.cat([scale_l, torch.zeros(pad_amount, device=scale_l.device, dtype=scale_l.dtype)], dim=0)
+
+    V_bits, scale_g_marlin, scale_l_marlin, workspace_size_v = pack_binary_marlin(V_sign.T, scale_g, scale_l)
+    U_bits, _, scale_h_marlin, workspace_size_u = pack_binary_marlin(U_sign.T, scale_l, scale_h)
+    workspace_size = max(workspace_size_v, workspace_size_u)
+    workspace = torch.zeros(workspace_size, device=dev, dtype=torch.int32)
+    return V_bits.contiguous(), U_bits.contiguous(), scale_g_marlin, scale_l_marlin, scale_h_marlin, workspace
+
+
+# Aliases of the reference (kernel/utils.py:503-506)
+binary_packer = pack_binary_gemv
+binary_unpacker = unpack_binary_gemv
+marlin_onebit_packer = pack_binary_marlin
+marlin_nanoquant_packer = pack_binary_marlin_fused

@@ -1,0 +1,320 @@
+"""Parity of the HIP path with the CPU oracle on the same seeded inputs (needs a gfx950 GPU).
+
+Bars (written here, checked per case):
+* packing, unpacking, reordering: bit-exact;
+* GEMV / GEMM outputs: max|y - y*| / max|y*| against the float64 oracle computed from
+  the same fp16/bf16 inputs, <= 1e-3 for fp16 (the stated bar) and <= 4e-3 (GEMV) /
+  1e-2 (GEMM, whose intermediate is rounded to bf16 for the MFMA) for bf16, whose
+  output rounding alone is 2^-9 relative. Outputs the oracle puts beyond the fp16
+  saturation bound are excluded from the ratio and must equal the bound.
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "marlin_vectors.npz")
+TOL = {("gemv", torch.float16): 1e-3, ("gemv", torch.bfloat16): 4e-3,
+       ("gemm", torch.float16): 1e-3, ("gemm", torch.bfloat16): 1e-2}
+SAT = {("gemv", torch.float16): 64504.0, ("gemm", torch.float16): 65504.0}
+NP_DTYPE = {torch.float16: np.float16}
+
+
+def announce(*what):
+    print("\n[case]", *what, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def nq():
+    import nanoquant_amd
+    from nanoquant_amd import _lib
+    _lib.load()  # fail loudly when the HIP library is missing
+    return nanoquant_amd
+
+
+def dev_t(a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    return t if dtype is None else t.to(dtype)
+
+
+def as_words(t):
+    return t.cpu().numpy().view(np.uint32)
+
+
+def rel_err(y, y64, kind, dtype):
+    y = y.float().cpu().numpy().astype(np.float64)
+    sat = SAT.get((kind, dtype))
+    mask = np.ones_like(y64, dtype=bool) if sat is None else np.abs(y64) < sat
+    if sat is not None and (~mask).any():
+        assert np.all(np.abs(y[~mask]) == sat), "saturated outputs must sit at the bound"
+    denom = np.abs(y64[mask]).max()
+    return float(np.abs(y[mask] - y64[mask]).max() / denom), int((~mask).sum())
+
+
+# --------------------------------------------------------------------------- packing
+
+PACK_SHAPES = [(1, 1), (3, 5), (7, 3), (4, 32), (5, 33), (17, 100), (64, 4096), (1632, 4096), (11008, 1632)]
+
+
+@pytest.mark.parametrize("method", ["lsb_first", "half2"])
+@pytest.mark.parametrize("shape", PACK_SHAPES)
+def test_pack_unpack_bit_exact(nq, shape, method):
+    announce("pack", shape, method)
+    rng = np.random.default_rng(hash(shape) % 1000)
+    s = np.where(rng.random(shape) < 0.5, -1, 1).astype(np.int8)
+    words = nq.pack_binary_gemv(dev_t(s), method=method)
+    torch.cuda.synchronize()
+    assert words.dtype == torch.int32 and tuple(words.shape) == (shape[0], (shape[1] + 31) // 32)
+    np.testing.assert_array_equal(as_words(words), O.pack_binary_gemv(s, method))
+    back = nq.unpack_binary_gemv(words, shape, method=method)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(back.cpu().numpy(), s)
+
+
+@pytest.mark.parametrize("shape", [(3, 5), (17, 100), (1632, 4096), (4096, 1632)])
+def test_repack_between_orders(nq, shape):
+    announce("repack", shape)
+    rng = np.random.default_rng(7)
+    s = np.where(rng.random(shape) < 0.5, -1, 1).astype(np.int8)
+    lsb = dev_t(O.pack_binary_gemv(s, "lsb_first").view(np.int32))
+    h2 = nq.repack_binary_gemv(lsb, shape, "lsb_first", "half2")
+    np.testing.assert_array_equal(as_words(h2), O.pack_binary_gemv(s, "half2"))
+    back = nq.repack_binary_gemv(h2, shape, "half2", "lsb_first")
+    np.testing.assert_array_equal(as_words(back), O.pack_binary_gemv(s, "lsb_first"))
+
+
+def test_marlin_packers_match_reference_vectors(nq):
+    g = np.load(GOLDEN, allow_pickle=False)
+    for i in range(int(g["n_single"])):
+        announce("marlin single", i, g[f"single{i}_w"].shape)
+        w, s_in_p, s_out_p, ws = nq.pack_binary_marlin(dev_t(g[f"single{i}_w"]), dev_t(g[f"single{i}_s_in"]),
+                                                       dev_t(g[f"single{i}_s_out"]))
+        np.testing.assert_array_equal(as_words(w), g[f"single{i}_words"])
+        np.testing.assert_array_equal(s_in_p.cpu().numpy().view(np.uint16), g[f"single{i}_s_in_p"].view(np.uint16))
+        np.testing.assert_array_equal(s_out_p.cpu().numpy().view(np.uint16), g[f"single{i}_s_out_p"].view(np.uint16))
+        assert ws == int(g[f"single{i}_ws"])
+    names = ["V_bits", "U_bits", "s_g_p", "s_l_p", "s_h_p", "workspace"]
+    for i in range(int(g["n_fused"])):
+        announce("marlin fused", i)
+        res = nq.pack_binary_marlin_fused(dev_t(g[f"fused{i}_V_sign"]), dev_t(g[f"fused{i}_U_sign"]),
+                                          dev_t(g[f"fused{i}_s_g"]), dev_t(g[f"fused{i}_s_l"]),
+                                          dev_t(g[f"fused{i}_s_h"]))
+        for name, got in zip(names, res):
+            exp = g[f"fused{i}_{name}"]
+            a = got.cpu().numpy()
+            if a.dtype == np.float16:
+                np.testing.assert_array_equal(a.view(np.uint16), exp.view(np.uint16), err_msg=name)
+            else:
+                np.testing.assert_array_equal(a.view(np.uint32) if name.endswith("bits") else a, exp, err_msg=name)
+
+
+@pytest.mark.parametrize("OK", [(64, 16), (4096, 1024), (11008, 1792), (1792, 4096)])
+def test_marlin_pack_large_and_unpack(nq, OK):
+    from nanoquant_amd import _lib
+    O_, K_ = OK
+    announce("marlin pack", OK)
+    rng = np.random.default_rng(O_ + K_)
+    w = np.where(rng.random((O_, K_)) < 0.5, -1, 1).astype(np.int8)
+    words, _, _, _ = nq.pack_binary_marlin(dev_t(w), torch.ones(K_, dtype=torch.float16, device="cuda"),
+                                           torch.ones(O_, dtype=torch.float16, device="cuda"))
+    exp, _, _, _ = O.pack_binary_marlin(w, np.ones(K_, np.float16), np.ones(O_, np.float16))
+    np.testing.assert_array_equal(as_words(words), exp)
+    back = torch.empty((O_, K_), dtype=torch.int8, device="cuda")
+    lib = _lib.load()
+    _lib.check(lib.nq_unpack_marlin(words.data_ptr(), back.data_ptr(), O_, K_, _lib.stream_of(back.device)), "unpack")
+    np.testing.assert_array_equal(back.cpu().numpy(), w)
+
+
+# --------------------------------------------------------------------------- GEMV
+
+GEMV_CASES = [
+    # name, m, n, r, batch, with_mid
+    ("cfg1", 4096, 4096, 1024, 1, False),
+    ("tails", 72, 40, 24, 3, True),
+    ("odd", 130, 200, 70, 5, False),
+    ("wide_batch", 96, 64, 64, 19, True),
+    ("llama7b_qkvo_055", 4096, 4096, 1120, 1, False),
+    ("llama7b_gate_055_b1", 11008, 4096, 1632, 1, False),
+    ("llama7b_gate_055_b4", 11008, 4096, 1632, 4, False),
+    ("llama7b_down_055_b16", 4096, 11008, 1632, 16, False),
+    ("llama7b_gate_10_b1", 11008, 4096, 2976, 1, False),
+]
+
+
+def gemv_run(nq, c, dtype, x_shape=None):
+    U_bits = nq.pack_binary_gemv(dev_t(c["U"]), method="half2")
+    V_bits = nq.pack_binary_gemv(dev_t(c["V"]), method="half2")
+    x = dev_t(c["x"], dtype)
+    if x_shape is not None:
+        x = x.reshape(x_shape)
+    s_mid = None if c["s_mid"] is None else dev_t(c["s_mid"], dtype)
+    y = torch.ops.binary_kernels.nanoquant_dyn_forward(
+        x, dev_t(c["s_in"], dtype), V_bits, s_mid, U_bits, dev_t(c["s_out"], dtype),
+        num_thread_stage1=128, num_thread_stage2=128, num_row_per_warp_stage1=2, num_row_per_warp_stage2=2,
+        num_acc_stage1=1, num_acc_stage2=1, num_pipeline_stage1=8, num_pipeline_stage2=8)
+    torch.cuda.synchronize()
+    return y, U_bits, V_bits
+
+
+def oracle_inputs(c, dtype):
+    """The exact values the device sees (fp16 as drawn, or rounded to bf16)."""
+    f = (lambda a: a.astype(np.float64)) if dtype == torch.float16 else \
+        (lambda a: torch.from_numpy(a.astype(np.float32)).to(torch.bfloat16).double().numpy())
+    return {k: (None if v is None else (f(v) if v.dtype == np.float16 else v)) for k, v in c.items()}
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("case", GEMV_CASES, ids=[c[0] for c in GEMV_CASES])
+def test_gemv_parity(nq, case, dtype):
+    name, m, n, r, B, mid = case
+    announce("gemv", name, dtype, (m, n, r, B))
+    c = O.random_case(11, m, n, r, B, with_mid=mid)
+    y, U_bits, V_bits = gemv_run(nq, c, dtype)
+    np.testing.assert_array_equal(as_words(U_bits), O.pack_binary_gemv(c["U"], "half2"))
+    np.testing.assert_array_equal(as_words(V_bits), O.pack_binary_gemv(c["V"], "half2"))
+    o = oracle_inputs(c, dtype)
+    y64 = O.nanoquant_forward_f64(o["x"], o["s_in"], c["V"], o["s_mid"], c["U"], o["s_out"])
+    assert tuple(y.shape) == (B, m) and y.dtype == dtype
+    err, nsat = rel_err(y, y64, "gemv", dtype)
+    print(f"[gemv] {name} {dtype} rel_err={err:.3e} saturated={nsat}", flush=True)
+    assert err <= TOL[("gemv", dtype)], err
+
+
+def test_gemv_1d_and_3d_inputs(nq):
+    announce("gemv shapes")
+    c = O.random_case(12, 96, 64, 32, 6)
+    y2, _, _ = gemv_run(nq, c, torch.float16)
+    y3, _, _ = gemv_run(nq, c, torch.float16, x_shape=(2, 3, 64))
+    assert tuple(y3.shape) == (2, 3, 96)
+    torch.testing.assert_close(y3.reshape(6, 96), y2, rtol=0, atol=0)
+    c1 = dict(c, x=c["x"][:1])
+    y1, _, _ = gemv_run(nq, c1, torch.float16, x_shape=(64,))
+    assert tuple(y1.shape) == (96,)
+    torch.testing.assert_close(y1, y2[0], rtol=0, atol=0)
+
+
+def test_gemv_saturates_like_the_reference(nq):
+    announce("gemv saturation")
+    c = O.random_case(13, 256, 4096, 1024, 2)
+    c["s_out"] = (c["s_out"].astype(np.float32) * 60).astype(np.float16)
+    y, _, _ = gemv_run(nq, c, torch.float16)
+    y64 = O.nanoquant_forward_f64(c["x"], c["s_in"], c["V"], None, c["U"], c["s_out"])
+    err, nsat = rel_err(y, y64, "gemv", torch.float16)
+    assert nsat > 0, "the case must saturate some outputs"
+    assert err <= 1e-3
+
+
+def test_gemv_errors(nq):
+    c = O.random_case(14, 64, 64, 32, 1)
+    U_bits = nq.pack_binary_gemv(dev_t(c["U"]), method="half2")
+    V_bits = nq.pack_binary_gemv(dev_t(c["V"]), method="half2")
+    x, s_in, s_out = dev_t(c["x"]), dev_t(c["s_in"]), dev_t(c["s_out"])
+    op = torch.ops.binary_kernels.nanoquant_dyn_forward
+    with pytest.raises(ValueError, match="n_acc1 should be one of \\[1, 2\\], but 4 was given"):
+        op(x, s_in, V_bits, None, U_bits, s_out)
+    kw = dict(num_acc_stage1=1, num_acc_stage2=1)
+    with pytest.raises(RuntimeError, match="scale_g must be float16 tensor"):
+        op(x, s_in.float(), V_bits, None, U_bits, s_out, **kw)
+    with pytest.raises(RuntimeError, match="scale_l size mismatch"):
+        op(x, s_in, V_bits, s_in, U_bits, s_out, **kw)
+    with pytest.raises(RuntimeError, match="Ubits must be"):
+        op(x, s_in, U_bits, None, V_bits, s_out, **kw)
+
+
+# --------------------------------------------------------------------------- GEMM
+
+GEMM_CASES = [
+    # name, batch, n, r, m, with_mid
+    ("small", 5, 64, 32, 64, False),
+    ("tails", 130, 272, 288, 192, True),
+    ("cfg1_b256", 256, 4096, 1024, 4096, False),
+    ("llama7b_gate_055_b256", 256, 4096, 1632, 11008, False),
+    ("llama7b_down_055_b256", 256, 11008, 1632, 4096, False),
+    ("llama7b_gate_055_b2048", 2048, 4096, 1632, 11008, False),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("case", GEMM_CASES, ids=[c[0] for c in GEMM_CASES])
+def test_gemm_parity(nq, case, dtype):
+    name, B, n, r, m, mid = case
+    announce("gemm", name, dtype, (B, n, r, m))
+    c = O.random_case(21, m, n, r, B, with_mid=mid)
+    s_mid = c["s_mid"] if mid else np.ones(r, np.float16)
+    packed = nq.pack_binary_marlin_fused(dev_t(c["V"].T), dev_t(c["U"].T), dev_t(c["s_in"], dtype),
+                                         dev_t(s_mid, dtype), dev_t(c["s_out"], dtype))
+    V_bits, U_bits, s1, s2, s3, ws = packed
+    if B <= 256:  # packing bit-exact against the oracle's fused packer
+        ref = O.pack_binary_marlin_fused(c["V"].T, c["U"].T, c["s_in"], s_mid, c["s_out"])
+        np.testing.assert_array_equal(as_words(V_bits), ref[0])
+        np.testing.assert_array_equal(as_words(U_bits), ref[1])
+    x = dev_t(c["x"], dtype)
+    y = torch.ops.binary_kernels.marlin_nanoquant_forward(x, V_bits, U_bits, s1, s2, s3, ws)
+    torch.cuda.synchronize()
+    o = oracle_inputs(dict(c, s_mid=s_mid), dtype)
+    y64 = O.nanoquant_forward_f64(o["x"], o["s_in"], c["V"], o["s_mid"], c["U"], o["s_out"])
+    assert tuple(y.shape) == (B, m) and y.dtype == dtype
+    err, nsat = rel_err(y, y64, "gemm", dtype)
+    print(f"[gemm] {name} {dtype} rel_err={err:.3e} saturated={nsat}", flush=True)
+    assert err <= TOL[("gemm", dtype)], err
+
+
+@pytest.mark.parametrize("scales", ["none", "in", "out", "both"])
+def test_gemm_onebit_scale_variants(nq, scales):
+    announce("gemm onebit", scales)
+    B, K, N = 33, 96, 192
+    rng = np.random.default_rng(5)
+    w = np.where(rng.random((N, K)) < 0.5, -1, 1).astype(np.int8)
+    s_in = np.abs(rng.normal(1, 0.2, K)).astype(np.float16)
+    s_out = np.abs(rng.normal(1, 0.2, N)).astype(np.float16)
+    x = rng.normal(size=(B, K)).astype(np.float16)
+    words, p_in, p_out, ws_size = nq.pack_binary_marlin(dev_t(w), dev_t(s_in), dev_t(s_out))
+    use_in, use_out = scales in ("in", "both"), scales in ("out", "both")
+    ws = torch.zeros(max(ws_size, 32), dtype=torch.int32, device="cuda")
+    y = torch.ops.binary_kernels.marlin_onebit_forward(dev_t(x), words, p_in if use_in else None,
+                                                       p_out if use_out else None, ws)
+    torch.cuda.synchronize()
+    y64 = (x.astype(np.float64) * (s_in.astype(np.float64) if use_in else 1.0)) @ w.T.astype(np.float64)
+    y64 = y64 * (s_out.astype(np.float64) if use_out else 1.0)
+    err, _ = rel_err(y, y64, "gemm", torch.float16)
+    assert err <= 1e-3, err
+
+
+# --------------------------------------------------------------------------- module
+
+@pytest.mark.parametrize("kernel", ["gemv", "gemm"])
+def test_nanoquant_linear_kernel_forward(nq, kernel):
+    announce("module", kernel)
+    from tests.test_host import make_layer
+    lin, c = make_layer(256, 320, 96, seed=9, with_mid=True, device="cuda")
+    x = torch.from_numpy(np.random.default_rng(1).normal(size=(2, 3, 256)).astype(np.float32)).cuda()
+    f = lambda t: t.detach().double().cpu().numpy().reshape(-1)  # noqa: E731
+    s_pre, s_mid, s_post = f(lin.scale_pre), f(lin.scale_mid), f(lin.scale_post)
+    lin._prepare_kernel(kernel, torch.float16)
+    y = lin(x)
+    torch.cuda.synchronize()
+    assert y.dtype == torch.float32 and tuple(y.shape) == (2, 3, 320)
+    x16 = x.half().double().cpu().numpy().reshape(6, 256)
+    y64 = O.nanoquant_forward_f64(x16, s_pre, c["V"], s_mid, c["U"], s_post)
+    err = np.abs(y.double().cpu().numpy().reshape(6, 320) - y64).max() / np.abs(y64).max()
+    assert err <= 1e-3, err
+
+
+def test_state_dict_round_trip_on_gpu(nq):
+    announce("state_dict")
+    from tests.test_host import make_layer
+    lin, c = make_layer(70, 33, 5, seed=4, device="cuda")
+    state = lin.state_dict()
+    assert state["V_packed"].dtype == torch.int32 and tuple(state["V_packed"].shape) == (5, 3)
+    np.testing.assert_array_equal(as_words(state["U_packed"]), O.pack_binary_gemv(c["U"], "lsb_first"))
+    other, _ = make_layer(70, 33, 5, seed=8, device="cuda")
+    other.load_state_dict(state, strict=True)
+    torch.testing.assert_close(other.V, lin.V)
+    torch.testing.assert_close(other.U, lin.U)
