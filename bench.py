@@ -1,0 +1,264 @@
+"""Benchmark of the NanoQuant inference path on one MI355X.
+
+One step = one decode GEMV (``torch.ops.binary_kernels.nanoquant_dyn_forward``) of the
+Llama-2-7B gate_proj shape at 0.55 bpw (m=11008, n=4096, r=1632), batch 1, fp16, on a
+weight copy that differs from the previous step's: a pool of ``--copies`` packed
+copies (default 128, 394 MB) is larger than the 256 MB Infinity Cache, so every
+step streams its weights from HBM. Steps are captured in a HIP graph and replayed;
+the timed region is bracketed by a device synchronisation on both sides and timed
+with HIP events on the capture stream.
+
+The same JSON line carries:
+* ``roofline``: packed bytes per GEMV / measured time per GEMV against 8 TB/s;
+* ``gemm``: the prefill GEMM (``marlin_nanoquant_forward``) at B=2048 on the same
+  shape, algorithmic TFLOP/s = 2*B*r*(n+m) / time, against 2.5 PFLOP/s dense fp16;
+* ``cpu_baseline``: the reference's dense dequantize-and-matmul forward (two
+  ``F.linear`` on dense +-1 bf16 factors, modules/linear.py:282-291) on the host
+  cores, batch 1, on a bounded sample, in the same unit;
+* ``parity``: relative error of one GEMV and one GEMM against the float64 oracle.
+
+Multi-GPU runs are not part of this build: ``--gpus`` above 1 exits with a message.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "decode GEMV µs + % HBM roofline; prefill GEMM TFLOP/s (Llama-7B shapes)"
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+M, N, R = 11008, 4096, 1632  # Llama-2-7B gate_proj at 0.55 bpw: r = round32(0.55*m*n/(m+n))
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def packed_bytes(m, n, r):
+    return 4 * r * ((n + 31) // 32) + 4 * m * ((r + 31) // 32)
+
+
+def gemv_total_bytes(m, n, r, batch):
+    return packed_bytes(m, n, r) + 2 * (n + m) + 2 * batch * (n + m)
+
+
+def gemv_kwargs():
+    # the tuning ints NanoQuantLinear passes (modules/linear.py:210-219)
+    return dict(num_thread_stage1=128, num_thread_stage2=128, num_row_per_warp_stage1=2, num_row_per_warp_stage2=2,
+                num_acc_stage1=1, num_acc_stage2=1, num_pipeline_stage1=8, num_pipeline_stage2=8)
+
+
+def time_graph(fn_steps, n_steps, replays, warmup_replays, stream):
+    """Capture ``fn_steps`` (which enqueues n_steps steps) in a graph; return ms per step."""
+    with torch.cuda.stream(stream):
+        fn_steps()  # eager warm-up on the capture stream (workspaces, allocator)
+    stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        outs = fn_steps()
+    for _ in range(warmup_replays):
+        graph.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for _ in range(replays):
+            graph.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / (replays * n_steps), graph, outs
+
+
+def bench_gemv(args, dev, log_parity=True):
+    import nanoquant_amd as nq
+    import oracle as O
+
+    dtype = torch.float16
+    batch = args.batch
+    c = O.random_case(2024, M, N, R, batch)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    # copy 0 is packed from known signs (parity); the others are random words, which are
+    # valid half2 words of random signs (the padding-free shape leaves no unused bits)
+    U0 = nq.pack_binary_gemv(t(c["U"]), method="half2")
+    V0 = nq.pack_binary_gemv(t(c["V"]), method="half2")
+    gen = torch.Generator(device=dev).manual_seed(7)
+    Us = [U0] + [torch.randint(-2**31, 2**31 - 1, U0.shape, dtype=torch.int32, device=dev, generator=gen)
+                 for _ in range(args.copies - 1)]
+    Vs = [V0] + [torch.randint(-2**31, 2**31 - 1, V0.shape, dtype=torch.int32, device=dev, generator=gen)
+                 for _ in range(args.copies - 1)]
+    x, s_in, s_out = t(c["x"]), t(c["s_in"]), t(c["s_out"])
+    op = torch.ops.binary_kernels.nanoquant_dyn_forward
+    kw = gemv_kwargs()
+
+    y_eager = op(x, s_in, V0, None, U0, s_out, **kw)
+    torch.cuda.synchronize()
+    y64 = O.nanoquant_forward_f64(c["x"], c["s_in"], c["V"], None, c["U"], c["s_out"])
+    rel = float(np.abs(y_eager.double().cpu().numpy() - y64).max() / np.abs(y64).max())
+
+    n_steps = args.copies
+
+    def steps():
+        return [op(x, s_in, Vs[i], None, Us[i], s_out, **kw) for i in range(n_steps)]
+
+    replays = max(1, args.steps // n_steps)
+    warm = max(1, args.warmup // n_steps)
+    stream = torch.cuda.Stream(device=dev)
+    ms, graph, outs = time_graph(steps, n_steps, replays, warm, stream)
+    graph_ok = bool(torch.equal(outs[0], y_eager))
+    pb = packed_bytes(M, N, R)
+    return dict(ms=ms, steps=replays * n_steps, warmup=warm * n_steps, rel_err=rel, graph_matches_eager=graph_ok,
+                packed_bytes=pb, total_bytes=gemv_total_bytes(M, N, R, batch), pool_bytes=pb * args.copies)
+
+
+def bench_gemm(args, dev):
+    import nanoquant_amd as nq
+    import oracle as O
+
+    dtype = torch.float16
+    B = args.gemm_batch
+    c = O.random_case(2025, M, N, R, B)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    packed = nq.pack_binary_marlin_fused(t(c["V"].T), t(c["U"].T), t(c["s_in"]),
+                                         torch.ones(R, dtype=dtype, device=dev), t(c["s_out"]))
+    x = t(c["x"])
+    op = torch.ops.binary_kernels.marlin_nanoquant_forward
+    y = op(x, *packed)
+    torch.cuda.synchronize()
+    y64 = O.nanoquant_forward_f64(c["x"], c["s_in"], c["V"], None, c["U"], c["s_out"])
+    rel = float(np.abs(y.double().cpu().numpy() - y64).max() / np.abs(y64).max())
+    n_steps = 4
+
+    def steps():
+        return [op(x, *packed) for _ in range(n_steps)]
+
+    stream = torch.cuda.Stream(device=dev)
+    ms, _, _ = time_graph(steps, n_steps, max(1, args.gemm_steps // n_steps), 2, stream)
+    flops = 2.0 * B * R * (N + M)
+    tflops = flops / (ms * 1e-3) / 1e12
+    return dict(ms=ms, tflops=tflops, rel_err=rel, flops=flops, r_pad=packed[1].shape[0] * 16)
+
+
+def cpu_baseline(args):
+    """The reference's dense path on the host cores (oracle.compute_forward_torch)."""
+    import oracle as O
+
+    cores = min(len(os.sched_getaffinity(0)), args.cpu_threads)
+    torch.set_num_threads(cores)
+    c = O.random_case(2026, M, N, R, 1)
+    dt = torch.bfloat16  # the reference module dtype (modules/linear.py:57)
+    V = torch.from_numpy(c["V"].astype(np.float32)).to(dt)
+    U = torch.from_numpy(c["U"].astype(np.float32)).to(dt)
+    s_in = torch.from_numpy(c["s_in"].astype(np.float32)).to(dt)
+    s_out = torch.from_numpy(c["s_out"].astype(np.float32)).to(dt)
+    x = torch.from_numpy(c["x"].astype(np.float32)).to(dt)
+    O.compute_forward_torch(x, V, U, s_in, None, s_out)  # warm-up
+    times = []
+    deadline = time.perf_counter() + args.cpu_seconds
+    while time.perf_counter() < deadline or len(times) < 10:
+        t0 = time.perf_counter()
+        O.compute_forward_torch(x, V, U, s_in, None, s_out)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 2000:
+            break
+    med = float(np.median(times))
+    gbs = packed_bytes(M, N, R) / med / 1e9
+    return dict(value=round(gbs, 4), unit="GB/s", cores=cores, kind="port",
+                sample=f"oracle compute_forward_torch (reference dense path, linear.py:282-291), bf16, B=1, "
+                       f"m={M} n={N} r={R}; median of {len(times)} calls = {med * 1e6:.1f} us/GEMV")
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2048, help="timed GEMV steps (rounded to whole graph replays)")
+    ap.add_argument("--warmup", type=int, default=256, help="untimed GEMV steps before timing")
+    ap.add_argument("--copies", type=int, default=128, help="distinct weight copies rotated through")
+    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--gemm-batch", type=int, default=2048)
+    ap.add_argument("--gemm-steps", type=int, default=64)
+    ap.add_argument("--skip-gemm", action="store_true")
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-threads", type=int, default=16)
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the path has no "
+              "multi-GPU collective to measure. Run with --gpus 1.", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU available", file=sys.stderr)
+        return 1
+
+    import nanoquant_amd  # noqa: F401
+    from nanoquant_amd import _lib
+    _lib.load()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+
+    log(f"[bench] gemv m={M} n={N} r={R} B={args.batch} copies={args.copies}")
+    g = bench_gemv(args, dev)
+    gemv_us = g["ms"] * 1e3
+    achieved = g["packed_bytes"] / (g["ms"] * 1e-3) / 1e9
+    log(f"[bench] gemv {gemv_us:.3f} us/step, {achieved:.1f} GB/s packed, rel_err {g['rel_err']:.2e}")
+
+    gemm = None
+    if not args.skip_gemm:
+        log(f"[bench] gemm B={args.gemm_batch}")
+        gm = bench_gemm(args, dev)
+        gemm = {"batch": args.gemm_batch, "us": round(gm["ms"] * 1e3, 2), "tflops": round(gm["tflops"], 2),
+                "roofline": {"bound": "mfma", "achieved": round(gm["tflops"], 2), "peak": MFMA_F16_PEAK_TFLOPS,
+                             "unit": "TFLOP/s", "frac": round(gm["tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
+                             "traffic": None},
+                "flops_per_call": gm["flops"], "r_pad": gm["r_pad"], "rel_err": gm["rel_err"]}
+        log(f"[bench] gemm {gm['ms'] * 1e3:.1f} us, {gm['tflops']:.1f} TFLOP/s, rel_err {gm['rel_err']:.2e}")
+
+    cpu = None
+    if not args.skip_cpu:
+        log("[bench] cpu baseline")
+        cpu = cpu_baseline(args)
+        log(f"[bench] cpu {cpu['value']} GB/s ({cpu['sample']})")
+
+    line = {
+        "metric": METRIC,
+        "value": round(achieved, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": g["steps"],
+        "warmup": g["warmup"],
+        "ms_per_step": round(g["ms"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": f"decode GEMV, Llama-2-7B gate_proj at 0.55 bpw (m={M}, n={N}, r={R}), batch "
+                               f"{args.batch}, fp16 in / fp32 accumulate, {args.copies} rotating packed weight copies "
+                               f"({g['pool_bytes'] / 1e6:.0f} MB) replayed in a HIP graph",
+                   "m": M, "n": N, "r": R, "batch": args.batch, "copies": args.copies},
+        "gemv_us": round(gemv_us, 4),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+        "gemv_total_bytes_gbs": round(g["total_bytes"] / (g["ms"] * 1e-3) / 1e9, 2),
+        "gemm": gemm,
+        "cpu_baseline": cpu,
+        "parity": {"gemv_rel_err": g["rel_err"], "gemv_graph_matches_eager": g["graph_matches_eager"],
+                   "gemm_rel_err": None if gemm is None else gemm["rel_err"], "bar": 1e-3},
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -22,6 +22,11 @@ constexpr size_t kHeaderBytes = 256;  // reserved words at the start of the work
 // Bit of element e (0..31) of a half2 word.
 __device__ inline int half2_bit(int e) { return 15 - (e >> 1) + 16 * (e & 1); }
 
+// v with its sign bit xor-ed with bit 31 of `mask`. Takes the float by value: a bit
+// cast applied directly to an ext_vector element reads the wrong element with this
+// compiler, so vector lanes are always copied to a scalar first.
+__device__ inline float flip_sign(float v, uint32_t mask) { return __uint_as_float(__float_as_uint(v) ^ mask); }
+
 template <typename T, int NB, bool kVec>
 __global__ __launch_bounds__(kThreads) void gemv_stage1_kernel(const uint16_t* __restrict__ x,
                                                                const uint16_t* __restrict__ s_in,
@@ -113,10 +118,10 @@ __global__ __launch_bounds__(kThreads) void gemv_stage2_kernel(const float* __re
                         // elements 4q..4q+3 = pairs p = 2q, 2q+1: lo of pair p at bit 15-p, hi at bit 31-p
                         const uint32_t t0 = bits << (2 * q);
                         const uint32_t t1 = bits << (2 * q + 1);
-                        acc[b] += __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v.x) ^ ((t0 << 16) & 0x80000000u));
-                        acc[b] += __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v.y) ^ (t0 & 0x80000000u));
-                        acc[b] += __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v.z) ^ ((t1 << 16) & 0x80000000u));
-                        acc[b] += __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v.w) ^ (t1 & 0x80000000u));
+                        acc[b] += flip_sign(v.x, (t0 << 16) & 0x80000000u);
+                        acc[b] += flip_sign(v.y, t0 & 0x80000000u);
+                        acc[b] += flip_sign(v.z, (t1 << 16) & 0x80000000u);
+                        acc[b] += flip_sign(v.w, t1 & 0x80000000u);
                     }
                 }
             }
