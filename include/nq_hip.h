@@ -91,7 +91,7 @@ int nq_permute_marlin_scales(const uint16_t* scale_in, uint16_t* scale_in_out, i
 
 /* ---------------------------------------------------------------- decode GEMV */
 
-/* Bytes of workspace nq_gemv needs (fp32 intermediate plus grid-barrier words). */
+/* Bytes of workspace nq_gemv needs (the intermediate as bf16 hi/lo pairs plus a header). */
 size_t nq_gemv_workspace_bytes(int64_t batch, int64_t n, int64_t r, int64_t m);
 
 /* y[b, :] = sat(s_out * (U * ((V * (s_in * x[b, :])) * s_mid)))  for b < batch.
@@ -100,10 +100,9 @@ size_t nq_gemv_workspace_bytes(int64_t batch, int64_t n, int64_t r, int64_t m);
  *   s_mid  dtype [r] or NULL
  *   u_bits uint32 [m, ceil(r/32)]     half2 words of U (+-1 [m, r])
  *   s_out  dtype [m]                  y     dtype [batch, m]
- * Accumulates in fp32; the intermediate stays fp32; fp16 outputs saturate at
- * +-64504 as the reference GEMV does. `workspace` must hold
- * nq_gemv_workspace_bytes(batch, n, r, m) bytes, 256-byte aligned, and be zero-filled
- * once before its first use; it is left ready for the next call.
+ * Accumulates in fp32; the intermediate is kept as a pair of bf16 values (hi + lo, 16
+ * significant bits, fp32 range); fp16 outputs saturate at +-64504 as the reference GEMV does.
+ * `workspace` must hold nq_gemv_workspace_bytes(batch, n, r, m) bytes, 256-byte aligned.
  * Replaces nanoquant_dyn_forward (src/nanoquant/kernel/cuda/gemv_kernel.cu:308-429;
  * declared at gemv.h:6-16, registered at pybind.cpp:85-90,110). */
 int nq_gemv(int dtype, const void* x, const void* s_in, const uint32_t* v_bits, const void* s_mid,
