@@ -66,6 +66,38 @@ struct BF16 {
     }
 };
 
+// v_mfma_f32_16x16x32_{f16,bf16}: lane l holds A[row l%16][k 8(l/16)..+7], B[k 8(l/16)..+7][col l%16]
+// as four dwords of two 16-bit values each, and C[rows 4(l/16)..+3][col l%16].
+template <typename T>
+__device__ inline f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c);
+
+template <>
+__device__ inline f32x4 mfma16x16x32<F16>(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                                  0);
+}
+
+template <>
+__device__ inline f32x4 mfma16x16x32<BF16>(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                   0, 0);
+}
+
+// (a & mask) | b in one v_and_or_b32; mask and b live in VGPRs (a VOP3 operand cannot take two
+// non-inline constants on this target), so the compiler keeps them in registers across a loop.
+__device__ inline uint32_t and_or(uint32_t a, uint32_t mask, uint32_t b) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(mask), "v"(b));
+    return r;
+}
+
+// (a & mask) | (b & ~mask) in one v_bfi_b32.
+__device__ inline uint32_t bit_select(uint32_t mask, uint32_t a, uint32_t b) {
+    uint32_t r;
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(mask), "v"(a), "v"(b));
+    return r;
+}
+
 template <typename T>
 __device__ inline uint16_t saturate_to(float v, float sat) {
     v = fminf(fmaxf(v, -sat), sat);  // as the reference's clamp: a NaN input becomes -sat

@@ -1,30 +1,43 @@
 // Decode GEMV: y = sat(s_out * (U * ((V * (s_in * x)) * s_mid))) with +-1 factors held as
-// half2-ordered sign words (element j of a 32-column block at bit 15 - j/2 + 16*(j%2)).
+// half2-ordered sign words (element e of a 32-column block at bit 15 - e/2 + 16*(e%2)).
 //
-// Two launches on the caller's stream. (A grid-wide barrier inside one launch costs more on
-// this part than the gap between two dependent launches: the agent-scope fences write back
-// and invalidate each XCD's L2, and same-address atomics from every block serialise.)
-//
+// Two launches on the caller's stream:
 //   stage 1  h[b, j] = s_mid[j] * sum_k sign(V[j,k]) * s_in[k] * x[b,k]
 //   stage 2  y[b, i] = sat(s_out[i] * sum_j sign(U[i,j]) * h[b,j])
+// A grid-wide barrier inside one launch costs more on this part than the gap between two
+// dependent launches (same-address device-scope atomics from every block serialise, and the
+// agent-scope fences write back and invalidate each XCD's L2), so the stages stay separate.
 //
-// The intermediate h lives in the workspace as a pair of bf16 arrays (hi, lo), [batch][kpad],
-// with h ~= hi + lo to 16 significant bits and the fp32 exponent range.
+// The intermediate h lives in the workspace as a pair of bf16 arrays (hi, lo), each
+// [batch][zpitch]: h ~= hi + lo to 16 significant bits with the fp32 exponent range. Columns
+// [r, zpitch) are zero (stage 1 writes them every call), so stage 2 may read past the rank.
 //
-// Stage 1 (s1_reg_kernel): each thread owns a fixed set of words of V's rows and keeps the
-// matching s_in and x pairs in registers for all the rows it visits; a word's sign bit pair
-// (15-p, 31-p) is moved onto the sign bits of the (s_in[k], s_in[k+1]) pair and v_dot2 forms
-// the exact fp16/bf16 products with an fp32 sum; rows are reduced across a wave with DPP.
+// What bounds these kernels at decode sizes is latency and instruction issue, not HBM
+// bandwidth: a 3 MB read is ~0.4 us of bandwidth against ~2 us of launch plus memory latency.
+// So every global load of a kernel is issued before the first use (unconditional loads from
+// clamped addresses; __builtin_amdgcn_sched_barrier keeps the scheduler from sinking them to
+// their uses), nothing waits on a branch, and the per-wave instruction count is kept small.
 //
-// Stage 2 (s2_mfma_kernel): v_mfma_f32_16x16x32_bf16 with U's signs as the A operand and
-// (hi, lo) as two B operands: lane group g of a wave takes sign pairs 4g..4g+3 of each word,
-// each a shift and an or away from a +-1 bf16 pair, and the matrix core does the sum. Batch
-// columns ride in the MFMA's N dimension.
+// Stage 1 (s1w_kernel, VALU): a group of WR waves owns R rows of V; each lane holds WPL words
+// of a row and the matching s_in and x pairs in registers for all R rows. The sign of s_in is
+// moved onto x once, a word's sign pair p then replaces the sign bits of the s_in pair (one
+// v_bfi) and v_dot2 adds the two exact products in fp32. Rows are summed with DPP.
 //
-// Generic kernels (one wave per output row) cover shapes the fast ones do not.
+// Stage 2 (s2t_kernel, MFMA): v_mfma_f32_16x16x32_bf16 with 16 rows of U as A, built from the
+// sign words with a shift and a v_and_or per dword, and the intermediate as B, whose columns
+// are (batch row, hi or lo): up to 8 batch rows per pass, hi and lo added after the MFMAs. A
+// block stages its rows of U and the intermediate in LDS with non-redundant 16-byte loads:
+// the number of vector-memory instructions per CU is what this size pays for.
+//
+// Generic kernels (one wave per output row) cover the shapes the fast ones do not.
 #include <algorithm>
 
 #include "nq_common.h"
+
+// Phase marks of the fast kernels; empty in the library (a timing build may define them).
+#ifndef NQ_STAMP
+#define NQ_STAMP(k)
+#endif
 
 namespace nq {
 namespace {
@@ -33,6 +46,8 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kMaxNB = 8;
 constexpr size_t kHeaderBytes = 256;  // reserved at the start of the workspace
+constexpr uint32_t kSignPair = 0x80008000u;
+constexpr uint32_t kBf16OnePair = 0x3F803F80u;
 
 // Bit of element e (0..31) of a half2 word.
 __device__ inline int half2_bit(int e) { return 15 - (e >> 1) + 16 * (e & 1); }
@@ -41,12 +56,26 @@ __device__ inline uint16_t bf16_bits(float v) { return __builtin_bit_cast(uint16
 __device__ inline float bf16_value(uint16_t b) { return __uint_as_float(static_cast<uint32_t>(b) << 16); }
 
 // Store h[b, j] as (hi, lo).
-__device__ inline void store_h(uint16_t* __restrict__ z_hi, uint16_t* __restrict__ z_lo, int kpad, int b, int j,
+__device__ inline void store_h(uint16_t* __restrict__ z_hi, uint16_t* __restrict__ z_lo, int zpitch, int b, int j,
                                float v) {
-    const size_t at = static_cast<size_t>(b) * kpad + j;
+    const size_t at = static_cast<size_t>(b) * zpitch + j;
     const uint16_t hi = bf16_bits(v);
     z_hi[at] = hi;
     z_lo[at] = bf16_bits(v - bf16_value(hi));
+}
+
+// Zero columns [kpad, zpitch) of batch rows b0 .. b0+nb-1 (with the block's threads).
+__device__ inline void zero_h_pad(uint16_t* __restrict__ z_hi, uint16_t* __restrict__ z_lo, int zpitch, int kpad,
+                                  int b0, int nb, int batch) {
+    const int width = zpitch - kpad;
+    for (int e = threadIdx.x; e < width * nb; e += blockDim.x) {
+        const int b = e / width;
+        if (b0 + b < batch) {
+            const size_t at = static_cast<size_t>(b0 + b) * zpitch + kpad + (e - b * width);
+            z_hi[at] = 0;
+            z_lo[at] = 0;
+        }
+    }
 }
 
 // Sum over the 64 lanes of a wave with DPP; every lane gets the total.
@@ -79,11 +108,12 @@ __global__ __launch_bounds__(kThreads) void gemv_stage1_kernel(const uint16_t* _
                                                                const uint16_t* __restrict__ s_mid,
                                                                uint16_t* __restrict__ z_hi,
                                                                uint16_t* __restrict__ z_lo, int batch, int n, int r,
-                                                               int wn, int kpad) {
+                                                               int wn, int kpad, int zpitch) {
     const int lane = threadIdx.x & 63;
+    const int b0 = blockIdx.y * NB;
+    if (blockIdx.x == 0) zero_h_pad(z_hi, z_lo, zpitch, kpad, b0, NB, batch);
     const int j = blockIdx.x * kWaves + (threadIdx.x >> 6);
     if (j >= kpad) return;
-    const int b0 = blockIdx.y * NB;
     float acc[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) acc[b] = 0.0f;
@@ -102,7 +132,7 @@ __global__ __launch_bounds__(kThreads) void gemv_stage1_kernel(const uint16_t* _
                 sp[4 * q + 3] = v.w;
             }
 #pragma unroll
-            for (int p = 0; p < 16; ++p) sp[p] ^= (bits << p) & 0x80008000u;
+            for (int p = 0; p < 16; ++p) sp[p] ^= (bits << p) & kSignPair;
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
                 if (b0 + b < batch) {
@@ -132,7 +162,7 @@ __global__ __launch_bounds__(kThreads) void gemv_stage1_kernel(const uint16_t* _
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
         const float v = wave_sum_dpp(acc[b]);
-        if (lane == 0 && b0 + b < batch) store_h(z_hi, z_lo, kpad, b0 + b, j, j < r ? v * mid : 0.0f);
+        if (lane == 0 && b0 + b < batch) store_h(z_hi, z_lo, zpitch, b0 + b, j, j < r ? v * mid : 0.0f);
     }
 }
 
@@ -143,7 +173,7 @@ __global__ __launch_bounds__(kThreads) void gemv_stage2_kernel(const uint16_t* _
                                                                const uint32_t* __restrict__ ubits,
                                                                const uint16_t* __restrict__ s_out,
                                                                uint16_t* __restrict__ y, int batch, int m, int wr,
-                                                               int kpad) {
+                                                               int zpitch) {
     const int lane = threadIdx.x & 63;
     const int i = blockIdx.x * kWaves + (threadIdx.x >> 6);
     if (i >= m) return;
@@ -157,7 +187,7 @@ __global__ __launch_bounds__(kThreads) void gemv_stage2_kernel(const uint16_t* _
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
             if (b0 + b < batch) {
-                const size_t at = static_cast<size_t>(b0 + b) * kpad + 32 * q;
+                const size_t at = static_cast<size_t>(b0 + b) * zpitch + 32 * q;
 #pragma unroll 4
                 for (int e = 0; e < 32; ++e) {
                     const float v = bf16_value(z_hi[at + e]) + bf16_value(z_lo[at + e]);
@@ -174,316 +204,316 @@ __global__ __launch_bounds__(kThreads) void gemv_stage2_kernel(const uint16_t* _
     }
 }
 
-// --------------------------------------------------------------------------- stage 1, registers
+// --------------------------------------------------------------------------- stage 1, VALU rows
+//
+// Block = 4 waves = 4/WR groups of WR waves; group gi owns rows j0 .. j0+R-1 (j0 = block row
+// base + gi*R). Lane p = (wave % WR)*64 + lane of a group holds words q_w = p + 64*WR*w
+// (w < WPL) of those rows: consecutive lanes read consecutive words. Requires n % 8 == 0
+// (an 8-column piece is wholly inside or outside a row) and 16-byte aligned x and s_in.
+template <typename T, int NB, int WPL, int WR, int R>
+__global__ __launch_bounds__(256) void s1w_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ s_in,
+                                                  const uint32_t* __restrict__ vbits,
+                                                  const uint16_t* __restrict__ s_mid, uint16_t* __restrict__ z_hi,
+                                                  uint16_t* __restrict__ z_lo, int batch, int n, int r, int wn,
+                                                  int kpad, int zpitch) {
+    constexpr int kGroups = 4 / WR;
+    constexpr int kRows = kGroups * R;
+    __shared__ float part[kGroups * R * NB * WR];
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int grp = wave / WR;
+    const int p = (wave % WR) * 64 + lane;
+    const int j0 = blockIdx.x * kRows + grp * R;
+    const int b0 = blockIdx.y * NB;
+    NQ_STAMP(0);
 
-// x and s_in pairs of one 32-column word as 16 dwords each; columns past n read as zero.
-template <int NB>
-__device__ inline void load_word_pairs(const uint16_t* __restrict__ x, const uint16_t* __restrict__ s_in, int n,
-                                       int batch, int b0, int w, uint32_t (&sp)[16], uint32_t (&xp)[NB][16]) {
-    const int k0 = w * 32;
-    if (k0 + 32 <= n) {
+    // every global load first
+    int qc[WPL];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const u32x4 v = *reinterpret_cast<const u32x4*>(s_in + k0 + 8 * q);
-            sp[4 * q + 0] = v.x;
-            sp[4 * q + 1] = v.y;
-            sp[4 * q + 2] = v.z;
-            sp[4 * q + 3] = v.w;
+    for (int w = 0; w < WPL; ++w) qc[w] = min(p + 64 * WR * w, wn - 1);
+    uint32_t vb[R][WPL];
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+        const uint32_t* row = vbits + static_cast<uint32_t>(min(j0 + k, r - 1)) * static_cast<uint32_t>(wn);
+#pragma unroll
+        for (int w = 0; w < WPL; ++w) vb[k][w] = row[qc[w]];
+    }
+    // the mid scales, raw until the end; without s_mid the (unused) loads read s_in
+    const uint16_t* msrc = s_mid != nullptr ? s_mid : s_in;
+    const int mlim = (s_mid != nullptr ? r : n) - 1;
+    uint16_t mid[R];
+#pragma unroll
+    for (int k = 0; k < R; ++k) mid[k] = msrc[min(j0 + k, mlim)];
+    uint32_t sp[WPL][16];
+    uint32_t xp[WPL][NB][16];
+#pragma unroll
+    for (int w = 0; w < WPL; ++w)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int k0 = min(32 * qc[w] + 8 * v, n - 8);
+            const u32x4 s = *reinterpret_cast<const u32x4*>(s_in + k0);
+            sp[w][4 * v + 0] = s.x;
+            sp[w][4 * v + 1] = s.y;
+            sp[w][4 * v + 2] = s.z;
+            sp[w][4 * v + 3] = s.w;
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const u32x4 xv = *reinterpret_cast<const u32x4*>(
+                    x + static_cast<uint32_t>(min(b0 + b, batch - 1)) * static_cast<uint32_t>(n) + k0);
+                xp[w][b][4 * v + 0] = xv.x;
+                xp[w][b][4 * v + 1] = xv.y;
+                xp[w][b][4 * v + 2] = xv.z;
+                xp[w][b][4 * v + 3] = xv.w;
+            }
         }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // zero what lies past the row or the batch; move s_in's sign onto x
+    const uint32_t mask = kSignPair;
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            if (b0 + b < batch) {
-                const uint16_t* xr = x + static_cast<size_t>(b0 + b) * n + k0;
+    for (int w = 0; w < WPL; ++w)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const u32x4 v = *reinterpret_cast<const u32x4*>(xr + 8 * q);
-                    xp[b][4 * q + 0] = v.x;
-                    xp[b][4 * q + 1] = v.y;
-                    xp[b][4 * q + 2] = v.z;
-                    xp[b][4 * q + 3] = v.w;
-                }
-            } else {
+        for (int v = 0; v < 4; ++v) {
+            const int q = p + 64 * WR * w;
+            const bool ok = q < wn && 32 * q + 8 * v < n;
 #pragma unroll
-                for (int p = 0; p < 16; ++p) xp[b][p] = 0u;
+            for (int d = 0; d < 4; ++d) {
+                const int pp = 4 * v + d;
+                const uint32_t s = ok ? sp[w][pp] : 0u;
+                const uint32_t sg = s & mask;
+                sp[w][pp] = s ^ sg;
+#pragma unroll
+                for (int b = 0; b < NB; ++b) xp[w][b][pp] = (ok && b0 + b < batch) ? (xp[w][b][pp] ^ sg) : 0u;
+            }
+        }
+
+    // Even and odd pairs accumulate separately and rows are innermost, so consecutive dot2
+    // instructions do not wait on each other.
+    float acc[2][R][NB];
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+#pragma unroll
+        for (int k = 0; k < R; ++k)
+#pragma unroll
+            for (int b = 0; b < NB; ++b) acc[e][k][b] = 0.0f;
+#pragma unroll
+    for (int w = 0; w < WPL; ++w)
+#pragma unroll
+        for (int pp = 0; pp < 16; ++pp)
+#pragma unroll
+            for (int k = 0; k < R; ++k) {
+                const uint32_t a = bit_select(mask, vb[k][w] << pp, sp[w][pp]);
+#pragma unroll
+                for (int b = 0; b < NB; ++b) acc[pp & 1][k][b] = T::dot2(a, xp[w][b][pp], acc[pp & 1][k][b]);
+            }
+
+    if (WR == 1) {
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+            const int j = j0 + k;
+            const float mf = s_mid != nullptr ? T::to_float(mid[k]) : 1.0f;
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const float v = wave_sum_dpp(acc[0][k][b] + acc[1][k][b]);
+                if (lane == 0 && j < kpad && b0 + b < batch) store_h(z_hi, z_lo, zpitch, b0 + b, j, j < r ? v * mf : 0.0f);
             }
         }
     } else {
 #pragma unroll
-        for (int p = 0; p < 16; ++p) {
-            const int c0 = k0 + 2 * p;
-            const uint32_t lo = c0 < n ? s_in[c0] : 0u;
-            const uint32_t hi = c0 + 1 < n ? s_in[c0 + 1] : 0u;
-            sp[p] = lo | (hi << 16);
+        for (int k = 0; k < R; ++k)
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
-                const uint16_t* xr = x + static_cast<size_t>(b0 + b) * n;
-                const bool ok = b0 + b < batch;
-                const uint32_t xl = ok && c0 < n ? xr[c0] : 0u;
-                const uint32_t xh = ok && c0 + 1 < n ? xr[c0 + 1] : 0u;
-                xp[b][p] = xl | (xh << 16);
+                const float v = wave_sum_dpp(acc[0][k][b] + acc[1][k][b]);
+                if (lane == 0) part[((grp * R + k) * NB + b) * WR + wave % WR] = v;
             }
-        }
-    }
-}
-
-// Thread t = (group g, slot u) with tpg = 1 << tpg_log2 threads per group and rg = 256 / tpg
-// groups; it owns words u + tpg*k (k < WPT) of rows j0 + g + rg*i (i < RPT) of the block's
-// rg*RPT rows. Rows in [r, kpad) store zeros.
-template <typename T, int NB, int WPT, int RPT>
-__global__ __launch_bounds__(256) void s1_reg_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ s_in,
-                                                     const uint32_t* __restrict__ vbits,
-                                                     const uint16_t* __restrict__ s_mid, uint16_t* __restrict__ z_hi,
-                                                     uint16_t* __restrict__ z_lo, int batch, int n, int r, int wn,
-                                                     int kpad, int tpg_log2) {
-    __shared__ float part[4][RPT * NB];
-    const int t = threadIdx.x;
-    const int lane = t & 63;
-    const int wave = t >> 6;
-    const int tpg = 1 << tpg_log2;
-    const int rg = 256 >> tpg_log2;
-    const int g = t >> tpg_log2;
-    const int u = t & (tpg - 1);
-    const int j0 = blockIdx.x * rg * RPT;
-    const int b0 = blockIdx.y * NB;
-
-    uint32_t bits[RPT][WPT];
+        __syncthreads();
+        if (lane == 0 && wave % WR == 0) {
 #pragma unroll
-    for (int i = 0; i < RPT; ++i) {
-        const int j = j0 + g + rg * i;
+            for (int k = 0; k < R; ++k) {
+                const int j = j0 + k;
+                const float mf = s_mid != nullptr ? T::to_float(mid[k]) : 1.0f;
 #pragma unroll
-        for (int k = 0; k < WPT; ++k) {
-            const int w = u + tpg * k;
-            bits[i][k] = (j < r && w < wn) ? __builtin_nontemporal_load(vbits + static_cast<size_t>(j) * wn + w) : 0u;
-        }
-    }
-
-    // the epilogue's mid scale, fetched with the rest
-    const int rows_pb = rg * RPT;
-    const int ep_j = j0 + t / NB;
-    const float ep_mid = (t < rows_pb * NB && ep_j < r && s_mid != nullptr) ? T::to_float(s_mid[ep_j]) : 1.0f;
-
-    float acc[RPT][NB];
+                for (int b = 0; b < NB; ++b) {
+                    float v = 0.0f;
 #pragma unroll
-    for (int i = 0; i < RPT; ++i)
-#pragma unroll
-        for (int b = 0; b < NB; ++b) acc[i][b] = 0.0f;
-
-#pragma unroll
-    for (int k = 0; k < WPT; ++k) {
-        const int w = u + tpg * k;
-        if (w < wn) {
-            uint32_t sp[16];
-            uint32_t xp[NB][16];
-            load_word_pairs<NB>(x, s_in, n, batch, b0, w, sp, xp);
-#pragma unroll
-            for (int i = 0; i < RPT; ++i) {
-                const uint32_t wb = bits[i][k];
-#pragma unroll
-                for (int p = 0; p < 16; ++p) {
-                    const uint32_t sg = sp[p] ^ ((wb << p) & 0x80008000u);
-#pragma unroll
-                    for (int b = 0; b < NB; ++b) acc[i][b] = T::dot2(sg, xp[b][p], acc[i][b]);
+                    for (int s = 0; s < WR; ++s) v += part[((grp * R + k) * NB + b) * WR + s];
+                    if (j < kpad && b0 + b < batch) store_h(z_hi, z_lo, zpitch, b0 + b, j, j < r ? v * mf : 0.0f);
                 }
             }
         }
     }
-
-#pragma unroll
-    for (int i = 0; i < RPT; ++i)
-#pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            const float v = wave_sum_dpp(acc[i][b]);
-            if (lane == 0) part[wave][i * NB + b] = v;
-        }
-    __syncthreads();
-    if (t < rows_pb * NB) {
-        const int jj = t / NB;
-        const int b = t - jj * NB;
-        const int gg = jj % rg;
-        const int i = jj / rg;
-        const int j = j0 + jj;
-        const int waves_per_group = tpg >> 6;
-        if (j < kpad && b0 + b < batch) {
-            float v = 0.0f;
-            if (j < r) {
-                for (int wv = gg * waves_per_group; wv < (gg + 1) * waves_per_group; ++wv) v += part[wv][i * NB + b];
-                v *= ep_mid;
-            }
-            store_h(z_hi, z_lo, kpad, b0 + b, j, v);
-        }
-    }
+    if (blockIdx.x == 0) zero_h_pad(z_hi, z_lo, zpitch, kpad, b0, NB, batch);
+    NQ_STAMP(3);
 }
 
 // --------------------------------------------------------------------------- stage 2, MFMA
-
-// One block per 16 rows of U and up to 16 batch columns. Its W waves split the row's words in
-// groups of four (wave w takes words 4w..4w+3, 4(w+W).., ...). Lane l: row i0 + l%16 of U
-// (A operand) and batch column b0 + l%16 (B operand) for k-slots 8g..8g+7, g = l/16: the
-// elements 8g..8g+7 of each 32-element word, i.e. the sign pairs p = 4g + d (bits 15-p and
-// 31-p) that a shift by p moves onto the sign bits of a bf16 pair. The B operand is then
-// eight consecutive elements of h.
-// Everything a block reads from memory goes to LDS first, with 16-byte loads that are all
-// issued before any is waited for: the block's rows of U (one contiguous run of words, laid
-// out with rows padded to a multiple of four words), the (hi, lo) intermediate of its batch
-// columns (one contiguous run in each array) and the output scales. Global loads are
-// unconditional (clamped addresses): a load under a branch is waited for where the branch
-// merges. Lanes past m or past the batch compute rows or columns that are never stored.
-constexpr int kS2MaxWr = 192;
-
-template <typename T, int W>
-__global__ __launch_bounds__(W * 64) void s2_mfma_kernel(const uint16_t* __restrict__ z_hi,
-                                                         const uint16_t* __restrict__ z_lo,
-                                                         const uint32_t* __restrict__ ubits,
-                                                         const uint16_t* __restrict__ s_out, uint16_t* __restrict__ y,
-                                                         int batch, int m, int wr, int kpad) {
-    constexpr int kThreadsK = W * 64;
-    constexpr int kTileLoads = (16 * kS2MaxWr / 4 + kThreadsK - 1) / kThreadsK;
-    extern __shared__ __attribute__((aligned(16))) uint32_t dyn[];  // [2][ncols][kpad/2]: hi, then lo
-    __shared__ f32x4 red[W][64];
-    __shared__ __attribute__((aligned(16))) uint32_t tile[16 * kS2MaxWr];  // [16][wr4]
+//
+// v_mfma_f32_16x16x32_bf16, lane l = (g = l / 16, c = l % 16), one block per 16 rows of U.
+// Word q of a row holds 32 elements; lane group g takes elements 8g..8g+7, the half2 pairs
+// p = 4g..4g+3, whose signs sit at bits 15-p and 31-p: the word shifted left by p carries
+// them on the sign bits of a bf16 pair, and an and-or with (+1, +1) makes the A dword.
+//   A: row c of the tile, k-slots of word q (from U's word (i0 + c, q));
+//   B: column c = (batch row b0 + c/2, hi or lo = c % 2), elements 32q + 8g .. +7 of h;
+//   C: column c, tile rows 4g .. 4g+3.
+// At decode sizes the vector-memory instruction count per CU, not bytes, is what a kernel
+// pays for, so the block first stages its 16 rows of U (one contiguous run of words) and the
+// intermediate of its NB batch rows in LDS with non-redundant 16-byte loads. The 4 waves then
+// take words q = wave + 4s (s < QW); words past wr meet the zero columns of h (U's row is
+// clamped), so every step is valid and the loop has no branch. Columns of batch rows past the
+// batch hold finite values that are never stored. The waves' partial tiles are added in LDS,
+// then hi + lo of each batch row (adjacent lanes) and s_out.
+template <typename T, int QW, int NB>
+__global__ __launch_bounds__(256) void s2t_kernel(const uint16_t* __restrict__ z_hi, const uint16_t* __restrict__ z_lo,
+                                                  const uint32_t* __restrict__ ubits,
+                                                  const uint16_t* __restrict__ s_out, uint16_t* __restrict__ y,
+                                                  int batch, int m, int wr, int zpitch) {
+    constexpr int NW = 4;
+    constexpr int kThr = 256;
+    constexpr int kWords = 16 * NW * QW;  // tile words (wr <= NW * QW)
+    constexpr int kUPieces = (kWords / 4 + kThr - 1) / kThr;
+    constexpr int kCols = 32 * NW * QW;  // h columns used per batch row (<= zpitch)
+    constexpr int kRowPieces = kCols / 8;
+    constexpr int kZPieces = (2 * NB * kRowPieces + kThr - 1) / kThr;
+    __shared__ __attribute__((aligned(16))) uint32_t tile[kWords + 4];
+    __shared__ __attribute__((aligned(16))) uint16_t hz[2 * NB][kCols];  // [hi rows, then lo rows][column]
+    __shared__ f32x4 red[NW][64];
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
     const int c = lane & 15;
     const int g = lane >> 4;
     const int i0 = blockIdx.x * 16;
-    const int b0 = blockIdx.y * 16;
-    const int ncols = min(16, batch - b0);
-    const int wr4 = (wr + 3) & ~3;
+    const int b0 = blockIdx.y * NB;
+    NQ_STAMP(0);
 
-    // 1. issue every global load
-    const int64_t total = static_cast<int64_t>(m) * wr;
-    const int64_t vec_end = total & ~static_cast<int64_t>(3);  // 16-byte loads stay below this
-    const int64_t base = static_cast<int64_t>(i0) * wr;
-    const int nwords = min(16, m - i0) * wr;
-    u32x4 tv[kTileLoads];
+    // 1. every global load: the tile's words as 16-byte pieces, h, the output scales
+    const uint32_t total = static_cast<uint32_t>(m) * static_cast<uint32_t>(wr);
+    const uint32_t vec_end = total & ~3u;  // the host guarantees total >= 4
+    const uint32_t base = static_cast<uint32_t>(i0) * static_cast<uint32_t>(wr);  // a multiple of 16
+    const int rows = min(16, m - i0);
+    const int nwords = rows * wr;
+    u32x4 pv[kUPieces];
 #pragma unroll
-    for (int it = 0; it < kTileLoads; ++it) {
-        const int64_t at = min(base + (t + it * kThreadsK) * 4, vec_end - 4);
-        tv[it] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ubits + at));
+    for (int it = 0; it < kUPieces; ++it)
+        pv[it] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(ubits + min(base + 4u * static_cast<uint32_t>(t + it * kThr), vec_end - 4u)));
+    const uint32_t tail_word = ubits[min(vec_end + static_cast<uint32_t>(t), total - 1u)];  // words past vec_end
+    u32x4 zv[kZPieces];
+#pragma unroll
+    for (int it = 0; it < kZPieces; ++it) {
+        const int pc = min(t + it * kThr, 2 * NB * kRowPieces - 1);
+        const int arr = pc / (NB * kRowPieces);
+        const int rem = pc - arr * (NB * kRowPieces);
+        const int b = rem / kRowPieces;
+        const int off = (rem - b * kRowPieces) * 8;
+        zv[it] = *reinterpret_cast<const u32x4*>(
+            (arr ? z_lo : z_hi) + static_cast<uint32_t>(min(b0 + b, batch - 1)) * static_cast<uint32_t>(zpitch) + off);
     }
-    const int zvec = ncols * kpad / 8;  // 16-byte pieces per half
-    const u32x4* zsrc_hi = reinterpret_cast<const u32x4*>(z_hi + static_cast<size_t>(b0) * kpad);
-    const u32x4* zsrc_lo = reinterpret_cast<const u32x4*>(z_lo + static_cast<size_t>(b0) * kpad);
-    constexpr int kZLoads = 2;  // pieces per thread per half issued up front; more are copied after
-    u32x4 zvh[kZLoads], zvl[kZLoads];
+    uint16_t so[4];  // raw until the epilogue
 #pragma unroll
-    for (int it = 0; it < kZLoads; ++it) {
-        const int v = min(t + it * kThreadsK, zvec - 1);
-        zvh[it] = zsrc_hi[v];
-        zvl[it] = zsrc_lo[v];
-    }
-    float so[4];  // branch-free (clamped) so that the four loads issue together
-#pragma unroll
-    for (int i = 0; i < 4; ++i) so[i] = T::to_float(s_out[min(i0 + 4 * g + i, m - 1)]);
+    for (int i = 0; i < 4; ++i) so[i] = s_out[min(i0 + 4 * g + i, m - 1)];
+    __builtin_amdgcn_sched_barrier(0);
 
-    // 2. LDS: U words with rows padded to wr4 (pad words zero), then h
+    // 2. into LDS; vec_end and base + e4 are multiples of 4, so a piece lies wholly below
+    //    vec_end or wholly past it, and words past it come from tail_word
 #pragma unroll
-    for (int it = 0; it < kTileLoads; ++it) {
-        const int e4 = (t + it * kThreadsK) * 4;
-        if (e4 < nwords) {
-            const u32x4 v = tv[it];
-            const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
-            const bool vec_ok = base + e4 + 4 <= vec_end;
-#pragma unroll
-            for (int z = 0; z < 4; ++z) {
-                const int e = e4 + z;
-                if (e < nwords) {
-                    const int rrow = e / wr;
-                    tile[rrow * wr4 + (e - rrow * wr)] = vec_ok ? vv[z] : ubits[base + e];
-                }
-            }
-        }
+    for (int it = 0; it < kUPieces; ++it) {
+        const int e4 = 4 * (t + it * kThr);
+        if (e4 < nwords && base + e4 + 4 <= vec_end) *reinterpret_cast<u32x4*>(tile + e4) = pv[it];
     }
-    if (wr4 != wr)
-        for (int e = t; e < 16 * (wr4 - wr); e += kThreadsK) {
-            const int rrow = e / (wr4 - wr);
-            tile[rrow * wr4 + wr + (e - rrow * (wr4 - wr))] = 0u;
-        }
-    u32x4* zdst = reinterpret_cast<u32x4*>(dyn);
-#pragma unroll
-    for (int it = 0; it < kZLoads; ++it) {
-        const int v = t + it * kThreadsK;
-        if (v < zvec) {
-            zdst[v] = zvh[it];
-            zdst[zvec + v] = zvl[it];
-        }
+    if (t < 3) {
+        const uint32_t w = vec_end + t;
+        if (w < total && w >= base && w < base + nwords) tile[w - base] = tail_word;
     }
-    for (int v = t + kZLoads * kThreadsK; v < zvec; v += kThreadsK) {
-        zdst[v] = zsrc_hi[v];
-        zdst[zvec + v] = zsrc_lo[v];
+#pragma unroll
+    for (int it = 0; it < kZPieces; ++it) {
+        const int pc = t + it * kThr;
+        if (pc < 2 * NB * kRowPieces) {
+            const int row = pc / kRowPieces;  // arr * NB + b
+            *reinterpret_cast<u32x4*>(&hz[row][(pc - row * kRowPieces) * 8]) = zv[it];
+        }
     }
     __syncthreads();
 
-    // 3. MFMAs, four words at a time: one 16-byte read of words, eight of h, 2 VALU ops per
-    //    A dword, two accumulators (hi, lo)
-    const int zc = min(c, ncols - 1);
-    const uint32_t* zrow_hi = dyn + zc * (kpad / 2) + 4 * g;
-    const uint32_t* zrow_lo = dyn + (ncols + zc) * (kpad / 2) + 4 * g;
-    const uint32_t* trow = tile + c * wr4;
+    // 3. MFMAs
+    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    const uint32_t mask = kSignPair, one = kBf16OnePair;
     const int sh = 4 * g;
-    f32x4 ah = f32x4{0.f, 0.f, 0.f, 0.f}, al = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int q0 = 4 * wave; q0 < wr; q0 += 4 * W) {
-        const u32x4 w4 = *reinterpret_cast<const u32x4*>(trow + q0);
-        u32x4 bh[4], bl[4];
+    const int bcol = c >> 1;
+    const uint16_t* hsrc = &hz[(c & 1) * NB + min(bcol, NB - 1)][8 * g];
+    const uint32_t* trow = tile + min(c, rows - 1) * wr;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int q = min(q0 + k, wr - 1);
-            bh[k] = *reinterpret_cast<const u32x4*>(zrow_hi + 16 * q);
-            bl[k] = *reinterpret_cast<const u32x4*>(zrow_lo + 16 * q);
-        }
-        const uint32_t ws[4] = {w4.x, w4.y, w4.z, w4.w};
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            if (q0 + k < wr) {
-                const uint32_t w = ws[k] << sh;
-                u32x4 a;
-                a.x = 0x3F803F80u | (w & 0x80008000u);
-                a.y = 0x3F803F80u | ((w << 1) & 0x80008000u);
-                a.z = 0x3F803F80u | ((w << 2) & 0x80008000u);
-                a.w = 0x3F803F80u | ((w << 3) & 0x80008000u);
-                ah = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                             __builtin_bit_cast(bf16x8, bh[k]), ah, 0, 0, 0);
-                al = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                             __builtin_bit_cast(bf16x8, bl[k]), al, 0, 0, 0);
-            }
-        }
+    for (int s = 0; s < QW; ++s) {
+        const int q = wave + NW * s;
+        const u32x4 b = *reinterpret_cast<const u32x4*>(hsrc + 32 * q);
+        const uint32_t w = trow[min(q, wr - 1)] << sh;
+        const u32x4 a = u32x4{and_or(w, mask, one), and_or(w << 1, mask, one), and_or(w << 2, mask, one),
+                              and_or(w << 3, mask, one)};
+        acc[s & 1] = mfma16x16x32<BF16>(a, b, acc[s & 1]);
     }
-    {
-        const f32x4 a0 = ah, a1 = al;
-        red[wave][lane] = f32x4{a0.x + a1.x, a0.y + a1.y, a0.z + a1.z, a0.w + a1.w};
-    }
+    red[wave][lane] = f32x4{acc[0].x + acc[1].x, acc[0].y + acc[1].y, acc[0].z + acc[1].z, acc[0].w + acc[1].w};
     __syncthreads();
+    NQ_STAMP(2);
 
-    // 4. wave 0 sums over the W waves and stores
-    const int col = b0 + c;
-    if (wave == 0 && col < batch) {
-        float s[4] = {0.f, 0.f, 0.f, 0.f};
+    // 4. sum the waves' tiles, add hi and lo, scale, store
+    if (wave == 0) {
+        f32x4 sum = red[0][lane];
 #pragma unroll
-        for (int w = 0; w < W; ++w) {
-            const f32x4 p = red[w][lane];
-            const float p0 = p.x, p1 = p.y, p2 = p.z, p3 = p.w;
-            s[0] += p0;
-            s[1] += p1;
-            s[2] += p2;
-            s[3] += p3;
+        for (int w = 1; w < NW; ++w) {
+            const f32x4 pr = red[w][lane];
+            sum = f32x4{sum.x + pr.x, sum.y + pr.y, sum.z + pr.z, sum.w + pr.w};
         }
-        // C layout: lane l holds column l%16 and rows 4*(l/16) + i
+        const float v[4] = {sum.x, sum.y, sum.z, sum.w};
+        const bool b_ok = (c & 1) == 0 && bcol < NB && b0 + bcol < batch;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int ro = i0 + 4 * g + i;
-            if (ro < m) y[static_cast<size_t>(col) * m + ro] = saturate_to<T>(s[i] * so[i], T::SAT);
+            // quad_perm [1,0,3,2]: the lo column's value from the neighbouring lane
+            const float lo = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v[i]), 0xB1, 0xF, 0xF, false));
+            const int row = i0 + 4 * g + i;
+            if (b_ok && row < m)
+                y[static_cast<size_t>(b0 + bcol) * m + row] = saturate_to<T>((v[i] + lo) * T::to_float(so[i]), T::SAT);
         }
     }
+    NQ_STAMP(3);
 }
 
-inline size_t s2_dyn_lds(int ncols, int kpad) { return static_cast<size_t>(ncols) * 2 * kpad * sizeof(uint16_t); }
+// --------------------------------------------------------------------------- plan and dispatch
 
-// --------------------------------------------------------------------------- dispatch
+constexpr int kS2Waves = 4;
+constexpr int kS2QwChoices[] = {2, 4, 6, 8, 10, 12, 14, 16, 20, 24, 28, 32, 36};
+constexpr int kS2MaxWr = kS2Waves * 36;
+
+struct Plan {
+    int wr;      // words per row of U
+    int kpad;    // 32 * wr
+    int s2_qw;   // words per wave of the MFMA stage 2, or 0 for the generic kernel
+    int zpitch;  // elements per batch row of each intermediate array
+};
 
 inline int64_t kpad_of(int64_t r) { return ceil_div(r, 32) * 32; }
-inline size_t z_bytes(int64_t batch, int64_t r) {
-    return (static_cast<size_t>(batch) * static_cast<size_t>(kpad_of(r)) * 2 + 255) / 256 * 256;
+
+inline Plan plan_of(int64_t r) {
+    Plan p;
+    p.wr = static_cast<int>(ceil_div(r, 32));
+    p.kpad = 32 * p.wr;
+    p.s2_qw = 0;
+    if (p.wr <= kS2MaxWr) {
+        const int need = static_cast<int>(ceil_div(p.wr, kS2Waves));
+        for (int q : kS2QwChoices)
+            if (q >= need) {
+                p.s2_qw = q;
+                break;
+            }
+    }
+    // stage 2 reads h up to column 32 * 4 * QW; keep a multiple of 64 columns (128 bytes)
+    const int64_t cols = std::max<int64_t>(p.kpad, 32 * kS2Waves * p.s2_qw);
+    p.zpitch = static_cast<int>(ceil_div(std::max<int64_t>(cols, 64), 64) * 64);
+    return p;
+}
+
+inline size_t z_bytes(int64_t batch, const Plan& p) {
+    return (static_cast<size_t>(batch) * static_cast<size_t>(p.zpitch) * 2 + 255) / 256 * 256;
 }
 
 struct GemvArgs {
@@ -494,7 +524,8 @@ struct GemvArgs {
     const uint32_t* u_bits;
     const uint16_t* s_out;
     uint16_t* y;
-    int batch, n, r, m, wn, wr, kpad;
+    int batch, n, r, m, wn;
+    Plan plan;
     uint16_t* z_hi;
     uint16_t* z_lo;
     hipStream_t stream;
@@ -502,97 +533,110 @@ struct GemvArgs {
 
 template <typename T, int NB>
 void launch_stage1_generic(const GemvArgs& a) {
-    const dim3 g1(static_cast<unsigned>(ceil_div(a.kpad, kWaves)), static_cast<unsigned>(ceil_div(a.batch, NB)));
+    const dim3 g1(static_cast<unsigned>(ceil_div(a.plan.kpad, kWaves)), static_cast<unsigned>(ceil_div(a.batch, NB)));
     const bool vec = (a.n % 8 == 0) && aligned(a.x, 16) && aligned(a.s_in, 16);
     if (vec)
         gemv_stage1_kernel<T, NB, true><<<g1, kThreads, 0, a.stream>>>(a.x, a.s_in, a.v_bits, a.s_mid, a.z_hi, a.z_lo,
-                                                                        a.batch, a.n, a.r, a.wn, a.kpad);
+                                                                        a.batch, a.n, a.r, a.wn, a.plan.kpad,
+                                                                        a.plan.zpitch);
     else
         gemv_stage1_kernel<T, NB, false><<<g1, kThreads, 0, a.stream>>>(a.x, a.s_in, a.v_bits, a.s_mid, a.z_hi,
-                                                                         a.z_lo, a.batch, a.n, a.r, a.wn, a.kpad);
+                                                                         a.z_lo, a.batch, a.n, a.r, a.wn, a.plan.kpad,
+                                                                         a.plan.zpitch);
 }
 
 template <typename T, int NB>
 void launch_stage2_generic(const GemvArgs& a) {
     const dim3 g2(static_cast<unsigned>(ceil_div(a.m, kWaves)), static_cast<unsigned>(ceil_div(a.batch, NB)));
     gemv_stage2_kernel<T, NB><<<g2, kThreads, 0, a.stream>>>(a.z_hi, a.z_lo, a.u_bits, a.s_out, a.y, a.batch, a.m,
-                                                             a.wr, a.kpad);
+                                                             a.plan.wr, a.plan.zpitch);
 }
 
-template <typename T, int NB, int WPT>
-void launch_s1_reg(const GemvArgs& a, int tpg_log2) {
-    const int rg = 256 >> tpg_log2;
-    // two rows per thread when that still gives a full wave of blocks, else four
-    const bool two = ceil_div(a.kpad, rg * 2) >= 256;
-    const int rows_pb = rg * (two ? 2 : 4);
-    const dim3 grid(static_cast<unsigned>(ceil_div(a.kpad, rows_pb)), static_cast<unsigned>(ceil_div(a.batch, NB)));
-    if (two)
-        s1_reg_kernel<T, NB, WPT, 2><<<grid, 256, 0, a.stream>>>(a.x, a.s_in, a.v_bits, a.s_mid, a.z_hi, a.z_lo,
-                                                                 a.batch, a.n, a.r, a.wn, a.kpad, tpg_log2);
-    else
-        s1_reg_kernel<T, NB, WPT, 4><<<grid, 256, 0, a.stream>>>(a.x, a.s_in, a.v_bits, a.s_mid, a.z_hi, a.z_lo,
-                                                                 a.batch, a.n, a.r, a.wn, a.kpad, tpg_log2);
+template <typename T, int NB, int WPL, int WR, int R>
+void launch_s1w(const GemvArgs& a) {
+    const int rows_pb = (4 / WR) * R;
+    const dim3 grid(static_cast<unsigned>(ceil_div(a.plan.kpad, rows_pb)), static_cast<unsigned>(ceil_div(a.batch, NB)));
+    s1w_kernel<T, NB, WPL, WR, R><<<grid, 256, 0, a.stream>>>(a.x, a.s_in, a.v_bits, a.s_mid, a.z_hi, a.z_lo, a.batch,
+                                                               a.n, a.r, a.wn, a.plan.kpad, a.plan.zpitch);
+}
+
+// Shapes measured on MI355X (graph-replayed, cold weights): n = 4096 is fastest with two waves
+// per row and one word per lane, two rows per group (3.3 us against 3.6-4.3 for the other
+// splits); n = 11008 with four waves per row, two words per lane, four rows per group.
+template <typename T, int NB>
+bool launch_s1w_nb(const GemvArgs& a) {
+    const int wn = a.wn;
+    if (wn <= 64) launch_s1w<T, NB, 1, 1, 2>(a);
+    else if (wn <= 128) launch_s1w<T, NB, 1, 2, 2>(a);
+    else if (wn <= 256) launch_s1w<T, NB, 2, 2, 2>(a);
+    else if (wn <= 512) launch_s1w<T, NB, 2, 4, 4>(a);
+    else return false;
+    return true;
 }
 
 template <typename T>
 void launch_stage1(const GemvArgs& a) {
-    const bool fast = (a.n % 8 == 0) && aligned(a.x, 16) && aligned(a.s_in, 16) && a.wn <= 1024;
-    if (!fast) {
-        if (a.batch <= 1) launch_stage1_generic<T, 1>(a);
-        else if (a.batch <= 2) launch_stage1_generic<T, 2>(a);
-        else if (a.batch <= 4) launch_stage1_generic<T, 4>(a);
-        else launch_stage1_generic<T, kMaxNB>(a);
-        return;
+    const bool fast = a.n >= 8 && a.n % 8 == 0 && aligned(a.x, 16) && aligned(a.s_in, 16) && a.wn <= 512;
+    if (fast) {
+        if (a.batch <= 1 ? launch_s1w_nb<T, 1>(a) : launch_s1w_nb<T, 2>(a)) return;
     }
-    const int wpt = a.wn <= 256 ? 1 : (a.wn <= 512 ? 2 : 4);
-    const int slots = static_cast<int>(ceil_div(a.wn, wpt));
-    const int tpg_log2 = slots <= 64 ? 6 : (slots <= 128 ? 7 : 8);
-    // batch rows per pass: registers hold WPT * NB * 16 x dwords, keep that <= 64
-    const int nb_cap = 4 / wpt;
-    const int nb = a.batch >= 4 && nb_cap >= 4 ? 4 : (a.batch >= 2 && nb_cap >= 2 ? 2 : 1);
-    if (wpt == 1) {
-        if (nb == 4) launch_s1_reg<T, 4, 1>(a, tpg_log2);
-        else if (nb == 2) launch_s1_reg<T, 2, 1>(a, tpg_log2);
-        else launch_s1_reg<T, 1, 1>(a, tpg_log2);
-    } else if (wpt == 2) {
-        if (nb == 2) launch_s1_reg<T, 2, 2>(a, tpg_log2);
-        else launch_s1_reg<T, 1, 2>(a, tpg_log2);
-    } else {
-        launch_s1_reg<T, 1, 4>(a, tpg_log2);
-    }
+    if (a.batch <= 1) launch_stage1_generic<T, 1>(a);
+    else if (a.batch <= 2) launch_stage1_generic<T, 2>(a);
+    else if (a.batch <= 4) launch_stage1_generic<T, 4>(a);
+    else launch_stage1_generic<T, kMaxNB>(a);
 }
 
-template <typename T, int W>
-void launch_s2_mfma(const GemvArgs& a) {
-    const dim3 grid(static_cast<unsigned>(ceil_div(a.m, 16)), static_cast<unsigned>(ceil_div(a.batch, 16)));
-    const size_t lds = s2_dyn_lds(std::min(16, a.batch), a.kpad);
-    static const bool lds_ok = [] {
-        return hipFuncSetAttribute(reinterpret_cast<const void*>(&s2_mfma_kernel<T, W>),
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024) == hipSuccess;
-    }();
-    (void)lds_ok;
-    s2_mfma_kernel<T, W><<<grid, W * 64, lds, a.stream>>>(a.z_hi, a.z_lo, a.u_bits, a.s_out, a.y, a.batch, a.m, a.wr,
-                                                          a.kpad);
+// NB batch rows of h per block (LDS holds 2 * NB * 128 * QW halves: NB * QW <= 128 keeps it
+// within 64 KB); larger batches take several passes over U.
+template <typename T, int QW>
+void launch_s2t(const GemvArgs& a) {
+    const int want = std::min(a.batch, 8);
+    int nb = want <= 1 ? 1 : (want <= 2 ? 2 : (want <= 4 ? 4 : 8));
+    while (nb > 1 && nb * QW > 128) nb >>= 1;
+    const dim3 grid(static_cast<unsigned>(ceil_div(a.m, 16)), static_cast<unsigned>(ceil_div(a.batch, nb)));
+    if (nb == 1)
+        s2t_kernel<T, QW, 1><<<grid, 256, 0, a.stream>>>(a.z_hi, a.z_lo, a.u_bits, a.s_out, a.y, a.batch, a.m,
+                                                          a.plan.wr, a.plan.zpitch);
+    else if (nb == 2)
+        s2t_kernel<T, QW, 2><<<grid, 256, 0, a.stream>>>(a.z_hi, a.z_lo, a.u_bits, a.s_out, a.y, a.batch, a.m,
+                                                          a.plan.wr, a.plan.zpitch);
+    else if (nb == 4)
+        s2t_kernel<T, QW, 4><<<grid, 256, 0, a.stream>>>(a.z_hi, a.z_lo, a.u_bits, a.s_out, a.y, a.batch, a.m,
+                                                          a.plan.wr, a.plan.zpitch);
+    else
+        s2t_kernel<T, QW, 8><<<grid, 256, 0, a.stream>>>(a.z_hi, a.z_lo, a.u_bits, a.s_out, a.y, a.batch, a.m,
+                                                          a.plan.wr, a.plan.zpitch);
 }
 
 template <typename T>
 void launch_stage2(const GemvArgs& a) {
-    const bool fast = aligned(a.z_hi, 16) && aligned(a.z_lo, 16) && aligned(a.u_bits, 16) && a.wr <= kS2MaxWr &&
-                      static_cast<int64_t>(a.m) * a.wr >= 4 && s2_dyn_lds(std::min(16, a.batch), a.kpad) <= 96 * 1024;
-    if (!fast) {
-        if (a.batch <= 1) launch_stage2_generic<T, 1>(a);
-        else if (a.batch <= 2) launch_stage2_generic<T, 2>(a);
-        else if (a.batch <= 4) launch_stage2_generic<T, 4>(a);
-        else launch_stage2_generic<T, kMaxNB>(a);
-        return;
+    const bool fast = aligned(a.z_hi, 16) && aligned(a.z_lo, 16) && aligned(a.u_bits, 16) &&
+                      static_cast<int64_t>(a.m) * a.plan.wr >= 4;
+    switch (fast ? a.plan.s2_qw : 0) {
+        case 2: launch_s2t<T, 2>(a); return;
+        case 4: launch_s2t<T, 4>(a); return;
+        case 6: launch_s2t<T, 6>(a); return;
+        case 8: launch_s2t<T, 8>(a); return;
+        case 10: launch_s2t<T, 10>(a); return;
+        case 12: launch_s2t<T, 12>(a); return;
+        case 14: launch_s2t<T, 14>(a); return;
+        case 16: launch_s2t<T, 16>(a); return;
+        case 20: launch_s2t<T, 20>(a); return;
+        case 24: launch_s2t<T, 24>(a); return;
+        case 28: launch_s2t<T, 28>(a); return;
+        case 32: launch_s2t<T, 32>(a); return;
+        case 36: launch_s2t<T, 36>(a); return;
+        default: break;
     }
-    if (a.wr <= 64) launch_s2_mfma<T, 4>(a);
-    else launch_s2_mfma<T, 8>(a);
+    if (a.batch <= 1) launch_stage2_generic<T, 1>(a);
+    else if (a.batch <= 2) launch_stage2_generic<T, 2>(a);
+    else if (a.batch <= 4) launch_stage2_generic<T, 4>(a);
+    else launch_stage2_generic<T, kMaxNB>(a);
 }
 
 template <typename T>
 int run_gemv(const GemvArgs& a) {
-    if (a.kpad > 0) {
+    if (a.r > 0) {
         launch_stage1<T>(a);
         if (int s = check_launch("nq_gemv stage 1")) return s;
     }
@@ -611,7 +655,7 @@ size_t nq_gemv_workspace_bytes(int64_t batch, int64_t n, int64_t r, int64_t m) {
     (void)n;
     (void)m;
     if (batch < 0 || r < 0) return 0;
-    return kHeaderBytes + 2 * z_bytes(batch, r);
+    return kHeaderBytes + 2 * z_bytes(batch, plan_of(r));
 }
 
 int nq_gemv(int dtype, const void* x, const void* s_in, const uint32_t* v_bits, const void* s_mid,
@@ -619,9 +663,10 @@ int nq_gemv(int dtype, const void* x, const void* s_in, const uint32_t* v_bits, 
             void* workspace, size_t workspace_bytes, nq_stream_t stream) {
     if (dtype != NQ_F16 && dtype != NQ_BF16) return fail(NQ_ERR_DTYPE, "nq_gemv: unsupported dtype %d", dtype);
     if (batch < 0 || n < 0 || r < 0 || m < 0) return fail(NQ_ERR_INVALID_ARGUMENT, "nq_gemv: negative size");
-    if (n > INT32_MAX / 2 || r > INT32_MAX / 2 || m > INT32_MAX / 2 || batch > INT32_MAX / 2 ||
-        batch * kpad_of(r) > INT32_MAX / 2)
-        return fail(NQ_ERR_UNSUPPORTED, "nq_gemv: sizes beyond 2^30 are not supported");
+    if (n > INT32_MAX / 4 || r > INT32_MAX / 4 || m > INT32_MAX / 4 || batch > INT32_MAX / 4 ||
+        batch * plan_of(r).zpitch > INT32_MAX / 4 || m * ceil_div(r, 32) > INT32_MAX / 4 ||
+        r * ceil_div(n, 32) > INT32_MAX / 4 || batch * n > INT32_MAX / 4)
+        return fail(NQ_ERR_UNSUPPORTED, "nq_gemv: sizes beyond 2^29 are not supported");
     if (batch == 0 || m == 0) return NQ_OK;
     if (!x || !s_in || !v_bits || !u_bits || !s_out || !y || !workspace)
         return fail(NQ_ERR_INVALID_ARGUMENT, "nq_gemv: null pointer");
@@ -645,11 +690,10 @@ int nq_gemv(int dtype, const void* x, const void* s_in, const uint32_t* v_bits, 
     a.r = static_cast<int>(r);
     a.m = static_cast<int>(m);
     a.wn = static_cast<int>(ceil_div(n, 32));
-    a.wr = static_cast<int>(ceil_div(r, 32));
-    a.kpad = static_cast<int>(kpad_of(r));
+    a.plan = plan_of(r);
     char* base = static_cast<char*>(workspace) + kHeaderBytes;
     a.z_hi = reinterpret_cast<uint16_t*>(base);
-    a.z_lo = reinterpret_cast<uint16_t*>(base + z_bytes(batch, r));
+    a.z_lo = reinterpret_cast<uint16_t*>(base + z_bytes(batch, a.plan));
     a.stream = as_stream(stream);
     return dtype == NQ_F16 ? run_gemv<F16>(a) : run_gemv<BF16>(a);
 }
