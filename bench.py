@@ -9,7 +9,13 @@ the timed region is bracketed by a device synchronisation on both sides and time
 with HIP events on the capture stream.
 
 The same JSON line carries:
-* ``roofline``: packed bytes per GEMV / measured time per GEMV against 8 TB/s;
+* ``value``: packed bytes per GEMV / measured time per GEMV (both launches), GB/s;
+* ``roofline``: the dominant kernel, stage 2 (U's sign words, 2.25 of the 3.08 MB),
+  timed on its own through ``nq_gemv_stage2`` in the same way: its packed bytes /
+  its time per launch against 8 TB/s; ``traffic`` is the HBM bytes per launch that
+  ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE`` measured for it, scaled by what the
+  same counters read for a copy of known size (``profiles/pmc_traffic.json``), when
+  that file describes this workload, else null;
 * ``gemm``: the prefill GEMM (``marlin_nanoquant_forward``) at B=2048 on the same
   shape, algorithmic TFLOP/s = 2*B*r*(n+m) / time, against 2.5 PFLOP/s dense fp16;
 * ``cpu_baseline``: the reference's dense dequantize-and-matmul forward (two
@@ -38,14 +44,23 @@ METRIC = "decode GEMV µs + % HBM roofline; prefill GEMM TFLOP/s (Llama-7B shape
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
 M, N, R = 11008, 4096, 1632  # Llama-2-7B gate_proj at 0.55 bpw: r = round32(0.55*m*n/(m+n))
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "pmc_traffic.json")
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def stage1_bytes(n, r):
+    return 4 * r * ((n + 31) // 32)
+
+
+def stage2_bytes(m, r):
+    return 4 * m * ((r + 31) // 32)
+
+
 def packed_bytes(m, n, r):
-    return 4 * r * ((n + 31) // 32) + 4 * m * ((r + 31) // 32)
+    return stage1_bytes(n, r) + stage2_bytes(m, r)
 
 
 def gemv_total_bytes(m, n, r, batch):
@@ -80,11 +95,11 @@ def time_graph(fn_steps, n_steps, replays, warmup_replays, stream):
     return start.elapsed_time(end) / (replays * n_steps), graph, outs
 
 
-def bench_gemv(args, dev, log_parity=True):
+def bench_gemv(args, dev):
     import nanoquant_amd as nq
     import oracle as O
+    from nanoquant_amd import _lib
 
-    dtype = torch.float16
     batch = args.batch
     c = O.random_case(2024, M, N, R, batch)
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
@@ -107,18 +122,41 @@ def bench_gemv(args, dev, log_parity=True):
     rel = float(np.abs(y_eager.double().cpu().numpy() - y64).max() / np.abs(y64).max())
 
     n_steps = args.copies
+    replays = max(1, args.steps // n_steps)
+    warm = max(1, args.warmup // n_steps)
 
     def steps():
         return [op(x, s_in, Vs[i], None, Us[i], s_out, **kw) for i in range(n_steps)]
 
-    replays = max(1, args.steps // n_steps)
-    warm = max(1, args.warmup // n_steps)
     stream = torch.cuda.Stream(device=dev)
     ms, graph, outs = time_graph(steps, n_steps, replays, warm, stream)
     graph_ok = bool(torch.equal(outs[0], y_eager))
+    del graph, outs
+
+    # each launch on its own, through the stage entry points, same rotation
+    lib = _lib.load()
+    ws = torch.zeros(lib.nq_gemv_workspace_bytes(batch, N, R, M), dtype=torch.uint8, device=dev)
+    y = torch.empty(batch, M, dtype=torch.float16, device=dev)
+
+    def stage1_steps():
+        st = torch.cuda.current_stream(dev).cuda_stream
+        for i in range(n_steps):
+            _lib.check(lib.nq_gemv_stage1(_lib.NQ_F16, x.data_ptr(), s_in.data_ptr(), Vs[i].data_ptr(), None, batch,
+                                          N, R, M, ws.data_ptr(), ws.numel(), st), "stage 1")
+
+    def stage2_steps():
+        st = torch.cuda.current_stream(dev).cuda_stream
+        for i in range(n_steps):
+            _lib.check(lib.nq_gemv_stage2(_lib.NQ_F16, Us[i].data_ptr(), s_out.data_ptr(), y.data_ptr(), batch, N,
+                                          R, M, ws.data_ptr(), ws.numel(), st), "stage 2")
+
+    ms1, g1, _ = time_graph(stage1_steps, n_steps, replays, warm, stream)
+    ms2, g2, _ = time_graph(stage2_steps, n_steps, replays, warm, stream)
+    del g1, g2
     pb = packed_bytes(M, N, R)
-    return dict(ms=ms, steps=replays * n_steps, warmup=warm * n_steps, rel_err=rel, graph_matches_eager=graph_ok,
-                packed_bytes=pb, total_bytes=gemv_total_bytes(M, N, R, batch), pool_bytes=pb * args.copies)
+    return dict(ms=ms, ms1=ms1, ms2=ms2, steps=replays * n_steps, warmup=warm * n_steps, rel_err=rel,
+                graph_matches_eager=graph_ok, packed_bytes=pb, total_bytes=gemv_total_bytes(M, N, R, batch),
+                pool_bytes=pb * args.copies)
 
 
 def bench_gemm(args, dev):
@@ -175,7 +213,35 @@ def cpu_baseline(args):
     gbs = packed_bytes(M, N, R) / med / 1e9
     return dict(value=round(gbs, 4), unit="GB/s", cores=cores, kind="port",
                 sample=f"oracle compute_forward_torch (reference dense path, linear.py:282-291), bf16, B=1, "
-                       f"m={M} n={N} r={R}; median of {len(times)} calls = {med * 1e6:.1f} us/GEMV")
+                       f"m={M} n={N} r={R}; median of {len(times)} calls = {med * 1e6:.1f} us/GEMV, packed bytes "
+                       f"of the factorised layer per call")
+
+
+def measured_traffic(batch):
+    """HBM bytes per launch of the stage-2 kernel from profiles/pmc_traffic.json, when it
+    describes this workload; else None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None, None
+    w = rec.get("workload", {})
+    if (w.get("m"), w.get("n"), w.get("r"), w.get("batch")) != (M, N, R, batch):
+        return None, None
+    k = rec.get("kernels", {}).get("gemv_stage2")
+    if not k:
+        return None, None
+    return int(k["fetch_bytes"] + k["write_bytes"]), rec.get("source")
+
+
+def calibration_copy(dev, mib):
+    """One device copy of a known size, for scaling PMC byte counters (run under rocprofv3)."""
+    src = torch.empty(mib << 20, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"[bench] calibration copy of {mib} MiB done")
 
 
 def main():
@@ -191,6 +257,8 @@ def main():
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="also run one device copy of this many MiB (PMC byte-counter calibration)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -211,7 +279,13 @@ def main():
     g = bench_gemv(args, dev)
     gemv_us = g["ms"] * 1e3
     achieved = g["packed_bytes"] / (g["ms"] * 1e-3) / 1e9
-    log(f"[bench] gemv {gemv_us:.3f} us/step, {achieved:.1f} GB/s packed, rel_err {g['rel_err']:.2e}")
+    s1_gbs = stage1_bytes(N, R) / (g["ms1"] * 1e-3) / 1e9
+    s2_gbs = stage2_bytes(M, R) / (g["ms2"] * 1e-3) / 1e9
+    log(f"[bench] gemv {gemv_us:.3f} us/step, {achieved:.1f} GB/s packed, rel_err {g['rel_err']:.2e}; "
+        f"stage 1 {g['ms1'] * 1e3:.3f} us ({s1_gbs:.1f} GB/s), stage 2 {g['ms2'] * 1e3:.3f} us ({s2_gbs:.1f} GB/s)")
+
+    if args.calib_copy_mib > 0:
+        calibration_copy(dev, args.calib_copy_mib)
 
     gemm = None
     if not args.skip_gemm:
@@ -230,6 +304,7 @@ def main():
         cpu = cpu_baseline(args)
         log(f"[bench] cpu {cpu['value']} GB/s ({cpu['sample']})")
 
+    traffic, traffic_src = measured_traffic(args.batch)
     line = {
         "metric": METRIC,
         "value": round(achieved, 2),
@@ -248,8 +323,15 @@ def main():
                                f"({g['pool_bytes'] / 1e6:.0f} MB) replayed in a HIP graph",
                    "m": M, "n": N, "r": R, "batch": args.batch, "copies": args.copies},
         "gemv_us": round(gemv_us, 4),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+        "roofline": {"bound": "hbm", "kernel": "GEMV stage 2 (s2t_kernel, U sign words)",
+                     "achieved": round(s2_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(s2_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "algorithmic_bytes": stage2_bytes(M, R), "us_per_launch": round(g["ms2"] * 1e3, 4),
+                     "traffic_source": traffic_src},
+        "gemv_stages": {"stage1_us": round(g["ms1"] * 1e3, 4), "stage1_gbs": round(s1_gbs, 2),
+                        "stage1_bytes": stage1_bytes(N, R), "stage2_us": round(g["ms2"] * 1e3, 4),
+                        "stage2_gbs": round(s2_gbs, 2), "stage2_bytes": stage2_bytes(M, R),
+                        "op_frac_of_hbm_peak": round(achieved / HBM_PEAK_GBS, 4)},
         "gemv_total_bytes_gbs": round(g["total_bytes"] / (g["ms"] * 1e-3) / 1e9, 2),
         "gemm": gemm,
         "cpu_baseline": cpu,

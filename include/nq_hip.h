@@ -109,6 +109,17 @@ int nq_gemv(int dtype, const void* x, const void* s_in, const uint32_t* v_bits, 
             const uint32_t* u_bits, const void* s_out, void* y, int64_t batch, int64_t n, int64_t r,
             int64_t m, void* workspace, size_t workspace_bytes, nq_stream_t stream);
 
+/* The two launches nq_gemv makes, one at a time, with the same arguments and workspace:
+ * stage 1 writes the intermediate h of x into the workspace, stage 2 turns the workspace's h
+ * into y. No counterpart in the reference (both are internal to nanoquant_dyn_forward,
+ * gemv_kernel.cu:365-401); they exist to time and profile each launch on its own and for
+ * callers that apply several U to one h. */
+int nq_gemv_stage1(int dtype, const void* x, const void* s_in, const uint32_t* v_bits, const void* s_mid,
+                   int64_t batch, int64_t n, int64_t r, int64_t m, void* workspace, size_t workspace_bytes,
+                   nq_stream_t stream);
+int nq_gemv_stage2(int dtype, const uint32_t* u_bits, const void* s_out, void* y, int64_t batch, int64_t n,
+                   int64_t r, int64_t m, void* workspace, size_t workspace_bytes, nq_stream_t stream);
+
 /* ---------------------------------------------------------------- prefill GEMM */
 
 /* C[M, N] = sat((A[M, K] * W) * s_out) with W[k, o] = sign(k, o) * s_in[k]:

@@ -47,6 +47,8 @@ SIGNATURES = {
     "nq_permute_marlin_scales": (_int, [_vp, _vp, _i64, _vp, _vp, _i64, _vp]),
     "nq_gemv_workspace_bytes": (_size, [_i64, _i64, _i64, _i64]),
     "nq_gemv": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _size, _vp]),
+    "nq_gemv_stage1": (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _size, _vp]),
+    "nq_gemv_stage2": (_int, [_int, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _size, _vp]),
     "nq_gemm_onebit": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "nq_gemm_nanoquant": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
 }

@@ -658,26 +658,35 @@ size_t nq_gemv_workspace_bytes(int64_t batch, int64_t n, int64_t r, int64_t m) {
     return kHeaderBytes + 2 * z_bytes(batch, plan_of(r));
 }
 
-int nq_gemv(int dtype, const void* x, const void* s_in, const uint32_t* v_bits, const void* s_mid,
-            const uint32_t* u_bits, const void* s_out, void* y, int64_t batch, int64_t n, int64_t r, int64_t m,
-            void* workspace, size_t workspace_bytes, nq_stream_t stream) {
-    if (dtype != NQ_F16 && dtype != NQ_BF16) return fail(NQ_ERR_DTYPE, "nq_gemv: unsupported dtype %d", dtype);
-    if (batch < 0 || n < 0 || r < 0 || m < 0) return fail(NQ_ERR_INVALID_ARGUMENT, "nq_gemv: negative size");
+}  // extern "C"
+
+namespace nq {
+namespace {
+
+enum Stages { kStage1 = 1, kStage2 = 2, kBoth = 3 };
+
+// Validates the arguments one or both stages use and fills `a`; returns NQ_OK, an error
+// status, or -1 when there is nothing to do.
+int setup_gemv(const char* name, int stages, int dtype, const void* x, const void* s_in, const uint32_t* v_bits,
+               const void* s_mid, const uint32_t* u_bits, const void* s_out, void* y, int64_t batch, int64_t n,
+               int64_t r, int64_t m, void* workspace, size_t workspace_bytes, nq_stream_t stream, GemvArgs& a) {
+    if (dtype != NQ_F16 && dtype != NQ_BF16) return fail(NQ_ERR_DTYPE, "%s: unsupported dtype %d", name, dtype);
+    if (batch < 0 || n < 0 || r < 0 || m < 0) return fail(NQ_ERR_INVALID_ARGUMENT, "%s: negative size", name);
     if (n > INT32_MAX / 4 || r > INT32_MAX / 4 || m > INT32_MAX / 4 || batch > INT32_MAX / 4 ||
         batch * plan_of(r).zpitch > INT32_MAX / 4 || m * ceil_div(r, 32) > INT32_MAX / 4 ||
         r * ceil_div(n, 32) > INT32_MAX / 4 || batch * n > INT32_MAX / 4)
-        return fail(NQ_ERR_UNSUPPORTED, "nq_gemv: sizes beyond 2^29 are not supported");
-    if (batch == 0 || m == 0) return NQ_OK;
-    if (!x || !s_in || !v_bits || !u_bits || !s_out || !y || !workspace)
-        return fail(NQ_ERR_INVALID_ARGUMENT, "nq_gemv: null pointer");
-    if (!aligned(workspace, 256)) return fail(NQ_ERR_ALIGNMENT, "nq_gemv: workspace must be 256-byte aligned");
-    if (!aligned(x, 2) || !aligned(s_in, 2) || !aligned(s_out, 2) || !aligned(y, 2) || !aligned(v_bits, 4) ||
-        !aligned(u_bits, 4) || (s_mid && !aligned(s_mid, 2)))
-        return fail(NQ_ERR_ALIGNMENT, "nq_gemv: misaligned operand");
+        return fail(NQ_ERR_UNSUPPORTED, "%s: sizes beyond 2^29 are not supported", name);
+    if (batch == 0 || (stages == kStage1 ? r == 0 : m == 0)) return -1;
+    const bool s1 = stages & kStage1, s2 = stages & kStage2;
+    if (!workspace || (s1 && (!x || !s_in || !v_bits)) || (s2 && (!u_bits || !s_out || !y)))
+        return fail(NQ_ERR_INVALID_ARGUMENT, "%s: null pointer", name);
+    if (!aligned(workspace, 256)) return fail(NQ_ERR_ALIGNMENT, "%s: workspace must be 256-byte aligned", name);
+    if ((s1 && (!aligned(x, 2) || !aligned(s_in, 2) || !aligned(v_bits, 4) || (s_mid && !aligned(s_mid, 2)))) ||
+        (s2 && (!aligned(s_out, 2) || !aligned(y, 2) || !aligned(u_bits, 4))))
+        return fail(NQ_ERR_ALIGNMENT, "%s: misaligned operand", name);
     const size_t need = nq_gemv_workspace_bytes(batch, n, r, m);
     if (workspace_bytes < need)
-        return fail(NQ_ERR_WORKSPACE, "nq_gemv: workspace has %zu bytes, needs %zu", workspace_bytes, need);
-    GemvArgs a;
+        return fail(NQ_ERR_WORKSPACE, "%s: workspace has %zu bytes, needs %zu", name, workspace_bytes, need);
     a.x = static_cast<const uint16_t*>(x);
     a.s_in = static_cast<const uint16_t*>(s_in);
     a.v_bits = v_bits;
@@ -695,7 +704,53 @@ int nq_gemv(int dtype, const void* x, const void* s_in, const uint32_t* v_bits, 
     a.z_hi = reinterpret_cast<uint16_t*>(base);
     a.z_lo = reinterpret_cast<uint16_t*>(base + z_bytes(batch, a.plan));
     a.stream = as_stream(stream);
+    return NQ_OK;
+}
+
+template <typename T>
+int run_stage1(const GemvArgs& a) {
+    launch_stage1<T>(a);
+    return check_launch("nq_gemv stage 1");
+}
+
+template <typename T>
+int run_stage2(const GemvArgs& a) {
+    launch_stage2<T>(a);
+    return check_launch("nq_gemv stage 2");
+}
+
+}  // namespace
+}  // namespace nq
+
+extern "C" {
+
+int nq_gemv(int dtype, const void* x, const void* s_in, const uint32_t* v_bits, const void* s_mid,
+            const uint32_t* u_bits, const void* s_out, void* y, int64_t batch, int64_t n, int64_t r, int64_t m,
+            void* workspace, size_t workspace_bytes, nq_stream_t stream) {
+    GemvArgs a;
+    const int s = setup_gemv("nq_gemv", kBoth, dtype, x, s_in, v_bits, s_mid, u_bits, s_out, y, batch, n, r, m,
+                             workspace, workspace_bytes, stream, a);
+    if (s != NQ_OK) return s < 0 ? NQ_OK : s;
     return dtype == NQ_F16 ? run_gemv<F16>(a) : run_gemv<BF16>(a);
+}
+
+int nq_gemv_stage1(int dtype, const void* x, const void* s_in, const uint32_t* v_bits, const void* s_mid,
+                   int64_t batch, int64_t n, int64_t r, int64_t m, void* workspace, size_t workspace_bytes,
+                   nq_stream_t stream) {
+    GemvArgs a;
+    const int s = setup_gemv("nq_gemv_stage1", kStage1, dtype, x, s_in, v_bits, s_mid, nullptr, nullptr, nullptr,
+                             batch, n, r, m, workspace, workspace_bytes, stream, a);
+    if (s != NQ_OK) return s < 0 ? NQ_OK : s;
+    return dtype == NQ_F16 ? run_stage1<F16>(a) : run_stage1<BF16>(a);
+}
+
+int nq_gemv_stage2(int dtype, const uint32_t* u_bits, const void* s_out, void* y, int64_t batch, int64_t n, int64_t r,
+                   int64_t m, void* workspace, size_t workspace_bytes, nq_stream_t stream) {
+    GemvArgs a;
+    const int s = setup_gemv("nq_gemv_stage2", kStage2, dtype, nullptr, nullptr, nullptr, nullptr, u_bits, s_out, y,
+                             batch, n, r, m, workspace, workspace_bytes, stream, a);
+    if (s != NQ_OK) return s < 0 ? NQ_OK : s;
+    return dtype == NQ_F16 ? run_stage2<F16>(a) : run_stage2<BF16>(a);
 }
 
 }  // extern "C"

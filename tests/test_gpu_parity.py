@@ -189,6 +189,27 @@ def test_gemv_parity(nq, case, dtype):
     assert err <= TOL[("gemv", dtype)], err
 
 
+@pytest.mark.parametrize("shape", [(4096, 4096, 1024, 1), (130, 200, 70, 5), (11008, 4096, 1632, 3)])
+def test_gemv_stage_entry_points_match_nq_gemv(nq, shape):
+    """nq_gemv_stage1 then nq_gemv_stage2 give nq_gemv's output bit for bit."""
+    from nanoquant_amd import _lib
+    m, n, r, B = shape
+    announce("gemv stages", shape)
+    c = O.random_case(15, m, n, r, B, with_mid=True)
+    y, U_bits, V_bits = gemv_run(nq, c, torch.float16)
+    lib = _lib.load()
+    x, s_in, s_mid, s_out = dev_t(c["x"]), dev_t(c["s_in"]), dev_t(c["s_mid"]), dev_t(c["s_out"])
+    ws = torch.zeros(lib.nq_gemv_workspace_bytes(B, n, r, m), dtype=torch.uint8, device="cuda")
+    y2 = torch.empty_like(y)
+    st = _lib.stream_of(x.device)
+    _lib.check(lib.nq_gemv_stage1(_lib.NQ_F16, x.data_ptr(), s_in.data_ptr(), V_bits.data_ptr(), s_mid.data_ptr(), B,
+                                  n, r, m, ws.data_ptr(), ws.numel(), st), "stage1")
+    _lib.check(lib.nq_gemv_stage2(_lib.NQ_F16, U_bits.data_ptr(), s_out.data_ptr(), y2.data_ptr(), B, n, r, m,
+                                  ws.data_ptr(), ws.numel(), st), "stage2")
+    torch.cuda.synchronize()
+    assert torch.equal(y2.view(torch.int16), y.view(torch.int16))
+
+
 def test_gemv_1d_and_3d_inputs(nq):
     announce("gemv shapes")
     c = O.random_case(12, 96, 64, 32, 6)
