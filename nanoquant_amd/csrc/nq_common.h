@@ -31,6 +31,7 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // Storage of both 16-bit float formats is uint16_t; the tag selects the arithmetic.
@@ -80,6 +81,23 @@ __device__ inline f32x4 mfma16x16x32<F16>(u32x4 a, u32x4 b, f32x4 c) {
 template <>
 __device__ inline f32x4 mfma16x16x32<BF16>(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                   0, 0);
+}
+
+// v_mfma_f32_32x32x16_{f16,bf16}: lane l holds A[row l%32][k 8(l/32)..+7], B[k 8(l/32)..+7][col l%32]
+// as four dwords each, and C[row 8(i/4) + 4(l/32) + i%4][col l%32] in register i (i < 16).
+template <typename T>
+__device__ inline f32x16 mfma32x32x16(u32x4 a, u32x4 b, f32x16 c);
+
+template <>
+__device__ inline f32x16 mfma32x32x16<F16>(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                                  0);
+}
+
+template <>
+__device__ inline f32x16 mfma32x32x16<BF16>(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
                                                    0, 0);
 }
 

@@ -184,6 +184,206 @@ int launch_onebit(const void* A, const uint32_t* W, const void* s_in, const void
     return check_launch("nq_gemm_onebit");
 }
 
+// ---------------------------------------------------------------------------- 32x32x16 kernel
+//
+// C[q, o] = sat(s_out[o] * sum_k A[q, k] * sign(k, o) * s_in[k]), computed as C^T = S * A^T on
+// v_mfma_f32_32x32x16: the MFMA's A operand is 32 output features by 16 k of +-s_in, made from
+// the Marlin words in registers; its B operand is 16 k by 32 rows of A, from a double-buffered
+// LDS tile. Lane l = (kg = l / 32, c = l % 32).
+//   sign operand: feature o = o0 + c; dword d = (r8 = d / 2, r2 = 2kg + d % 2) holds the pair
+//     k = 16tr + 8r8 + 2r2 + {0, 1}: Marlin word (tr, 32(o/64) + 4(o%8) + r2) shifted left by
+//     2((o%16)/8) + 4((o%64)/16) + r8 has their signs on bits 15 and 31, and they go onto the
+//     permuted s_in pair at 16tr + 4r2 + 2r8 (one 16-byte load per (tr, kg) covers all four);
+//   A operand: row q0 + c, the same k: A[q][16tr + 4kg .. +3] and A[q][16tr + 8 + 4kg .. +3];
+//   C: lane holds C^T[o0 + 8(i/4) + 4kg + i%4][q0 + c], four consecutive features per group of
+//      four registers, stored as one 8-byte write of C[q][o .. o+3].
+// The grid runs q tiles fastest: blocks i, i+8, ... land on one XCD, so with q_tiles dividing
+// 8 or a multiple of 8 each XCD streams its own rows of A through its L2.
+template <typename T, bool kSin, bool kSout, int BP, int BQ, int WP, int WQ, int BKK>
+__global__ __launch_bounds__((BP / WP) * (BQ / WQ) * 64) void gemm_sx_kernel(
+    const uint16_t* __restrict__ A, const uint32_t* __restrict__ W, const uint16_t* __restrict__ s_in,
+    const uint16_t* __restrict__ s_out, uint16_t* __restrict__ C, int M, int K, int N, int q_tiles) {
+    constexpr int NWP = BP / WP;
+    constexpr int NWQ = BQ / WQ;
+    constexpr int NT = NWP * NWQ * 64;
+    constexpr int TP = WP / 32;
+    constexpr int TQ = WQ / 32;
+    constexpr int KT = BKK / 16;          // 16-k tiles per iteration
+    constexpr int LDX = BKK + 8;          // LDS row pitch of the A tile in halves
+    constexpr int XPIECES = BQ * BKK / 8; // 16-byte pieces of the A tile
+    constexpr int XPT = XPIECES / NT;
+    static_assert(XPIECES % NT == 0, "tile pieces must divide evenly");
+    __shared__ __attribute__((aligned(16))) uint16_t xs[2][BQ * LDX];
+    __shared__ uint16_t sos[BP];
+
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int c = lane & 31;
+    const int kg = lane >> 5;
+    const int wp = wave % NWP;
+    const int wq = wave / NWP;
+    const int qt = blockIdx.x % q_tiles;
+    const int pt = blockIdx.x / q_tiles;
+    const int q0 = qt * BQ;
+    const int p0 = pt * BP;
+    const uint32_t half_n = static_cast<uint32_t>(N) >> 1;
+    const int k_iters = K / BKK;
+
+    int wcol[TP], shb[TP];
+#pragma unroll
+    for (int tp = 0; tp < TP; ++tp) {
+        const int o = min(p0 + wp * WP + 32 * tp + c, N - 1);
+        wcol[tp] = 32 * (o >> 6) + 4 * (o & 7) + 2 * kg;
+        shb[tp] = 2 * ((o & 15) >> 3) + 4 * ((o & 63) >> 4);
+    }
+    const uint16_t* xsrc[XPT];
+    int xdst[XPT];
+#pragma unroll
+    for (int j = 0; j < XPT; ++j) {
+        const int piece = t + j * NT;
+        const int row = piece / (BKK / 8);
+        const int c8 = piece - row * (BKK / 8);
+        xsrc[j] = A + static_cast<size_t>(min(q0 + row, M - 1)) * K + 8 * c8;
+        xdst[j] = row * LDX + 8 * c8;
+    }
+    for (int e = t; e < BP; e += NT) sos[e] = kSout ? s_out[perm_out(min(p0 + e, N - 1))] : uint16_t(0);
+
+    // Operands of an iteration: the A tile (to LDS) and the sign words and s_in pairs (kept in
+    // registers). They are loaded two iterations ahead, so a load has two iterations of MFMAs
+    // to land before its LDS write, and the sign operand of iteration it is in registers when
+    // it starts.
+    struct Ops {
+        u32x4 x[XPT];
+        uint2 w[TP][KT];
+        u32x4 s[KT];
+    };
+    auto load_ops = [&](Ops& o, int iter) {
+        const int k0 = iter * BKK;
+#pragma unroll
+        for (int j = 0; j < XPT; ++j) o.x[j] = *reinterpret_cast<const u32x4*>(xsrc[j] + k0);
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) {
+            const uint32_t tr = static_cast<uint32_t>(iter * KT + kt);
+#pragma unroll
+            for (int tp = 0; tp < TP; ++tp) o.w[tp][kt] = *reinterpret_cast<const uint2*>(W + tr * half_n + wcol[tp]);
+            o.s[kt] = kSin ? *reinterpret_cast<const u32x4*>(s_in + 16 * tr + 8 * kg)
+                           : u32x4{T::ONE_PAIR, T::ONE_PAIR, T::ONE_PAIR, T::ONE_PAIR};
+        }
+    };
+    Ops cur, nxt, nn;
+    load_ops(cur, 0);
+    if (k_iters > 1) load_ops(nxt, 1);
+#pragma unroll
+    for (int j = 0; j < XPT; ++j) *reinterpret_cast<u32x4*>(&xs[0][xdst[j]]) = cur.x[j];
+    __syncthreads();
+
+    f32x16 acc[TP][TQ];
+#pragma unroll
+    for (int tp = 0; tp < TP; ++tp)
+#pragma unroll
+        for (int tq = 0; tq < TQ; ++tq)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[tp][tq][i] = 0.0f;
+
+    const uint32_t mask = 0x80008000u;
+    for (int it = 0; it < k_iters; ++it) {
+        const int buf = it & 1;
+        if (it + 2 < k_iters) load_ops(nn, it + 2);
+        __builtin_amdgcn_sched_barrier(0);
+
+        const uint16_t* xb = &xs[buf][(wq * WQ + c) * LDX + 4 * kg];
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) {
+            u32x4 bx[TQ];
+#pragma unroll
+            for (int tq = 0; tq < TQ; ++tq) {
+                const uint16_t* p = xb + 32 * tq * LDX + 16 * kt;
+                const uint2 lo = *reinterpret_cast<const uint2*>(p);
+                const uint2 hi = *reinterpret_cast<const uint2*>(p + 8);
+                bx[tq] = u32x4{lo.x, lo.y, hi.x, hi.y};
+            }
+#pragma unroll
+            for (int tp = 0; tp < TP; ++tp) {
+                const uint32_t w0 = cur.w[tp][kt].x, w1 = cur.w[tp][kt].y;
+                const int sft = shb[tp];
+                const u32x4 sv = cur.s[kt];
+                const u32x4 a = u32x4{sv.x ^ ((w0 << sft) & mask), sv.z ^ ((w1 << sft) & mask),
+                                      sv.y ^ ((w0 << (sft + 1)) & mask), sv.w ^ ((w1 << (sft + 1)) & mask)};
+#pragma unroll
+                for (int tq = 0; tq < TQ; ++tq) acc[tp][tq] = mfma32x32x16<T>(a, bx[tq], acc[tp][tq]);
+            }
+        }
+
+        if (it + 1 < k_iters) {
+#pragma unroll
+            for (int j = 0; j < XPT; ++j) *reinterpret_cast<u32x4*>(&xs[buf ^ 1][xdst[j]]) = nxt.x[j];
+        }
+        cur = nxt;
+        nxt = nn;
+        __syncthreads();
+    }
+
+    // epilogue: scale, saturate, four consecutive features per 8-byte store
+#pragma unroll
+    for (int tp = 0; tp < TP; ++tp)
+#pragma unroll
+        for (int tq = 0; tq < TQ; ++tq) {
+            const int q = q0 + wq * WQ + 32 * tq + c;
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const int ol = wp * WP + 32 * tp + 8 * g4 + 4 * kg;  // feature offset in the block
+                const int o = p0 + ol;
+                uint16_t h[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float sc = kSout ? T::to_float(sos[ol + e]) : 1.0f;
+                    h[e] = saturate_to<T>(acc[tp][tq][4 * g4 + e] * sc, T::SAT_GEMM);
+                }
+                if (q < M && o < N) {
+                    uint2 v;
+                    v.x = static_cast<uint32_t>(h[0]) | (static_cast<uint32_t>(h[1]) << 16);
+                    v.y = static_cast<uint32_t>(h[2]) | (static_cast<uint32_t>(h[3]) << 16);
+                    *reinterpret_cast<uint2*>(C + static_cast<size_t>(q) * N + o) = v;
+                }
+            }
+        }
+}
+
+template <typename T, int BP, int BQ, int WP, int WQ, int BKK = 64>
+void launch_sx(const void* A, const uint32_t* W, const void* s_in, const void* s_out, void* C, int64_t M, int64_t K,
+               int64_t N, hipStream_t stream) {
+    const int q_tiles = static_cast<int>(ceil_div(M, BQ));
+    const int p_tiles = static_cast<int>(ceil_div(N, BP));
+    const dim3 grid(static_cast<unsigned>(q_tiles * p_tiles));
+    constexpr int NT = (BP / WP) * (BQ / WQ) * 64;
+    const auto* a = static_cast<const uint16_t*>(A);
+    const auto* si = static_cast<const uint16_t*>(s_in);
+    const auto* so = static_cast<const uint16_t*>(s_out);
+    auto* c = static_cast<uint16_t*>(C);
+    const int m = static_cast<int>(M), k = static_cast<int>(K), n = static_cast<int>(N);
+    if (s_in && s_out)
+        gemm_sx_kernel<T, true, true, BP, BQ, WP, WQ, BKK><<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles);
+    else if (s_in)
+        gemm_sx_kernel<T, true, false, BP, BQ, WP, WQ, BKK><<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles);
+    else if (s_out)
+        gemm_sx_kernel<T, false, true, BP, BQ, WP, WQ, BKK><<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles);
+    else
+        gemm_sx_kernel<T, false, false, BP, BQ, WP, WQ, BKK><<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles);
+}
+
+// The 32x32x16 kernel needs whole 64-k iterations, 16-byte s_in pairs loads, 8-byte output
+// stores and 32-bit word offsets; anything else runs on the 16x16x32 kernel.
+template <typename T>
+int launch_gemm(const char* name, const void* A, const uint32_t* W, const void* s_in, const void* s_out, void* C,
+                int64_t M, int64_t K, int64_t N, hipStream_t stream) {
+    const bool sx = K % 64 == 0 && K > 0 && (!s_in || aligned(s_in, 16)) && aligned(C, 8) &&
+                    (K / 16) * (N / 2) < ((int64_t)1 << 31);
+    if (!sx) return launch_onebit<T>(A, W, s_in, s_out, C, M, K, N, stream);
+    launch_sx<T, 128, 128, 64, 64, 64>(A, W, s_in, s_out, C, M, K, N, stream);
+    return check_launch(name);
+}
+
 int check_onebit(const char* name, int dtype, const void* A, const uint32_t* W, const void* s_in, const void* s_out,
                  const void* C, int64_t M, int64_t K, int64_t N) {
     if (dtype != NQ_F16 && dtype != NQ_BF16) return fail(NQ_ERR_DTYPE, "%s: unsupported dtype %d", name, dtype);
@@ -212,8 +412,9 @@ int nq_gemm_onebit(int dtype, const void* A, const uint32_t* w_bits, const void*
                    int64_t M, int64_t K, int64_t N, nq_stream_t stream) {
     if (int s = check_onebit("nq_gemm_onebit", dtype, A, w_bits, s_in, s_out, C, M, K, N)) return s;
     if (M == 0 || N == 0) return NQ_OK;
-    if (dtype == NQ_F16) return launch_onebit<F16>(A, w_bits, s_in, s_out, C, M, K, N, as_stream(stream));
-    return launch_onebit<BF16>(A, w_bits, s_in, s_out, C, M, K, N, as_stream(stream));
+    hipStream_t st = as_stream(stream);
+    if (dtype == NQ_F16) return launch_gemm<F16>("nq_gemm_onebit", A, w_bits, s_in, s_out, C, M, K, N, st);
+    return launch_gemm<BF16>("nq_gemm_onebit", A, w_bits, s_in, s_out, C, M, K, N, st);
 }
 
 int nq_gemm_nanoquant(int dtype, const void* A, const uint32_t* v_bits, const uint32_t* u_bits, const void* s_g,
@@ -224,12 +425,13 @@ int nq_gemm_nanoquant(int dtype, const void* A, const uint32_t* v_bits, const ui
     if (M == 0 || m == 0) return NQ_OK;
     hipStream_t st = as_stream(stream);
     if (r_pad > 0) {
-        const int s1 = dtype == NQ_F16 ? launch_onebit<F16>(A, v_bits, s_g, s_l, imm, M, n, r_pad, st)
-                                       : launch_onebit<BF16>(A, v_bits, s_g, s_l, imm, M, n, r_pad, st);
+        const int s1 = dtype == NQ_F16
+                           ? launch_gemm<F16>("nq_gemm_nanoquant stage 1", A, v_bits, s_g, s_l, imm, M, n, r_pad, st)
+                           : launch_gemm<BF16>("nq_gemm_nanoquant stage 1", A, v_bits, s_g, s_l, imm, M, n, r_pad, st);
         if (s1) return s1;
     }
-    return dtype == NQ_F16 ? launch_onebit<F16>(imm, u_bits, nullptr, s_h, C, M, r_pad, m, st)
-                           : launch_onebit<BF16>(imm, u_bits, nullptr, s_h, C, M, r_pad, m, st);
+    return dtype == NQ_F16 ? launch_gemm<F16>("nq_gemm_nanoquant stage 2", imm, u_bits, nullptr, s_h, C, M, r_pad, m, st)
+                           : launch_gemm<BF16>("nq_gemm_nanoquant stage 2", imm, u_bits, nullptr, s_h, C, M, r_pad, m, st);
 }
 
 }  // extern "C"

@@ -289,10 +289,12 @@ def test_gemm_parity(nq, case, dtype):
     assert err <= TOL[("gemm", dtype)], err
 
 
+@pytest.mark.parametrize("K", [96, 192], ids=["k96_mfma16", "k192_mfma32"])
 @pytest.mark.parametrize("scales", ["none", "in", "out", "both"])
-def test_gemm_onebit_scale_variants(nq, scales):
-    announce("gemm onebit", scales)
-    B, K, N = 33, 96, 192
+def test_gemm_onebit_scale_variants(nq, scales, K):
+    # K % 64 != 0 runs the 16x16x32 kernel, K % 64 == 0 the 32x32x16 one
+    announce("gemm onebit", scales, K)
+    B, N = 33, 192
     rng = np.random.default_rng(5)
     w = np.where(rng.random((N, K)) < 0.5, -1, 1).astype(np.int8)
     s_in = np.abs(rng.normal(1, 0.2, K)).astype(np.float16)
