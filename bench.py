@@ -18,6 +18,10 @@ The same JSON line carries:
   that file describes this workload, else null;
 * ``gemm``: the prefill GEMM (``marlin_nanoquant_forward``) at B=2048 on the same
   shape, algorithmic TFLOP/s = 2*B*r*(n+m) / time, against 2.5 PFLOP/s dense fp16;
+* ``decode_e2e``: greedy decode of a random-init Llama-2-7B-architecture model with
+  every linear NanoQuant-factorised at 0.55 bpw (prompt 128, 256 new tokens, batch 1),
+  tokens/s as the reference's decode harness reports it, with the bytes one step must
+  read against 8 TB/s;
 * ``cpu_baseline``: the reference's dense dequantize-and-matmul forward (two
   ``F.linear`` on dense +-1 bf16 factors, modules/linear.py:282-291) on the host
   cores, batch 1, on a bounded sample, in the same unit;
@@ -244,6 +248,56 @@ def calibration_copy(dev, mib):
     log(f"[bench] calibration copy of {mib} MiB done")
 
 
+def bench_decode(args, dev):
+    """Greedy decode of a random-init Llama-2-7B-architecture model (32 layers, hidden 4096,
+    32 heads, FFN 11008, vocab 32000) with all seven linears per layer NanoQuant-factorised at
+    0.55 bpw on the GEMV kernel: prompt of ``--e2e-prompt`` uniform-random ids, then
+    ``--e2e-new`` tokens, the one-token step replayed from a HIP graph.
+    tokens/s = B * (new - 1) / decode wall time, as the reference's harness reports it."""
+    from nanoquant_amd.decode import LlamaShape, generate, random_llama
+
+    shape = LlamaShape()
+    t0 = time.perf_counter()
+    model = random_llama(shape, bpw=0.55, seed=0, device=dev, kernel_type="gemv", dtype=torch.float16)
+    torch.cuda.synchronize(dev)
+    build_s = time.perf_counter() - t0
+    B, T, new = args.e2e_batch, args.e2e_prompt, args.e2e_new
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1)
+    prompt = torch.randint(0, shape.vocab, (B, T), device=dev, generator=gen)
+    runs = {}
+    for spg in sorted({1, args.e2e_steps_per_graph}):
+        if (new - 1) % spg:
+            continue
+        generate(model, prompt, 1 + spg, steps_per_graph=spg)  # warm-up of the kernels and allocator
+        ids, tps, prof = generate(model, prompt, new, steps_per_graph=spg)
+        runs[spg] = (tps, prof, ids)
+        log(f"[bench] decode e2e B={B} steps/graph={spg}: {tps:.1f} tok/s, {prof['ms_per_token']:.3f} ms/token")
+    best = max(runs, key=lambda k: runs[k][0])
+    tps, prof, ids = runs[best]
+    same = all(torch.equal(r[2], ids) for r in runs.values())
+    # bytes one step must read: packed sign words and scales of every linear, the fp16
+    # lm_head, one embedding row, and the K/V cache up to the step's position (mean over steps)
+    lin_bytes = 0
+    for lin in model.linears():
+        lin_bytes += (lin.U_int8.numel() + lin.V_int8.numel()) * 4
+        lin_bytes += 2 * (lin.scale_pre.numel() + lin.scale_post.numel())
+    head_bytes = model.lm_head.weight.numel() * 2 + shape.hidden * 2
+    mean_pos = T + (new - 1) / 2.0
+    kv_bytes = 2 * shape.layers * B * shape.kv_heads * shape.head_dim * 2 * mean_pos
+    step_bytes = lin_bytes + head_bytes + kv_bytes
+    gbs = step_bytes / (prof["ms_per_token"] * 1e-3) / 1e9
+    return {"model": "random-init Llama-2-7B architecture, 7 NanoQuant linears per layer at 0.55 bpw (GEMV kernel)",
+            "batch": B, "prompt": T, "new_tokens": new, "tokens_per_s": round(tps, 2),
+            "ms_per_token": round(prof["ms_per_token"], 4), "steps_per_graph": best,
+            "tokens_per_s_by_steps_per_graph": {str(k): round(v[0], 2) for k, v in runs.items()},
+            "same_tokens_across_graph_sizes": bool(same), "prefill_s": round(prof["prefill_time_s_wall"], 4),
+            "model_build_s": round(build_s, 2),
+            "roofline": {"bound": "hbm", "bytes_per_step": int(step_bytes), "achieved": round(gbs, 2),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "tokens_per_s_at_peak": round(B * HBM_PEAK_GBS * 1e9 / step_bytes, 1)}}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -257,6 +311,11 @@ def main():
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--skip-decode", action="store_true", help="skip the end-to-end decode measurement")
+    ap.add_argument("--e2e-batch", type=int, default=1)
+    ap.add_argument("--e2e-prompt", type=int, default=128)
+    ap.add_argument("--e2e-new", type=int, default=256)
+    ap.add_argument("--e2e-steps-per-graph", type=int, default=15)
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="also run one device copy of this many MiB (PMC byte-counter calibration)")
     args = ap.parse_args()
@@ -298,6 +357,11 @@ def main():
                 "flops_per_call": gm["flops"], "r_pad": gm["r_pad"], "rel_err": gm["rel_err"]}
         log(f"[bench] gemm {gm['ms'] * 1e3:.1f} us, {gm['tflops']:.1f} TFLOP/s, rel_err {gm['rel_err']:.2e}")
 
+    decode = None
+    if not args.skip_decode:
+        log(f"[bench] decode e2e B={args.e2e_batch} prompt={args.e2e_prompt} new={args.e2e_new}")
+        decode = bench_decode(args, dev)
+
     cpu = None
     if not args.skip_cpu:
         log("[bench] cpu baseline")
@@ -334,6 +398,7 @@ def main():
                         "op_frac_of_hbm_peak": round(achieved / HBM_PEAK_GBS, 4)},
         "gemv_total_bytes_gbs": round(g["total_bytes"] / (g["ms"] * 1e-3) / 1e9, 2),
         "gemm": gemm,
+        "decode_e2e": decode,
         "cpu_baseline": cpu,
         "parity": {"gemv_rel_err": g["rel_err"], "gemv_graph_matches_eager": g["graph_matches_eager"],
                    "gemm_rel_err": None if gemm is None else gemm["rel_err"], "bar": 1e-3},

@@ -1,0 +1,382 @@
+"""Greedy decode of a Llama-2-architecture model whose seven linears per layer are
+``NanoQuantLinear``, with the one-token step replayed from a HIP graph.
+
+This is the decode harness of the reference (``src/nanoquant/kernel/test_decode.py``):
+one prefill forward over the prompt, then one-token steps on a static KV cache
+(``make_cache`` :420-422, ``generate`` :474-693), reporting
+``tokens/s = B * (new - 1) / decode wall time`` (:617, :684-685). The reference wraps
+a Hugging Face ``LlamaForCausalLM`` and compiles its step with
+``torch.compile(mode="reduce-overhead")`` (:385-402). Here the whole step (embedding,
+every layer, final norm, lm_head, greedy argmax, the KV-cache write, the token and
+position update) is recorded once into a ``torch.cuda.CUDAGraph`` (a HIP graph on
+ROCm) and replayed per token: the position lives in a device tensor, so replays need
+no host synchronisation and several steps can be recorded into one graph.
+
+The layers follow Hugging Face's Llama (RMSNorm in fp32, rotate-half RoPE, SiLU-gated
+MLP, grouped-query attention, untied lm_head) and keep its module names
+(``model.layers.{i}.self_attn.q_proj`` ...), so the packed state dict of a converted
+checkpoint maps onto this model key for key.
+"""
+from __future__ import annotations
+
+import math
+import time
+from dataclasses import dataclass
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .modules.linear import NanoQuantLinear
+
+LINEAR_NAMES = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
+
+
+@dataclass(frozen=True)
+class LlamaShape:
+    """Architecture sizes (defaults: Llama-2-7B)."""
+
+    hidden: int = 4096
+    layers: int = 32
+    heads: int = 32
+    kv_heads: int = 32
+    ffn: int = 11008
+    vocab: int = 32000
+    rms_eps: float = 1e-5
+    rope_theta: float = 10000.0
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden // self.heads
+
+    def linear_shapes(self):
+        """(name, in_features, out_features) of the seven linears of one layer."""
+        h, kv = self.hidden, self.kv_heads * self.head_dim
+        return (("q_proj", h, h), ("k_proj", h, kv), ("v_proj", h, kv), ("o_proj", h, h),
+                ("gate_proj", h, self.ffn), ("up_proj", h, self.ffn), ("down_proj", self.ffn, h))
+
+
+def rank_for_bpw(out_features: int, in_features: int, bpw: float) -> int:
+    """Rank whose two sign factors cost ``bpw`` bits per weight, rounded to a multiple of 32.
+
+    r = round32(bpw * m * n / (m + n)): 1632 for 11008x4096 and 1120 for 4096x4096 at 0.55.
+    """
+    r = bpw * out_features * in_features / (out_features + in_features)
+    return max(32, int(round(r / 32.0)) * 32)
+
+
+def random_nanoquant_linear(in_features: int, out_features: int, rank: int, generator: torch.Generator,
+                            device, with_mid: bool = False) -> NanoQuantLinear:
+    """A NanoQuantLinear in its dense (unpacked) state with random +-1 factors.
+
+    Scales are |N(1, 0.2)| divided by sqrt(in_features) (scale_pre) and sqrt(rank)
+    (scale_post), so an input of unit RMS gives an output of about unit RMS.
+    """
+    # the state init_for_inference (linear.py:116-129) leaves, without its placeholder tensors
+    lin = nn.Linear(in_features, out_features, bias=False, device="meta")
+    lin.__class__ = NanoQuantLinear
+    lin.rank, lin.do_train, lin._binarized, lin.dtype = rank, False, True, torch.float32
+    del lin._parameters["weight"]
+    lin.register_parameter("weight", None)
+    kw = dict(device=device, generator=generator)
+
+    def signs(rows, cols):
+        return torch.randint(0, 2, (rows, cols), dtype=torch.int8, **kw).mul_(2).sub_(1).float()
+
+    def scales(k, div):
+        return (torch.randn(1, k, **kw) * 0.2 + 1.0).abs_() / div
+
+    lin.V = nn.Parameter(signs(rank, in_features), requires_grad=False)
+    lin.U = nn.Parameter(signs(out_features, rank), requires_grad=False)
+    lin.scale_pre = nn.Parameter(scales(in_features, math.sqrt(in_features)), requires_grad=False)
+    lin.scale_post = nn.Parameter(scales(out_features, math.sqrt(rank)), requires_grad=False)
+    if with_mid:
+        lin.scale_mid = nn.Parameter(scales(rank, 1.0), requires_grad=False)
+    return lin
+
+
+class RMSNorm(nn.Module):
+    """Hugging Face LlamaRMSNorm: normalise in fp32, cast back, then scale."""
+
+    def __init__(self, dim: int, eps: float, device=None, dtype=torch.float32):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(dim, device=device, dtype=dtype), requires_grad=False)
+        self.eps = eps
+
+    def forward(self, x):
+        xf = x.float()
+        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
+        return self.weight * xf.to(x.dtype)
+
+
+def _rotate_half(x):
+    h = x.shape[-1] // 2
+    return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
+
+
+class StaticKVCache:
+    """Per-layer K and V of ``batch`` sequences up to ``max_len`` positions.
+
+    K is kept transposed, [B, kv_heads, head_dim, max_len], so the score product
+    q @ K reads a contiguous right operand; V is [B, kv_heads, max_len, head_dim].
+    Mirrors ``make_cache`` (test_decode.py:420-422): preallocated once, written in
+    place at the step's position.
+    """
+
+    def __init__(self, shape: LlamaShape, batch: int, max_len: int, device, dtype):
+        self.batch, self.max_len = batch, max_len
+        kv, d = shape.kv_heads, shape.head_dim
+        self.k_t = [torch.zeros(batch, kv, d, max_len, device=device, dtype=dtype) for _ in range(shape.layers)]
+        self.v = [torch.zeros(batch, kv, max_len, d, device=device, dtype=dtype) for _ in range(shape.layers)]
+        self.key_index = torch.arange(max_len, device=device)
+
+
+class LlamaAttention(nn.Module):
+    def __init__(self, shape: LlamaShape, layer: int):
+        super().__init__()
+        self.shape, self.layer = shape, layer
+        self.scaling = shape.head_dim ** -0.5
+
+    def forward(self, x, cos, sin, positions, cache: StaticKVCache):
+        s = self.shape
+        B, T, _ = x.shape
+        H, KV, D = s.heads, s.kv_heads, s.head_dim
+        G = H // KV
+        q = self.q_proj(x).view(B, T, H, D).transpose(1, 2)
+        k = self.k_proj(x).view(B, T, KV, D).transpose(1, 2)
+        v = self.v_proj(x).view(B, T, KV, D).transpose(1, 2)
+        q = q * cos + _rotate_half(q) * sin
+        k = k * cos + _rotate_half(k) * sin
+        k_t, v_c = cache.k_t[self.layer], cache.v[self.layer]
+        k_t.index_copy_(3, positions, k.transpose(2, 3).to(k_t.dtype))
+        v_c.index_copy_(2, positions, v.to(v_c.dtype))
+        # queries of one kv head side by side: [B, KV, G*T, D] @ [B, KV, D, L]
+        qg = q.reshape(B, KV, G * T, D)
+        scores = torch.matmul(qg, k_t).float() * self.scaling
+        visible = cache.key_index.view(1, -1) <= positions.view(-1, 1)  # [T, L]
+        scores = scores.view(B, KV, G, T, -1).masked_fill(~visible, float("-inf"))
+        p = torch.softmax(scores, dim=-1).to(v_c.dtype).view(B, KV, G * T, -1)
+        out = torch.matmul(p, v_c).view(B, H, T, D).transpose(1, 2).reshape(B, T, H * D)
+        return self.o_proj(out.to(x.dtype))
+
+
+class LlamaMLP(nn.Module):
+    def forward(self, x):
+        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+
+
+class LlamaDecoderLayer(nn.Module):
+    def __init__(self, shape: LlamaShape, layer: int, device, dtype):
+        super().__init__()
+        self.self_attn = LlamaAttention(shape, layer)
+        self.mlp = LlamaMLP()
+        self.input_layernorm = RMSNorm(shape.hidden, shape.rms_eps, device, dtype)
+        self.post_attention_layernorm = RMSNorm(shape.hidden, shape.rms_eps, device, dtype)
+
+    def forward(self, x, cos, sin, positions, cache):
+        x = x + self.self_attn(self.input_layernorm(x), cos, sin, positions, cache)
+        return x + self.mlp(self.post_attention_layernorm(x))
+
+
+class _Body(nn.Module):
+    def __init__(self, shape: LlamaShape, device, dtype):
+        super().__init__()
+        self.embed_tokens = nn.Embedding(shape.vocab, shape.hidden, device=device, dtype=dtype)
+        self.layers = nn.ModuleList(LlamaDecoderLayer(shape, i, device, dtype) for i in range(shape.layers))
+        self.norm = RMSNorm(shape.hidden, shape.rms_eps, device, dtype)
+
+
+class NanoQuantLlama(nn.Module):
+    """Llama-2-architecture causal LM with NanoQuantLinear projections.
+
+    ``forward(ids [B, T], positions [T], cache)`` returns fp32 logits [B, T, vocab];
+    ``positions`` is a device tensor of absolute positions, so the same call serves
+    prefill (0..T-1) and a graph-captured one-token step (a position held on the device).
+    """
+
+    def __init__(self, shape: LlamaShape, device=None, dtype=torch.float32):
+        super().__init__()
+        self.shape = shape
+        self.dtype = dtype
+        self.model = _Body(shape, device, dtype)
+        self.lm_head = nn.Linear(shape.hidden, shape.vocab, bias=False, device=device, dtype=dtype)
+        d = shape.head_dim
+        inv_freq = 1.0 / (shape.rope_theta ** (torch.arange(0, d, 2, dtype=torch.float32, device=device) / d))
+        self.register_buffer("inv_freq", inv_freq, persistent=False)
+
+    def linears(self):
+        for layer in self.model.layers:
+            for name in LINEAR_NAMES:
+                owner = layer.self_attn if name.endswith(("q_proj", "k_proj", "v_proj", "o_proj")) else layer.mlp
+                yield getattr(owner, name)
+
+    def rope(self, positions, dtype):
+        freqs = positions.float().view(-1, 1) * self.inv_freq.view(1, -1)
+        emb = torch.cat((freqs, freqs), dim=-1)
+        return emb.cos().to(dtype), emb.sin().to(dtype)
+
+    def forward(self, ids, positions, cache: StaticKVCache):
+        x = self.model.embed_tokens(ids)
+        cos, sin = self.rope(positions, x.dtype)
+        for layer in self.model.layers:
+            x = layer(x, cos, sin, positions, cache)
+        x = self.model.norm(x)
+        return self.lm_head(x).float()
+
+    def prepare_kernels(self, kernel_type: str = "gemv", dtype=torch.float16):
+        """Pack every linear for ``kernel_type`` and cast the rest of the model to ``dtype``
+        (the reference calls ``_prepare_kernel`` on each NanoQuantLinear, test_decode.py:1228-1234)."""
+        for lin in self.linears():
+            lin._prepare_kernel(kernel_type, dtype)
+        return self.cast_non_linears(dtype)
+
+    def cast_non_linears(self, dtype):
+        self.model.embed_tokens.to(dtype)
+        self.model.norm.to(dtype)
+        for layer in self.model.layers:
+            layer.input_layernorm.to(dtype)
+            layer.post_attention_layernorm.to(dtype)
+        self.lm_head.to(dtype)
+        self.dtype = dtype
+        return self
+
+
+def random_llama(shape: LlamaShape, bpw: float = 0.55, seed: int = 0, device="cuda", with_mid: bool = False,
+                 kernel_type: str | None = None, dtype=torch.float16) -> NanoQuantLlama:
+    """Random-init model: N(0, 0.02) embedding and lm_head, random NanoQuant factors of
+    rank ``rank_for_bpw`` for all seven linears of every layer.
+
+    With ``kernel_type`` None the model stays dense in fp32 (the reference path of every
+    linear); otherwise each linear is packed for that kernel as soon as it is drawn (so the
+    dense factors of only one linear exist at a time) and the model is cast to ``dtype``.
+    """
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    model = NanoQuantLlama(shape, device=device, dtype=torch.float32)
+    with torch.no_grad():
+        model.model.embed_tokens.weight.normal_(0.0, 0.02, generator=gen)
+        model.lm_head.weight.normal_(0.0, 0.02, generator=gen)
+        for layer in model.model.layers:
+            for name, n_in, n_out in shape.linear_shapes():
+                owner = layer.self_attn if name in ("q_proj", "k_proj", "v_proj", "o_proj") else layer.mlp
+                lin = random_nanoquant_linear(n_in, n_out, rank_for_bpw(n_out, n_in, bpw), gen, device, with_mid)
+                if kernel_type is not None:
+                    lin._prepare_kernel(kernel_type, dtype)
+                setattr(owner, name, lin)
+    if kernel_type is not None:
+        model.cast_non_linears(dtype)
+    return model.eval()
+
+
+class GraphDecoder:
+    """Greedy decoding with ``steps_per_graph`` one-token steps recorded in one HIP graph.
+
+    Device state: ``ids`` [B, max_len] (prompt, then generated tokens) and ``pos``
+    (the position of the last token so far). A step embeds ``ids[:, pos]``, runs the
+    model at ``pos`` (writing K/V there), takes the argmax of the logits, stores it at
+    ``ids[:, pos + 1]`` and advances ``pos``. Nothing in a step reads the host.
+    """
+
+    def __init__(self, model: NanoQuantLlama, batch: int, max_len: int, steps_per_graph: int = 1,
+                 device="cuda"):
+        self.model, self.batch, self.max_len = model, batch, max_len
+        self.steps_per_graph = steps_per_graph
+        self.device = torch.device(device)
+        self.cache = StaticKVCache(model.shape, batch, max_len, self.device, model.dtype)
+        self.ids = torch.zeros(batch, max_len, dtype=torch.long, device=self.device)
+        self.pos = torch.zeros(1, dtype=torch.long, device=self.device)
+        self.last_logits = None
+        self.graph = None
+        self.stream = None
+
+    def _step(self):
+        tok = self.ids.index_select(1, self.pos)  # [B, 1]
+        logits = self.model(tok, self.pos, self.cache)[:, -1]  # [B, V] fp32
+        nxt = logits.argmax(dim=-1, keepdim=True)
+        self.pos.add_(1)
+        self.ids.index_copy_(1, self.pos, nxt)
+        return logits
+
+    def _steps(self):
+        logits = None
+        for _ in range(self.steps_per_graph):
+            logits = self._step()
+        return logits
+
+    @torch.no_grad()
+    def capture(self, warmup: int = 2):
+        """Warm up on the capture stream (allocates workspaces outside the graph), then record."""
+        saved = self.pos.clone()
+        if self.stream is None:
+            self.stream = torch.cuda.Stream(self.device)
+        self.stream.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(self.stream):
+            for _ in range(warmup):
+                self.pos.zero_()
+                self._steps()
+        torch.cuda.current_stream(self.device).wait_stream(self.stream)
+        torch.cuda.synchronize(self.device)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph, stream=self.stream):
+            self.last_logits = self._steps()
+        self.pos.copy_(saved)
+        torch.cuda.synchronize(self.device)
+        return self
+
+    @torch.no_grad()
+    def prefill(self, prompt: torch.Tensor) -> torch.Tensor:
+        """Run the prompt [B, T] at positions 0..T-1 and place its greedy next token."""
+        B, T = prompt.shape
+        if B != self.batch or T + 1 > self.max_len:
+            raise ValueError(f"prompt {tuple(prompt.shape)} does not fit batch {self.batch}, max_len {self.max_len}")
+        self.ids[:, :T].copy_(prompt)
+        positions = torch.arange(T, device=self.device)
+        logits = self.model(self.ids[:, :T], positions, self.cache)[:, -1]
+        self.ids[:, T] = logits.argmax(dim=-1)
+        self.pos.fill_(T)
+        return logits
+
+    @torch.no_grad()
+    def decode(self, steps: int, use_graph: bool = True):
+        """Run ``steps`` one-token steps (a multiple of ``steps_per_graph`` when graphed)."""
+        if use_graph:
+            if self.graph is None:
+                raise RuntimeError("capture() the decode graph first")
+            if steps % self.steps_per_graph:
+                raise ValueError(f"steps ({steps}) must be a multiple of steps_per_graph ({self.steps_per_graph})")
+            for _ in range(steps // self.steps_per_graph):
+                self.graph.replay()
+            return self.last_logits
+        logits = None
+        for _ in range(steps):
+            logits = self._step()
+        return logits
+
+
+@torch.no_grad()
+def generate(model: NanoQuantLlama, prompt: torch.Tensor, max_new_tokens: int, steps_per_graph: int = 1,
+             use_graph: bool = True, decoder: GraphDecoder | None = None):
+    """Greedy generation with decode timing (test_decode.py:474-693, greedy instead of top-k sampling).
+
+    Returns (ids [B, T + max_new_tokens], tokens_per_s, prof). Token 1 comes from the
+    prefill; the timed loop produces tokens 2..max_new_tokens, and
+    tokens/s = B * (max_new_tokens - 1) / decode wall time, as the reference reports it.
+    """
+    B, T = prompt.shape
+    if decoder is None:
+        decoder = GraphDecoder(model, B, T + max_new_tokens, steps_per_graph, device=prompt.device)
+        if use_graph:
+            decoder.capture()
+    steps = max_new_tokens - 1
+    torch.cuda.synchronize(prompt.device)
+    t0 = time.perf_counter()
+    decoder.prefill(prompt)
+    torch.cuda.synchronize(prompt.device)
+    t1 = time.perf_counter()
+    decoder.decode(steps, use_graph=use_graph)
+    torch.cuda.synchronize(prompt.device)
+    t2 = time.perf_counter()
+    tps = B * steps / max(t2 - t1, 1e-9)
+    prof = {"prefill_time_s_wall": t1 - t0, "decode_time_s_wall": t2 - t1, "decode_tokens_total": B * steps,
+            "ms_per_token": 1e3 * (t2 - t1) / max(steps, 1)}
+    return decoder.ids[:, :T + max_new_tokens].clone(), tps, prof
