@@ -120,6 +120,47 @@ int nq_gemv_stage1(int dtype, const void* x, const void* s_in, const uint32_t* v
 int nq_gemv_stage2(int dtype, const uint32_t* u_bits, const void* s_out, void* y, int64_t batch, int64_t n,
                    int64_t r, int64_t m, void* workspace, size_t workspace_bytes, nq_stream_t stream);
 
+/* ---------------------------------------------------------------- grouped decode GEMV
+ *
+ * Up to four linears in one launch per stage, for the decode step of a transformer layer:
+ * q, k and v read the same input, so do gate and up. No counterpart in the reference, whose
+ * decode step calls nanoquant_dyn_forward once per linear (modules/linear.py:156-160); the
+ * arithmetic of each item is that of nq_gemv. `items` is a host array of `count` items. */
+typedef struct nq_gemv_item {
+    const uint32_t* v_bits; /* stage 1: half2 words of V, [r, ceil(n/32)] */
+    const void* s_in;       /* stage 1: [n], 16-byte aligned */
+    const void* s_mid;      /* stage 1: [r] or NULL */
+    const uint32_t* u_bits; /* stage 2: half2 words of U, [m, ceil(r/32)], 16-byte aligned */
+    const void* s_out;      /* stage 2: [m] */
+    void* y;                /* stage 2: output, batch rows of y_stride elements */
+    const void* resid;      /* stage 2 with NQ_EPI_RESIDUAL: same layout as y (may be y itself) */
+    int64_t r;
+    int64_t m;
+    int64_t y_stride; /* elements between batch rows of y and resid, >= m */
+} nq_gemv_item;
+
+typedef enum {
+    NQ_EPI_STORE = 0,    /* y = sat(s_out * acc) */
+    NQ_EPI_RESIDUAL = 1, /* y = resid + sat(s_out * acc), each rounded to dtype as two operations */
+    NQ_EPI_GATED = 2     /* two items (gate, up) of equal m and r: y of item 0 = silu(gate) * up */
+} nq_epilogue;
+
+/* Bytes of workspace the two grouped stages need for these items (0 on bad arguments). */
+size_t nq_gemv_group_workspace_bytes(int64_t count, const nq_gemv_item* items, int64_t batch);
+
+/* Stage 1 of every item over the shared input x [batch, n]. With rms_eps >= 0 the input is
+ * RMS-normalised first: h is multiplied by rsqrt(mean(x^2) + rms_eps) per batch row; the
+ * norm's weight is expected folded into each item's s_in. Needs n % 8 == 0, 8 <= n <= 16384,
+ * 16-byte aligned x and s_in; NQ_ERR_UNSUPPORTED otherwise. */
+int nq_gemv_group_stage1(int dtype, int64_t count, const nq_gemv_item* items, const void* x, int64_t batch,
+                         int64_t n, float rms_eps, void* workspace, size_t workspace_bytes, nq_stream_t stream);
+
+/* Stage 2 of every item from the workspace stage 1 filled, with one of the nq_epilogue
+ * stores: one launch per set of items whose ranks share a kernel configuration (equal ranks
+ * always do). Needs r <= 4608 and 16-byte aligned u_bits; NQ_ERR_UNSUPPORTED otherwise. */
+int nq_gemv_group_stage2(int dtype, int64_t count, const nq_gemv_item* items, int64_t batch, int epilogue,
+                         void* workspace, size_t workspace_bytes, nq_stream_t stream);
+
 /* ---------------------------------------------------------------- prefill GEMM */
 
 /* C[M, N] = sat((A[M, K] * W) * s_out) with W[k, o] = sign(k, o) * s_in[k]:
@@ -140,6 +181,31 @@ int nq_gemm_onebit(int dtype, const void* A, const uint32_t* w_bits, const void*
 int nq_gemm_nanoquant(int dtype, const void* A, const uint32_t* v_bits, const uint32_t* u_bits,
                       const void* s_g, const void* s_l, const void* s_h, void* imm, void* C, int64_t M,
                       int64_t n, int64_t r_pad, int64_t m, nq_stream_t stream);
+
+/* ---------------------------------------------------------------- decode attention */
+
+/* Attention of one new token per sequence at the position *position (device int64, equal for
+ * every sequence), with the rotary embedding and the KV-cache write:
+ *   q, k, v   rows of qkv_stride elements (>= heads * head_dim), e.g. slices of one
+ *             [batch, (heads + 2 kv_heads) * head_dim] projection output; q holds heads
+ *             heads, k and v kv_heads heads, each head_dim wide
+ *   k_cache, v_cache  [batch, kv_heads, max_len, head_dim], 16-byte aligned; row *position
+ *             receives the rotated key and the value
+ *   rope_cos, rope_sin  [max_len, head_dim] (the rotate-half convention)
+ *   out       [batch, heads * head_dim] = softmax(q k^T * scaling) v over positions <= *position
+ * Query head h uses kv head h / (heads / kv_heads). Rounding follows the unfused torch path:
+ * rotary products and sum in dtype, scores rounded to dtype then scaled in fp32, softmax in
+ * fp32, probabilities rounded to dtype, fp32 accumulation of the output. A position outside
+ * [0, max_len) writes zeros to out and nothing to the caches. head_dim must be 128 and
+ * heads / kv_heads one of 1, 2, 4, 8, with (heads / kv_heads) * max_len * 4 bytes of scores
+ * within about 62 KB of LDS (max_len up to ~15800 for MHA, ~1980 for 8 query heads per kv
+ * head); NQ_ERR_UNSUPPORTED otherwise. No counterpart in the reference,
+ * whose decode step runs Hugging Face's attention (kernel/test_decode.py:385-402); this is
+ * the part of a decode step between the q/k/v and o projections. */
+int nq_attention_decode(int dtype, const void* q, const void* k, const void* v, int64_t qkv_stride,
+                        void* k_cache, void* v_cache, const void* rope_cos, const void* rope_sin,
+                        const int64_t* position, void* out, int64_t batch, int64_t heads, int64_t kv_heads,
+                        int64_t head_dim, int64_t max_len, float scaling, nq_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -34,6 +34,22 @@ _i64 = ctypes.c_int64
 _int = ctypes.c_int
 _size = ctypes.c_size_t
 
+NQ_EPI_STORE = 0
+NQ_EPI_RESIDUAL = 1
+NQ_EPI_GATED = 2
+
+
+class GemvItem(ctypes.Structure):
+    """``nq_gemv_item`` of include/nq_hip.h."""
+
+    _fields_ = [
+        ("v_bits", _vp), ("s_in", _vp), ("s_mid", _vp), ("u_bits", _vp), ("s_out", _vp), ("y", _vp),
+        ("resid", _vp), ("r", _i64), ("m", _i64), ("y_stride", _i64),
+    ]
+
+
+_items_p = ctypes.POINTER(GemvItem)
+
 # name -> (restype, argtypes); every function declared in include/nq_hip.h
 SIGNATURES = {
     "nq_status_string": (ctypes.c_char_p, [_int]),
@@ -49,9 +65,15 @@ SIGNATURES = {
     "nq_gemv": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _size, _vp]),
     "nq_gemv_stage1": (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _size, _vp]),
     "nq_gemv_stage2": (_int, [_int, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _size, _vp]),
+    "nq_gemv_group_workspace_bytes": (_size, [_i64, _items_p, _i64]),
+    "nq_gemv_group_stage1": (_int, [_int, _i64, _items_p, _vp, _i64, _i64, ctypes.c_float, _vp, _size, _vp]),
+    "nq_gemv_group_stage2": (_int, [_int, _i64, _items_p, _i64, _int, _vp, _size, _vp]),
+    "nq_attention_decode": (_int, [_int, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
+                                   _i64, ctypes.c_float, _vp]),
     "nq_gemm_onebit": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "nq_gemm_nanoquant": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
 }
+
 
 _lock = threading.Lock()
 _lib = None

@@ -204,27 +204,88 @@ __global__ __launch_bounds__(kThreads) void gemv_stage2_kernel(const uint16_t* _
     }
 }
 
+// --------------------------------------------------------------------------- item tables
+//
+// The fast kernels take a table of up to kMaxItems linears launched together (one block
+// range per item): the q, k, v projections of an attention layer share their input, so do
+// gate and up. A single GEMV is a one-item table.
+constexpr int kMaxItems = 4;
+
+struct S1Item {
+    const uint32_t* v_bits;
+    const uint16_t* s_in;
+    const uint16_t* s_mid;  // or nullptr
+    uint16_t* z_hi;
+    uint16_t* z_lo;
+    int r, kpad, zpitch;
+    int block_begin;  // first blockIdx.x of the item
+};
+
+struct S1Table {
+    S1Item item[kMaxItems];
+    int count;
+};
+
+struct S2Item {
+    const uint32_t* u_bits;
+    const uint16_t* s_out;
+    uint16_t* y;
+    const uint16_t* resid;  // residual added in the epilogue, or nullptr
+    const uint16_t* z_hi;
+    const uint16_t* z_lo;
+    int m, wr, zpitch;
+    int ystride;  // elements between batch rows of y and resid
+    int block_begin;
+};
+
+struct S2Table {
+    S2Item item[kMaxItems];
+    int count;
+};
+
+// Stage-2 epilogues: y = sat(s_out * acc); y = resid + that (rounded as two T operations);
+// gated pair (items 0 and 1 over the same rows): y0 = silu(gate) * up, each a T value;
+// kEpiStoreOne is kEpiStore for a one-item table (no item lookup).
+enum Epilogue { kEpiStore = 0, kEpiResidual = 1, kEpiGated = 2, kEpiStoreOne = 3 };
+
+// The item of this block. Every item is read with a constant index and the choice is a
+// select, so the kernel arguments come in one batch of scalar loads (an index computed from
+// loaded values would cost a second, dependent round of loads).
+template <typename Item, typename Table>
+__device__ inline Item pick_item(const Table& tab) {
+    Item it = tab.item[0];
+#pragma unroll
+    for (int i = 1; i < kMaxItems; ++i)
+        if (i < tab.count && static_cast<int>(blockIdx.x) >= tab.item[i].block_begin) it = tab.item[i];
+    return it;
+}
+
 // --------------------------------------------------------------------------- stage 1, VALU rows
 //
 // Block = 4 waves = 4/WR groups of WR waves; group gi owns rows j0 .. j0+R-1 (j0 = block row
-// base + gi*R). Lane p = (wave % WR)*64 + lane of a group holds words q_w = p + 64*WR*w
-// (w < WPL) of those rows: consecutive lanes read consecutive words. Requires n % 8 == 0
-// (an 8-column piece is wholly inside or outside a row) and 16-byte aligned x and s_in.
-template <typename T, int NB, int WPL, int WR, int R>
-__global__ __launch_bounds__(256) void s1w_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ s_in,
-                                                  const uint32_t* __restrict__ vbits,
-                                                  const uint16_t* __restrict__ s_mid, uint16_t* __restrict__ z_hi,
-                                                  uint16_t* __restrict__ z_lo, int batch, int n, int r, int wn,
-                                                  int kpad, int zpitch) {
+// base + gi*R) of its item. Lane p = (wave % WR)*64 + lane of a group holds words
+// q_w = p + 64*WR*w (w < WPL) of those rows: consecutive lanes read consecutive words.
+// Requires n % 8 == 0 (an 8-column piece is wholly inside or outside a row) and 16-byte
+// aligned x and s_in.
+//
+// kNorm folds an RMSNorm of x into the stage: every group also sums x^2 over the whole row
+// (the lanes hold all of x anyway) and h is multiplied by rsqrt(sum / n + eps); the norm's
+// weight is expected inside s_in.
+template <typename T, int NB, int WPL, int WR, int R, bool kNorm, bool kOne>
+__global__ __launch_bounds__(256) void s1w_kernel(const S1Table tab, const uint16_t* __restrict__ x, int batch, int n,
+                                                  int wn, float eps) {
     constexpr int kGroups = 4 / WR;
     constexpr int kRows = kGroups * R;
-    __shared__ float part[kGroups * R * NB * WR];
+    constexpr int kPartRows = R + (kNorm ? 1 : 0);
+    __shared__ float part[kGroups * kPartRows * NB * WR];
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
     const int grp = wave / WR;
     const int p = (wave % WR) * 64 + lane;
-    const int j0 = blockIdx.x * kRows + grp * R;
+    const S1Item it = kOne ? tab.item[0] : pick_item<S1Item>(tab);
+    const int r = it.r;
+    const int j0 = (static_cast<int>(blockIdx.x) - it.block_begin) * kRows + grp * R;
     const int b0 = blockIdx.y * NB;
     NQ_STAMP(0);
 
@@ -235,13 +296,13 @@ __global__ __launch_bounds__(256) void s1w_kernel(const uint16_t* __restrict__ x
     uint32_t vb[R][WPL];
 #pragma unroll
     for (int k = 0; k < R; ++k) {
-        const uint32_t* row = vbits + static_cast<uint32_t>(min(j0 + k, r - 1)) * static_cast<uint32_t>(wn);
+        const uint32_t* row = it.v_bits + static_cast<uint32_t>(min(j0 + k, r - 1)) * static_cast<uint32_t>(wn);
 #pragma unroll
         for (int w = 0; w < WPL; ++w) vb[k][w] = row[qc[w]];
     }
     // the mid scales, raw until the end; without s_mid the (unused) loads read s_in
-    const uint16_t* msrc = s_mid != nullptr ? s_mid : s_in;
-    const int mlim = (s_mid != nullptr ? r : n) - 1;
+    const uint16_t* msrc = it.s_mid != nullptr ? it.s_mid : it.s_in;
+    const int mlim = (it.s_mid != nullptr ? r : n) - 1;
     uint16_t mid[R];
 #pragma unroll
     for (int k = 0; k < R; ++k) mid[k] = msrc[min(j0 + k, mlim)];
@@ -252,7 +313,7 @@ __global__ __launch_bounds__(256) void s1w_kernel(const uint16_t* __restrict__ x
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const int k0 = min(32 * qc[w] + 8 * v, n - 8);
-            const u32x4 s = *reinterpret_cast<const u32x4*>(s_in + k0);
+            const u32x4 s = *reinterpret_cast<const u32x4*>(it.s_in + k0);
             sp[w][4 * v + 0] = s.x;
             sp[w][4 * v + 1] = s.y;
             sp[w][4 * v + 2] = s.z;
@@ -307,43 +368,73 @@ __global__ __launch_bounds__(256) void s1w_kernel(const uint16_t* __restrict__ x
 #pragma unroll
                 for (int b = 0; b < NB; ++b) acc[pp & 1][k][b] = T::dot2(a, xp[w][b][pp], acc[pp & 1][k][b]);
             }
+    // sum of squares of x (a sign flip does not change a square; zeroed slots add nothing)
+    float ss[2][NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) ss[0][b] = ss[1][b] = 0.0f;
+    if (kNorm) {
+#pragma unroll
+        for (int w = 0; w < WPL; ++w)
+#pragma unroll
+            for (int pp = 0; pp < 16; ++pp)
+#pragma unroll
+                for (int b = 0; b < NB; ++b) ss[pp & 1][b] = T::dot2(xp[w][b][pp], xp[w][b][pp], ss[pp & 1][b]);
+    }
 
     if (WR == 1) {
+        float rs[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+            rs[b] = kNorm ? rsqrtf(wave_sum_dpp(ss[0][b] + ss[1][b]) / static_cast<float>(n) + eps) : 1.0f;
 #pragma unroll
         for (int k = 0; k < R; ++k) {
             const int j = j0 + k;
-            const float mf = s_mid != nullptr ? T::to_float(mid[k]) : 1.0f;
+            const float mf = it.s_mid != nullptr ? T::to_float(mid[k]) : 1.0f;
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
-                const float v = wave_sum_dpp(acc[0][k][b] + acc[1][k][b]);
-                if (lane == 0 && j < kpad && b0 + b < batch) store_h(z_hi, z_lo, zpitch, b0 + b, j, j < r ? v * mf : 0.0f);
+                const float v = wave_sum_dpp(acc[0][k][b] + acc[1][k][b]) * rs[b];
+                if (lane == 0 && j < it.kpad && b0 + b < batch)
+                    store_h(it.z_hi, it.z_lo, it.zpitch, b0 + b, j, j < r ? v * mf : 0.0f);
             }
         }
     } else {
 #pragma unroll
-        for (int k = 0; k < R; ++k)
+        for (int k = 0; k < kPartRows; ++k)
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
-                const float v = wave_sum_dpp(acc[0][k][b] + acc[1][k][b]);
-                if (lane == 0) part[((grp * R + k) * NB + b) * WR + wave % WR] = v;
+                const float v = wave_sum_dpp(k < R ? acc[0][k][b] + acc[1][k][b] : ss[0][b] + ss[1][b]);
+                if (lane == 0) part[((grp * kPartRows + k) * NB + b) * WR + wave % WR] = v;
             }
         __syncthreads();
         if (lane == 0 && wave % WR == 0) {
+            float rs[NB];
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                rs[b] = 1.0f;
+                if (kNorm) {
+                    float v = 0.0f;
+#pragma unroll
+                    for (int s = 0; s < WR; ++s) v += part[((grp * kPartRows + R) * NB + b) * WR + s];
+                    rs[b] = rsqrtf(v / static_cast<float>(n) + eps);
+                }
+            }
 #pragma unroll
             for (int k = 0; k < R; ++k) {
                 const int j = j0 + k;
-                const float mf = s_mid != nullptr ? T::to_float(mid[k]) : 1.0f;
+                const float mf = it.s_mid != nullptr ? T::to_float(mid[k]) : 1.0f;
 #pragma unroll
                 for (int b = 0; b < NB; ++b) {
                     float v = 0.0f;
 #pragma unroll
-                    for (int s = 0; s < WR; ++s) v += part[((grp * R + k) * NB + b) * WR + s];
-                    if (j < kpad && b0 + b < batch) store_h(z_hi, z_lo, zpitch, b0 + b, j, j < r ? v * mf : 0.0f);
+                    for (int s = 0; s < WR; ++s) v += part[((grp * kPartRows + k) * NB + b) * WR + s];
+                    v *= rs[b];
+                    if (j < it.kpad && b0 + b < batch)
+                        store_h(it.z_hi, it.z_lo, it.zpitch, b0 + b, j, j < r ? v * mf : 0.0f);
                 }
             }
         }
     }
-    if (blockIdx.x == 0) zero_h_pad(z_hi, z_lo, zpitch, kpad, b0, NB, batch);
+    if (static_cast<int>(blockIdx.x) == it.block_begin) zero_h_pad(it.z_hi, it.z_lo, it.zpitch, it.kpad, b0, NB, batch);
     NQ_STAMP(3);
 }
 
@@ -363,116 +454,170 @@ __global__ __launch_bounds__(256) void s1w_kernel(const uint16_t* __restrict__ x
 // clamped), so every step is valid and the loop has no branch. Columns of batch rows past the
 // batch hold finite values that are never stored. The waves' partial tiles are added in LDS,
 // then hi + lo of each batch row (adjacent lanes) and s_out.
-template <typename T, int QW, int NB>
-__global__ __launch_bounds__(256) void s2t_kernel(const uint16_t* __restrict__ z_hi, const uint16_t* __restrict__ z_lo,
-                                                  const uint32_t* __restrict__ ubits,
-                                                  const uint16_t* __restrict__ s_out, uint16_t* __restrict__ y,
-                                                  int batch, int m, int wr, int zpitch) {
+//
+// With the gated epilogue a block runs two items (gate, up) over the same 16 rows, each with
+// its own U tile and intermediate, and stores silu(gate) * up.
+template <typename T>
+__device__ inline float silu_of(float g) {
+    return g / (1.0f + expf(-g));
+}
+
+template <typename T, int QW, int NB, int EPI>
+__global__ __launch_bounds__(256) void s2t_kernel(const S2Table tab, int batch) {
     constexpr int NW = 4;
     constexpr int kThr = 256;
+    constexpr int P = EPI == kEpiGated ? 2 : 1;  // items per block
     constexpr int kWords = 16 * NW * QW;  // tile words (wr <= NW * QW)
     constexpr int kUPieces = (kWords / 4 + kThr - 1) / kThr;
     constexpr int kCols = 32 * NW * QW;  // h columns used per batch row (<= zpitch)
     constexpr int kRowPieces = kCols / 8;
     constexpr int kZPieces = (2 * NB * kRowPieces + kThr - 1) / kThr;
-    __shared__ __attribute__((aligned(16))) uint32_t tile[kWords + 4];
-    __shared__ __attribute__((aligned(16))) uint16_t hz[2 * NB][kCols];  // [hi rows, then lo rows][column]
-    __shared__ f32x4 red[NW][64];
+    __shared__ __attribute__((aligned(16))) uint32_t tile[P][kWords + 4];
+    __shared__ __attribute__((aligned(16))) uint16_t hz[P][2 * NB][kCols];  // [hi rows, then lo rows][column]
+    __shared__ f32x4 red[P][NW][64];
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
     const int c = lane & 15;
     const int g = lane >> 4;
-    const int i0 = blockIdx.x * 16;
+    S2Item its[P];
+    its[0] = (EPI == kEpiGated || EPI == kEpiStoreOne) ? tab.item[0] : pick_item<S2Item>(tab);
+    if (P == 2) its[P - 1] = tab.item[1];
+    const int m = its[0].m;
+    const int wr = its[0].wr;  // gated items share m and wr
+    const int i0 = (static_cast<int>(blockIdx.x) - its[0].block_begin) * 16;
     const int b0 = blockIdx.y * NB;
     NQ_STAMP(0);
 
-    // 1. every global load: the tile's words as 16-byte pieces, h, the output scales
+    // 1. every global load: the tiles' words as 16-byte pieces, h, the output scales
     const uint32_t total = static_cast<uint32_t>(m) * static_cast<uint32_t>(wr);
     const uint32_t vec_end = total & ~3u;  // the host guarantees total >= 4
     const uint32_t base = static_cast<uint32_t>(i0) * static_cast<uint32_t>(wr);  // a multiple of 16
     const int rows = min(16, m - i0);
     const int nwords = rows * wr;
-    u32x4 pv[kUPieces];
+    u32x4 pv[P][kUPieces];
+    uint32_t tail_word[P];
+    u32x4 zv[P][kZPieces];
+    uint16_t so[P][4];  // raw until the epilogue
 #pragma unroll
-    for (int it = 0; it < kUPieces; ++it)
-        pv[it] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4*>(ubits + min(base + 4u * static_cast<uint32_t>(t + it * kThr), vec_end - 4u)));
-    const uint32_t tail_word = ubits[min(vec_end + static_cast<uint32_t>(t), total - 1u)];  // words past vec_end
-    u32x4 zv[kZPieces];
+    for (int pi = 0; pi < P; ++pi) {
+        const S2Item& it = its[pi];
 #pragma unroll
-    for (int it = 0; it < kZPieces; ++it) {
-        const int pc = min(t + it * kThr, 2 * NB * kRowPieces - 1);
-        const int arr = pc / (NB * kRowPieces);
-        const int rem = pc - arr * (NB * kRowPieces);
-        const int b = rem / kRowPieces;
-        const int off = (rem - b * kRowPieces) * 8;
-        zv[it] = *reinterpret_cast<const u32x4*>(
-            (arr ? z_lo : z_hi) + static_cast<uint32_t>(min(b0 + b, batch - 1)) * static_cast<uint32_t>(zpitch) + off);
+        for (int k = 0; k < kUPieces; ++k)
+            pv[pi][k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+                it.u_bits + min(base + 4u * static_cast<uint32_t>(t + k * kThr), vec_end - 4u)));
+        tail_word[pi] = it.u_bits[min(vec_end + static_cast<uint32_t>(t), total - 1u)];  // words past vec_end
+#pragma unroll
+        for (int k = 0; k < kZPieces; ++k) {
+            const int pc = min(t + k * kThr, 2 * NB * kRowPieces - 1);
+            const int arr = pc / (NB * kRowPieces);
+            const int rem = pc - arr * (NB * kRowPieces);
+            const int b = rem / kRowPieces;
+            const int off = (rem - b * kRowPieces) * 8;
+            zv[pi][k] = *reinterpret_cast<const u32x4*>((arr ? it.z_lo : it.z_hi) +
+                                                        static_cast<uint32_t>(min(b0 + b, batch - 1)) *
+                                                            static_cast<uint32_t>(it.zpitch) +
+                                                        off);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) so[pi][i] = it.s_out[min(i0 + 4 * g + i, m - 1)];
     }
-    uint16_t so[4];  // raw until the epilogue
+    // the residual of this lane's outputs (batch row b0 + c/2, rows i0 + 4g + i)
+    uint16_t res[4] = {0, 0, 0, 0};
+    if (EPI == kEpiResidual) {
+        const uint32_t rb = static_cast<uint32_t>(min(b0 + min(c >> 1, NB - 1), batch - 1));
 #pragma unroll
-    for (int i = 0; i < 4; ++i) so[i] = s_out[min(i0 + 4 * g + i, m - 1)];
+        for (int i = 0; i < 4; ++i)
+            res[i] = its[0].resid[rb * static_cast<uint32_t>(its[0].ystride) + min(i0 + 4 * g + i, m - 1)];
+    }
     __builtin_amdgcn_sched_barrier(0);
 
     // 2. into LDS; vec_end and base + e4 are multiples of 4, so a piece lies wholly below
     //    vec_end or wholly past it, and words past it come from tail_word
 #pragma unroll
-    for (int it = 0; it < kUPieces; ++it) {
-        const int e4 = 4 * (t + it * kThr);
-        if (e4 < nwords && base + e4 + 4 <= vec_end) *reinterpret_cast<u32x4*>(tile + e4) = pv[it];
-    }
-    if (t < 3) {
-        const uint32_t w = vec_end + t;
-        if (w < total && w >= base && w < base + nwords) tile[w - base] = tail_word;
-    }
+    for (int pi = 0; pi < P; ++pi) {
 #pragma unroll
-    for (int it = 0; it < kZPieces; ++it) {
-        const int pc = t + it * kThr;
-        if (pc < 2 * NB * kRowPieces) {
-            const int row = pc / kRowPieces;  // arr * NB + b
-            *reinterpret_cast<u32x4*>(&hz[row][(pc - row * kRowPieces) * 8]) = zv[it];
+        for (int k = 0; k < kUPieces; ++k) {
+            const int e4 = 4 * (t + k * kThr);
+            if (e4 < nwords && base + e4 + 4 <= vec_end) *reinterpret_cast<u32x4*>(tile[pi] + e4) = pv[pi][k];
+        }
+        if (t < 3) {
+            const uint32_t w = vec_end + t;
+            if (w < total && w >= base && w < base + nwords) tile[pi][w - base] = tail_word[pi];
+        }
+#pragma unroll
+        for (int k = 0; k < kZPieces; ++k) {
+            const int pc = t + k * kThr;
+            if (pc < 2 * NB * kRowPieces) {
+                const int row = pc / kRowPieces;  // arr * NB + b
+                *reinterpret_cast<u32x4*>(&hz[pi][row][(pc - row * kRowPieces) * 8]) = zv[pi][k];
+            }
         }
     }
     __syncthreads();
 
     // 3. MFMAs
-    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
     const uint32_t mask = kSignPair, one = kBf16OnePair;
     const int sh = 4 * g;
     const int bcol = c >> 1;
-    const uint16_t* hsrc = &hz[(c & 1) * NB + min(bcol, NB - 1)][8 * g];
-    const uint32_t* trow = tile + min(c, rows - 1) * wr;
 #pragma unroll
-    for (int s = 0; s < QW; ++s) {
-        const int q = wave + NW * s;
-        const u32x4 b = *reinterpret_cast<const u32x4*>(hsrc + 32 * q);
-        const uint32_t w = trow[min(q, wr - 1)] << sh;
-        const u32x4 a = u32x4{and_or(w, mask, one), and_or(w << 1, mask, one), and_or(w << 2, mask, one),
-                              and_or(w << 3, mask, one)};
-        acc[s & 1] = mfma16x16x32<BF16>(a, b, acc[s & 1]);
+    for (int pi = 0; pi < P; ++pi) {
+        f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+        const uint16_t* hsrc = &hz[pi][(c & 1) * NB + min(bcol, NB - 1)][8 * g];
+        const uint32_t* trow = tile[pi] + min(c, rows - 1) * wr;
+#pragma unroll
+        for (int s = 0; s < QW; ++s) {
+            const int q = wave + NW * s;
+            const u32x4 b = *reinterpret_cast<const u32x4*>(hsrc + 32 * q);
+            const uint32_t w = trow[min(q, wr - 1)] << sh;
+            const u32x4 a = u32x4{and_or(w, mask, one), and_or(w << 1, mask, one), and_or(w << 2, mask, one),
+                                  and_or(w << 3, mask, one)};
+            acc[s & 1] = mfma16x16x32<BF16>(a, b, acc[s & 1]);
+        }
+        red[pi][wave][lane] =
+            f32x4{acc[0].x + acc[1].x, acc[0].y + acc[1].y, acc[0].z + acc[1].z, acc[0].w + acc[1].w};
     }
-    red[wave][lane] = f32x4{acc[0].x + acc[1].x, acc[0].y + acc[1].y, acc[0].z + acc[1].z, acc[0].w + acc[1].w};
     __syncthreads();
     NQ_STAMP(2);
 
     // 4. sum the waves' tiles, add hi and lo, scale, store
     if (wave == 0) {
-        f32x4 sum = red[0][lane];
+        float v[P][4];
 #pragma unroll
-        for (int w = 1; w < NW; ++w) {
-            const f32x4 pr = red[w][lane];
-            sum = f32x4{sum.x + pr.x, sum.y + pr.y, sum.z + pr.z, sum.w + pr.w};
+        for (int pi = 0; pi < P; ++pi) {
+            f32x4 sum = red[pi][0][lane];
+#pragma unroll
+            for (int w = 1; w < NW; ++w) {
+                const f32x4 pr = red[pi][w][lane];
+                sum = f32x4{sum.x + pr.x, sum.y + pr.y, sum.z + pr.z, sum.w + pr.w};
+            }
+            v[pi][0] = sum.x;
+            v[pi][1] = sum.y;
+            v[pi][2] = sum.z;
+            v[pi][3] = sum.w;
         }
-        const float v[4] = {sum.x, sum.y, sum.z, sum.w};
         const bool b_ok = (c & 1) == 0 && bcol < NB && b0 + bcol < batch;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             // quad_perm [1,0,3,2]: the lo column's value from the neighbouring lane
-            const float lo = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v[i]), 0xB1, 0xF, 0xF, false));
+            float out[P];
+#pragma unroll
+            for (int pi = 0; pi < P; ++pi) {
+                const float lo = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v[pi][i]), 0xB1, 0xF, 0xF, false));
+                out[pi] = (v[pi][i] + lo) * T::to_float(so[pi][i]);
+            }
             const int row = i0 + 4 * g + i;
-            if (b_ok && row < m)
-                y[static_cast<size_t>(b0 + bcol) * m + row] = saturate_to<T>((v[i] + lo) * T::to_float(so[i]), T::SAT);
+            if (b_ok && row < m) {
+                uint16_t val = saturate_to<T>(out[0], T::SAT);
+                if (EPI == kEpiResidual) {
+                    val = T::from_float(T::to_float(res[i]) + T::to_float(val));
+                } else if (EPI == kEpiGated) {
+                    const float gate = T::to_float(val);
+                    const float up = T::to_float(saturate_to<T>(out[P - 1], T::SAT));
+                    val = T::from_float(T::to_float(T::from_float(silu_of<T>(gate))) * up);
+                }
+                its[0].y[static_cast<size_t>(b0 + bcol) * its[0].ystride + row] = val;
+            }
         }
     }
     NQ_STAMP(3);
@@ -533,7 +678,9 @@ struct GemvArgs {
 
 template <typename T, int NB>
 void launch_stage1_generic(const GemvArgs& a) {
-    const dim3 g1(static_cast<unsigned>(ceil_div(a.plan.kpad, kWaves)), static_cast<unsigned>(ceil_div(a.batch, NB)));
+    // at least one block: with r == 0 it only zeroes the intermediate that stage 2 reads
+    const dim3 g1(static_cast<unsigned>(std::max<int64_t>(1, ceil_div(a.plan.kpad, kWaves))),
+                  static_cast<unsigned>(ceil_div(a.batch, NB)));
     const bool vec = (a.n % 8 == 0) && aligned(a.x, 16) && aligned(a.s_in, 16);
     if (vec)
         gemv_stage1_kernel<T, NB, true><<<g1, kThreads, 0, a.stream>>>(a.x, a.s_in, a.v_bits, a.s_mid, a.z_hi, a.z_lo,
@@ -552,33 +699,82 @@ void launch_stage2_generic(const GemvArgs& a) {
                                                              a.plan.wr, a.plan.zpitch);
 }
 
-template <typename T, int NB, int WPL, int WR, int R>
-void launch_s1w(const GemvArgs& a) {
-    const int rows_pb = (4 / WR) * R;
-    const dim3 grid(static_cast<unsigned>(ceil_div(a.plan.kpad, rows_pb)), static_cast<unsigned>(ceil_div(a.batch, NB)));
-    s1w_kernel<T, NB, WPL, WR, R><<<grid, 256, 0, a.stream>>>(a.x, a.s_in, a.v_bits, a.s_mid, a.z_hi, a.z_lo, a.batch,
-                                                               a.n, a.r, a.wn, a.plan.kpad, a.plan.zpitch);
-}
-
+// Rows of V per block of the stage-1 configuration used for wn words per row (0: none).
 // Shapes measured on MI355X (graph-replayed, cold weights): n = 4096 is fastest with two waves
 // per row and one word per lane, two rows per group (3.3 us against 3.6-4.3 for the other
 // splits); n = 11008 with four waves per row, two words per lane, four rows per group.
+inline int s1w_rows_per_block(int wn) {
+    if (wn <= 64) return 4 * 2;      // <WPL 1, WR 1, R 2>
+    if (wn <= 128) return 2 * 2;     // <1, 2, 2>
+    if (wn <= 256) return 2 * 2;     // <2, 2, 2>
+    if (wn <= 512) return 1 * 4;     // <2, 4, 4>
+    return 0;
+}
+
+template <typename T, int NB, bool kNorm, bool kOne>
+void launch_s1w_cfg(const S1Table& tab, int blocks, const uint16_t* x, int batch, int n, int wn, float eps,
+                    hipStream_t st) {
+    const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(ceil_div(batch, NB)));
+    if (wn <= 64) s1w_kernel<T, NB, 1, 1, 2, kNorm, kOne><<<grid, 256, 0, st>>>(tab, x, batch, n, wn, eps);
+    else if (wn <= 128) s1w_kernel<T, NB, 1, 2, 2, kNorm, kOne><<<grid, 256, 0, st>>>(tab, x, batch, n, wn, eps);
+    else if (wn <= 256) s1w_kernel<T, NB, 2, 2, 2, kNorm, kOne><<<grid, 256, 0, st>>>(tab, x, batch, n, wn, eps);
+    else s1w_kernel<T, NB, 2, 4, 4, kNorm, kOne><<<grid, 256, 0, st>>>(tab, x, batch, n, wn, eps);
+}
+
 template <typename T, int NB>
-bool launch_s1w_nb(const GemvArgs& a) {
-    const int wn = a.wn;
-    if (wn <= 64) launch_s1w<T, NB, 1, 1, 2>(a);
-    else if (wn <= 128) launch_s1w<T, NB, 1, 2, 2>(a);
-    else if (wn <= 256) launch_s1w<T, NB, 2, 2, 2>(a);
-    else if (wn <= 512) launch_s1w<T, NB, 2, 4, 4>(a);
-    else return false;
-    return true;
+void launch_s1w_nb(const S1Table& tab, int blocks, const uint16_t* x, int batch, int n, int wn, bool norm, float eps,
+                   hipStream_t st) {
+    if (tab.count == 1) {
+        if (norm) launch_s1w_cfg<T, NB, true, true>(tab, blocks, x, batch, n, wn, eps, st);
+        else launch_s1w_cfg<T, NB, false, true>(tab, blocks, x, batch, n, wn, eps, st);
+    } else {
+        if (norm) launch_s1w_cfg<T, NB, true, false>(tab, blocks, x, batch, n, wn, eps, st);
+        else launch_s1w_cfg<T, NB, false, false>(tab, blocks, x, batch, n, wn, eps, st);
+    }
+}
+
+// One launch over every item of `tab` (block ranges filled in here). The caller checked that
+// the fast stage 1 applies: n >= 8, n % 8 == 0, wn <= 512, x and each s_in 16-byte aligned,
+// every r > 0.
+template <typename T>
+void launch_s1w_table(S1Table& tab, const uint16_t* x, int batch, int n, int wn, bool norm, float eps,
+                      hipStream_t st) {
+    const int rpb = s1w_rows_per_block(wn);
+    int blocks = 0;
+    for (int k = 0; k < tab.count; ++k) {
+        tab.item[k].block_begin = blocks;
+        blocks += static_cast<int>(ceil_div(tab.item[k].kpad, rpb));
+    }
+    if (batch <= 1) launch_s1w_nb<T, 1>(tab, blocks, x, batch, n, wn, norm, eps, st);
+    else launch_s1w_nb<T, 2>(tab, blocks, x, batch, n, wn, norm, eps, st);
+}
+
+inline bool s1w_applies(const uint16_t* x, const uint16_t* s_in, int n, int wn, int r) {
+    return n >= 8 && n % 8 == 0 && wn <= 512 && r > 0 && aligned(x, 16) && aligned(s_in, 16);
+}
+
+inline S1Item s1_item_of(const GemvArgs& a) {
+    S1Item it;
+    it.v_bits = a.v_bits;
+    it.s_in = a.s_in;
+    it.s_mid = a.s_mid;
+    it.z_hi = a.z_hi;
+    it.z_lo = a.z_lo;
+    it.r = a.r;
+    it.kpad = a.plan.kpad;
+    it.zpitch = a.plan.zpitch;
+    it.block_begin = 0;
+    return it;
 }
 
 template <typename T>
 void launch_stage1(const GemvArgs& a) {
-    const bool fast = a.n >= 8 && a.n % 8 == 0 && aligned(a.x, 16) && aligned(a.s_in, 16) && a.wn <= 512;
-    if (fast) {
-        if (a.batch <= 1 ? launch_s1w_nb<T, 1>(a) : launch_s1w_nb<T, 2>(a)) return;
+    if (s1w_applies(a.x, a.s_in, a.n, a.wn, a.r)) {
+        S1Table tab;
+        tab.count = 1;
+        tab.item[0] = s1_item_of(a);
+        launch_s1w_table<T>(tab, a.x, a.batch, a.n, a.wn, false, 0.0f, a.stream);
+        return;
     }
     if (a.batch <= 1) launch_stage1_generic<T, 1>(a);
     else if (a.batch <= 2) launch_stage1_generic<T, 2>(a);
@@ -586,47 +782,78 @@ void launch_stage1(const GemvArgs& a) {
     else launch_stage1_generic<T, kMaxNB>(a);
 }
 
-// NB batch rows of h per block (LDS holds 2 * NB * 128 * QW halves: NB * QW <= 128 keeps it
-// within 64 KB); larger batches take several passes over U.
-template <typename T, int QW>
-void launch_s2t(const GemvArgs& a) {
-    const int want = std::min(a.batch, 8);
+// Only the batch splits that fit in LDS are instantiated (the host never picks the others).
+template <typename T, int QW, int NB, int EPI>
+void launch_s2t_nb(const S2Table& tab, dim3 grid, int batch, hipStream_t st) {
+    if constexpr (NB == 1 || (EPI == kEpiGated ? 2 : 1) * NB * QW <= 128)
+        s2t_kernel<T, QW, NB, EPI><<<grid, 256, 0, st>>>(tab, batch);
+}
+
+// NB batch rows of h per block (LDS holds P * 2 * NB * 128 * QW halves: P * NB * QW <= 128
+// keeps it within 64 KB); larger batches take several passes over U.
+template <typename T, int QW, int EPI>
+void launch_s2t_table(S2Table& tab, int batch, hipStream_t st) {
+    constexpr int P = EPI == kEpiGated ? 2 : 1;
+    const int want = std::min(batch, 8);
     int nb = want <= 1 ? 1 : (want <= 2 ? 2 : (want <= 4 ? 4 : 8));
-    while (nb > 1 && nb * QW > 128) nb >>= 1;
-    const dim3 grid(static_cast<unsigned>(ceil_div(a.m, 16)), static_cast<unsigned>(ceil_div(a.batch, nb)));
-    if (nb == 1)
-        s2t_kernel<T, QW, 1><<<grid, 256, 0, a.stream>>>(a.z_hi, a.z_lo, a.u_bits, a.s_out, a.y, a.batch, a.m,
-                                                          a.plan.wr, a.plan.zpitch);
-    else if (nb == 2)
-        s2t_kernel<T, QW, 2><<<grid, 256, 0, a.stream>>>(a.z_hi, a.z_lo, a.u_bits, a.s_out, a.y, a.batch, a.m,
-                                                          a.plan.wr, a.plan.zpitch);
-    else if (nb == 4)
-        s2t_kernel<T, QW, 4><<<grid, 256, 0, a.stream>>>(a.z_hi, a.z_lo, a.u_bits, a.s_out, a.y, a.batch, a.m,
-                                                          a.plan.wr, a.plan.zpitch);
-    else
-        s2t_kernel<T, QW, 8><<<grid, 256, 0, a.stream>>>(a.z_hi, a.z_lo, a.u_bits, a.s_out, a.y, a.batch, a.m,
-                                                          a.plan.wr, a.plan.zpitch);
+    while (nb > 1 && P * nb * QW > 128) nb >>= 1;
+    int blocks = 0;
+    const int items = EPI == kEpiGated ? 1 : tab.count;  // a gated pair runs item 1 inside item 0's blocks
+    for (int k = 0; k < items; ++k) {
+        tab.item[k].block_begin = blocks;
+        blocks += static_cast<int>(ceil_div(tab.item[k].m, 16));
+    }
+    const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(ceil_div(batch, nb)));
+    if (nb == 1) launch_s2t_nb<T, QW, 1, EPI>(tab, grid, batch, st);
+    else if (nb == 2) launch_s2t_nb<T, QW, 2, EPI>(tab, grid, batch, st);
+    else if (nb == 4) launch_s2t_nb<T, QW, 4, EPI>(tab, grid, batch, st);
+    else launch_s2t_nb<T, QW, 8, EPI>(tab, grid, batch, st);
+}
+
+// Launches the MFMA stage 2 for words-per-wave choice qw; false when qw is not one of them.
+template <typename T, int EPI>
+bool launch_s2t_qw(S2Table& tab, int qw, int batch, hipStream_t st) {
+    switch (qw) {
+        case 2: launch_s2t_table<T, 2, EPI>(tab, batch, st); return true;
+        case 4: launch_s2t_table<T, 4, EPI>(tab, batch, st); return true;
+        case 6: launch_s2t_table<T, 6, EPI>(tab, batch, st); return true;
+        case 8: launch_s2t_table<T, 8, EPI>(tab, batch, st); return true;
+        case 10: launch_s2t_table<T, 10, EPI>(tab, batch, st); return true;
+        case 12: launch_s2t_table<T, 12, EPI>(tab, batch, st); return true;
+        case 14: launch_s2t_table<T, 14, EPI>(tab, batch, st); return true;
+        case 16: launch_s2t_table<T, 16, EPI>(tab, batch, st); return true;
+        case 20: launch_s2t_table<T, 20, EPI>(tab, batch, st); return true;
+        case 24: launch_s2t_table<T, 24, EPI>(tab, batch, st); return true;
+        case 28: launch_s2t_table<T, 28, EPI>(tab, batch, st); return true;
+        case 32: launch_s2t_table<T, 32, EPI>(tab, batch, st); return true;
+        case 36: launch_s2t_table<T, 36, EPI>(tab, batch, st); return true;
+        default: return false;
+    }
+}
+
+inline bool s2t_applies(const void* z_hi, const void* z_lo, const uint32_t* u_bits, int m, const Plan& plan) {
+    return aligned(z_hi, 16) && aligned(z_lo, 16) && aligned(u_bits, 16) && static_cast<int64_t>(m) * plan.wr >= 4 &&
+           plan.s2_qw > 0;
 }
 
 template <typename T>
 void launch_stage2(const GemvArgs& a) {
-    const bool fast = aligned(a.z_hi, 16) && aligned(a.z_lo, 16) && aligned(a.u_bits, 16) &&
-                      static_cast<int64_t>(a.m) * a.plan.wr >= 4;
-    switch (fast ? a.plan.s2_qw : 0) {
-        case 2: launch_s2t<T, 2>(a); return;
-        case 4: launch_s2t<T, 4>(a); return;
-        case 6: launch_s2t<T, 6>(a); return;
-        case 8: launch_s2t<T, 8>(a); return;
-        case 10: launch_s2t<T, 10>(a); return;
-        case 12: launch_s2t<T, 12>(a); return;
-        case 14: launch_s2t<T, 14>(a); return;
-        case 16: launch_s2t<T, 16>(a); return;
-        case 20: launch_s2t<T, 20>(a); return;
-        case 24: launch_s2t<T, 24>(a); return;
-        case 28: launch_s2t<T, 28>(a); return;
-        case 32: launch_s2t<T, 32>(a); return;
-        case 36: launch_s2t<T, 36>(a); return;
-        default: break;
+    if (s2t_applies(a.z_hi, a.z_lo, a.u_bits, a.m, a.plan)) {
+        S2Table tab;
+        tab.count = 1;
+        S2Item& it = tab.item[0];
+        it.u_bits = a.u_bits;
+        it.s_out = a.s_out;
+        it.y = a.y;
+        it.resid = nullptr;
+        it.z_hi = a.z_hi;
+        it.z_lo = a.z_lo;
+        it.m = a.m;
+        it.wr = a.plan.wr;
+        it.zpitch = a.plan.zpitch;
+        it.ystride = a.m;
+        it.block_begin = 0;
+        if (launch_s2t_qw<T, kEpiStoreOne>(tab, a.plan.s2_qw, a.batch, a.stream)) return;
     }
     if (a.batch <= 1) launch_stage2_generic<T, 1>(a);
     else if (a.batch <= 2) launch_stage2_generic<T, 2>(a);
@@ -636,10 +863,8 @@ void launch_stage2(const GemvArgs& a) {
 
 template <typename T>
 int run_gemv(const GemvArgs& a) {
-    if (a.r > 0) {
-        launch_stage1<T>(a);
-        if (int s = check_launch("nq_gemv stage 1")) return s;
-    }
+    launch_stage1<T>(a);
+    if (int s = check_launch("nq_gemv stage 1")) return s;
     launch_stage2<T>(a);
     return check_launch("nq_gemv stage 2");
 }
@@ -676,7 +901,8 @@ int setup_gemv(const char* name, int stages, int dtype, const void* x, const voi
         batch * plan_of(r).zpitch > INT32_MAX / 4 || m * ceil_div(r, 32) > INT32_MAX / 4 ||
         r * ceil_div(n, 32) > INT32_MAX / 4 || batch * n > INT32_MAX / 4)
         return fail(NQ_ERR_UNSUPPORTED, "%s: sizes beyond 2^29 are not supported", name);
-    if (batch == 0 || (stages == kStage1 ? r == 0 : m == 0)) return -1;
+    // stage 1 with r == 0 still runs: it zeroes the intermediate stage 2 reads
+    if (batch == 0 || (stages != kStage1 && m == 0)) return -1;
     const bool s1 = stages & kStage1, s2 = stages & kStage2;
     if (!workspace || (s1 && (!x || !s_in || !v_bits)) || (s2 && (!u_bits || !s_out || !y)))
         return fail(NQ_ERR_INVALID_ARGUMENT, "%s: null pointer", name);
@@ -751,6 +977,178 @@ int nq_gemv_stage2(int dtype, const uint32_t* u_bits, const void* s_out, void* y
                              batch, n, r, m, workspace, workspace_bytes, stream, a);
     if (s != NQ_OK) return s < 0 ? NQ_OK : s;
     return dtype == NQ_F16 ? run_stage2<F16>(a) : run_stage2<BF16>(a);
+}
+
+}  // extern "C"
+
+// --------------------------------------------------------------------------- grouped calls
+
+namespace nq {
+namespace {
+
+// Workspace of a group: the header, then each item's (hi, lo) intermediate in item order.
+struct GroupLayout {
+    Plan plan[kMaxItems];
+    uint16_t* z_hi[kMaxItems];
+    uint16_t* z_lo[kMaxItems];
+    size_t bytes;
+};
+
+int group_layout(const char* name, int64_t count, const nq_gemv_item* items, int64_t batch, void* workspace,
+                 GroupLayout& g) {
+    if (count < 1 || count > kMaxItems || !items)
+        return fail(NQ_ERR_INVALID_ARGUMENT, "%s: count must be 1..%d with an item array, got %lld", name, kMaxItems,
+                    (long long)count);
+    size_t off = kHeaderBytes;
+    for (int64_t k = 0; k < count; ++k) {
+        const int64_t r = items[k].r;
+        if (r <= 0 || r > INT32_MAX / 4 || batch * plan_of(r).zpitch > INT32_MAX / 4)
+            return fail(NQ_ERR_SHAPE, "%s: item %lld has rank %lld (needs 1 .. 2^29)", name, (long long)k,
+                        (long long)r);
+        g.plan[k] = plan_of(r);
+        const size_t zb = z_bytes(batch, g.plan[k]);
+        char* base = static_cast<char*>(workspace);
+        g.z_hi[k] = base ? reinterpret_cast<uint16_t*>(base + off) : nullptr;
+        g.z_lo[k] = base ? reinterpret_cast<uint16_t*>(base + off + zb) : nullptr;
+        off += 2 * zb;
+    }
+    g.bytes = off;
+    return NQ_OK;
+}
+
+int check_group_common(const char* name, int dtype, int64_t batch, void* workspace, size_t workspace_bytes,
+                       const GroupLayout& g) {
+    if (dtype != NQ_F16 && dtype != NQ_BF16) return fail(NQ_ERR_DTYPE, "%s: unsupported dtype %d", name, dtype);
+    if (batch < 0 || batch > INT32_MAX / 4) return fail(NQ_ERR_INVALID_ARGUMENT, "%s: bad batch %lld", name,
+                                                        (long long)batch);
+    if (!workspace) return fail(NQ_ERR_INVALID_ARGUMENT, "%s: null workspace", name);
+    if (!aligned(workspace, 256)) return fail(NQ_ERR_ALIGNMENT, "%s: workspace must be 256-byte aligned", name);
+    if (workspace_bytes < g.bytes)
+        return fail(NQ_ERR_WORKSPACE, "%s: workspace has %zu bytes, needs %zu", name, workspace_bytes, g.bytes);
+    return NQ_OK;
+}
+
+}  // namespace
+}  // namespace nq
+
+extern "C" {
+
+size_t nq_gemv_group_workspace_bytes(int64_t count, const nq_gemv_item* items, int64_t batch) {
+    GroupLayout g;
+    if (batch < 0 || group_layout("nq_gemv_group_workspace_bytes", count, items, batch, nullptr, g) != NQ_OK) return 0;
+    return g.bytes;
+}
+
+int nq_gemv_group_stage1(int dtype, int64_t count, const nq_gemv_item* items, const void* x, int64_t batch, int64_t n,
+                         float rms_eps, void* workspace, size_t workspace_bytes, nq_stream_t stream) {
+    const char* name = "nq_gemv_group_stage1";
+    GroupLayout g;
+    if (int s = group_layout(name, count, items, batch, workspace, g)) return s;
+    if (int s = check_group_common(name, dtype, batch, workspace, workspace_bytes, g)) return s;
+    if (n <= 0 || n > INT32_MAX / 4 || batch * n > INT32_MAX / 4)
+        return fail(NQ_ERR_SHAPE, "%s: bad n %lld", name, (long long)n);
+    if (batch == 0) return NQ_OK;
+    const int wn = static_cast<int>(ceil_div(n, 32));
+    const auto* xp = static_cast<const uint16_t*>(x);
+    if (!x) return fail(NQ_ERR_INVALID_ARGUMENT, "%s: null x", name);
+    S1Table tab;
+    tab.count = static_cast<int>(count);
+    for (int64_t k = 0; k < count; ++k) {
+        const nq_gemv_item& in = items[k];
+        if (!in.v_bits || !in.s_in) return fail(NQ_ERR_INVALID_ARGUMENT, "%s: item %lld: null pointer", name, (long long)k);
+        if (in.r * ceil_div(n, 32) > INT32_MAX / 4) return fail(NQ_ERR_UNSUPPORTED, "%s: item too large", name);
+        if (!aligned(in.v_bits, 4) || (in.s_mid && !aligned(in.s_mid, 2)))
+            return fail(NQ_ERR_ALIGNMENT, "%s: item %lld: misaligned operand", name, (long long)k);
+        if (!s1w_applies(xp, static_cast<const uint16_t*>(in.s_in), static_cast<int>(n), wn, static_cast<int>(in.r)))
+            return fail(NQ_ERR_UNSUPPORTED,
+                        "%s: needs n %% 8 == 0, 8 <= n <= 16384 and 16-byte aligned x and s_in (item %lld)", name,
+                        (long long)k);
+        S1Item& it = tab.item[k];
+        it.v_bits = in.v_bits;
+        it.s_in = static_cast<const uint16_t*>(in.s_in);
+        it.s_mid = static_cast<const uint16_t*>(in.s_mid);
+        it.z_hi = g.z_hi[k];
+        it.z_lo = g.z_lo[k];
+        it.r = static_cast<int>(in.r);
+        it.kpad = g.plan[k].kpad;
+        it.zpitch = g.plan[k].zpitch;
+        it.block_begin = 0;
+    }
+    const bool norm = rms_eps >= 0.0f;
+    if (dtype == NQ_F16)
+        launch_s1w_table<F16>(tab, xp, static_cast<int>(batch), static_cast<int>(n), wn, norm, rms_eps, as_stream(stream));
+    else
+        launch_s1w_table<BF16>(tab, xp, static_cast<int>(batch), static_cast<int>(n), wn, norm, rms_eps, as_stream(stream));
+    return check_launch(name);
+}
+
+int nq_gemv_group_stage2(int dtype, int64_t count, const nq_gemv_item* items, int64_t batch, int epilogue,
+                         void* workspace, size_t workspace_bytes, nq_stream_t stream) {
+    const char* name = "nq_gemv_group_stage2";
+    GroupLayout g;
+    if (int s = group_layout(name, count, items, batch, workspace, g)) return s;
+    if (int s = check_group_common(name, dtype, batch, workspace, workspace_bytes, g)) return s;
+    if (epilogue != NQ_EPI_STORE && epilogue != NQ_EPI_RESIDUAL && epilogue != NQ_EPI_GATED)
+        return fail(NQ_ERR_INVALID_ARGUMENT, "%s: unknown epilogue %d", name, epilogue);
+    if (epilogue == NQ_EPI_GATED && (count != 2 || items[0].m != items[1].m || items[0].r != items[1].r))
+        return fail(NQ_ERR_SHAPE, "%s: the gated epilogue takes two items (gate, up) of equal m and r", name);
+    if (batch == 0) return NQ_OK;
+    S2Item all[kMaxItems];
+    for (int64_t k = 0; k < count; ++k) {
+        const nq_gemv_item& in = items[k];
+        const int64_t m = in.m;
+        if (m <= 0 || m > INT32_MAX / 4 || m * ceil_div(in.r, 32) > INT32_MAX / 4 || in.y_stride < m ||
+            batch * in.y_stride > INT32_MAX / 4)
+            return fail(NQ_ERR_SHAPE, "%s: item %lld: bad m %lld or y_stride %lld", name, (long long)k, (long long)m,
+                        (long long)in.y_stride);
+        if (!in.u_bits || !in.s_out || !in.y || (epilogue == NQ_EPI_RESIDUAL && !in.resid))
+            return fail(NQ_ERR_INVALID_ARGUMENT, "%s: item %lld: null pointer", name, (long long)k);
+        if (!aligned(in.s_out, 2) || !aligned(in.y, 2) || (in.resid && !aligned(in.resid, 2)))
+            return fail(NQ_ERR_ALIGNMENT, "%s: item %lld: misaligned operand", name, (long long)k);
+        if (!s2t_applies(g.z_hi[k], g.z_lo[k], in.u_bits, static_cast<int>(m), g.plan[k]))
+            return fail(NQ_ERR_UNSUPPORTED, "%s: needs 16-byte aligned u_bits, r <= 4608 and m * ceil(r/32) >= 4 "
+                        "(item %lld)", name, (long long)k);
+        S2Item& it = all[k];
+        it.u_bits = in.u_bits;
+        it.s_out = static_cast<const uint16_t*>(in.s_out);
+        it.y = static_cast<uint16_t*>(in.y);
+        it.resid = static_cast<const uint16_t*>(in.resid);
+        it.z_hi = g.z_hi[k];
+        it.z_lo = g.z_lo[k];
+        it.m = static_cast<int>(m);
+        it.wr = g.plan[k].wr;
+        it.zpitch = g.plan[k].zpitch;
+        it.ystride = static_cast<int>(in.y_stride);
+        it.block_begin = 0;
+    }
+    // one launch per class of items that share the stage-2 word split (equal ranks always do)
+    const int b = static_cast<int>(batch);
+    hipStream_t st = as_stream(stream);
+    bool done[kMaxItems] = {false, false, false, false};
+    for (int64_t k0 = 0; k0 < count; ++k0) {
+        if (done[k0]) continue;
+        const int qw = g.plan[k0].s2_qw;
+        S2Table tab;
+        tab.count = 0;
+        for (int64_t k = k0; k < count; ++k)
+            if (!done[k] && g.plan[k].s2_qw == qw) {
+                tab.item[tab.count++] = all[k];
+                done[k] = true;
+            }
+        bool ok;
+        if (dtype == NQ_F16) {
+            ok = epilogue == NQ_EPI_STORE      ? launch_s2t_qw<F16, kEpiStore>(tab, qw, b, st)
+                 : epilogue == NQ_EPI_RESIDUAL ? launch_s2t_qw<F16, kEpiResidual>(tab, qw, b, st)
+                                               : launch_s2t_qw<F16, kEpiGated>(tab, qw, b, st);
+        } else {
+            ok = epilogue == NQ_EPI_STORE      ? launch_s2t_qw<BF16, kEpiStore>(tab, qw, b, st)
+                 : epilogue == NQ_EPI_RESIDUAL ? launch_s2t_qw<BF16, kEpiResidual>(tab, qw, b, st)
+                                               : launch_s2t_qw<BF16, kEpiGated>(tab, qw, b, st);
+        }
+        if (!ok) return fail(NQ_ERR_UNSUPPORTED, "%s: no stage-2 configuration for this rank", name);
+        if (int s = check_launch(name)) return s;
+    }
+    return NQ_OK;
 }
 
 }  // extern "C"

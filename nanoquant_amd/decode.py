@@ -117,16 +117,15 @@ def _rotate_half(x):
 class StaticKVCache:
     """Per-layer K and V of ``batch`` sequences up to ``max_len`` positions.
 
-    K is kept transposed, [B, kv_heads, head_dim, max_len], so the score product
-    q @ K reads a contiguous right operand; V is [B, kv_heads, max_len, head_dim].
-    Mirrors ``make_cache`` (test_decode.py:420-422): preallocated once, written in
+    Both are [B, kv_heads, max_len, head_dim]: a position's key or value is one contiguous
+    row. Mirrors ``make_cache`` (test_decode.py:420-422): preallocated once, written in
     place at the step's position.
     """
 
     def __init__(self, shape: LlamaShape, batch: int, max_len: int, device, dtype):
         self.batch, self.max_len = batch, max_len
         kv, d = shape.kv_heads, shape.head_dim
-        self.k_t = [torch.zeros(batch, kv, d, max_len, device=device, dtype=dtype) for _ in range(shape.layers)]
+        self.k = [torch.zeros(batch, kv, max_len, d, device=device, dtype=dtype) for _ in range(shape.layers)]
         self.v = [torch.zeros(batch, kv, max_len, d, device=device, dtype=dtype) for _ in range(shape.layers)]
         self.key_index = torch.arange(max_len, device=device)
 
@@ -147,12 +146,13 @@ class LlamaAttention(nn.Module):
         v = self.v_proj(x).view(B, T, KV, D).transpose(1, 2)
         q = q * cos + _rotate_half(q) * sin
         k = k * cos + _rotate_half(k) * sin
-        k_t, v_c = cache.k_t[self.layer], cache.v[self.layer]
-        k_t.index_copy_(3, positions, k.transpose(2, 3).to(k_t.dtype))
+        k_c, v_c = cache.k[self.layer], cache.v[self.layer]
+        k_c.index_copy_(2, positions, k.to(k_c.dtype))
         v_c.index_copy_(2, positions, v.to(v_c.dtype))
-        # queries of one kv head side by side: [B, KV, G*T, D] @ [B, KV, D, L]
+        # queries of one kv head side by side: [B, KV, G*T, D] @ [B, KV, D, L] (a contiguous copy
+        # of K^T, so the batched product never takes a transposed operand)
         qg = q.reshape(B, KV, G * T, D)
-        scores = torch.matmul(qg, k_t).float() * self.scaling
+        scores = torch.matmul(qg, k_c.transpose(2, 3).contiguous()).float() * self.scaling
         visible = cache.key_index.view(1, -1) <= positions.view(-1, 1)  # [T, L]
         scores = scores.view(B, KV, G, T, -1).masked_fill(~visible, float("-inf"))
         p = torch.softmax(scores, dim=-1).to(v_c.dtype).view(B, KV, G * T, -1)
@@ -353,9 +353,139 @@ class GraphDecoder:
         return logits
 
 
+class FusedDecoder(GraphDecoder):
+    """GraphDecoder whose one-token step runs each layer in nine launches of the HIP library:
+
+    1. q, k, v stage 1 in one launch, with input_layernorm folded in (its weight multiplied
+       into each s_in, the rsqrt(mean(x^2) + eps) factor applied to h);
+    2. q, k, v stage 2 in one launch, into one [B, (heads + 2 kv_heads) * head_dim] buffer;
+    3. rotary embedding, KV-cache write and attention (``nq_attention_decode``);
+    4, 5. o_proj, its stage 2 adding the residual;
+    6. gate and up stage 1 in one launch, post_attention_layernorm folded in;
+    7. gate and up stage 2 in one launch storing silu(gate) * up;
+    8, 9. down_proj, its stage 2 adding the residual.
+    The embedding lookup, final norm, lm_head and argmax stay torch ops. Prefill runs the
+    unfused model (it fills the same cache layout). Needs the model packed for the ``gemv``
+    kernel in float16 or bfloat16 and head_dim 128.
+    """
+
+    def __init__(self, model: NanoQuantLlama, batch: int, max_len: int, steps_per_graph: int = 1,
+                 device="cuda"):
+        super().__init__(model, batch, max_len, steps_per_graph, device)
+        from . import _lib
+
+        self._lib = _lib
+        self.lib = _lib.load()
+        s = model.shape
+        dt = model.dtype
+        if dt not in (torch.float16, torch.bfloat16):
+            raise ValueError(f"the fused decode step needs a float16 or bfloat16 model, got {dt}")
+        if s.head_dim != 128:
+            raise ValueError(f"the fused decode step needs head_dim 128, got {s.head_dim}")
+        for lin in model.linears():
+            if getattr(lin, "kernel_type", None) != "gemv":
+                raise ValueError("the fused decode step needs every linear prepared for the 'gemv' kernel")
+        dev = self.device
+        H, KV, D = s.heads, s.kv_heads, s.head_dim
+        self.dcode = _lib.dtype_code(dt)
+        self.qkv_width = (H + 2 * KV) * D
+        self.x = torch.zeros(batch, s.hidden, device=dev, dtype=dt)
+        self.h = torch.zeros(batch, s.hidden, device=dev, dtype=dt)
+        self.qkv = torch.zeros(batch, self.qkv_width, device=dev, dtype=dt)
+        self.attn = torch.zeros(batch, H * D, device=dev, dtype=dt)
+        self.act = torch.zeros(batch, s.ffn, device=dev, dtype=dt)
+        cos, sin = model.rope(torch.arange(max_len, device=dev), dt)
+        self.rope_cos, self.rope_sin = cos.contiguous(), sin.contiguous()
+        self._keep = []  # tensors whose addresses the item tables hold
+        self.plans = [self._layer_plan(layer) for layer in model.model.layers]
+        need = 0
+        for plan in self.plans:
+            for items, count in (plan["qkv"], plan["o"], plan["gu"], plan["down"]):
+                need = max(need, self.lib.nq_gemv_group_workspace_bytes(count, items, batch))
+        self.ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=dev)
+
+    def _scale_in(self, lin, norm_weight):
+        s_in = lin.scale_pre
+        if norm_weight is not None:
+            s_in = (s_in.float() * norm_weight.float()).to(s_in.dtype)
+        s_in = s_in.contiguous()
+        self._keep.append(s_in)
+        return s_in
+
+    def _items(self, entries):
+        arr = (self._lib.GemvItem * len(entries))()
+        for i, (lin, norm_weight, y, y_off, y_stride, resid) in enumerate(entries):
+            it = arr[i]
+            it.v_bits = lin.V_int8.data_ptr()
+            it.s_in = self._scale_in(lin, norm_weight).data_ptr()
+            mid = getattr(lin, "scale_mid", None)
+            it.s_mid = None if mid is None else mid.data_ptr()
+            it.u_bits = lin.U_int8.data_ptr()
+            it.s_out = lin.scale_post.data_ptr()
+            it.y = y.data_ptr() + y_off * y.element_size()
+            it.resid = None if resid is None else resid.data_ptr()
+            it.r = lin.V_int8.shape[0]
+            it.m = lin.scale_post.numel()
+            it.y_stride = y_stride
+        return arr, len(entries)
+
+    def _layer_plan(self, layer):
+        s = self.model.shape
+        H, KV, D = s.heads, s.kv_heads, s.head_dim
+        a, mlp = layer.self_attn, layer.mlp
+        w1, w2 = layer.input_layernorm.weight, layer.post_attention_layernorm.weight
+        W = self.qkv_width
+        return {
+            "qkv": self._items([(a.q_proj, w1, self.qkv, 0, W, None), (a.k_proj, w1, self.qkv, H * D, W, None),
+                                (a.v_proj, w1, self.qkv, (H + KV) * D, W, None)]),
+            "o": self._items([(a.o_proj, None, self.h, 0, s.hidden, self.x)]),
+            "gu": self._items([(mlp.gate_proj, w2, self.act, 0, s.ffn, None),
+                               (mlp.up_proj, w2, self.act, 0, s.ffn, None)]),
+            "down": self._items([(mlp.down_proj, None, self.x, 0, s.hidden, self.h)]),
+            "eps1": layer.input_layernorm.eps, "eps2": layer.post_attention_layernorm.eps,
+        }
+
+    def _check(self, status, what):
+        self._lib.check(status, what)
+
+    def _step(self):
+        lib, s, B = self.lib, self.model.shape, self.batch
+        H, KV, D = s.heads, s.kv_heads, s.head_dim
+        dt, ws, wsb = self.dcode, self.ws.data_ptr(), self.ws.numel()
+        st = self._lib.stream_of(self.device)
+        tok = self.ids.index_select(1, self.pos).view(-1)
+        torch.index_select(self.model.model.embed_tokens.weight, 0, tok, out=self.x)
+        x, h, qkv, attn, act = (t.data_ptr() for t in (self.x, self.h, self.qkv, self.attn, self.act))
+        esz = self.qkv.element_size()
+        for li, plan in enumerate(self.plans):
+            items, n = plan["qkv"]
+            self._check(lib.nq_gemv_group_stage1(dt, n, items, x, B, s.hidden, plan["eps1"], ws, wsb, st), "qkv 1")
+            self._check(lib.nq_gemv_group_stage2(dt, n, items, B, self._lib.NQ_EPI_STORE, ws, wsb, st), "qkv 2")
+            self._check(lib.nq_attention_decode(
+                dt, qkv, qkv + H * D * esz, qkv + (H + KV) * D * esz, self.qkv_width,
+                self.cache.k[li].data_ptr(), self.cache.v[li].data_ptr(), self.rope_cos.data_ptr(),
+                self.rope_sin.data_ptr(), self.pos.data_ptr(), attn, B, H, KV, D, self.max_len,
+                D ** -0.5, st), "attention")
+            items, n = plan["o"]
+            self._check(lib.nq_gemv_group_stage1(dt, n, items, attn, B, H * D, -1.0, ws, wsb, st), "o 1")
+            self._check(lib.nq_gemv_group_stage2(dt, n, items, B, self._lib.NQ_EPI_RESIDUAL, ws, wsb, st), "o 2")
+            items, n = plan["gu"]
+            self._check(lib.nq_gemv_group_stage1(dt, n, items, h, B, s.hidden, plan["eps2"], ws, wsb, st), "gu 1")
+            self._check(lib.nq_gemv_group_stage2(dt, n, items, B, self._lib.NQ_EPI_GATED, ws, wsb, st), "gu 2")
+            items, n = plan["down"]
+            self._check(lib.nq_gemv_group_stage1(dt, n, items, act, B, s.ffn, -1.0, ws, wsb, st), "down 1")
+            self._check(lib.nq_gemv_group_stage2(dt, n, items, B, self._lib.NQ_EPI_RESIDUAL, ws, wsb, st),
+                        "down 2")
+        logits = self.model.lm_head(self.model.model.norm(self.x)).float()
+        nxt = logits.argmax(dim=-1, keepdim=True)
+        self.pos.add_(1)
+        self.ids.index_copy_(1, self.pos, nxt)
+        return logits
+
+
 @torch.no_grad()
 def generate(model: NanoQuantLlama, prompt: torch.Tensor, max_new_tokens: int, steps_per_graph: int = 1,
-             use_graph: bool = True, decoder: GraphDecoder | None = None):
+             use_graph: bool = True, decoder: GraphDecoder | None = None, fused: bool = False):
     """Greedy generation with decode timing (test_decode.py:474-693, greedy instead of top-k sampling).
 
     Returns (ids [B, T + max_new_tokens], tokens_per_s, prof). Token 1 comes from the
@@ -364,7 +494,8 @@ def generate(model: NanoQuantLlama, prompt: torch.Tensor, max_new_tokens: int, s
     """
     B, T = prompt.shape
     if decoder is None:
-        decoder = GraphDecoder(model, B, T + max_new_tokens, steps_per_graph, device=prompt.device)
+        cls = FusedDecoder if fused else GraphDecoder
+        decoder = cls(model, B, T + max_new_tokens, steps_per_graph, device=prompt.device)
         if use_graph:
             decoder.capture()
     steps = max_new_tokens - 1

@@ -111,3 +111,51 @@ def test_gemm_kernel_decode(models):
     prompt = torch.randint(0, SHAPE.vocab, (3, 12), generator=torch.Generator().manual_seed(8))
     ids, lg = run(model, prompt, 5, use_graph=False)
     check_against_dense(models, ids, lg, prompt.shape[1])
+
+
+# --------------------------------------------------------------------------- fused decode step
+
+FUSED_SHAPES = {
+    "gqa": LlamaShape(hidden=512, layers=2, heads=4, kv_heads=2, ffn=1024, vocab=1000),
+    "mha": LlamaShape(hidden=512, layers=2, heads=4, kv_heads=4, ffn=768, vocab=1000),
+}
+
+
+def run_fused(model, prompt, new, use_graph, steps_per_graph=1):
+    from nanoquant_amd.decode import FusedDecoder
+    B, T = prompt.shape
+    dec = FusedDecoder(model, B, T + new, steps_per_graph=steps_per_graph)
+    if use_graph:
+        dec.capture()
+    logits = [dec.prefill(prompt.cuda()).clone()]
+    if use_graph:
+        for _ in range((new - 1) // steps_per_graph):
+            dec.decode(steps_per_graph, use_graph=True)
+            logits.append(dec.last_logits.clone())
+    else:
+        for _ in range(new - 1):
+            logits.append(dec.decode(1, use_graph=False).clone())
+    torch.cuda.synchronize()
+    return dec.ids[:, :T + new].cpu(), [lg.cpu() for lg in logits]
+
+
+@pytest.mark.parametrize("name", list(FUSED_SHAPES))
+def test_fused_decode_matches_dense(name):
+    shape = FUSED_SHAPES[name]
+    announce("fused decode", name, shape)
+    from nanoquant_amd import _lib
+    _lib.load()
+    dense = random_llama(shape, bpw=0.55, seed=13, device="cpu", with_mid=(name == "gqa"))
+    with torch.no_grad():
+        for layer in dense.model.layers:  # norm weights away from 1 so that the fold is exercised
+            layer.input_layernorm.weight.uniform_(0.5, 1.5)
+            layer.post_attention_layernorm.weight.uniform_(0.5, 1.5)
+    model = kernel_model(dense, "gemv")
+    prompt = torch.randint(0, shape.vocab, (2, 12), generator=torch.Generator().manual_seed(3))
+    new = 9
+    ids_g, lg_g = run_fused(model, prompt, new, use_graph=True, steps_per_graph=2)
+    ids_e, lg_e = run_fused(model, prompt, new, use_graph=False)
+    assert torch.equal(ids_g, ids_e)
+    for j, (a, b) in enumerate(zip(lg_g, lg_e[::2])):
+        assert torch.equal(a, b), j
+    check_against_dense(dense, ids_e, lg_e, prompt.shape[1])

@@ -1,0 +1,251 @@
+"""The fused decode-step entry points on the GPU: grouped GEMV stages (with the RMSNorm fold
+and the residual / gated epilogues) and decode attention, through the C ABI.
+
+Bars (written here):
+* grouped GEMV without a norm or epilogue: bit-identical to nq_gemv per item;
+* norm fold, residual and gated epilogues: max|y - y*| / max|y*| against float64 on the same
+  fp16 inputs, <= 1e-3 (norm, residual) and <= 2e-3 (gated: three more fp16 roundings);
+* attention: the rotated key stored in the cache is bit-identical to torch's fp16 rotary
+  arithmetic; the stored value is the input value; rows other than the position are
+  untouched; the output is within 2e-3 of float64 attention (relative to its max);
+* a position outside the cache leaves the caches untouched and writes zeros.
+"""
+import ctypes
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def announce(*what):
+    print("\n[case]", *what, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from nanoquant_amd import _lib
+    return _lib.load()
+
+
+def words(signs):
+    return torch.from_numpy(O.pack_binary_gemv(signs, "half2").view(np.int32)).cuda()
+
+
+def item(_lib, v_bits, s_in, s_mid, u_bits, s_out, y, y_off, y_stride, resid, r, m):
+    it = _lib.GemvItem()
+    it.v_bits, it.s_in = v_bits.data_ptr(), s_in.data_ptr()
+    it.s_mid = None if s_mid is None else s_mid.data_ptr()
+    it.u_bits, it.s_out = u_bits.data_ptr(), s_out.data_ptr()
+    it.y = y.data_ptr() + y_off * y.element_size()
+    it.resid = None if resid is None else resid.data_ptr()
+    it.r, it.m, it.y_stride = r, m, y_stride
+    return it
+
+
+def make_linear(seed, m, n, r, with_mid=False):
+    c = O.random_case(seed, m, n, r, 1, with_mid=with_mid)
+    return c
+
+
+def group_call(lib, dtype_code, items, x, batch, n, eps, epilogue):
+    from nanoquant_amd import _lib
+    arr = (_lib.GemvItem * len(items))(*items)
+    need = lib.nq_gemv_group_workspace_bytes(len(items), arr, batch)
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    _lib.check(lib.nq_gemv_group_stage1(dtype_code, len(items), arr, x.data_ptr(), batch, n, eps, ws.data_ptr(),
+                                        need, st), "group stage 1")
+    _lib.check(lib.nq_gemv_group_stage2(dtype_code, len(items), arr, batch, epilogue, ws.data_ptr(), need, st),
+               "group stage 2")
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("batch", [1, 3])
+def test_group_matches_single_gemv(lib, dtype, batch):
+    from nanoquant_amd import _lib
+    announce("group vs single", dtype, batch)
+    n = 256
+    shapes = [(192, 96), (64, 352), (64, 96)]  # (m, r): two stage-2 configurations
+    x = torch.from_numpy(np.random.default_rng(3).normal(size=(batch, n)).astype(np.float16)).cuda().to(dtype)
+    width = sum(m for m, _ in shapes)
+    yg = torch.zeros(batch, width, dtype=dtype, device="cuda")
+    items, refs, off = [], [], 0
+    keep = []
+    for i, (m, r) in enumerate(shapes):
+        c = make_linear(10 + i, m, n, r, with_mid=(i == 1))
+        V, U = words(c["V"]), words(c["U"])
+        s_in = torch.from_numpy(c["s_in"]).cuda().to(dtype)
+        s_out = torch.from_numpy(c["s_out"]).cuda().to(dtype)
+        s_mid = None if c["s_mid"] is None else torch.from_numpy(c["s_mid"]).cuda().to(dtype)
+        keep += [V, U, s_in, s_out, s_mid]
+        refs.append(torch.ops.binary_kernels.nanoquant_dyn_forward(
+            x, s_in, V, s_mid, U, s_out, num_acc_stage1=1, num_acc_stage2=1))
+        items.append(item(_lib, V, s_in, s_mid, U, s_out, yg, off, width, None, r, m))
+        off += m
+    group_call(lib, _lib.dtype_code(dtype), items, x, batch, n, -1.0, _lib.NQ_EPI_STORE)
+    off = 0
+    for (m, _), ref in zip(shapes, refs):
+        got = yg[:, off:off + m]
+        assert torch.equal(got.contiguous().view(torch.int16), ref.view(torch.int16)), (m, off)
+        off += m
+
+
+def rel(y, y64):
+    y = y.float().cpu().numpy().astype(np.float64)
+    return float(np.abs(y - y64).max() / np.abs(y64).max())
+
+
+@pytest.mark.parametrize("batch", [1, 2])
+def test_group_norm_and_residual(lib, batch):
+    from nanoquant_amd import _lib
+    announce("group norm + residual", batch)
+    n, m, r, eps = 512, 320, 160, 1e-5
+    c = make_linear(21, m, n, r, with_mid=True)
+    rng = np.random.default_rng(5)
+    x = (rng.normal(size=(batch, n)) * 3.0).astype(np.float16)
+    w = np.abs(rng.normal(1.0, 0.3, n)).astype(np.float16)
+    s_in_folded = (c["s_in"].astype(np.float32) * w.astype(np.float32)).astype(np.float16)
+    resid = rng.normal(size=(batch, m)).astype(np.float16)
+    V, U = words(c["V"]), words(c["U"])
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    s_in, s_mid, s_out, xg, rg = t(s_in_folded), t(c["s_mid"]), t(c["s_out"]), t(x), t(resid)
+    y = torch.zeros(batch, m, dtype=torch.float16, device="cuda")
+    it = item(_lib, V, s_in, s_mid, U, s_out, y, 0, m, rg, r, m)
+    group_call(lib, _lib.NQ_F16, [it], xg, batch, n, eps, _lib.NQ_EPI_RESIDUAL)
+    x64 = x.astype(np.float64)
+    rstd = 1.0 / np.sqrt((x64 ** 2).mean(axis=1, keepdims=True) + eps)
+    lin = O.nanoquant_forward_f64(x64 * rstd, s_in_folded, c["V"], c["s_mid"], c["U"], c["s_out"])
+    err = rel(y, resid.astype(np.float64) + lin)
+    print(f"[fused] norm+residual rel err {err:.3e}", flush=True)
+    assert err <= 1e-3, err
+    # in place: y is also the residual
+    y2 = rg.clone()
+    it2 = item(_lib, V, s_in, s_mid, U, s_out, y2, 0, m, y2, r, m)
+    group_call(lib, _lib.NQ_F16, [it2], xg, batch, n, eps, _lib.NQ_EPI_RESIDUAL)
+    assert torch.equal(y2, y)
+
+
+def test_group_gated(lib):
+    from nanoquant_amd import _lib
+    announce("group gated")
+    batch, n, m, r = 2, 256, 448, 96
+    cg, cu = make_linear(31, m, n, r), make_linear(32, m, n, r)
+    for c in (cg, cu):  # gate and up of order 10, so that silu(gate) * up stays inside fp16
+        c["s_out"] = (c["s_out"].astype(np.float32) / 16).astype(np.float16)
+    x = torch.from_numpy(np.random.default_rng(7).normal(size=(batch, n)).astype(np.float16)).cuda()
+    keep, its = [], []
+    act = torch.zeros(batch, m, dtype=torch.float16, device="cuda")
+    for c in (cg, cu):
+        V, U = words(c["V"]), words(c["U"])
+        s_in, s_out = torch.from_numpy(c["s_in"]).cuda(), torch.from_numpy(c["s_out"]).cuda()
+        keep += [V, U, s_in, s_out]
+        its.append(item(_lib, V, s_in, None, U, s_out, act, 0, m, None, r, m))
+    group_call(lib, _lib.NQ_F16, its, x, batch, n, -1.0, _lib.NQ_EPI_GATED)
+    x64 = x.double().cpu().numpy()
+    g = O.nanoquant_forward_f64(x64, cg["s_in"], cg["V"], None, cg["U"], cg["s_out"])
+    u = O.nanoquant_forward_f64(x64, cu["s_in"], cu["V"], None, cu["U"], cu["s_out"])
+    want = g / (1.0 + np.exp(-g)) * u
+    err = rel(act, want)
+    print(f"[fused] gated rel err {err:.3e}", flush=True)
+    assert err <= 2e-3, err
+
+
+def test_group_argument_errors(lib):
+    from nanoquant_amd import _lib
+    arr = (_lib.GemvItem * 3)()
+    for it in arr:
+        it.r, it.m, it.y_stride = 32, 64, 64
+    ws = torch.zeros(1 << 16, dtype=torch.uint8, device="cuda")
+    assert lib.nq_gemv_group_stage2(0, 3, arr, 1, _lib.NQ_EPI_GATED, ws.data_ptr(), ws.numel(), None) == \
+        _lib.NQ_ERR_SHAPE
+    assert lib.nq_gemv_group_stage1(0, 0, arr, None, 1, 64, -1.0, ws.data_ptr(), ws.numel(), None) == \
+        _lib.NQ_ERR_INVALID_ARGUMENT
+
+
+# --------------------------------------------------------------------------- attention
+
+def rotate_half(x):
+    h = x.shape[-1] // 2
+    return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
+
+
+@pytest.mark.parametrize("G", [1, 2, 4, 8])
+@pytest.mark.parametrize("pos", [0, 17, 39])
+def test_attention_decode(lib, G, pos):
+    from nanoquant_amd import _lib
+    announce("attention", G, pos)
+    B, KV, D, L = 2, 2, 128, 40
+    H = KV * G
+    gen = torch.Generator().manual_seed(100 * G + pos)
+    qkv = torch.randn(B, (H + 2 * KV) * D, generator=gen).half()
+    kc = torch.randn(B, KV, L, D, generator=gen).half()
+    vc = torch.randn(B, KV, L, D, generator=gen).half()
+    inv = 1.0 / (10000.0 ** (torch.arange(0, D, 2).float() / D))
+    fr = torch.arange(L).float().view(-1, 1) * inv.view(1, -1)
+    emb = torch.cat((fr, fr), dim=-1)
+    cos, sin = emb.cos().half(), emb.sin().half()
+    d_qkv, d_kc, d_vc = qkv.cuda(), kc.clone().cuda(), vc.clone().cuda()
+    d_cos, d_sin = cos.cuda(), sin.cuda()
+    d_pos = torch.tensor([pos], dtype=torch.int64, device="cuda")
+    out = torch.zeros(B, H * D, dtype=torch.float16, device="cuda")
+    W = (H + 2 * KV) * D
+    p0 = d_qkv.data_ptr()
+    st = torch.cuda.current_stream().cuda_stream
+    _lib.check(lib.nq_attention_decode(_lib.NQ_F16, p0, p0 + 2 * H * D, p0 + 2 * (H + KV) * D, W, d_kc.data_ptr(),
+                                       d_vc.data_ptr(), d_cos.data_ptr(), d_sin.data_ptr(), d_pos.data_ptr(),
+                                       out.data_ptr(), B, H, KV, D, L, D ** -0.5, st), "attention")
+    torch.cuda.synchronize()
+    q = qkv[:, :H * D].view(B, H, D)
+    k = qkv[:, H * D:(H + KV) * D].view(B, KV, D)
+    v = qkv[:, (H + KV) * D:].view(B, KV, D)
+    # the cache rows: rotary arithmetic in fp16 as torch rounds it
+    k_rot = (k * cos[pos]) + (rotate_half(k) * sin[pos])
+    got_kc, got_vc = d_kc.cpu(), d_vc.cpu()
+    assert torch.equal(got_kc[:, :, pos].view(torch.int16), k_rot.view(torch.int16))
+    assert torch.equal(got_vc[:, :, pos], v)
+    others = [j for j in range(L) if j != pos]
+    assert torch.equal(got_kc[:, :, others], kc[:, :, others])
+    assert torch.equal(got_vc[:, :, others], vc[:, :, others])
+    # attention in float64 over positions 0..pos
+    q_rot = ((q * cos[pos]) + (rotate_half(q) * sin[pos])).double()
+    keys = got_kc[:, :, :pos + 1].double()  # [B, KV, P, D]
+    vals = got_vc[:, :, :pos + 1].double()
+    kk = keys.repeat_interleave(G, dim=1)
+    vv = vals.repeat_interleave(G, dim=1)
+    s = torch.einsum("bhd,bhpd->bhp", q_rot, kk) * D ** -0.5
+    p = torch.softmax(s, dim=-1)
+    want = torch.einsum("bhp,bhpd->bhd", p, vv).reshape(B, H * D).numpy()
+    err = rel(out, want)
+    assert err <= 2e-3, err
+
+
+def test_attention_position_outside_cache(lib):
+    from nanoquant_amd import _lib
+    announce("attention position outside")
+    B, KV, H, D, L = 1, 2, 2, 128, 16
+    qkv = torch.randn(B, (H + 2 * KV) * D, device="cuda").half()
+    kc = torch.randn(B, KV, L, D, device="cuda").half()
+    vc = torch.randn(B, KV, L, D, device="cuda").half()
+    kc0, vc0 = kc.clone(), vc.clone()
+    cs = torch.ones(L, D, device="cuda").half()
+    out = torch.ones(B, H * D, dtype=torch.float16, device="cuda")
+    W = (H + 2 * KV) * D
+    p0 = qkv.data_ptr()
+    for bad in (L, -1):
+        d_pos = torch.tensor([bad], dtype=torch.int64, device="cuda")
+        _lib.check(lib.nq_attention_decode(_lib.NQ_F16, p0, p0 + 2 * H * D, p0 + 2 * (H + KV) * D, W,
+                                           kc.data_ptr(), vc.data_ptr(), cs.data_ptr(), cs.data_ptr(),
+                                           d_pos.data_ptr(), out.data_ptr(), B, H, KV, D, L, 0.1, None), "attn")
+        torch.cuda.synchronize()
+        assert torch.equal(kc, kc0) and torch.equal(vc, vc0)
+        assert torch.count_nonzero(out) == 0
+    assert lib.nq_attention_decode(_lib.NQ_F16, p0, p0, p0, W, kc.data_ptr(), vc.data_ptr(), cs.data_ptr(),
+                                   cs.data_ptr(), d_pos.data_ptr(), out.data_ptr(), B, H, KV, 64, L, 0.1,
+                                   None) == _lib.NQ_ERR_UNSUPPORTED
