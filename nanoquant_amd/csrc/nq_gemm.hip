@@ -188,19 +188,30 @@ int launch_onebit(const void* A, const uint32_t* W, const void* s_in, const void
 //
 // C[q, o] = sat(s_out[o] * sum_k A[q, k] * sign(k, o) * s_in[k]), computed as C^T = S * A^T on
 // v_mfma_f32_32x32x16: the MFMA's A operand is 32 output features by 16 k of +-s_in, made from
-// the Marlin words in registers; its B operand is 16 k by 32 rows of A, from a double-buffered
-// LDS tile. Lane l = (kg = l / 32, c = l % 32).
+// the Marlin words in registers; its B operand is 16 k by 32 rows of A. Lane l = (kg = l / 32,
+// c = l % 32).
 //   sign operand: feature o = o0 + c; dword d = (r8 = d / 2, r2 = 2kg + d % 2) holds the pair
 //     k = 16tr + 8r8 + 2r2 + {0, 1}: Marlin word (tr, 32(o/64) + 4(o%8) + r2) shifted left by
 //     2((o%16)/8) + 4((o%64)/16) + r8 has their signs on bits 15 and 31, and they go onto the
-//     permuted s_in pair at 16tr + 4r2 + 2r8 (one 16-byte load per (tr, kg) covers all four);
-//   A operand: row q0 + c, the same k: A[q][16tr + 4kg .. +3] and A[q][16tr + 8 + 4kg .. +3];
+//     permuted s_in pair at 16tr + 4r2 + 2r8 (one 16-byte read per (tr, kg) covers all four);
+//   A operand: row q0 + c, the same k: A[q][16tr + 4kg .. +3] and A[q][16tr + 8 + 4kg .. +3],
+//     one 16-byte LDS read (the tile is stored with each 16-k group as k 0-3, 8-11, 4-7, 12-15);
 //   C: lane holds C^T[o0 + 8(i/4) + 4kg + i%4][q0 + c], four consecutive features per group of
 //      four registers, stored as one 8-byte write of C[q][o .. o+3].
+// Per 64-k step a block needs its A tile (BQ x 64 halves), the sign words of its BP features
+// (4 rows of BP/2 consecutive words: 1 KB at BP = 128) and 64 s_in values. Each is loaded once
+// per block, coalesced, two steps ahead into registers, and staged through double-buffered
+// LDS; lanes then read their words and s_in pairs from LDS (4 and 32 lanes share an address,
+// which LDS broadcasts). Loading the words per lane instead (4 lanes and 2 tiles per word,
+// and every wave of the block again) kept the texture data path ~70% busy.
 // The grid runs q tiles fastest: blocks i, i+8, ... land on one XCD, so with q_tiles dividing
 // 8 or a multiple of 8 each XCD streams its own rows of A through its L2.
+#ifndef NQ_SX_WAVES_PER_EU
+#define NQ_SX_WAVES_PER_EU 2
+#endif
 template <typename T, bool kSin, bool kSout, int BP, int BQ, int WP, int WQ, int BKK>
-__global__ __launch_bounds__((BP / WP) * (BQ / WQ) * 64) void gemm_sx_kernel(
+__global__ __launch_bounds__((BP / WP) * (BQ / WQ) * 64) __attribute__((amdgpu_waves_per_eu(NQ_SX_WAVES_PER_EU)))
+void gemm_sx_kernel(
     const uint16_t* __restrict__ A, const uint32_t* __restrict__ W, const uint16_t* __restrict__ s_in,
     const uint16_t* __restrict__ s_out, uint16_t* __restrict__ C, int M, int K, int N, int q_tiles) {
     constexpr int NWP = BP / WP;
@@ -208,12 +219,21 @@ __global__ __launch_bounds__((BP / WP) * (BQ / WQ) * 64) void gemm_sx_kernel(
     constexpr int NT = NWP * NWQ * 64;
     constexpr int TP = WP / 32;
     constexpr int TQ = WQ / 32;
-    constexpr int KT = BKK / 16;          // 16-k tiles per iteration
-    constexpr int LDX = BKK + 8;          // LDS row pitch of the A tile in halves
-    constexpr int XPIECES = BQ * BKK / 8; // 16-byte pieces of the A tile
+    constexpr int TG = WP / 64;            // 64-feature word groups per wave
+    constexpr int KT = BKK / 16;           // 16-k tiles per step
+    constexpr int LDX = BKK + 8;           // LDS row pitch of the A tile in halves
+    constexpr int XPIECES = BQ * BKK / 8;  // 16-byte pieces of the A tile
     constexpr int XPT = XPIECES / NT;
-    static_assert(XPIECES % NT == 0, "tile pieces must divide evenly");
+    constexpr int WROW = BP / 2;           // sign words per k-tile row of the block
+    constexpr int WWORDS = KT * WROW;      // sign words per step
+    constexpr int WPT = (WWORDS + NT - 1) / NT;  // sign words per thread (the last round may be partial)
+    constexpr int SDW = BKK / 2;           // s_in dwords per step
+    static_assert(XPIECES % NT == 0 && (WWORDS % NT == 0 || WWORDS < NT), "tile pieces must divide evenly");
+    static_assert(WP % 64 == 0 && BP % 64 == 0, "features come in whole 64-feature word groups");
+    static_assert(SDW <= NT, "one s_in dword per thread");
     __shared__ __attribute__((aligned(16))) uint16_t xs[2][BQ * LDX];
+    __shared__ __attribute__((aligned(16))) uint32_t ws[2][WWORDS];
+    __shared__ __attribute__((aligned(16))) uint32_t ss[2][SDW];
     __shared__ uint16_t sos[BP];
 
     const int t = threadIdx.x;
@@ -230,13 +250,16 @@ __global__ __launch_bounds__((BP / WP) * (BQ / WQ) * 64) void gemm_sx_kernel(
     const uint32_t half_n = static_cast<uint32_t>(N) >> 1;
     const int k_iters = K / BKK;
 
-    int wcol[TP], shb[TP];
+    // lane constants: the word of feature o (per 64-feature group) and its shift per tile
+    int wl[TG], shb[TP];
+#pragma unroll
+    for (int g = 0; g < TG; ++g) wl[g] = 32 * (wp * TG + g) + 4 * (c & 7) + 2 * kg;
 #pragma unroll
     for (int tp = 0; tp < TP; ++tp) {
-        const int o = min(p0 + wp * WP + 32 * tp + c, N - 1);
-        wcol[tp] = 32 * (o >> 6) + 4 * (o & 7) + 2 * kg;
+        const int o = wp * WP + 32 * tp + c;  // feature offset in the block
         shb[tp] = 2 * ((o & 15) >> 3) + 4 * ((o & 63) >> 4);
     }
+    // load sources: A pieces, sign words (row kt = word / WROW of the step), s_in dwords
     const uint16_t* xsrc[XPT];
     int xdst[XPT];
 #pragma unroll
@@ -245,38 +268,52 @@ __global__ __launch_bounds__((BP / WP) * (BQ / WQ) * 64) void gemm_sx_kernel(
         const int row = piece / (BKK / 8);
         const int c8 = piece - row * (BKK / 8);
         xsrc[j] = A + static_cast<size_t>(min(q0 + row, M - 1)) * K + 8 * c8;
-        xdst[j] = row * LDX + 8 * c8;
+        xdst[j] = row * LDX + 8 * c8;  // with the exchange, piece 2m + e holds half e of group m
     }
+    uint32_t wsrc[WPT];
+#pragma unroll
+    for (int j = 0; j < WPT; ++j) {
+        const int word = min(t + j * NT, WWORDS - 1);
+        const int kt = word / WROW;
+        wsrc[j] = kt * half_n + min(static_cast<uint32_t>(p0 / 2 + (word - kt * WROW)), half_n - 1);
+    }
+    const int sd = t % SDW;
     for (int e = t; e < BP; e += NT) sos[e] = kSout ? s_out[perm_out(min(p0 + e, N - 1))] : uint16_t(0);
 
-    // Operands of an iteration: the A tile (to LDS) and the sign words and s_in pairs (kept in
-    // registers). They are loaded two iterations ahead, so a load has two iterations of MFMAs
-    // to land before its LDS write, and the sign operand of iteration it is in registers when
-    // it starts.
     struct Ops {
         u32x4 x[XPT];
-        uint2 w[TP][KT];
-        u32x4 s[KT];
+        uint32_t w[WPT];
+        uint32_t s;  // used with kSin only
     };
     auto load_ops = [&](Ops& o, int iter) {
         const int k0 = iter * BKK;
 #pragma unroll
         for (int j = 0; j < XPT; ++j) o.x[j] = *reinterpret_cast<const u32x4*>(xsrc[j] + k0);
+        const uint32_t wrow = static_cast<uint32_t>(iter * KT) * half_n;
 #pragma unroll
-        for (int kt = 0; kt < KT; ++kt) {
-            const uint32_t tr = static_cast<uint32_t>(iter * KT + kt);
-#pragma unroll
-            for (int tp = 0; tp < TP; ++tp) o.w[tp][kt] = *reinterpret_cast<const uint2*>(W + tr * half_n + wcol[tp]);
-            o.s[kt] = kSin ? *reinterpret_cast<const u32x4*>(s_in + 16 * tr + 8 * kg)
-                           : u32x4{T::ONE_PAIR, T::ONE_PAIR, T::ONE_PAIR, T::ONE_PAIR};
-        }
+        for (int j = 0; j < WPT; ++j) o.w[j] = W[wrow + wsrc[j]];
+        if (kSin) o.s = *reinterpret_cast<const uint32_t*>(s_in + k0 + 2 * sd);
     };
-    Ops cur, nxt, nn;
-    load_ops(cur, 0);
-    if (k_iters > 1) load_ops(nxt, 1);
+    auto store_ops = [&](const Ops& o, int buf) {
+        // A piece is 8 halves of a row; lanes t (even) and t + 1 hold the two pieces of one
+        // 16-k group. The tile is stored with each group as k 0-3, 8-11, 4-7, 12-15, so that a
+        // lane's B fragment (k 4kg .. +3 and 8 + 4kg .. +3) is one 16-byte read: the even lane
+        // keeps its low half and takes its neighbour's low half, the odd lane the high halves.
+        const bool odd = t & 1;
 #pragma unroll
-    for (int j = 0; j < XPT; ++j) *reinterpret_cast<u32x4*>(&xs[0][xdst[j]]) = cur.x[j];
-    __syncthreads();
+        for (int j = 0; j < XPT; ++j) {
+            const u32x4 v = o.x[j];
+            const uint32_t s0 = odd ? v.x : v.z, s1 = odd ? v.y : v.w;
+            const uint32_t r0 = __builtin_amdgcn_mov_dpp(s0, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+            const uint32_t r1 = __builtin_amdgcn_mov_dpp(s1, 0xB1, 0xF, 0xF, false);
+            const u32x4 out = odd ? u32x4{r0, r1, v.z, v.w} : u32x4{v.x, v.y, r0, r1};
+            *reinterpret_cast<u32x4*>(&xs[buf][xdst[j]]) = out;
+        }
+#pragma unroll
+        for (int j = 0; j < WPT; ++j)
+            if (WWORDS % NT == 0 || t + j * NT < WWORDS) ws[buf][t + j * NT] = o.w[j];
+        if (kSin && t < SDW) ss[buf][t] = o.s;
+    };
 
     f32x16 acc[TP][TQ];
 #pragma unroll
@@ -287,41 +324,64 @@ __global__ __launch_bounds__((BP / WP) * (BQ / WQ) * 64) void gemm_sx_kernel(
             for (int i = 0; i < 16; ++i) acc[tp][tq][i] = 0.0f;
 
     const uint32_t mask = 0x80008000u;
-    for (int it = 0; it < k_iters; ++it) {
-        const int buf = it & 1;
-        if (it + 2 < k_iters) load_ops(nn, it + 2);
+    // One step: issue the loads of step it + 2 into `fill`, run the MFMAs of step it from LDS
+    // buffer it % 2, put `nxt` (step it + 1) into the other buffer. The three register sets
+    // rotate through a loop unrolled three times, so no register is ever copied (a copy of a
+    // just-issued load would wait for it).
+    // Loads and stores are unconditional (the tail reloads the last step): a load under a branch
+    // makes the wait counts at the merge assume it may be the newest load, and the stores at the
+    // end of the step would then wait for the loads just issued for two steps later.
+    auto step = [&](Ops& nxt, Ops& fill, int it) {
+        load_ops(fill, min(it + 2, k_iters - 1));
         __builtin_amdgcn_sched_barrier(0);
-
-        const uint16_t* xb = &xs[buf][(wq * WQ + c) * LDX + 4 * kg];
+        const int buf = it & 1;
+        const uint16_t* xb = &xs[buf][(wq * WQ + c) * LDX + 8 * kg];
+        // every LDS read of the step first (one latency per step, not one per k tile), then the
+        // sign operands and MFMAs as the reads land
+        u32x4 bx[KT][TQ];
+        uint2 wv[KT][TG];
+        u32x4 sv[KT];
 #pragma unroll
         for (int kt = 0; kt < KT; ++kt) {
-            u32x4 bx[TQ];
+#pragma unroll
+            for (int g = 0; g < TG; ++g) wv[kt][g] = *reinterpret_cast<const uint2*>(&ws[buf][kt * WROW + wl[g]]);
+            sv[kt] = kSin ? *reinterpret_cast<const u32x4*>(&ss[buf][8 * kt + 4 * kg])
+                          : u32x4{T::ONE_PAIR, T::ONE_PAIR, T::ONE_PAIR, T::ONE_PAIR};
 #pragma unroll
             for (int tq = 0; tq < TQ; ++tq) {
-                const uint16_t* p = xb + 32 * tq * LDX + 16 * kt;
-                const uint2 lo = *reinterpret_cast<const uint2*>(p);
-                const uint2 hi = *reinterpret_cast<const uint2*>(p + 8);
-                bx[tq] = u32x4{lo.x, lo.y, hi.x, hi.y};
+                bx[kt][tq] = *reinterpret_cast<const u32x4*>(xb + 32 * tq * LDX + 16 * kt);
             }
+        }
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) {
 #pragma unroll
             for (int tp = 0; tp < TP; ++tp) {
-                const uint32_t w0 = cur.w[tp][kt].x, w1 = cur.w[tp][kt].y;
+                const uint32_t w0 = wv[kt][tp / 2].x, w1 = wv[kt][tp / 2].y;
                 const int sft = shb[tp];
-                const u32x4 sv = cur.s[kt];
-                const u32x4 a = u32x4{sv.x ^ ((w0 << sft) & mask), sv.z ^ ((w1 << sft) & mask),
-                                      sv.y ^ ((w0 << (sft + 1)) & mask), sv.w ^ ((w1 << (sft + 1)) & mask)};
+                const u32x4 a = u32x4{sv[kt].x ^ ((w0 << sft) & mask), sv[kt].z ^ ((w1 << sft) & mask),
+                                      sv[kt].y ^ ((w0 << (sft + 1)) & mask), sv[kt].w ^ ((w1 << (sft + 1)) & mask)};
 #pragma unroll
-                for (int tq = 0; tq < TQ; ++tq) acc[tp][tq] = mfma32x32x16<T>(a, bx[tq], acc[tp][tq]);
+                for (int tq = 0; tq < TQ; ++tq) acc[tp][tq] = mfma32x32x16<T>(a, bx[kt][tq], acc[tp][tq]);
             }
         }
-
-        if (it + 1 < k_iters) {
-#pragma unroll
-            for (int j = 0; j < XPT; ++j) *reinterpret_cast<u32x4*>(&xs[buf ^ 1][xdst[j]]) = nxt.x[j];
-        }
-        cur = nxt;
-        nxt = nn;
+        store_ops(nxt, buf ^ 1);  // past the last step this writes a buffer nobody reads
         __syncthreads();
+    };
+
+    Ops o0, o1, o2;
+    load_ops(o0, 0);
+    load_ops(o1, min(1, k_iters - 1));
+    store_ops(o0, 0);
+    __syncthreads();
+    int it = 0;
+    for (; it + 3 <= k_iters; it += 3) {
+        step(o1, o2, it);
+        step(o2, o0, it + 1);
+        step(o0, o1, it + 2);
+    }
+    if (it < k_iters) {
+        step(o1, o2, it);
+        if (it + 1 < k_iters) step(o2, o0, it + 1);
     }
 
     // epilogue: scale, saturate, four consecutive features per 8-byte store
