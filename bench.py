@@ -328,6 +328,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--skip-decode", action="store_true", help="skip the end-to-end decode measurement")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="run only the end-to-end decode and print its result alone (for kernel traces)")
     ap.add_argument("--e2e-batch", type=int, default=1)
     ap.add_argument("--e2e-prompt", type=int, default=128)
     ap.add_argument("--e2e-new", type=int, default=256)
@@ -349,6 +351,11 @@ def main():
     _lib.load()
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+
+    if args.decode_only:  # profiling aid: only the end-to-end decode, reported on its own line
+        log(f"[bench] decode e2e B={args.e2e_batch} prompt={args.e2e_prompt} new={args.e2e_new}")
+        print(json.dumps({"decode_e2e": bench_decode(args, dev)}), flush=True)
+        return 0
 
     log(f"[bench] gemv m={M} n={N} r={R} B={args.batch} copies={args.copies}")
     g = bench_gemv(args, dev)
