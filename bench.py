@@ -25,7 +25,12 @@ The same JSON line carries:
 * ``cpu_baseline``: the reference's dense dequantize-and-matmul forward (two
   ``F.linear`` on dense +-1 bf16 factors, modules/linear.py:282-291) on the host
   cores, batch 1, on a bounded sample, in the same unit;
-* ``parity``: relative error of one GEMV and one GEMM against the float64 oracle.
+* ``parity``: relative error of one GEMV and one GEMM against the float64 oracle on the
+  same inputs, computed in the CPU leg (null with ``--skip-cpu``).
+
+``--sweep`` instead prints one line per config shape: the GEMV at batch 1, 4, 16 and
+the GEMM at batch 256 and 2048 on Llama-2-7B (1.0 and 0.55 bpw) and Llama-3-70B
+(0.55 bpw, uniform and mixture-of-rank) linears.
 
 Multi-GPU runs are not part of this build: ``--gpus`` above 1 exits with a message.
 """
@@ -99,13 +104,24 @@ def time_graph(fn_steps, n_steps, replays, warmup_replays, stream):
     return start.elapsed_time(end) / (replays * n_steps), graph, outs
 
 
+def make_case(seed, m, n, r, batch):
+    """Seeded synthetic inputs in a fixed draw order: U signs [m, r], V signs [r, n], s_in [n], s_out [m] as
+    fp16 |N(1, 0.2)|, x [batch, n] fp16 N(0, 1)."""
+    rng = np.random.default_rng(seed)
+    U = np.where(rng.random((m, r)) < 0.5, -1, 1).astype(np.int8)
+    V = np.where(rng.random((r, n)) < 0.5, -1, 1).astype(np.int8)
+    s_in = np.abs(rng.normal(1.0, 0.2, n)).astype(np.float16)
+    s_out = np.abs(rng.normal(1.0, 0.2, m)).astype(np.float16)
+    x = rng.normal(0.0, 1.0, (batch, n)).astype(np.float16)
+    return dict(U=U, V=V, s_in=s_in, s_out=s_out, x=x)
+
+
 def bench_gemv(args, dev):
     import nanoquant_amd as nq
-    import oracle as O
     from nanoquant_amd import _lib
 
     batch = args.batch
-    c = O.random_case(2024, M, N, R, batch)
+    c = make_case(2024, M, N, R, batch)
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
     # copy 0 is packed from known signs (parity); the others are random words, which are
     # valid half2 words of random signs (the padding-free shape leaves no unused bits)
@@ -122,8 +138,6 @@ def bench_gemv(args, dev):
 
     y_eager = op(x, s_in, V0, None, U0, s_out, **kw)
     torch.cuda.synchronize()
-    y64 = O.nanoquant_forward_f64(c["x"], c["s_in"], c["V"], None, c["U"], c["s_out"])
-    rel = float(np.abs(y_eager.double().cpu().numpy() - y64).max() / np.abs(y64).max())
 
     n_steps = args.copies
     replays = max(1, args.steps // n_steps)
@@ -158,18 +172,18 @@ def bench_gemv(args, dev):
     ms2, g2, _ = time_graph(stage2_steps, n_steps, replays, warm, stream)
     del g1, g2
     pb = packed_bytes(M, N, R)
-    return dict(ms=ms, ms1=ms1, ms2=ms2, steps=replays * n_steps, warmup=warm * n_steps, rel_err=rel,
+    return dict(ms=ms, ms1=ms1, ms2=ms2, steps=replays * n_steps, warmup=warm * n_steps, case=c,
+                y=y_eager.double().cpu().numpy(),
                 graph_matches_eager=graph_ok, packed_bytes=pb, total_bytes=gemv_total_bytes(M, N, R, batch),
                 pool_bytes=pb * args.copies)
 
 
 def bench_gemm(args, dev):
     import nanoquant_amd as nq
-    import oracle as O
 
     dtype = torch.float16
     B = args.gemm_batch
-    c = O.random_case(2025, M, N, R, B)
+    c = make_case(2025, M, N, R, B)
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
     packed = nq.pack_binary_marlin_fused(t(c["V"].T), t(c["U"].T), t(c["s_in"]),
                                          torch.ones(R, dtype=dtype, device=dev), t(c["s_out"]))
@@ -177,8 +191,6 @@ def bench_gemm(args, dev):
     op = torch.ops.binary_kernels.marlin_nanoquant_forward
     y = op(x, *packed)
     torch.cuda.synchronize()
-    y64 = O.nanoquant_forward_f64(c["x"], c["s_in"], c["V"], None, c["U"], c["s_out"])
-    rel = float(np.abs(y.double().cpu().numpy() - y64).max() / np.abs(y64).max())
     n_steps = 4
 
     def steps():
@@ -188,7 +200,22 @@ def bench_gemm(args, dev):
     ms, _, _ = time_graph(steps, n_steps, max(1, args.gemm_steps // n_steps), 2, stream)
     flops = 2.0 * B * R * (N + M)
     tflops = flops / (ms * 1e-3) / 1e12
-    return dict(ms=ms, tflops=tflops, rel_err=rel, flops=flops, r_pad=packed[1].shape[0] * 16)
+    return dict(ms=ms, tflops=tflops, flops=flops, r_pad=packed[1].shape[0] * 16, case=c,
+                y=y.double().cpu().numpy())
+
+
+def check_parity(results):
+    """Relative error of the GPU outputs against the float64 oracle on the same inputs (the CPU leg of the
+    bench: the oracle is the checker here, never the measured path). ``results`` maps a name to a dict with
+    ``case`` and ``y``."""
+    import oracle as O
+
+    out = {}
+    for name, res in results.items():
+        c = res["case"]
+        y64 = O.nanoquant_forward_f64(c["x"], c["s_in"], c["V"], None, c["U"], c["s_out"])
+        out[name] = float(np.abs(res["y"] - y64).max() / np.abs(y64).max())
+    return out
 
 
 def cpu_baseline(args):
@@ -197,7 +224,7 @@ def cpu_baseline(args):
 
     cores = min(len(os.sched_getaffinity(0)), args.cpu_threads)
     torch.set_num_threads(cores)
-    c = O.random_case(2026, M, N, R, 1)
+    c = make_case(2026, M, N, R, 1)
     dt = torch.bfloat16  # the reference module dtype (modules/linear.py:57)
     V = torch.from_numpy(c["V"].astype(np.float32)).to(dt)
     U = torch.from_numpy(c["U"].astype(np.float32)).to(dt)
@@ -314,6 +341,76 @@ def bench_decode(args, dev):
                          "tokens_per_s_at_peak": round(B * HBM_PEAK_GBS * 1e9 / step_bytes, 1)}}
 
 
+def sweep_shapes():
+    """(model, linear, m, n, r) of the benchmark configs: Llama-2-7B at 1.0 and 0.55 bpw and Llama-3-70B at
+    0.55 bpw, then Llama-3-70B with mixture-of-rank (each rank uniform in [0.8, 1.2] x the 0.55 rank, to 32)."""
+    from nanoquant_amd.decode import rank_for_bpw
+
+    l2 = [("q,k,v,o", 4096, 4096), ("gate,up", 11008, 4096), ("down", 4096, 11008)]
+    l3 = [("q,o", 8192, 8192), ("k,v", 1024, 8192), ("gate,up", 28672, 8192), ("down", 8192, 28672)]
+    out = []
+    for bpw in (1.0, 0.55):
+        out += [(f"llama2-7b@{bpw}", name, m, n, rank_for_bpw(m, n, bpw)) for name, m, n in l2]
+    out += [("llama3-70b@0.55", name, m, n, rank_for_bpw(m, n, 0.55)) for name, m, n in l3]
+    rng = np.random.default_rng(2024)
+    for name, m, n in [("q", 8192, 8192), ("k", 1024, 8192), ("v", 1024, 8192), ("o", 8192, 8192),
+                       ("gate", 28672, 8192), ("up", 28672, 8192), ("down", 8192, 28672)]:
+        base = rank_for_bpw(m, n, 0.55)
+        out.append(("llama3-70b@0.55 mixed", name, m, n, int(round(rng.uniform(0.8, 1.2) * base / 32.0)) * 32))
+    return out
+
+
+def run_sweep(args, dev):
+    """One JSON line per (shape, kind, batch): GEMV at batch 1, 4, 16 over rotating packed copies (more than 512 MB
+    in total, so the weights stream from HBM), GEMM at batch 256 and 2048. Weights are random sign words."""
+    op_gemv = torch.ops.binary_kernels.nanoquant_dyn_forward
+    op_gemm = torch.ops.binary_kernels.marlin_nanoquant_forward
+    kw = gemv_kwargs()
+    gen = torch.Generator(device=dev).manual_seed(11)
+    stream = torch.cuda.Stream(device=dev)
+    words = lambda *shape: torch.randint(-2**31, 2**31 - 1, shape, dtype=torch.int32, device=dev,  # noqa: E731
+                                         generator=gen)
+    scales = lambda k: (torch.rand(k, device=dev, generator=gen) * 0.4 + 0.8).half()  # noqa: E731
+    for model, name, m, n, r in sweep_shapes():
+        pb = packed_bytes(m, n, r)
+        copies = int(min(128, max(8, -(-(512 << 20) // pb))))
+        Vs = [words(r, (n + 31) // 32) for _ in range(copies)]
+        Us = [words(m, (r + 31) // 32) for _ in range(copies)]
+        s_in, s_out = scales(n), scales(m)
+        for B in (1, 4, 16):
+            x = torch.randn(B, n, device=dev, generator=gen).half()
+
+            def steps():
+                return [op_gemv(x, s_in, Vs[i], None, Us[i], s_out, **kw) for i in range(copies)]
+
+            ms, graph, _ = time_graph(steps, copies, max(1, 1024 // copies), 1, stream)
+            del graph
+            print(json.dumps({"kind": "gemv", "model": model, "linear": name, "m": m, "n": n, "r": r, "batch": B,
+                              "us": round(ms * 1e3, 3), "packed_gbs": round(pb / (ms * 1e-3) / 1e9, 1),
+                              "frac_hbm": round(pb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                              "copies": copies}), flush=True)
+        del Vs, Us
+        r_pad = -(-r // 256) * 256
+        wv, wu = words(n // 16, r_pad // 2), words(r_pad // 16, m // 2)
+        s_g, s_l, s_h = scales(n), scales(r_pad), scales(m)
+        ws = torch.zeros(m // 128 * 32, dtype=torch.int32, device=dev)
+        for B in (256, 2048):
+            x = torch.randn(B, n, device=dev, generator=gen).half()
+
+            def gsteps():
+                return [op_gemm(x, wv, wu, s_g, s_l, s_h, ws) for _ in range(4)]
+
+            ms, graph, _ = time_graph(gsteps, 4, 8, 1, stream)
+            del graph
+            flops = 2.0 * B * r * (n + m)
+            print(json.dumps({"kind": "gemm", "model": model, "linear": name, "m": m, "n": n, "r": r, "r_pad": r_pad,
+                              "batch": B, "us": round(ms * 1e3, 2),
+                              "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+                              "frac_mfma": round(flops / (ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}),
+                  flush=True)
+        torch.cuda.empty_cache()
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -328,6 +425,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--skip-decode", action="store_true", help="skip the end-to-end decode measurement")
+    ap.add_argument("--sweep", action="store_true",
+                    help="measure GEMV (batch 1/4/16) and GEMM (batch 256/2048) on every config shape instead")
     ap.add_argument("--decode-only", action="store_true",
                     help="run only the end-to-end decode and print its result alone (for kernel traces)")
     ap.add_argument("--e2e-batch", type=int, default=1)
@@ -352,6 +451,11 @@ def main():
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
 
+    if args.sweep:  # every config shape, one JSON line each (not the headline line)
+        import nanoquant_amd  # noqa: F401
+        run_sweep(args, dev)
+        return 0
+
     if args.decode_only:  # profiling aid: only the end-to-end decode, reported on its own line
         log(f"[bench] decode e2e B={args.e2e_batch} prompt={args.e2e_prompt} new={args.e2e_new}")
         print(json.dumps({"decode_e2e": bench_decode(args, dev)}), flush=True)
@@ -363,7 +467,7 @@ def main():
     achieved = g["packed_bytes"] / (g["ms"] * 1e-3) / 1e9
     s1_gbs = stage1_bytes(N, R) / (g["ms1"] * 1e-3) / 1e9
     s2_gbs = stage2_bytes(M, R) / (g["ms2"] * 1e-3) / 1e9
-    log(f"[bench] gemv {gemv_us:.3f} us/step, {achieved:.1f} GB/s packed, rel_err {g['rel_err']:.2e}; "
+    log(f"[bench] gemv {gemv_us:.3f} us/step, {achieved:.1f} GB/s packed; "
         f"stage 1 {g['ms1'] * 1e3:.3f} us ({s1_gbs:.1f} GB/s), stage 2 {g['ms2'] * 1e3:.3f} us ({s2_gbs:.1f} GB/s)")
 
     if args.calib_copy_mib > 0:
@@ -377,8 +481,8 @@ def main():
                 "roofline": {"bound": "mfma", "achieved": round(gm["tflops"], 2), "peak": MFMA_F16_PEAK_TFLOPS,
                              "unit": "TFLOP/s", "frac": round(gm["tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
                              "traffic": None},
-                "flops_per_call": gm["flops"], "r_pad": gm["r_pad"], "rel_err": gm["rel_err"]}
-        log(f"[bench] gemm {gm['ms'] * 1e3:.1f} us, {gm['tflops']:.1f} TFLOP/s, rel_err {gm['rel_err']:.2e}")
+                "flops_per_call": gm["flops"], "r_pad": gm["r_pad"]}
+        log(f"[bench] gemm {gm['ms'] * 1e3:.1f} us, {gm['tflops']:.1f} TFLOP/s")
 
     decode = None
     if not args.skip_decode:
@@ -386,10 +490,14 @@ def main():
         decode = bench_decode(args, dev)
 
     cpu = None
+    parity = {"gemv_rel_err": None, "gemm_rel_err": None}
     if not args.skip_cpu:
-        log("[bench] cpu baseline")
+        log("[bench] cpu baseline and parity check")
         cpu = cpu_baseline(args)
         log(f"[bench] cpu {cpu['value']} GB/s ({cpu['sample']})")
+        checked = check_parity({"gemv": g} if gemm is None else {"gemv": g, "gemm": gm})
+        parity = {"gemv_rel_err": checked["gemv"], "gemm_rel_err": checked.get("gemm")}
+        log(f"[bench] parity {parity}")
 
     traffic, traffic_src = measured_traffic(args.batch)
     line = {
@@ -423,8 +531,7 @@ def main():
         "gemm": gemm,
         "decode_e2e": decode,
         "cpu_baseline": cpu,
-        "parity": {"gemv_rel_err": g["rel_err"], "gemv_graph_matches_eager": g["graph_matches_eager"],
-                   "gemm_rel_err": None if gemm is None else gemm["rel_err"], "bar": 1e-3},
+        "parity": {**parity, "gemv_graph_matches_eager": g["graph_matches_eager"], "bar": 1e-3},
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -312,6 +312,45 @@ def test_gemm_onebit_scale_variants(nq, scales, K):
     assert err <= 1e-3, err
 
 
+# --------------------------------------------------------------------------- Llama-3-70B shapes
+
+def mixed_rank(base: int, seed: int) -> int:
+    """Mixture-of-rank draw: uniform in [0.8, 1.2] x the 0.55-bpw rank, rounded to 32."""
+    return int(round(np.random.default_rng(seed).uniform(0.8, 1.2) * base / 32.0)) * 32
+
+
+BIG_CASES = [
+    # kind, name, batch, m, n, r  (Llama-3-70B linears at 0.55 bpw; mixed ranks drawn as above)
+    ("gemv", "l3_70b_kv_b4", 4, 1024, 8192, 512),
+    ("gemv", "l3_70b_qo_b1", 1, 8192, 8192, 2240),
+    ("gemv", "l3_70b_gate_b16", 16, 28672, 8192, 3520),
+    ("gemv", "l3_70b_down_b1", 1, 8192, 28672, 3520),
+    ("gemv", "l3_70b_gate_mixed_b1", 1, 28672, 8192, mixed_rank(3520, 7)),
+    ("gemv", "l3_70b_o_mixed_b4", 4, 8192, 8192, mixed_rank(2240, 3)),
+    ("gemv", "l3_70b_gate_r4800_b1", 1, 28672, 8192, 4800),  # past the MFMA stage 2's largest rank
+    ("gemm", "l3_70b_kv_b256", 256, 1024, 8192, 512),
+    ("gemm", "l3_70b_qo_mixed_b256", 256, 8192, 8192, mixed_rank(2240, 5)),
+]
+
+
+@pytest.mark.parametrize("case", BIG_CASES, ids=[c[1] for c in BIG_CASES])
+def test_llama3_70b_shapes(nq, case):
+    kind, name, B, m, n, r = case
+    announce(kind, name, (B, m, n, r))
+    c = O.random_case(33, m, n, r, B)
+    if kind == "gemv":
+        y, _, _ = gemv_run(nq, c, torch.float16)
+    else:
+        packed = nq.pack_binary_marlin_fused(dev_t(c["V"].T), dev_t(c["U"].T), dev_t(c["s_in"]),
+                                             dev_t(np.ones(r, np.float16)), dev_t(c["s_out"]))
+        y = torch.ops.binary_kernels.marlin_nanoquant_forward(dev_t(c["x"]), *packed)
+        torch.cuda.synchronize()
+    y64 = O.nanoquant_forward_f64(c["x"], c["s_in"], c["V"], None, c["U"], c["s_out"])
+    err, nsat = rel_err(y, y64, kind, torch.float16)
+    print(f"[{kind}] {name} r={r} rel_err={err:.3e} saturated={nsat}", flush=True)
+    assert err <= TOL[(kind, torch.float16)], err
+
+
 # --------------------------------------------------------------------------- module
 
 @pytest.mark.parametrize("kernel", ["gemv", "gemm"])
