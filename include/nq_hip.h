@@ -150,8 +150,8 @@ size_t nq_gemv_group_workspace_bytes(int64_t count, const nq_gemv_item* items, i
 
 /* Stage 1 of every item over the shared input x [batch, n]. With rms_eps >= 0 the input is
  * RMS-normalised first: h is multiplied by rsqrt(mean(x^2) + rms_eps) per batch row; the
- * norm's weight is expected folded into each item's s_in. Needs n % 8 == 0, 8 <= n <= 16384,
- * 16-byte aligned x and s_in; NQ_ERR_UNSUPPORTED otherwise. */
+ * norm's weight is expected folded into each item's s_in. Needs n % 8 == 0, 8 <= n <= 32768, 16-byte
+ * aligned x and s_in; NQ_ERR_UNSUPPORTED otherwise. */
 int nq_gemv_group_stage1(int dtype, int64_t count, const nq_gemv_item* items, const void* x, int64_t batch,
                          int64_t n, float rms_eps, void* workspace, size_t workspace_bytes, nq_stream_t stream);
 

@@ -438,6 +438,132 @@ __global__ __launch_bounds__(256) void s1w_kernel(const S1Table tab, const uint1
     NQ_STAMP(3);
 }
 
+// --------------------------------------------------------------------------- stage 1, MFMA (batches)
+//
+// For three or more batch rows: v_mfma_f32_16x16x32_{f16,bf16} with A = 16 rows of V x 32 k of
+// +-s_in and B = 32 k x 16 batch rows of x, so one pass over V serves 16 batch rows (the VALU
+// kernel above takes two per pass). Lane l = (c = l % 16, g = l / 16). For word q of row j0 + c,
+// lane group g takes the pairs p = 4g .. 4g+3 (k = 32q + 8g .. +7): the word shifted left by p
+// carries pair p's signs on the sign bits of a 16-bit pair, and one xor puts them onto the s_in
+// pair of those k. B: lane (c, g) holds x[b0 + c][32q + 8g .. +7]. The NW waves split the words
+// of the rows and add their tiles in LDS. Each wave issues the loads of CH words before their
+// MFMAs. kNorm sums x^2 of each batch row on the way (the B fragments of the block's lanes cover
+// every k of a batch row once) and scales h by rsqrt(mean(x^2) + eps).
+template <typename T, int NW, bool kNorm, bool kOne, bool kSinLds>
+__global__ __launch_bounds__(NW * 64) void s1m_kernel(const S1Table tab, const uint16_t* __restrict__ x, int batch,
+                                                      int n, int wn, float eps) {
+    constexpr int CH = 8;
+    constexpr int NT = NW * 64;
+    constexpr int kMaxLoads = 16;  // dwords per thread staged (the host checks the staged words fit)
+    // [16][wn] sign words, then (kSinLds) s_in as [n / 2] pairs; wider rows read s_in from global
+    // (after the MFMAs the same memory holds the waves' partial tiles)
+    extern __shared__ uint32_t lds[];
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int c = lane & 15;
+    const int g = lane >> 4;
+    const S1Item it = kOne ? tab.item[0] : pick_item<S1Item>(tab);
+    const int r = it.r;
+    const int j0 = (static_cast<int>(blockIdx.x) - it.block_begin) * 16;
+    const int b0 = blockIdx.y * 16;
+    const uint16_t* xrow = x + static_cast<uint32_t>(min(b0 + c, batch - 1)) * static_cast<uint32_t>(n);
+    const bool b_ok = b0 + c < batch;
+    const uint32_t mask = kSignPair;
+    uint32_t* vt = lds;
+    uint32_t* si = lds + 16 * wn;
+
+    // 1. stage the block's rows of V (consecutive in memory) and s_in, dword by dword, coalesced;
+    //    rows past r repeat the last row (their h is never stored)
+    const int vwords = 16 * wn;
+    const int total = vwords + (kSinLds ? n / 2 : 0);
+    const uint32_t vbase = static_cast<uint32_t>(min(j0, r - 1)) * static_cast<uint32_t>(wn);
+    const uint32_t vlast = static_cast<uint32_t>(r) * static_cast<uint32_t>(wn) - 1;
+    const uint32_t* s_in32 = reinterpret_cast<const uint32_t*>(it.s_in);
+    uint32_t vals[kMaxLoads];
+#pragma unroll
+    for (int i = 0; i < kMaxLoads; ++i) {
+        const int e = min(t + i * NT, total - 1);
+        vals[i] = (!kSinLds || e < vwords) ? it.v_bits[min(vbase + static_cast<uint32_t>(e), vlast)]
+                                           : s_in32[e - vwords];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < kMaxLoads; ++i)
+        if (t + i * NT < total) lds[t + i * NT] = vals[i];
+    __syncthreads();
+
+    // 2. MFMAs: wave w takes words w, w + NW, ...; x comes from global CH words at a time
+    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    float ss[2] = {0.0f, 0.0f};
+    for (int q0 = wave; q0 < wn; q0 += NW * CH) {
+        u32x4 xv[CH], sg[CH];
+#pragma unroll
+        for (int u = 0; u < CH; ++u) {
+            const int qc = min(q0 + NW * u, wn - 1);
+            const int k = min(32 * qc + 8 * g, n - 8);
+            xv[u] = *reinterpret_cast<const u32x4*>(xrow + k);
+            if (!kSinLds) sg[u] = *reinterpret_cast<const u32x4*>(it.s_in + k);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < CH; ++u) {
+            const int q = q0 + NW * u;
+            const int qc = min(q, wn - 1);
+            const bool ok = q < wn && 32 * q + 8 * g < n;
+            const u32x4 sp = kSinLds ? *reinterpret_cast<const u32x4*>(&si[min(16 * qc + 4 * g, n / 2 - 4)]) : sg[u];
+            const u32x4 s = ok ? sp : u32x4{0u, 0u, 0u, 0u};
+            const u32x4 xb = (ok && b_ok) ? xv[u] : u32x4{0u, 0u, 0u, 0u};
+            const uint32_t ws = vt[c * wn + qc] << (4 * g);
+            const u32x4 a = u32x4{s.x ^ (ws & mask), s.y ^ ((ws << 1) & mask), s.z ^ ((ws << 2) & mask),
+                                  s.w ^ ((ws << 3) & mask)};
+            acc[u & 1] = mfma16x16x32<T>(a, xb, acc[u & 1]);
+            if (kNorm) {
+                ss[u & 1] = T::dot2(xb.x, xb.x, ss[u & 1]);
+                ss[u & 1] = T::dot2(xb.y, xb.y, ss[u & 1]);
+                ss[u & 1] = T::dot2(xb.z, xb.z, ss[u & 1]);
+                ss[u & 1] = T::dot2(xb.w, xb.w, ss[u & 1]);
+            }
+        }
+    }
+    __syncthreads();  // every wave is done with the staged words
+    f32x4* red = reinterpret_cast<f32x4*>(lds);               // [NW][64]
+    float* ssr = reinterpret_cast<float*>(lds) + 4 * NW * 64;  // [NW][64]
+    red[wave * 64 + lane] =
+        f32x4{acc[0].x + acc[1].x, acc[0].y + acc[1].y, acc[0].z + acc[1].z, acc[0].w + acc[1].w};
+    if (kNorm) ssr[wave * 64 + lane] = ss[0] + ss[1];
+    __syncthreads();
+
+    // 3. sum the waves' tiles, scale, store
+    if (wave == 0) {
+        f32x4 sum = red[lane];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) {
+            const f32x4 pr = red[w * 64 + lane];
+            sum = f32x4{sum.x + pr.x, sum.y + pr.y, sum.z + pr.z, sum.w + pr.w};
+        }
+        float rs = 1.0f;
+        if (kNorm) {
+            float tot = 0.0f;
+#pragma unroll
+            for (int w = 0; w < NW; ++w)
+#pragma unroll
+                for (int gg = 0; gg < 4; ++gg) tot += ssr[w * 64 + 16 * gg + c];
+            rs = rsqrtf(tot / static_cast<float>(n) + eps);
+        }
+        const float v[4] = {sum.x, sum.y, sum.z, sum.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int j = j0 + 4 * g + i;
+            if (b_ok && j < it.kpad) {
+                const float mf = (it.s_mid != nullptr && j < r) ? T::to_float(it.s_mid[j]) : 1.0f;
+                store_h(it.z_hi, it.z_lo, it.zpitch, b0 + c, j, j < r ? v[i] * rs * mf : 0.0f);
+            }
+        }
+    }
+    if (static_cast<int>(blockIdx.x) == it.block_begin) zero_h_pad(it.z_hi, it.z_lo, it.zpitch, it.kpad, b0, 16, batch);
+}
+
 // --------------------------------------------------------------------------- stage 2, MFMA
 //
 // v_mfma_f32_16x16x32_bf16, lane l = (g = l / 16, c = l % 16), one block per 16 rows of U.
@@ -749,8 +875,66 @@ void launch_s1w_table(S1Table& tab, const uint16_t* x, int batch, int n, int wn,
     else launch_s1w_nb<T, 2>(tab, blocks, x, batch, n, wn, norm, eps, st);
 }
 
+// Dwords s1m_kernel stages in LDS: 16 rows of sign words, and the s_in pairs when they fit too
+// (64 KB, 16 dwords per thread of a 1024-thread block).
+constexpr int kS1mMaxStaged = 16 * 16 * 64;
+inline bool s1m_sin_lds(int n, int wn) { return 16 * wn + n / 2 <= kS1mMaxStaged; }
+inline size_t s1m_lds_bytes(int n, int wn) {
+    const size_t staged = static_cast<size_t>(16 * wn + (s1m_sin_lds(n, wn) ? n / 2 : 0)) * 4;
+    const size_t reduce = static_cast<size_t>(16) * 64 * (16 + 4);  // the waves' tiles and x^2 sums
+    return std::max(staged, reduce);
+}
+// Whether the MFMA stage 1 takes rows of n columns at all (up to n = 32768).
+inline bool s1m_fits(int n, int wn) {
+    (void)n;
+    return 16 * wn <= kS1mMaxStaged;
+}
+
+template <typename T, int NW>
+void launch_s1m_nw(const S1Table& tab, dim3 grid, const uint16_t* x, int batch, int n, int wn, bool norm, float eps,
+                   hipStream_t st) {
+    const size_t lds = s1m_lds_bytes(n, wn);
+    const bool sl = s1m_sin_lds(n, wn);
+#define NQ_S1M(NORM, ONE)                                                                              \
+    (sl ? (s1m_kernel<T, NW, NORM, ONE, true><<<grid, NW * 64, lds, st>>>(tab, x, batch, n, wn, eps)) \
+        : (s1m_kernel<T, NW, NORM, ONE, false><<<grid, NW * 64, lds, st>>>(tab, x, batch, n, wn, eps)))
+    if (tab.count == 1) {
+        if (norm) NQ_S1M(true, true);
+        else NQ_S1M(false, true);
+    } else {
+        if (norm) NQ_S1M(true, false);
+        else NQ_S1M(false, false);
+    }
+#undef NQ_S1M
+}
+
+// The MFMA stage 1 over every item of `tab` (16 rows per block, 16 batch rows per grid row).
+template <typename T>
+void launch_s1m_table(S1Table& tab, const uint16_t* x, int batch, int n, int wn, bool norm, float eps,
+                      hipStream_t st) {
+    int blocks = 0;
+    for (int k = 0; k < tab.count; ++k) {
+        tab.item[k].block_begin = blocks;
+        blocks += static_cast<int>(ceil_div(tab.item[k].kpad, 16));
+    }
+    // 16 waves per block: a 4096-wide row is one round of loads per wave (latency, not bytes, is
+    // what a decode-size stage pays for)
+    const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(ceil_div(batch, 16)));
+    launch_s1m_nw<T, 16>(tab, grid, x, batch, n, wn, norm, eps, st);
+}
+
+// Stage 1 of a table: the VALU kernel for one or two batch rows of up to 16384 columns, the MFMA
+// kernel from three rows on and for wider rows.
+template <typename T>
+void launch_stage1_table(S1Table& tab, const uint16_t* x, int batch, int n, int wn, bool norm, float eps,
+                         hipStream_t st) {
+    if ((batch >= 3 || wn > 512) && s1m_fits(n, wn)) launch_s1m_table<T>(tab, x, batch, n, wn, norm, eps, st);
+    else launch_s1w_table<T>(tab, x, batch, n, wn, norm, eps, st);
+}
+
+// The fast stage 1 (s1w up to 16384 columns, s1m up to 32768, by launch_stage1_table) applies.
 inline bool s1w_applies(const uint16_t* x, const uint16_t* s_in, int n, int wn, int r) {
-    return n >= 8 && n % 8 == 0 && wn <= 512 && r > 0 && aligned(x, 16) && aligned(s_in, 16);
+    return n >= 8 && n % 8 == 0 && r > 0 && aligned(x, 16) && aligned(s_in, 16) && (wn <= 512 || s1m_fits(n, wn));
 }
 
 inline S1Item s1_item_of(const GemvArgs& a) {
@@ -773,7 +957,7 @@ void launch_stage1(const GemvArgs& a) {
         S1Table tab;
         tab.count = 1;
         tab.item[0] = s1_item_of(a);
-        launch_s1w_table<T>(tab, a.x, a.batch, a.n, a.wn, false, 0.0f, a.stream);
+        launch_stage1_table<T>(tab, a.x, a.batch, a.n, a.wn, false, 0.0f, a.stream);
         return;
     }
     if (a.batch <= 1) launch_stage1_generic<T, 1>(a);
@@ -1061,7 +1245,7 @@ int nq_gemv_group_stage1(int dtype, int64_t count, const nq_gemv_item* items, co
             return fail(NQ_ERR_ALIGNMENT, "%s: item %lld: misaligned operand", name, (long long)k);
         if (!s1w_applies(xp, static_cast<const uint16_t*>(in.s_in), static_cast<int>(n), wn, static_cast<int>(in.r)))
             return fail(NQ_ERR_UNSUPPORTED,
-                        "%s: needs n %% 8 == 0, 8 <= n <= 16384 and 16-byte aligned x and s_in (item %lld)", name,
+                        "%s: needs n %% 8 == 0, 8 <= n <= 32768 and 16-byte aligned x and s_in (item %lld)", name,
                         (long long)k);
         S1Item& it = tab.item[k];
         it.v_bits = in.v_bits;
@@ -1076,9 +1260,11 @@ int nq_gemv_group_stage1(int dtype, int64_t count, const nq_gemv_item* items, co
     }
     const bool norm = rms_eps >= 0.0f;
     if (dtype == NQ_F16)
-        launch_s1w_table<F16>(tab, xp, static_cast<int>(batch), static_cast<int>(n), wn, norm, rms_eps, as_stream(stream));
+        launch_stage1_table<F16>(tab, xp, static_cast<int>(batch), static_cast<int>(n), wn, norm, rms_eps,
+                                 as_stream(stream));
     else
-        launch_s1w_table<BF16>(tab, xp, static_cast<int>(batch), static_cast<int>(n), wn, norm, rms_eps, as_stream(stream));
+        launch_stage1_table<BF16>(tab, xp, static_cast<int>(batch), static_cast<int>(n), wn, norm, rms_eps,
+                                  as_stream(stream));
     return check_launch(name);
 }
 

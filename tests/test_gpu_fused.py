@@ -67,7 +67,7 @@ def group_call(lib, dtype_code, items, x, batch, n, eps, epilogue):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
-@pytest.mark.parametrize("batch", [1, 3])
+@pytest.mark.parametrize("batch", [1, 3, 17])
 def test_group_matches_single_gemv(lib, dtype, batch):
     from nanoquant_amd import _lib
     announce("group vs single", dtype, batch)
@@ -102,7 +102,7 @@ def rel(y, y64):
     return float(np.abs(y - y64).max() / np.abs(y64).max())
 
 
-@pytest.mark.parametrize("batch", [1, 2])
+@pytest.mark.parametrize("batch", [1, 2, 5, 18])  # VALU stage 1 for 1-2 rows, MFMA stage 1 from 3
 def test_group_norm_and_residual(lib, batch):
     from nanoquant_amd import _lib
     announce("group norm + residual", batch)
