@@ -184,6 +184,11 @@ int nq_gemm_nanoquant(int dtype, const void* A, const uint32_t* v_bits, const ui
 
 /* ---------------------------------------------------------------- decode attention */
 
+/* Bytes of workspace nq_attention_decode needs (0 on bad arguments): the partial results of
+ * every (sequence, kv head, 64-position chunk). */
+size_t nq_attention_decode_workspace_bytes(int64_t batch, int64_t heads, int64_t kv_heads, int64_t head_dim,
+                                           int64_t max_len);
+
 /* Attention of one new token per sequence at the position *position (device int64, equal for
  * every sequence), with the rotary embedding and the KV-cache write:
  *   q, k, v   rows of qkv_stride elements (>= heads * head_dim), e.g. slices of one
@@ -193,19 +198,22 @@ int nq_gemm_nanoquant(int dtype, const void* A, const uint32_t* v_bits, const ui
  *             receives the rotated key and the value
  *   rope_cos, rope_sin  [max_len, head_dim] (the rotate-half convention)
  *   out       [batch, heads * head_dim] = softmax(q k^T * scaling) v over positions <= *position
- * Query head h uses kv head h / (heads / kv_heads). Rounding follows the unfused torch path:
- * rotary products and sum in dtype, scores rounded to dtype then scaled in fp32, softmax in
- * fp32, probabilities rounded to dtype, fp32 accumulation of the output. A position outside
- * [0, max_len) writes zeros to out and nothing to the caches. head_dim must be 128 and
- * heads / kv_heads one of 1, 2, 4, 8, with (heads / kv_heads) * max_len * 4 bytes of scores
- * within about 62 KB of LDS (max_len up to ~15800 for MHA, ~1980 for 8 query heads per kv
- * head); NQ_ERR_UNSUPPORTED otherwise. No counterpart in the reference,
- * whose decode step runs Hugging Face's attention (kernel/test_decode.py:385-402); this is
- * the part of a decode step between the q/k/v and o projections. */
+ *   workspace nq_attention_decode_workspace_bytes(...) bytes, 256-byte aligned (no initial
+ *             contents needed); calls sharing a workspace must not overlap.
+ * Query head h uses kv head h / (heads / kv_heads). Two launches: one block per 64-position
+ * chunk writes a partial result, then one block per (sequence, kv head) combines the chunks.
+ * Rounding: rotary products and sum in dtype as the unfused torch path does, scores rounded to
+ * dtype then scaled in fp32, softmax and the value product in fp32, output rounded to dtype
+ * (the unfused path also rounds the probabilities to dtype). A position outside [0, max_len)
+ * writes zeros to out and nothing to the caches. head_dim must be 128 and heads / kv_heads one
+ * of 1, 2, 4, 8; NQ_ERR_UNSUPPORTED otherwise. No counterpart in the reference, whose decode
+ * step runs Hugging Face's attention (kernel/test_decode.py:385-402); this is the part of a
+ * decode step between the q/k/v and o projections. */
 int nq_attention_decode(int dtype, const void* q, const void* k, const void* v, int64_t qkv_stride,
                         void* k_cache, void* v_cache, const void* rope_cos, const void* rope_sin,
                         const int64_t* position, void* out, int64_t batch, int64_t heads, int64_t kv_heads,
-                        int64_t head_dim, int64_t max_len, float scaling, nq_stream_t stream);
+                        int64_t head_dim, int64_t max_len, float scaling, void* workspace, size_t workspace_bytes,
+                        nq_stream_t stream);
 
 #ifdef __cplusplus
 }

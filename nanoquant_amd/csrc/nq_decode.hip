@@ -1,21 +1,26 @@
 // Decode attention of one new token per sequence, with the rotary embedding and the KV-cache
 // write fused in: the part of a Llama decode step between the q/k/v projections and o_proj.
 //
-// One block per (sequence b, kv head); it serves the G = heads / kv_heads query heads that
-// share the kv head. The position p of the new token is read from device memory, so the
-// launch can be replayed from a graph while the position advances.
-//   1. rotate q (G heads) and the new k with the cos/sin rows of p, as the unfused path rounds
-//      it: (x * cos) and (rotate_half(x) * sin) each rounded to T, then their sum; write k and
-//      v into the cache at p;
-//   2. scores s[g][j] = T(q_g . k_j) * scaling for j <= p, one position per thread (a lane
-//      holds the key row in registers and runs the G heads over it; 512 threads, so up to
-//      512 keys are in flight at once);
-//   3. softmax over j in fp32, probabilities rounded to T;
-//   4. out[g][d] = T(sum_j p[g][j] * v[j][d]) in fp32: lane pairs of d, waves over j, the
-//      values of 32 positions per wave in flight at once.
-// The cache layout is [batch, kv_heads, max_len, head_dim] for both K and V; head_dim 128.
-// Row p of the caches is only written here: the block reads the new key and value back from
-// LDS, never from the cache it has just written.
+// The positions 0..p of each (sequence, kv head) are split into chunks of 64; one block per
+// (sequence, kv head, chunk), for every chunk the cache could hold, so the grid is fixed while
+// the position p (read from device memory) advances under graph replay; blocks of chunks wholly
+// after p exit once they have read it. A block:
+//   1. rotates q (the G = heads / kv_heads query heads of its kv head) with the cos/sin row of
+//      p, as the unfused path rounds it: (x * cos) and (rotate_half(x) * sin) each rounded to T,
+//      then their sum; the block whose chunk holds p also rotates the new key and writes the key
+//      and value into the cache at p (it reads them back from LDS, never from the cache);
+//   2. scores s[g][j] = T(q_g . k_j) * scaling for its chunk's positions j <= p, four lanes per
+//      position (32 dimensions each, summed with lane swaps);
+//   3. per head: m = max_j s, e_j = exp(s_j - m), l = sum_j e_j (fp32);
+//   4. o[g][d] = sum_j e_j v[j][d] (fp32; lane pairs of d, waves over j, values loaded ahead);
+//   5. writes (m, l, o) to the workspace.
+// A second launch (attn_combine_kernel, one block per sequence and kv head) combines the chunks:
+// M = max m, L = sum l exp(m - M), out = T(sum o exp(m - M) / L). (Combining inside the first
+// launch, by the last block to finish, needs device-scope fences, which write back the L2 of
+// each XCD and cost more than the second launch.)
+// Unlike the unfused path, probabilities are not rounded to T before the value product (the
+// chunks' sums are combined first). The cache layout is [batch, kv_heads, max_len, head_dim]
+// for K and V; head_dim 128.
 #include <algorithm>
 
 #include "nq_common.h"
@@ -24,9 +29,8 @@ namespace nq {
 namespace {
 
 constexpr int kHeadDim = 128;
-constexpr int kAttnThreads = 512;
-constexpr int kPvChunk = 32;  // positions whose values a wave loads before using them
-constexpr size_t kAttnLdsBudget = 64 * 1024;
+constexpr int kAttnThreads = 256;
+constexpr int kChunk = 64;  // positions per block
 
 __device__ inline float wave_max(float v) {
 #pragma unroll
@@ -34,205 +38,281 @@ __device__ inline float wave_max(float v) {
     return v;
 }
 
-// Block-wide max or sum of one value per thread (every thread gets the result).
-template <bool kMax>
-__device__ inline float block_reduce(float v, float* buf) {
-    v = kMax ? wave_max(v) : wave_sum(v);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (lane == 0) buf[wave] = v;
-    __syncthreads();
-    float r = buf[0];
-#pragma unroll
-    for (int w = 1; w < kAttnThreads / 64; ++w) r = kMax ? fmaxf(r, buf[w]) : r + buf[w];
-    __syncthreads();
-    return r;
-}
+inline int64_t attn_chunks(int64_t max_len) { return ceil_div(max_len, kChunk); }
+// floats of one chunk's partial result: (m, l) and o[128] per query head
+inline int64_t attn_part_floats(int64_t g) { return g * (2 + kHeadDim); }
 
 template <typename T, int G>
 __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int qkv_stride,
     uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache, const uint16_t* __restrict__ rope_cos,
     const uint16_t* __restrict__ rope_sin, const int64_t* __restrict__ position, uint16_t* __restrict__ out,
-    int kv_heads, int max_len, float scaling) {
+    int kv_heads, int max_len, float scaling, float* __restrict__ parts) {
     // every rounding below is meant: no product may be fused into a following add
 #pragma clang fp contract(off)
     constexpr int D = kHeadDim;
     constexpr int NW = kAttnThreads / 64;
-    // [G][max_len]: scores, then probabilities; afterwards the waves' partial outputs
-    // [NW][G][D] (the host sizes it for the larger of the two)
-    extern __shared__ float sc[];
+    constexpr int PF = G * (2 + D);
     __shared__ __attribute__((aligned(16))) uint16_t qs[G][D];
-    __shared__ __attribute__((aligned(16))) uint16_t knew[D];  // the new key and value, read
-    __shared__ __attribute__((aligned(16))) uint16_t vnew[D];  // back from here, not the cache
-    __shared__ float rbuf[NW];
+    __shared__ __attribute__((aligned(16))) uint16_t knew[D];
+    __shared__ __attribute__((aligned(16))) uint16_t vnew[D];
+    __shared__ float sc[G][kChunk];
+    __shared__ float mls[G][2];
+    __shared__ float red[NW][G][D];
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
-    const int b = blockIdx.x / kv_heads;
-    const int kvh = blockIdx.x - b * kv_heads;
+    const int n_chunks = (max_len + kChunk - 1) / kChunk;
+    const int bh = blockIdx.x / n_chunks;  // sequence * kv_heads + kv head
+    const int ch = blockIdx.x - bh * n_chunks;
+    const int b = bh / kv_heads;
+    const int kvh = bh - b * kv_heads;
     const int heads = kv_heads * G;
     uint16_t* orow = out + (static_cast<size_t>(b) * heads + static_cast<size_t>(kvh) * G) * D;
-    const int64_t p64 = *position;
-    if (p64 < 0 || p64 >= max_len) {  // a position outside the cache: zeros, nothing written
-        for (int e = t; e < G * D; e += kAttnThreads) orow[e] = 0;
-        return;
-    }
-    const int p = static_cast<int>(p64);
-    const size_t head_base = (static_cast<size_t>(b) * kv_heads + kvh) * static_cast<size_t>(max_len) * D;
-
-    // 1. rotary embedding, cache write
+    const int lo = ch * kChunk;
+    const size_t head_base = static_cast<size_t>(bh) * static_cast<size_t>(max_len) * D;
     const uint16_t* qrow = q + static_cast<size_t>(b) * qkv_stride + static_cast<size_t>(kvh) * G * D;
     const uint16_t* krow = k + static_cast<size_t>(b) * qkv_stride + static_cast<size_t>(kvh) * D;
     const uint16_t* vrow = v + static_cast<size_t>(b) * qkv_stride + static_cast<size_t>(kvh) * D;
-    for (int e = t; e < (G + 2) * D; e += kAttnThreads) {
+
+    // 0. the projection elements the rotary step uses (element e of the G query heads, the key
+    //    and the value, with its rotate-half partner), loaded together with the position
+    constexpr int PW = kChunk / NW;
+    constexpr int E = ((G + 2) * D + kAttnThreads - 1) / kAttnThreads;
+    uint16_t xe[E], xp[E];
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+        const int e = min(t + i * kAttnThreads, (G + 2) * D - 1);
         const int hh = e / D;
         const int d = e - hh * D;
-        if (hh <= G) {  // G query heads, then the key
-            const uint16_t* src = hh < G ? qrow + hh * D : krow;
-            const float x = T::to_float(src[d]);
-            const float xr = d < D / 2 ? -T::to_float(src[d + D / 2]) : T::to_float(src[d - D / 2]);
-            const float c = T::to_float(rope_cos[static_cast<size_t>(p) * D + d]);
-            const float s = T::to_float(rope_sin[static_cast<size_t>(p) * D + d]);
-            const float a0 = T::to_float(T::from_float(x * c));
-            const float a1 = T::to_float(T::from_float(xr * s));
-            const uint16_t r = T::from_float(a0 + a1);
-            if (hh < G) {
-                qs[hh][d] = r;
-            } else {
-                knew[d] = r;
-                k_cache[head_base + static_cast<size_t>(p) * D + d] = r;
+        const uint16_t* src = hh < G ? qrow + hh * D : (hh == G ? krow : vrow);
+        xe[i] = src[d];
+        xp[i] = src[d ^ (D / 2)];
+    }
+    const int64_t p64 = *position;
+    __builtin_amdgcn_sched_barrier(0);
+    if (p64 < 0 || p64 >= max_len) {  // a position outside the cache: zeros, nothing written
+        if (ch == 0)
+            for (int e = t; e < G * D; e += kAttnThreads) orow[e] = 0;
+        return;
+    }
+    const int p = static_cast<int>(p64);
+    if (lo > p) return;  // a chunk wholly after p: nothing to do, the combine skips it
+    const int count = min(kChunk, p + 1 - lo);  // positions of this chunk that are visible
+    const bool owner = p < lo + kChunk;
+
+    // then every load that needs only p, issued before any result is used: this chunk's keys
+    // (thread t: row lo + t / 4, dimensions 32 (t % 4) .. +31), values (lane pairs of d, PW rows per
+    // wave; rows past p read row p, whose result is never used) and the cos/sin entries
+    const int jj = t >> 2;
+    const int part = t & 3;
+    u32x4 kv4[4];
+    {
+        const uint16_t* kr = k_cache + head_base + static_cast<size_t>(min(lo + jj, p)) * D + 32 * part;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kv4[i] = *reinterpret_cast<const u32x4*>(kr + 8 * i);
+    }
+    uint32_t vv[PW];
+#pragma unroll
+    for (int u = 0; u < PW; ++u)
+        vv[u] = *reinterpret_cast<const uint32_t*>(v_cache + head_base +
+                                                   static_cast<size_t>(min(lo + wave + NW * u, p)) * D + 2 * lane);
+    uint16_t cs[E], sn[E];
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+        const int e = min(t + i * kAttnThreads, (G + 2) * D - 1);
+        const int d = e % D;
+        cs[i] = rope_cos[static_cast<size_t>(p) * D + d];
+        sn[i] = rope_sin[static_cast<size_t>(p) * D + d];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 1. rotary embedding; the owner writes the new key and value
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+        const int e = t + i * kAttnThreads;
+        if (e < (G + 2) * D) {
+            const int hh = e / D;
+            const int d = e - hh * D;
+            if (hh <= G) {  // G query heads, then the key
+                const float x = T::to_float(xe[i]);
+                const float xr = d < D / 2 ? -T::to_float(xp[i]) : T::to_float(xp[i]);
+                const float a0 = T::to_float(T::from_float(x * T::to_float(cs[i])));
+                const float a1 = T::to_float(T::from_float(xr * T::to_float(sn[i])));
+                const uint16_t r = T::from_float(a0 + a1);
+                if (hh < G) {
+                    qs[hh][d] = r;
+                } else if (owner) {
+                    knew[d] = r;
+                    k_cache[head_base + static_cast<size_t>(p) * D + d] = r;
+                }
+            } else if (owner) {
+                vnew[d] = xe[i];
+                v_cache[head_base + static_cast<size_t>(p) * D + d] = xe[i];
             }
-        } else {
-            const uint16_t vd = vrow[d];
-            vnew[d] = vd;
-            v_cache[head_base + static_cast<size_t>(p) * D + d] = vd;
         }
     }
     __syncthreads();
 
-    // 2. scores
-    const uint16_t* kb = k_cache + head_base;
-    for (int j = t; j <= p; j += kAttnThreads) {
-        u32x4 kr[D / 8];
+    // 2. scores: thread t takes position lo + t / 4, dimensions 32 * (t % 4) .. +31; the new
+    //    position's key comes from LDS (its row in the prefetched cache is stale)
+    if (owner && lo + jj == p) {
 #pragma unroll
-        for (int i = 0; i < D / 8; ++i) kr[i] = *reinterpret_cast<const u32x4*>(kb + static_cast<size_t>(j) * D + 8 * i);
-        if (j == p) {
-#pragma unroll
-            for (int i = 0; i < D / 8; ++i) kr[i] = *reinterpret_cast<const u32x4*>(&knew[8 * i]);
-        }
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            // the query comes from LDS head by head (broadcast reads); without this the compiler
-            // keeps all G heads in registers across the loop and spills from G = 2 on
-            asm volatile("" ::: "memory");
-            float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-            for (int i = 0; i < D / 8; ++i) {
-                const u32x4 qv = *reinterpret_cast<const u32x4*>(&qs[g][8 * i]);
-                a0 = T::dot2(qv.x, kr[i].x, a0);
-                a1 = T::dot2(qv.y, kr[i].y, a1);
-                a0 = T::dot2(qv.z, kr[i].z, a0);
-                a1 = T::dot2(qv.w, kr[i].w, a1);
-            }
-            sc[g * max_len + j] = T::to_float(T::from_float(a0 + a1)) * scaling;
-        }
+        for (int i = 0; i < 4; ++i) kv4[i] = *reinterpret_cast<const u32x4*>(&knew[32 * part + 8 * i]);
     }
-    __syncthreads();
-
-    // 3. softmax over positions 0..p, per head
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        float* row = sc + g * max_len;
-        float mx = -INFINITY;
-        for (int j = t; j <= p; j += kAttnThreads) mx = fmaxf(mx, row[j]);
-        mx = block_reduce<true>(mx, rbuf);
-        float sum = 0.0f;
-        for (int j = t; j <= p; j += kAttnThreads) {
-            const float e = expf(row[j] - mx);
-            row[j] = e;
-            sum += e;
+        float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const u32x4 qv = *reinterpret_cast<const u32x4*>(&qs[g][32 * part + 8 * i]);
+            a0 = T::dot2(qv.x, kv4[i].x, a0);
+            a1 = T::dot2(qv.y, kv4[i].y, a1);
+            a0 = T::dot2(qv.z, kv4[i].z, a0);
+            a1 = T::dot2(qv.w, kv4[i].w, a1);
         }
-        sum = block_reduce<false>(sum, rbuf);
-        for (int j = t; j <= p; j += kAttnThreads) row[j] = T::to_float(T::from_float(row[j] / sum));
+        float sum = a0 + a1;
+        sum += __shfl_xor(sum, 1, 64);
+        sum += __shfl_xor(sum, 2, 64);
+        if (part == 0) sc[g][jj] = jj < count ? T::to_float(T::from_float(sum)) * scaling : -INFINITY;
     }
     __syncthreads();
 
-    // 4. probabilities times values: lane holds d = 2 lane, 2 lane + 1; wave w takes positions
-    //    w, w + NW, ...; each round loads kPvChunk positions' values (clamped addresses, so the
-    //    loads are unconditional) before the first multiply-add
-    float acc[G][2];
+    // 3. chunk softmax statistics, one wave per head
+    for (int g = wave; g < G; g += NW) {
+        const float s = sc[g][lane];
+        const float m = wave_max(s);
+        const float e = lane < count ? expf(s - m) : 0.0f;
+        sc[g][lane] = e;
+        const float l = wave_sum(e);
+        if (lane == 0) {
+            mls[g][0] = m;
+            mls[g][1] = l;
+        }
+    }
+    __syncthreads();
+
+    // 4. o[g][d] = sum_j e_j v[j][d]: lane holds d = 2 lane, 2 lane + 1; wave w takes positions
+    //    w, w + NW, ...
+    {
+        float acc[G][2];
 #pragma unroll
-    for (int g = 0; g < G; ++g) acc[g][0] = acc[g][1] = 0.0f;
-    const uint16_t* vb = v_cache + head_base + 2 * lane;
-    const uint32_t vl = *reinterpret_cast<const uint32_t*>(&vnew[2 * lane]);
-    for (int j0 = wave; j0 <= p; j0 += NW * kPvChunk) {
-        uint32_t vv[kPvChunk];
+        for (int g = 0; g < G; ++g) acc[g][0] = acc[g][1] = 0.0f;
+        const uint32_t vl = *reinterpret_cast<const uint32_t*>(&vnew[2 * lane]);
 #pragma unroll
-        for (int u = 0; u < kPvChunk; ++u)
-            vv[u] = *reinterpret_cast<const uint32_t*>(vb + static_cast<size_t>(min(j0 + NW * u, p)) * D);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int u = 0; u < kPvChunk; ++u) {
-            const int j = j0 + NW * u;
-            if (j <= p) {
-                const uint32_t w = j == p ? vl : vv[u];
+        for (int u = 0; u < PW; ++u) {
+            const int j = wave + NW * u;
+            if (j < count) {
+                const uint32_t w = (owner && lo + j == p) ? vl : vv[u];
                 const float v0 = T::to_float(static_cast<uint16_t>(w & 0xFFFFu));
                 const float v1 = T::to_float(static_cast<uint16_t>(w >> 16));
 #pragma unroll
                 for (int g = 0; g < G; ++g) {
-                    const float pj = sc[g * max_len + j];
+                    const float pj = sc[g][j];
                     acc[g][0] = fmaf(pj, v0, acc[g][0]);
                     acc[g][1] = fmaf(pj, v1, acc[g][1]);
                 }
             }
         }
-    }
-    __syncthreads();  // every wave is done with the probabilities
-    float* part = sc;  // [NW][G][D]
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        part[(wave * G + g) * D + 2 * lane] = acc[g][0];
-        part[(wave * G + g) * D + 2 * lane + 1] = acc[g][1];
+        for (int g = 0; g < G; ++g) {
+            red[wave][g][2 * lane] = acc[g][0];
+            red[wave][g][2 * lane + 1] = acc[g][1];
+        }
     }
     __syncthreads();
+
+    // 5. this chunk's partial result
+    float* mypart = parts + (static_cast<size_t>(bh) * n_chunks + ch) * PF;
     for (int e = t; e < G * D; e += kAttnThreads) {
+        const int g = e / D;
         float s = 0.0f;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) s += part[w * G * D + e];
-        orow[e] = T::from_float(s);
+        for (int w = 0; w < NW; ++w) s += red[w][g][e - g * D];
+        mypart[2 * G + e] = s;
+    }
+    if (t < 2 * G) mypart[t] = mls[t >> 1][t & 1];
+}
+
+// Combine the chunks of one (sequence, kv head): thread e < G * 128 takes output element e.
+template <typename T, int G>
+__global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(const float* __restrict__ parts,
+                                                                    const int64_t* __restrict__ position,
+                                                                    uint16_t* __restrict__ out, int kv_heads,
+                                                                    int max_len) {
+    constexpr int D = kHeadDim;
+    constexpr int PF = G * (2 + D);
+    const int64_t p64 = *position;
+    if (p64 < 0 || p64 >= max_len) return;  // the first launch wrote zeros
+    const int n_chunks = (max_len + kChunk - 1) / kChunk;
+    const int used = static_cast<int>(p64) / kChunk + 1;  // chunks holding positions <= p
+    const int bh = blockIdx.x;
+    const int b = bh / kv_heads;
+    const int kvh = bh - b * kv_heads;
+    uint16_t* orow = out + (static_cast<size_t>(b) * kv_heads * G + static_cast<size_t>(kvh) * G) * D;
+    const float* hp = parts + static_cast<size_t>(bh) * n_chunks * PF;
+    constexpr int R = 16;  // chunks whose partials are loaded together
+    for (int e = threadIdx.x; e < G * D; e += kAttnThreads) {
+        const int g = e / D;
+        float M = -INFINITY, L = 0.0f, O = 0.0f;  // running combination
+        for (int c0 = 0; c0 < used; c0 += R) {
+            float m[R], l[R], o[R];
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                const int c = min(c0 + i, used - 1);
+                m[i] = hp[c * PF + 2 * g];
+                l[i] = hp[c * PF + 2 * g + 1];
+                o[i] = hp[c * PF + 2 * G + e];
+            }
+            float bm = M;
+#pragma unroll
+            for (int i = 0; i < R; ++i) bm = fmaxf(bm, m[i]);  // clamped entries repeat a used chunk
+            const float scale = expf(M - bm);  // 0 on the first batch (M = -inf, bm finite)
+            L *= scale;
+            O *= scale;
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                if (c0 + i < used) {
+                    const float f = expf(m[i] - bm);
+                    L = fmaf(l[i], f, L);
+                    O = fmaf(o[i], f, O);
+                }
+            }
+            M = bm;
+        }
+        orow[e] = T::from_float(O / L);
     }
 }
 
 template <typename T, int G>
 void launch_attn(const void* q, const void* k, const void* v, int64_t qkv_stride, void* k_cache, void* v_cache,
                  const void* rope_cos, const void* rope_sin, const int64_t* position, void* out, int64_t batch,
-                 int64_t kv_heads, int64_t max_len, float scaling, size_t lds, hipStream_t st) {
-    const dim3 grid(static_cast<unsigned>(batch * kv_heads));
-    attn_decode_kernel<T, G><<<grid, kAttnThreads, lds, st>>>(
+                 int64_t kv_heads, int64_t max_len, float scaling, float* parts, hipStream_t st) {
+    const dim3 grid(static_cast<unsigned>(batch * kv_heads * attn_chunks(max_len)));
+    attn_decode_kernel<T, G><<<grid, kAttnThreads, 0, st>>>(
         static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
         static_cast<int>(qkv_stride), static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache),
         static_cast<const uint16_t*>(rope_cos), static_cast<const uint16_t*>(rope_sin), position,
-        static_cast<uint16_t*>(out), static_cast<int>(kv_heads), static_cast<int>(max_len), scaling);
+        static_cast<uint16_t*>(out), static_cast<int>(kv_heads), static_cast<int>(max_len), scaling, parts);
+    attn_combine_kernel<T, G><<<dim3(static_cast<unsigned>(batch * kv_heads)), kAttnThreads, 0, st>>>(
+        parts, position, static_cast<uint16_t*>(out), static_cast<int>(kv_heads), static_cast<int>(max_len));
 }
 
 template <typename T>
 bool launch_attn_g(int g, const void* q, const void* k, const void* v, int64_t qkv_stride, void* k_cache,
                    void* v_cache, const void* rope_cos, const void* rope_sin, const int64_t* position, void* out,
-                   int64_t batch, int64_t kv_heads, int64_t max_len, float scaling, size_t lds, hipStream_t st) {
+                   int64_t batch, int64_t kv_heads, int64_t max_len, float scaling, float* parts, hipStream_t st) {
+#define NQ_ATTN(G_)                                                                                              \
+    launch_attn<T, G_>(q, k, v, qkv_stride, k_cache, v_cache, rope_cos, rope_sin, position, out, batch, kv_heads, \
+                       max_len, scaling, parts, st)
     switch (g) {
-        case 1: launch_attn<T, 1>(q, k, v, qkv_stride, k_cache, v_cache, rope_cos, rope_sin, position, out, batch, kv_heads, max_len, scaling, lds, st); return true;
-        case 2: launch_attn<T, 2>(q, k, v, qkv_stride, k_cache, v_cache, rope_cos, rope_sin, position, out, batch, kv_heads, max_len, scaling, lds, st); return true;
-        case 4: launch_attn<T, 4>(q, k, v, qkv_stride, k_cache, v_cache, rope_cos, rope_sin, position, out, batch, kv_heads, max_len, scaling, lds, st); return true;
-        case 8: launch_attn<T, 8>(q, k, v, qkv_stride, k_cache, v_cache, rope_cos, rope_sin, position, out, batch, kv_heads, max_len, scaling, lds, st); return true;
+        case 1: NQ_ATTN(1); return true;
+        case 2: NQ_ATTN(2); return true;
+        case 4: NQ_ATTN(4); return true;
+        case 8: NQ_ATTN(8); return true;
         default: return false;
     }
-}
-
-// LDS of attn_decode_kernel<G>: static (queries, new key and value, reduction slots) and
-// dynamic (score rows, reused for the waves' partial outputs).
-inline size_t attn_static_lds(int64_t g) { return static_cast<size_t>(g) * kHeadDim * 2 + 4 * kHeadDim + 64; }
-inline size_t attn_dynamic_lds(int64_t g, int64_t max_len) {
-    return static_cast<size_t>(std::max<int64_t>(g * max_len, (kAttnThreads / 64) * g * kHeadDim)) * sizeof(float);
+#undef NQ_ATTN
 }
 
 }  // namespace
@@ -242,10 +322,18 @@ using namespace nq;
 
 extern "C" {
 
+size_t nq_attention_decode_workspace_bytes(int64_t batch, int64_t heads, int64_t kv_heads, int64_t head_dim,
+                                           int64_t max_len) {
+    if (batch < 0 || heads <= 0 || kv_heads <= 0 || max_len <= 0 || head_dim != kHeadDim || heads % kv_heads)
+        return 0;
+    const int64_t g = heads / kv_heads;
+    return static_cast<size_t>(batch * kv_heads * attn_chunks(max_len) * attn_part_floats(g)) * sizeof(float);
+}
+
 int nq_attention_decode(int dtype, const void* q, const void* k, const void* v, int64_t qkv_stride, void* k_cache,
                         void* v_cache, const void* rope_cos, const void* rope_sin, const int64_t* position, void* out,
                         int64_t batch, int64_t heads, int64_t kv_heads, int64_t head_dim, int64_t max_len,
-                        float scaling, nq_stream_t stream) {
+                        float scaling, void* workspace, size_t workspace_bytes, nq_stream_t stream) {
     const char* name = "nq_attention_decode";
     if (dtype != NQ_F16 && dtype != NQ_BF16) return fail(NQ_ERR_DTYPE, "%s: unsupported dtype %d", name, dtype);
     if (batch < 0 || heads <= 0 || kv_heads <= 0 || max_len <= 0 || head_dim <= 0)
@@ -255,28 +343,29 @@ int nq_attention_decode(int dtype, const void* q, const void* k, const void* v, 
     const int64_t g = heads / kv_heads;
     if (g != 1 && g != 2 && g != 4 && g != 8)
         return fail(NQ_ERR_UNSUPPORTED, "%s: heads / kv_heads must be 1, 2, 4 or 8", name);
-    const size_t lds = attn_dynamic_lds(g, max_len);
-    if (lds + attn_static_lds(g) > kAttnLdsBudget)
-        return fail(NQ_ERR_UNSUPPORTED, "%s: max_len %lld too long for (heads / kv_heads) = %lld", name,
-                    (long long)max_len, (long long)g);
     if (qkv_stride < heads * head_dim)
         return fail(NQ_ERR_SHAPE, "%s: qkv_stride %lld too small", name, (long long)qkv_stride);
-    if (batch * kv_heads > INT32_MAX / 2 || batch * kv_heads * max_len * head_dim > ((int64_t)1 << 40) ||
-        batch * qkv_stride > INT32_MAX / 2)
+    if (batch * kv_heads * attn_chunks(max_len) > INT32_MAX / 2 || max_len > INT32_MAX / 2 ||
+        batch * kv_heads * max_len * head_dim > ((int64_t)1 << 40) || batch * qkv_stride > INT32_MAX / 2)
         return fail(NQ_ERR_UNSUPPORTED, "%s: sizes too large", name);
     if (batch == 0) return NQ_OK;
-    if (!q || !k || !v || !k_cache || !v_cache || !rope_cos || !rope_sin || !position || !out)
+    if (!q || !k || !v || !k_cache || !v_cache || !rope_cos || !rope_sin || !position || !out || !workspace)
         return fail(NQ_ERR_INVALID_ARGUMENT, "%s: null pointer", name);
     if (!aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(q, 2) || !aligned(k, 2) || !aligned(v, 2) ||
-        !aligned(out, 2) || !aligned(rope_cos, 2) || !aligned(rope_sin, 2) || !aligned(position, 8))
-        return fail(NQ_ERR_ALIGNMENT, "%s: misaligned operand (the caches need 16 bytes)", name);
+        !aligned(out, 2) || !aligned(rope_cos, 2) || !aligned(rope_sin, 2) || !aligned(position, 8) ||
+        !aligned(workspace, 256))
+        return fail(NQ_ERR_ALIGNMENT, "%s: misaligned operand (the caches need 16 bytes, the workspace 256)", name);
+    const size_t need = nq_attention_decode_workspace_bytes(batch, heads, kv_heads, head_dim, max_len);
+    if (workspace_bytes < need)
+        return fail(NQ_ERR_WORKSPACE, "%s: workspace has %zu bytes, needs %zu", name, workspace_bytes, need);
+    float* parts = static_cast<float*>(workspace);
     hipStream_t st = as_stream(stream);
     const bool ok = dtype == NQ_F16 ? launch_attn_g<F16>(static_cast<int>(g), q, k, v, qkv_stride, k_cache, v_cache,
                                                          rope_cos, rope_sin, position, out, batch, kv_heads, max_len,
-                                                         scaling, lds, st)
+                                                         scaling, parts, st)
                                     : launch_attn_g<BF16>(static_cast<int>(g), q, k, v, qkv_stride, k_cache, v_cache,
                                                           rope_cos, rope_sin, position, out, batch, kv_heads, max_len,
-                                                          scaling, lds, st);
+                                                          scaling, parts, st);
     if (!ok) return fail(NQ_ERR_UNSUPPORTED, "%s: no kernel for this head grouping", name);
     return check_launch(name);
 }

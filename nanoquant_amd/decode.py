@@ -403,6 +403,11 @@ class FusedDecoder(GraphDecoder):
             for items, count in (plan["qkv"], plan["o"], plan["gu"], plan["down"]):
                 need = max(need, self.lib.nq_gemv_group_workspace_bytes(count, items, batch))
         self.ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=dev)
+        # attention workspace: the partial results of the 64-position chunks
+        abytes = self.lib.nq_attention_decode_workspace_bytes(batch, H, KV, D, max_len)
+        if abytes == 0:
+            raise ValueError("nq_attention_decode does not take this head layout")
+        self.attn_ws = torch.zeros(abytes, dtype=torch.uint8, device=dev)
 
     def _scale_in(self, lin, norm_weight):
         s_in = lin.scale_pre
@@ -465,7 +470,7 @@ class FusedDecoder(GraphDecoder):
                 dt, qkv, qkv + H * D * esz, qkv + (H + KV) * D * esz, self.qkv_width,
                 self.cache.k[li].data_ptr(), self.cache.v[li].data_ptr(), self.rope_cos.data_ptr(),
                 self.rope_sin.data_ptr(), self.pos.data_ptr(), attn, B, H, KV, D, self.max_len,
-                D ** -0.5, st), "attention")
+                D ** -0.5, self.attn_ws.data_ptr(), self.attn_ws.numel(), st), "attention")
             items, n = plan["o"]
             self._check(lib.nq_gemv_group_stage1(dt, n, items, attn, B, H * D, -1.0, ws, wsb, st), "o 1")
             self._check(lib.nq_gemv_group_stage2(dt, n, items, B, self._lib.NQ_EPI_RESIDUAL, ws, wsb, st), "o 2")

@@ -7,7 +7,8 @@ Bars (written here):
   fp16 inputs, <= 1e-3 (norm, residual) and <= 2e-3 (gated: three more fp16 roundings);
 * attention: the rotated key stored in the cache is bit-identical to torch's fp16 rotary
   arithmetic; the stored value is the input value; rows other than the position are
-  untouched; the output is within 2e-3 of float64 attention (relative to its max);
+  untouched; the output is within 2e-3 of float64 attention (relative to its max), across
+  one and several 64-position chunks;
 * a position outside the cache leaves the caches untouched and writes zeros.
 """
 import ctypes
@@ -177,11 +178,11 @@ def rotate_half(x):
 
 
 @pytest.mark.parametrize("G", [1, 2, 4, 8])
-@pytest.mark.parametrize("pos", [0, 17, 39])
+@pytest.mark.parametrize("pos", [0, 17, 63, 64, 130, 199])
 def test_attention_decode(lib, G, pos):
     from nanoquant_amd import _lib
     announce("attention", G, pos)
-    B, KV, D, L = 2, 2, 128, 40
+    B, KV, D, L = 2, 2, 128, 200
     H = KV * G
     gen = torch.Generator().manual_seed(100 * G + pos)
     qkv = torch.randn(B, (H + 2 * KV) * D, generator=gen).half()
@@ -198,9 +199,11 @@ def test_attention_decode(lib, G, pos):
     W = (H + 2 * KV) * D
     p0 = d_qkv.data_ptr()
     st = torch.cuda.current_stream().cuda_stream
+    ws = torch.empty(lib.nq_attention_decode_workspace_bytes(B, H, KV, D, L), dtype=torch.uint8, device="cuda")
     _lib.check(lib.nq_attention_decode(_lib.NQ_F16, p0, p0 + 2 * H * D, p0 + 2 * (H + KV) * D, W, d_kc.data_ptr(),
                                        d_vc.data_ptr(), d_cos.data_ptr(), d_sin.data_ptr(), d_pos.data_ptr(),
-                                       out.data_ptr(), B, H, KV, D, L, D ** -0.5, st), "attention")
+                                       out.data_ptr(), B, H, KV, D, L, D ** -0.5, ws.data_ptr(), ws.numel(), st),
+               "attention")
     torch.cuda.synchronize()
     q = qkv[:, :H * D].view(B, H, D)
     k = qkv[:, H * D:(H + KV) * D].view(B, KV, D)
@@ -236,16 +239,21 @@ def test_attention_position_outside_cache(lib):
     kc0, vc0 = kc.clone(), vc.clone()
     cs = torch.ones(L, D, device="cuda").half()
     out = torch.ones(B, H * D, dtype=torch.float16, device="cuda")
+    ws = torch.zeros(lib.nq_attention_decode_workspace_bytes(B, H, KV, D, L), dtype=torch.uint8, device="cuda")
     W = (H + 2 * KV) * D
     p0 = qkv.data_ptr()
     for bad in (L, -1):
         d_pos = torch.tensor([bad], dtype=torch.int64, device="cuda")
         _lib.check(lib.nq_attention_decode(_lib.NQ_F16, p0, p0 + 2 * H * D, p0 + 2 * (H + KV) * D, W,
                                            kc.data_ptr(), vc.data_ptr(), cs.data_ptr(), cs.data_ptr(),
-                                           d_pos.data_ptr(), out.data_ptr(), B, H, KV, D, L, 0.1, None), "attn")
+                                           d_pos.data_ptr(), out.data_ptr(), B, H, KV, D, L, 0.1, ws.data_ptr(),
+                                           ws.numel(), None), "attn")
         torch.cuda.synchronize()
         assert torch.equal(kc, kc0) and torch.equal(vc, vc0)
         assert torch.count_nonzero(out) == 0
     assert lib.nq_attention_decode(_lib.NQ_F16, p0, p0, p0, W, kc.data_ptr(), vc.data_ptr(), cs.data_ptr(),
                                    cs.data_ptr(), d_pos.data_ptr(), out.data_ptr(), B, H, KV, 64, L, 0.1,
-                                   None) == _lib.NQ_ERR_UNSUPPORTED
+                                   ws.data_ptr(), ws.numel(), None) == _lib.NQ_ERR_UNSUPPORTED
+    assert lib.nq_attention_decode(_lib.NQ_F16, p0, p0, p0, W, kc.data_ptr(), vc.data_ptr(), cs.data_ptr(),
+                                   cs.data_ptr(), d_pos.data_ptr(), out.data_ptr(), B, H, KV, D, L, 0.1,
+                                   ws.data_ptr(), 16, None) == _lib.NQ_ERR_WORKSPACE

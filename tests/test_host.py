@@ -61,13 +61,16 @@ def test_c_abi_argument_errors_need_no_gpu():
     assert lib.nq_gemv_group_workspace_bytes(5, items, 1) == 0
     assert lib.nq_gemv_group_stage2(0, 2, items, 1, 7, None, 0, None) == _lib.NQ_ERR_INVALID_ARGUMENT
     attn = lambda dtype, hd, heads, kv, L: lib.nq_attention_decode(  # noqa: E731
-        dtype, None, None, None, heads * hd, None, None, None, None, None, None, 1, heads, kv, hd, L, 1.0, None)
+        dtype, None, None, None, heads * hd, None, None, None, None, None, None, 1, heads, kv, hd, L, 1.0, None, 0,
+        None)
     assert attn(9, 128, 32, 32, 384) == _lib.NQ_ERR_DTYPE
     assert attn(0, 64, 32, 32, 384) == _lib.NQ_ERR_UNSUPPORTED
     assert attn(0, 128, 24, 8, 384) == _lib.NQ_ERR_UNSUPPORTED  # 3 query heads per kv head
-    assert attn(0, 128, 64, 8, 4096) == _lib.NQ_ERR_UNSUPPORTED  # scores exceed LDS
     assert attn(0, 128, 30, 8, 64) == _lib.NQ_ERR_SHAPE
     assert attn(0, 128, 32, 32, 384) == _lib.NQ_ERR_INVALID_ARGUMENT  # null pointers
+    # (2 + 128) floats per query head per 64-position chunk
+    assert lib.nq_attention_decode_workspace_bytes(1, 32, 32, 128, 384) == 32 * 6 * 130 * 4
+    assert lib.nq_attention_decode_workspace_bytes(1, 32, 32, 64, 384) == 0
 
 
 def test_schemas_are_the_reference_schemas():
