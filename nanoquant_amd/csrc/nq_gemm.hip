@@ -1,5 +1,7 @@
 // Prefill GEMM on the Marlin sign layout: C[M, N] = sat((A[M, K] * W) * s_out) with
-// W[k, o] = sign(k, o) * s_in[k], on gfx950 MFMA (v_mfma_f32_16x16x32_{f16,bf16}).
+// W[k, o] = sign(k, o) * s_in[k], on gfx950 MFMA. Two kernels: gemm_dm_kernel
+// (v_mfma_f32_32x32x16, operands fetched into LDS by DMA; K a multiple of 64) and
+// gemm_onebit_kernel (v_mfma_f32_16x16x32, any K that is a multiple of 16), described here.
 //
 // Marlin word (tr, col) of the [K/16, N/2] array holds o = 64*(col/32) + 16*o16 + 8*o8 + o1
 // (o1 = (col%32)/4) by k = 16*tr + 8*r8 + 2*r2 + r1 (r2 = col%4), element at bit
@@ -184,61 +186,63 @@ int launch_onebit(const void* A, const uint32_t* W, const void* s_in, const void
     return check_launch("nq_gemm_onebit");
 }
 
-// ---------------------------------------------------------------------------- 32x32x16 kernel
+// ------------------------------------------------------------------ LDS-DMA natural-k kernel
 //
-// C[q, o] = sat(s_out[o] * sum_k A[q, k] * sign(k, o) * s_in[k]), computed as C^T = S * A^T on
-// v_mfma_f32_32x32x16: the MFMA's A operand is 32 output features by 16 k of +-s_in, made from
-// the Marlin words in registers; its B operand is 16 k by 32 rows of A. Lane l = (kg = l / 32,
-// c = l % 32).
-//   sign operand: feature o = o0 + c; dword d = (r8 = d / 2, r2 = 2kg + d % 2) holds the pair
-//     k = 16tr + 8r8 + 2r2 + {0, 1}: Marlin word (tr, 32(o/64) + 4(o%8) + r2) shifted left by
-//     2((o%16)/8) + 4((o%64)/16) + r8 has their signs on bits 15 and 31, and they go onto the
-//     permuted s_in pair at 16tr + 4r2 + 2r8 (one 16-byte read per (tr, kg) covers all four);
-//   A operand: row q0 + c, the same k: A[q][16tr + 4kg .. +3] and A[q][16tr + 8 + 4kg .. +3],
-//     one 16-byte LDS read (the tile is stored with each 16-k group as k 0-3, 8-11, 4-7, 12-15);
-//   C: lane holds C^T[o0 + 8(i/4) + 4kg + i%4][q0 + c], four consecutive features per group of
-//      four registers, stored as one 8-byte write of C[q][o .. o+3].
-// Per 64-k step a block needs its A tile (BQ x 64 halves), the sign words of its BP features
-// (4 rows of BP/2 consecutive words: 1 KB at BP = 128) and 64 s_in values. Each is loaded once
-// per block, coalesced, two steps ahead into registers, and staged through double-buffered
-// LDS; lanes then read their words and s_in pairs from LDS (4 and 32 lanes share an address,
-// which LDS broadcasts). Loading the words per lane instead (4 lanes and 2 tiles per word,
-// and every wave of the block again) kept the texture data path ~70% busy.
-// The grid runs q tiles fastest: blocks i, i+8, ... land on one XCD, so with q_tiles dividing
-// 8 or a multiple of 8 each XCD streams its own rows of A through its L2.
-#ifndef NQ_SX_WAVES_PER_EU
-#define NQ_SX_WAVES_PER_EU 2
-#endif
-template <typename T, bool kSin, bool kSout, int BP, int BQ, int WP, int WQ, int BKK>
-__global__ __launch_bounds__((BP / WP) * (BQ / WQ) * 64) __attribute__((amdgpu_waves_per_eu(NQ_SX_WAVES_PER_EU)))
-void gemm_sx_kernel(
+// The natural-k product with every operand of a 64-k step fetched by global_load_lds (16 bytes
+// a lane for the A tile, 4 for sign words and s_in) straight into one of three LDS buffers,
+// two steps ahead, so no register holds a tile in flight. A wave's DMA writes 64 consecutive
+// LDS slots, so the A tile is unpadded (128-byte rows) and bank conflicts are avoided by where
+// each lane fetches from: LDS chunk p of row r holds the row's 16-byte chunk p ^ (r % 8). s_in
+// is fetched in the order the operands read it (every wave keeps its own copy, so every wave
+// issues the same number of DMAs per step). The three buffers are distinct LDS arrays, so the
+// compiler's wait counts for a buffer's reads cover only that buffer's DMAs; before the barrier
+// that ends a step each wave waits for its own DMAs of the next step.
+template <int N>
+__device__ inline void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt has 6 bits");
+    // gfx9 s_waitcnt: vmcnt in bits 3:0 and 15:14; expcnt (6:4) and lgkmcnt (11:8) not waited on
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+__device__ inline void dma_to_lds16(const void* src, void* lds) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                     (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+
+__device__ inline void dma_to_lds4(const void* src, void* lds) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                     (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
+}
+
+template <typename T, bool kSin, bool kSout, int BP, int BQ, int WP, int WQ, int WPE>
+__global__ __launch_bounds__((BP / WP) * (BQ / WQ) * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
+void gemm_dm_kernel(
     const uint16_t* __restrict__ A, const uint32_t* __restrict__ W, const uint16_t* __restrict__ s_in,
     const uint16_t* __restrict__ s_out, uint16_t* __restrict__ C, int M, int K, int N, int q_tiles) {
+    constexpr int BKK = 64;
     constexpr int NWP = BP / WP;
     constexpr int NWQ = BQ / WQ;
     constexpr int NT = NWP * NWQ * 64;
     constexpr int TP = WP / 32;
     constexpr int TQ = WQ / 32;
-    constexpr int TG = WP / 64;            // 64-feature word groups per wave
-    constexpr int KT = BKK / 16;           // 16-k tiles per step
-    constexpr int LDX = BKK + 8;           // LDS row pitch of the A tile in halves
-    constexpr int XPIECES = BQ * BKK / 8;  // 16-byte pieces of the A tile
-    constexpr int XPT = XPIECES / NT;
-    constexpr int WROW = BP / 2;           // sign words per k-tile row of the block
-    constexpr int WWORDS = KT * WROW;      // sign words per step
-    constexpr int WPT = (WWORDS + NT - 1) / NT;  // sign words per thread (the last round may be partial)
-    constexpr int SDW = BKK / 2;           // s_in dwords per step
-    static_assert(XPIECES % NT == 0 && (WWORDS % NT == 0 || WWORDS < NT), "tile pieces must divide evenly");
+    constexpr int TG = WP / 64;        // 64-feature word groups per wave
+    constexpr int KT = BKK / 16;       // 16-k tiles per step
+    constexpr int XCH = BQ * BKK / 8;  // 16-byte chunks of the A tile
+    constexpr int XPT = XCH / NT;
+    constexpr int WROW = BP / 2;       // sign words per k-tile row of the block
+    constexpr int WWORDS = KT * WROW;  // sign words per step
+    constexpr int WPT = WWORDS / NT;
+    constexpr int kIssued = XPT + WPT + (kSin ? 1 : 0);  // DMAs per step and wave
+    static_assert(XCH % NT == 0 && WWORDS % NT == 0, "tile pieces must divide evenly");
     static_assert(WP % 64 == 0 && BP % 64 == 0, "features come in whole 64-feature word groups");
-    static_assert(SDW <= NT, "one s_in dword per thread");
-    __shared__ __attribute__((aligned(16))) uint16_t xs[2][BQ * LDX];
-    __shared__ __attribute__((aligned(16))) uint32_t ws[2][WWORDS];
-    __shared__ __attribute__((aligned(16))) uint32_t ss[2][SDW];
+    __shared__ __attribute__((aligned(16))) uint16_t xs0[BQ * BKK], xs1[BQ * BKK], xs2[BQ * BKK];
+    __shared__ __attribute__((aligned(16))) uint32_t ws0[WWORDS], ws1[WWORDS], ws2[WWORDS];
+    __shared__ __attribute__((aligned(16))) uint32_t ss0[kSin ? NT : 4], ss1[kSin ? NT : 4], ss2[kSin ? NT : 4];
     __shared__ uint16_t sos[BP];
 
     const int t = threadIdx.x;
     const int lane = t & 63;
-    const int wave = t >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int c = lane & 31;
     const int kg = lane >> 5;
     const int wp = wave % NWP;
@@ -250,69 +254,46 @@ void gemm_sx_kernel(
     const uint32_t half_n = static_cast<uint32_t>(N) >> 1;
     const int k_iters = K / BKK;
 
-    // lane constants: the word of feature o (per 64-feature group) and its shift per tile
+    // lane constants: the first of the four words of its feature per 64-feature group, the shift
+    // per 32-feature tile, its A-tile rows and the swizzled chunk of its 8 k per k tile
     int wl[TG], shb[TP];
 #pragma unroll
-    for (int g = 0; g < TG; ++g) wl[g] = 32 * (wp * TG + g) + 4 * (c & 7) + 2 * kg;
+    for (int g = 0; g < TG; ++g) wl[g] = 32 * (wp * TG + g) + 4 * (c & 7);
 #pragma unroll
     for (int tp = 0; tp < TP; ++tp) {
         const int o = wp * WP + 32 * tp + c;  // feature offset in the block
-        shb[tp] = 2 * ((o & 15) >> 3) + 4 * ((o & 63) >> 4);
+        shb[tp] = 2 * ((o & 15) >> 3) + 4 * ((o & 63) >> 4) + kg;
     }
-    // load sources: A pieces, sign words (row kt = word / WROW of the step), s_in dwords
-    const uint16_t* xsrc[XPT];
-    int xdst[XPT];
+    const int xrow = (wq * WQ + c) * BKK;  // halves; rows of tile tq are 32 tq further
+    // DMA sources: A chunks (32-bit element offsets), sign words, s_in dwords in read order
+    uint32_t xoff[XPT];
 #pragma unroll
     for (int j = 0; j < XPT; ++j) {
-        const int piece = t + j * NT;
-        const int row = piece / (BKK / 8);
-        const int c8 = piece - row * (BKK / 8);
-        xsrc[j] = A + static_cast<size_t>(min(q0 + row, M - 1)) * K + 8 * c8;
-        xdst[j] = row * LDX + 8 * c8;  // with the exchange, piece 2m + e holds half e of group m
+        const int ci = j * NT + t;
+        const int r = ci >> 3;
+        xoff[j] = static_cast<uint32_t>(min(q0 + r, M - 1)) * static_cast<uint32_t>(K) + 8 * ((ci & 7) ^ (r & 7));
     }
     uint32_t wsrc[WPT];
 #pragma unroll
     for (int j = 0; j < WPT; ++j) {
-        const int word = min(t + j * NT, WWORDS - 1);
-        const int kt = word / WROW;
-        wsrc[j] = kt * half_n + min(static_cast<uint32_t>(p0 / 2 + (word - kt * WROW)), half_n - 1);
+        const int wi = j * NT + t;
+        const int kt = wi / WROW;
+        wsrc[j] = kt * half_n + min(static_cast<uint32_t>(p0 / 2 + (wi - kt * WROW)), half_n - 1);
     }
-    const int sd = t % SDW;
+    // s_in comes permuted: dword 8tr + 2r2 + r8 holds the pair k = 16tr + 8r8 + 2r2 + {0, 1}; LDS
+    // slot 8tr + 4r8 + r2 of the wave's copy takes it, so the pairs r2 = 0..3 of one r8 are adjacent
+    const int sl = lane & 31;
+    const int sidx = (sl & ~7) | ((sl & 3) << 1) | ((sl >> 2) & 1);
     for (int e = t; e < BP; e += NT) sos[e] = kSout ? s_out[perm_out(min(p0 + e, N - 1))] : uint16_t(0);
 
-    struct Ops {
-        u32x4 x[XPT];
-        uint32_t w[WPT];
-        uint32_t s;  // used with kSin only
-    };
-    auto load_ops = [&](Ops& o, int iter) {
-        const int k0 = iter * BKK;
+    auto issue = [&](int iter, uint16_t* xs, uint32_t* ws, uint32_t* ss) {
+        const uint32_t k0 = static_cast<uint32_t>(iter * BKK);
 #pragma unroll
-        for (int j = 0; j < XPT; ++j) o.x[j] = *reinterpret_cast<const u32x4*>(xsrc[j] + k0);
+        for (int j = 0; j < XPT; ++j) dma_to_lds16(A + (xoff[j] + k0), xs + (j * NT + wave * 64) * 8);
         const uint32_t wrow = static_cast<uint32_t>(iter * KT) * half_n;
 #pragma unroll
-        for (int j = 0; j < WPT; ++j) o.w[j] = W[wrow + wsrc[j]];
-        if (kSin) o.s = *reinterpret_cast<const uint32_t*>(s_in + k0 + 2 * sd);
-    };
-    auto store_ops = [&](const Ops& o, int buf) {
-        // A piece is 8 halves of a row; lanes t (even) and t + 1 hold the two pieces of one
-        // 16-k group. The tile is stored with each group as k 0-3, 8-11, 4-7, 12-15, so that a
-        // lane's B fragment (k 4kg .. +3 and 8 + 4kg .. +3) is one 16-byte read: the even lane
-        // keeps its low half and takes its neighbour's low half, the odd lane the high halves.
-        const bool odd = t & 1;
-#pragma unroll
-        for (int j = 0; j < XPT; ++j) {
-            const u32x4 v = o.x[j];
-            const uint32_t s0 = odd ? v.x : v.z, s1 = odd ? v.y : v.w;
-            const uint32_t r0 = __builtin_amdgcn_mov_dpp(s0, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
-            const uint32_t r1 = __builtin_amdgcn_mov_dpp(s1, 0xB1, 0xF, 0xF, false);
-            const u32x4 out = odd ? u32x4{r0, r1, v.z, v.w} : u32x4{v.x, v.y, r0, r1};
-            *reinterpret_cast<u32x4*>(&xs[buf][xdst[j]]) = out;
-        }
-#pragma unroll
-        for (int j = 0; j < WPT; ++j)
-            if (WWORDS % NT == 0 || t + j * NT < WWORDS) ws[buf][t + j * NT] = o.w[j];
-        if (kSin && t < SDW) ss[buf][t] = o.s;
+        for (int j = 0; j < WPT; ++j) dma_to_lds4(W + (wrow + wsrc[j]), ws + j * NT + wave * 64);
+        if (kSin) dma_to_lds4(s_in + (k0 + 2 * sidx), ss + wave * 64);
     };
 
     f32x16 acc[TP][TQ];
@@ -323,65 +304,67 @@ void gemm_sx_kernel(
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[tp][tq][i] = 0.0f;
 
+    // +-1 pairs kept in a register, so that each sign operand dword is one shift and one v_bitop3
+    uint32_t one = T::ONE_PAIR;
+    asm volatile("" : "+v"(one));
+    struct Frag {
+        u32x4 w[TG];
+        u32x4 s;
+        u32x4 x[TQ];
+    };
+    auto read_kt = [&](Frag& f, const uint16_t* xs, const uint32_t* ws, const uint32_t* ss, int kt) {
+        const int pos = (2 * kt + kg) ^ (c & 7);
+#pragma unroll
+        for (int g = 0; g < TG; ++g) f.w[g] = *reinterpret_cast<const u32x4*>(ws + kt * WROW + wl[g]);
+        f.s = kSin ? *reinterpret_cast<const u32x4*>(ss + wave * 64 + 8 * kt + 4 * kg) : u32x4{one, one, one, one};
+#pragma unroll
+        for (int tq = 0; tq < TQ; ++tq)
+            f.x[tq] = *reinterpret_cast<const u32x4*>(xs + xrow + 32 * tq * BKK + 8 * pos);
+    };
     const uint32_t mask = 0x80008000u;
-    // One step: issue the loads of step it + 2 into `fill`, run the MFMAs of step it from LDS
-    // buffer it % 2, put `nxt` (step it + 1) into the other buffer. The three register sets
-    // rotate through a loop unrolled three times, so no register is ever copied (a copy of a
-    // just-issued load would wait for it).
-    // Loads and stores are unconditional (the tail reloads the last step): a load under a branch
-    // makes the wait counts at the merge assume it may be the newest load, and the stores at the
-    // end of the step would then wait for the loads just issued for two steps later.
-    auto step = [&](Ops& nxt, Ops& fill, int it) {
-        load_ops(fill, min(it + 2, k_iters - 1));
-        __builtin_amdgcn_sched_barrier(0);
-        const int buf = it & 1;
-        const uint16_t* xb = &xs[buf][(wq * WQ + c) * LDX + 8 * kg];
-        // every LDS read of the step first (one latency per step, not one per k tile), then the
-        // sign operands and MFMAs as the reads land
-        u32x4 bx[KT][TQ];
-        uint2 wv[KT][TG];
-        u32x4 sv[KT];
+    auto compute_kt = [&](const Frag& f) {
 #pragma unroll
-        for (int kt = 0; kt < KT; ++kt) {
+        for (int tp = 0; tp < TP; ++tp) {
+            const u32x4 w = f.w[tp / 2];
+            const int sft = shb[tp];
+            const u32x4 a = u32x4{f.s.x ^ ((w.x << sft) & mask), f.s.y ^ ((w.y << sft) & mask),
+                                  f.s.z ^ ((w.z << sft) & mask), f.s.w ^ ((w.w << sft) & mask)};
 #pragma unroll
-            for (int g = 0; g < TG; ++g) wv[kt][g] = *reinterpret_cast<const uint2*>(&ws[buf][kt * WROW + wl[g]]);
-            sv[kt] = kSin ? *reinterpret_cast<const u32x4*>(&ss[buf][8 * kt + 4 * kg])
-                          : u32x4{T::ONE_PAIR, T::ONE_PAIR, T::ONE_PAIR, T::ONE_PAIR};
-#pragma unroll
-            for (int tq = 0; tq < TQ; ++tq) {
-                bx[kt][tq] = *reinterpret_cast<const u32x4*>(xb + 32 * tq * LDX + 16 * kt);
-            }
+            for (int tq = 0; tq < TQ; ++tq) acc[tp][tq] = mfma32x32x16<T>(a, f.x[tq], acc[tp][tq]);
         }
-#pragma unroll
-        for (int kt = 0; kt < KT; ++kt) {
-#pragma unroll
-            for (int tp = 0; tp < TP; ++tp) {
-                const uint32_t w0 = wv[kt][tp / 2].x, w1 = wv[kt][tp / 2].y;
-                const int sft = shb[tp];
-                const u32x4 a = u32x4{sv[kt].x ^ ((w0 << sft) & mask), sv[kt].z ^ ((w1 << sft) & mask),
-                                      sv[kt].y ^ ((w0 << (sft + 1)) & mask), sv[kt].w ^ ((w1 << (sft + 1)) & mask)};
-#pragma unroll
-                for (int tq = 0; tq < TQ; ++tq) acc[tp][tq] = mfma32x32x16<T>(a, bx[kt][tq], acc[tp][tq]);
-            }
-        }
-        store_ops(nxt, buf ^ 1);  // past the last step this writes a buffer nobody reads
+    };
+    // One step: DMA step it + 2 into the buffer step it - 1 used, run the MFMAs of step it (each k
+    // tile's reads issued before the previous tile's MFMAs), wait for this wave's DMAs of step
+    // it + 1, barrier. The tail re-fetches the last step into the free buffer.
+    auto step = [&](const uint16_t* xc, const uint32_t* wc, const uint32_t* sc, uint16_t* xf, uint32_t* wf,
+                    uint32_t* sf, int it) {
+        issue(min(it + 2, k_iters - 1), xf, wf, sf);
+        Frag f0, f1;
+        read_kt(f0, xc, wc, sc, 0);
+        read_kt(f1, xc, wc, sc, 1);
+        compute_kt(f0);
+        read_kt(f0, xc, wc, sc, 2);
+        compute_kt(f1);
+        read_kt(f1, xc, wc, sc, 3);
+        compute_kt(f0);
+        compute_kt(f1);
+        wait_vmcnt<kIssued>();
         __syncthreads();
     };
 
-    Ops o0, o1, o2;
-    load_ops(o0, 0);
-    load_ops(o1, min(1, k_iters - 1));
-    store_ops(o0, 0);
+    issue(0, xs0, ws0, ss0);
+    issue(min(1, k_iters - 1), xs1, ws1, ss1);
+    wait_vmcnt<kIssued>();
     __syncthreads();
     int it = 0;
     for (; it + 3 <= k_iters; it += 3) {
-        step(o1, o2, it);
-        step(o2, o0, it + 1);
-        step(o0, o1, it + 2);
+        step(xs0, ws0, ss0, xs2, ws2, ss2, it);
+        step(xs1, ws1, ss1, xs0, ws0, ss0, it + 1);
+        step(xs2, ws2, ss2, xs1, ws1, ss1, it + 2);
     }
     if (it < k_iters) {
-        step(o1, o2, it);
-        if (it + 1 < k_iters) step(o2, o0, it + 1);
+        step(xs0, ws0, ss0, xs2, ws2, ss2, it);
+        if (it + 1 < k_iters) step(xs1, ws1, ss1, xs0, ws0, ss0, it + 1);
     }
 
     // epilogue: scale, saturate, four consecutive features per 8-byte store
@@ -408,10 +391,11 @@ void gemm_sx_kernel(
                 }
             }
         }
+    wait_vmcnt<0>();  // the tail's re-fetches land before the block's LDS is released
 }
 
-template <typename T, int BP, int BQ, int WP, int WQ, int BKK = 64>
-void launch_sx(const void* A, const uint32_t* W, const void* s_in, const void* s_out, void* C, int64_t M, int64_t K,
+template <typename T, int BP, int BQ, int WP, int WQ, int WPE>
+void launch_dm(const void* A, const uint32_t* W, const void* s_in, const void* s_out, void* C, int64_t M, int64_t K,
                int64_t N, hipStream_t stream) {
     const int q_tiles = static_cast<int>(ceil_div(M, BQ));
     const int p_tiles = static_cast<int>(ceil_div(N, BP));
@@ -423,24 +407,28 @@ void launch_sx(const void* A, const uint32_t* W, const void* s_in, const void* s
     auto* c = static_cast<uint16_t*>(C);
     const int m = static_cast<int>(M), k = static_cast<int>(K), n = static_cast<int>(N);
     if (s_in && s_out)
-        gemm_sx_kernel<T, true, true, BP, BQ, WP, WQ, BKK><<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles);
+        gemm_dm_kernel<T, true, true, BP, BQ, WP, WQ, WPE><<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles);
     else if (s_in)
-        gemm_sx_kernel<T, true, false, BP, BQ, WP, WQ, BKK><<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles);
+        gemm_dm_kernel<T, true, false, BP, BQ, WP, WQ, WPE><<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles);
     else if (s_out)
-        gemm_sx_kernel<T, false, true, BP, BQ, WP, WQ, BKK><<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles);
+        gemm_dm_kernel<T, false, true, BP, BQ, WP, WQ, WPE><<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles);
     else
-        gemm_sx_kernel<T, false, false, BP, BQ, WP, WQ, BKK><<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles);
+        gemm_dm_kernel<T, false, false, BP, BQ, WP, WQ, WPE><<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n,
+                                                                                       q_tiles);
 }
 
-// The 32x32x16 kernel needs whole 64-k iterations, 16-byte s_in pairs loads, 8-byte output
-// stores and 32-bit word offsets; anything else runs on the 16x16x32 kernel.
+// The 32x32x16 kernel needs whole 64-k iterations, 8-byte output stores and 32-bit element
+// offsets into A and the words; anything else runs on the 16x16x32 kernel. Block tile 256
+// features x 64 rows, four waves of 64 x 64: at B = 2048 on the Llama-2-7B shapes this beat
+// 128 x 128, 256 x 128 (waves of 64 x 128 or 128 x 64) and 256 x 128 with one 128 x 128 wave per
+// SIMD, whose 1376 wave tiles leave a third of the second round of the chip idle.
 template <typename T>
 int launch_gemm(const char* name, const void* A, const uint32_t* W, const void* s_in, const void* s_out, void* C,
                 int64_t M, int64_t K, int64_t N, hipStream_t stream) {
-    const bool sx = K % 64 == 0 && K > 0 && (!s_in || aligned(s_in, 16)) && aligned(C, 8) &&
+    const bool dm = K % 64 == 0 && K > 0 && aligned(C, 8) && M * K < ((int64_t)1 << 31) &&
                     (K / 16) * (N / 2) < ((int64_t)1 << 31);
-    if (!sx) return launch_onebit<T>(A, W, s_in, s_out, C, M, K, N, stream);
-    launch_sx<T, 128, 128, 64, 64, 64>(A, W, s_in, s_out, C, M, K, N, stream);
+    if (!dm) return launch_onebit<T>(A, W, s_in, s_out, C, M, K, N, stream);
+    launch_dm<T, 256, 64, 64, 64, 2>(A, W, s_in, s_out, C, M, K, N, stream);
     return check_launch(name);
 }
 
