@@ -197,6 +197,9 @@ int launch_onebit(const void* A, const uint32_t* W, const void* s_in, const void
 // issues the same number of DMAs per step). The three buffers are distinct LDS arrays, so the
 // compiler's wait counts for a buffer's reads cover only that buffer's DMAs; before the barrier
 // that ends a step each wave waits for its own DMAs of the next step.
+// With KS = 2 the block holds two groups of waves with buffers of their own, each over half of
+// the k steps (for outputs too few to give every SIMD two waves); group 1 hands its accumulators
+// to group 0 through LDS at the end.
 template <int N>
 __device__ inline void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt has 6 bits");
@@ -214,45 +217,53 @@ __device__ inline void dma_to_lds4(const void* src, void* lds) {
                                      (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
 }
 
-template <typename T, bool kSin, bool kSout, int BP, int BQ, int WP, int WQ, int WPE>
-__global__ __launch_bounds__((BP / WP) * (BQ / WQ) * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
+template <typename T, bool kSin, bool kSout, int BP, int BQ, int WP, int WQ, int WPE, int KS>
+__global__ __launch_bounds__((BP / WP) * (BQ / WQ) * 64 * KS) __attribute__((amdgpu_waves_per_eu(WPE)))
 void gemm_dm_kernel(
     const uint16_t* __restrict__ A, const uint32_t* __restrict__ W, const uint16_t* __restrict__ s_in,
     const uint16_t* __restrict__ s_out, uint16_t* __restrict__ C, int M, int K, int N, int q_tiles) {
     constexpr int BKK = 64;
     constexpr int NWP = BP / WP;
     constexpr int NWQ = BQ / WQ;
-    constexpr int NT = NWP * NWQ * 64;
+    constexpr int NTG = NWP * NWQ * 64;  // threads of one k group
+    constexpr int NT = NTG * KS;
     constexpr int TP = WP / 32;
     constexpr int TQ = WQ / 32;
     constexpr int TG = WP / 64;        // 64-feature word groups per wave
     constexpr int KT = BKK / 16;       // 16-k tiles per step
     constexpr int XCH = BQ * BKK / 8;  // 16-byte chunks of the A tile
-    constexpr int XPT = XCH / NT;
+    constexpr int XPT = XCH / NTG;
     constexpr int WROW = BP / 2;       // sign words per k-tile row of the block
     constexpr int WWORDS = KT * WROW;  // sign words per step
-    constexpr int WPT = WWORDS / NT;
+    constexpr int WPT = WWORDS / NTG;
     constexpr int kIssued = XPT + WPT + (kSin ? 1 : 0);  // DMAs per step and wave
-    static_assert(XCH % NT == 0 && WWORDS % NT == 0, "tile pieces must divide evenly");
+    constexpr int kAcc = TP * TQ * 16;                   // accumulators per lane
+    static_assert(XCH % NTG == 0 && WWORDS % NTG == 0, "tile pieces must divide evenly");
     static_assert(WP % 64 == 0 && BP % 64 == 0, "features come in whole 64-feature word groups");
-    __shared__ __attribute__((aligned(16))) uint16_t xs0[BQ * BKK], xs1[BQ * BKK], xs2[BQ * BKK];
-    __shared__ __attribute__((aligned(16))) uint32_t ws0[WWORDS], ws1[WWORDS], ws2[WWORDS];
+    static_assert(KS == 1 || KS == 2, "one or two k groups");
+    __shared__ __attribute__((aligned(16))) uint16_t xs0[KS][BQ * BKK], xs1[KS][BQ * BKK], xs2[KS][BQ * BKK];
+    __shared__ __attribute__((aligned(16))) uint32_t ws0[KS][WWORDS], ws1[KS][WWORDS], ws2[KS][WWORDS];
     __shared__ __attribute__((aligned(16))) uint32_t ss0[kSin ? NT : 4], ss1[kSin ? NT : 4], ss2[kSin ? NT : 4];
+    __shared__ float red[KS == 2 ? kAcc * NTG : 1];
     __shared__ uint16_t sos[BP];
 
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int grp = wave / (NWP * NWQ);  // k group
+    const int gw = wave - grp * (NWP * NWQ);
+    const int tg = t - grp * NTG;
     const int c = lane & 31;
     const int kg = lane >> 5;
-    const int wp = wave % NWP;
-    const int wq = wave / NWP;
+    const int wp = gw % NWP;
+    const int wq = gw / NWP;
     const int qt = blockIdx.x % q_tiles;
     const int pt = blockIdx.x / q_tiles;
     const int q0 = qt * BQ;
     const int p0 = pt * BP;
     const uint32_t half_n = static_cast<uint32_t>(N) >> 1;
-    const int k_iters = K / BKK;
+    const int k_iters = K / BKK / KS;  // steps of each k group (the host makes K / 64 divide by KS)
+    const int k_first = grp * k_iters;
 
     // lane constants: the first of the four words of its feature per 64-feature group, the shift
     // per 32-feature tile, its A-tile rows and the swizzled chunk of its 8 k per k tile
@@ -269,14 +280,14 @@ void gemm_dm_kernel(
     uint32_t xoff[XPT];
 #pragma unroll
     for (int j = 0; j < XPT; ++j) {
-        const int ci = j * NT + t;
+        const int ci = j * NTG + tg;
         const int r = ci >> 3;
         xoff[j] = static_cast<uint32_t>(min(q0 + r, M - 1)) * static_cast<uint32_t>(K) + 8 * ((ci & 7) ^ (r & 7));
     }
     uint32_t wsrc[WPT];
 #pragma unroll
     for (int j = 0; j < WPT; ++j) {
-        const int wi = j * NT + t;
+        const int wi = j * NTG + tg;
         const int kt = wi / WROW;
         wsrc[j] = kt * half_n + min(static_cast<uint32_t>(p0 / 2 + (wi - kt * WROW)), half_n - 1);
     }
@@ -287,12 +298,12 @@ void gemm_dm_kernel(
     for (int e = t; e < BP; e += NT) sos[e] = kSout ? s_out[perm_out(min(p0 + e, N - 1))] : uint16_t(0);
 
     auto issue = [&](int iter, uint16_t* xs, uint32_t* ws, uint32_t* ss) {
-        const uint32_t k0 = static_cast<uint32_t>(iter * BKK);
+        const uint32_t k0 = static_cast<uint32_t>((k_first + iter) * BKK);
 #pragma unroll
-        for (int j = 0; j < XPT; ++j) dma_to_lds16(A + (xoff[j] + k0), xs + (j * NT + wave * 64) * 8);
-        const uint32_t wrow = static_cast<uint32_t>(iter * KT) * half_n;
+        for (int j = 0; j < XPT; ++j) dma_to_lds16(A + (xoff[j] + k0), xs + (j * NTG + gw * 64) * 8);
+        const uint32_t wrow = static_cast<uint32_t>((k_first + iter) * KT) * half_n;
 #pragma unroll
-        for (int j = 0; j < WPT; ++j) dma_to_lds4(W + (wrow + wsrc[j]), ws + j * NT + wave * 64);
+        for (int j = 0; j < WPT; ++j) dma_to_lds4(W + (wrow + wsrc[j]), ws + j * NTG + gw * 64);
         if (kSin) dma_to_lds4(s_in + (k0 + 2 * sidx), ss + wave * 64);
     };
 
@@ -352,19 +363,45 @@ void gemm_dm_kernel(
         __syncthreads();
     };
 
-    issue(0, xs0, ws0, ss0);
-    issue(min(1, k_iters - 1), xs1, ws1, ss1);
+    uint16_t* x0 = xs0[grp];
+    uint16_t* x1 = xs1[grp];
+    uint16_t* x2 = xs2[grp];
+    uint32_t* w0 = ws0[grp];
+    uint32_t* w1 = ws1[grp];
+    uint32_t* w2 = ws2[grp];
+    issue(0, x0, w0, ss0);
+    issue(min(1, k_iters - 1), x1, w1, ss1);
     wait_vmcnt<kIssued>();
     __syncthreads();
     int it = 0;
     for (; it + 3 <= k_iters; it += 3) {
-        step(xs0, ws0, ss0, xs2, ws2, ss2, it);
-        step(xs1, ws1, ss1, xs0, ws0, ss0, it + 1);
-        step(xs2, ws2, ss2, xs1, ws1, ss1, it + 2);
+        step(x0, w0, ss0, x2, w2, ss2, it);
+        step(x1, w1, ss1, x0, w0, ss0, it + 1);
+        step(x2, w2, ss2, x1, w1, ss1, it + 2);
     }
     if (it < k_iters) {
-        step(xs0, ws0, ss0, xs2, ws2, ss2, it);
-        if (it + 1 < k_iters) step(xs1, ws1, ss1, xs0, ws0, ss0, it + 1);
+        step(x0, w0, ss0, x2, w2, ss2, it);
+        if (it + 1 < k_iters) step(x1, w1, ss1, x0, w0, ss0, it + 1);
+    }
+    wait_vmcnt<0>();  // the tail's re-fetches land before the block's LDS is reused or released
+
+    if (KS == 2) {  // group 1's sums join group 0's (lane-contiguous, conflict-free)
+        if (grp == 1) {
+#pragma unroll
+            for (int tp = 0; tp < TP; ++tp)
+#pragma unroll
+                for (int tq = 0; tq < TQ; ++tq)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) red[((tp * TQ + tq) * 16 + i) * NTG + tg] = acc[tp][tq][i];
+        }
+        __syncthreads();
+        if (grp == 1) return;
+#pragma unroll
+        for (int tp = 0; tp < TP; ++tp)
+#pragma unroll
+            for (int tq = 0; tq < TQ; ++tq)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[tp][tq][i] += red[((tp * TQ + tq) * 16 + i) * NTG + tg];
     }
 
     // epilogue: scale, saturate, four consecutive features per 8-byte store
@@ -391,29 +428,28 @@ void gemm_dm_kernel(
                 }
             }
         }
-    wait_vmcnt<0>();  // the tail's re-fetches land before the block's LDS is released
 }
 
-template <typename T, int BP, int BQ, int WP, int WQ, int WPE>
+template <typename T, int BP, int BQ, int WP, int WQ, int WPE, int KS>
 void launch_dm(const void* A, const uint32_t* W, const void* s_in, const void* s_out, void* C, int64_t M, int64_t K,
                int64_t N, hipStream_t stream) {
     const int q_tiles = static_cast<int>(ceil_div(M, BQ));
     const int p_tiles = static_cast<int>(ceil_div(N, BP));
     const dim3 grid(static_cast<unsigned>(q_tiles * p_tiles));
-    constexpr int NT = (BP / WP) * (BQ / WQ) * 64;
+    constexpr int NT = (BP / WP) * (BQ / WQ) * 64 * KS;
     const auto* a = static_cast<const uint16_t*>(A);
     const auto* si = static_cast<const uint16_t*>(s_in);
     const auto* so = static_cast<const uint16_t*>(s_out);
     auto* c = static_cast<uint16_t*>(C);
     const int m = static_cast<int>(M), k = static_cast<int>(K), n = static_cast<int>(N);
     if (s_in && s_out)
-        gemm_dm_kernel<T, true, true, BP, BQ, WP, WQ, WPE><<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles);
+        gemm_dm_kernel<T, true, true, BP, BQ, WP, WQ, WPE, KS><<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles);
     else if (s_in)
-        gemm_dm_kernel<T, true, false, BP, BQ, WP, WQ, WPE><<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles);
+        gemm_dm_kernel<T, true, false, BP, BQ, WP, WQ, WPE, KS><<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles);
     else if (s_out)
-        gemm_dm_kernel<T, false, true, BP, BQ, WP, WQ, WPE><<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles);
+        gemm_dm_kernel<T, false, true, BP, BQ, WP, WQ, WPE, KS><<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles);
     else
-        gemm_dm_kernel<T, false, false, BP, BQ, WP, WQ, WPE><<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n,
+        gemm_dm_kernel<T, false, false, BP, BQ, WP, WQ, WPE, KS><<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n,
                                                                                        q_tiles);
 }
 
@@ -421,14 +457,20 @@ void launch_dm(const void* A, const uint32_t* W, const void* s_in, const void* s
 // offsets into A and the words; anything else runs on the 16x16x32 kernel. Block tile 256
 // features x 64 rows, four waves of 64 x 64: at B = 2048 on the Llama-2-7B shapes this beat
 // 128 x 128, 256 x 128 (waves of 64 x 128 or 128 x 64) and 256 x 128 with one 128 x 128 wave per
-// SIMD, whose 1376 wave tiles leave a third of the second round of the chip idle.
+// SIMD, whose 1376 wave tiles leave a third of the second round of the chip idle. A grid of
+// fewer than two blocks per CU (e.g. the rank-wide first stage, N = r) splits K over two wave
+// groups per block instead (B = 2048, K = 4096, N = 1792: 46 -> 38 us).
 template <typename T>
 int launch_gemm(const char* name, const void* A, const uint32_t* W, const void* s_in, const void* s_out, void* C,
                 int64_t M, int64_t K, int64_t N, hipStream_t stream) {
     const bool dm = K % 64 == 0 && K > 0 && aligned(C, 8) && M * K < ((int64_t)1 << 31) &&
                     (K / 16) * (N / 2) < ((int64_t)1 << 31);
     if (!dm) return launch_onebit<T>(A, W, s_in, s_out, C, M, K, N, stream);
-    launch_dm<T, 256, 64, 64, 64, 2>(A, W, s_in, s_out, C, M, K, N, stream);
+    const int64_t blocks = ceil_div(M, 64) * ceil_div(N, 256);
+    if (blocks < 2 * 256 && (K / 64) % 2 == 0)
+        launch_dm<T, 256, 64, 64, 64, 2, 2>(A, W, s_in, s_out, C, M, K, N, stream);
+    else
+        launch_dm<T, 256, 64, 64, 64, 2, 1>(A, W, s_in, s_out, C, M, K, N, stream);
     return check_launch(name);
 }
 

@@ -257,6 +257,10 @@ GEMM_CASES = [
     # name, batch, n, r, m, with_mid
     ("small", 5, 64, 32, 64, False),
     ("tails", 130, 272, 288, 192, True),
+    # 64-k step kernel with its k range split over two wave groups, ragged rows and features
+    ("ragged_ksplit", 100, 512, 256, 320, True),
+    # an odd number of 64-k steps in stage 1 (one wave group), a split stage 2
+    ("odd_steps", 70, 192, 192, 320, False),
     ("cfg1_b256", 256, 4096, 1024, 4096, False),
     ("llama7b_gate_055_b256", 256, 4096, 1632, 11008, False),
     ("llama7b_down_055_b256", 256, 11008, 1632, 4096, False),
