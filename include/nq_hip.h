@@ -168,19 +168,30 @@ int nq_gemv_group_stage2(int dtype, int64_t count, const nq_gemv_item* items, in
  *   s_in, s_out: permuted as pack_binary_marlin returns them, or NULL (= ones)
  *   C  dtype [M, N]
  * K % 16 == 0, N % 64 == 0. fp32 accumulation; fp16 outputs saturate at +-65504.
+ * workspace: device memory (16-byte aligned) of nq_gemm_onebit_workspace_bytes(M, K, N) bytes
+ * lets a small grid split K across blocks (fp32 partial sums, added in a fixed order by a second
+ * launch); NULL or a smaller one runs unsplit. Calls that share a workspace must be ordered (one
+ * stream). The counterpart of the reference's Marlin workspace, which holds the locks of its
+ * cross-block reduction (gemm.cpp:36-56).
  * Replaces marlin_onebit_forward (src/nanoquant/kernel/cuda/gemm.cpp:59-98,
  * registered at pybind.cpp:93-98,113). */
+size_t nq_gemm_onebit_workspace_bytes(int64_t M, int64_t K, int64_t N);
 int nq_gemm_onebit(int dtype, const void* A, const uint32_t* w_bits, const void* s_in, const void* s_out,
-                   void* C, int64_t M, int64_t K, int64_t N, nq_stream_t stream);
+                   void* C, int64_t M, int64_t K, int64_t N, void* workspace, size_t workspace_bytes,
+                   nq_stream_t stream);
 
 /* Both stages: imm = A * (V_bits, s_g, s_l) [M, r_pad], then C = imm * (U_bits, s_h) [M, m].
  *   v_bits [n/16, r_pad/2], u_bits [r_pad/16, m/2], s_g [n], s_l [r_pad] or NULL, s_h [m] or NULL
- *   (all permuted as pack_binary_marlin_fused returns them); imm dtype [M, r_pad] is caller memory.
+ *   (all permuted as pack_binary_marlin_fused returns them); imm dtype [M, r_pad] is caller memory;
+ *   workspace as for nq_gemm_onebit, nq_gemm_nanoquant_workspace_bytes(M, n, r_pad, m) bytes
+ *   (the larger need of the two stages, which use it one after the other).
  * Replaces marlin_nanoquant_forward (src/nanoquant/kernel/cuda/gemm.cpp:112-122,
  * registered at pybind.cpp:99-104,114). */
+size_t nq_gemm_nanoquant_workspace_bytes(int64_t M, int64_t n, int64_t r_pad, int64_t m);
 int nq_gemm_nanoquant(int dtype, const void* A, const uint32_t* v_bits, const uint32_t* u_bits,
                       const void* s_g, const void* s_l, const void* s_h, void* imm, void* C, int64_t M,
-                      int64_t n, int64_t r_pad, int64_t m, nq_stream_t stream);
+                      int64_t n, int64_t r_pad, int64_t m, void* workspace, size_t workspace_bytes,
+                      nq_stream_t stream);
 
 /* ---------------------------------------------------------------- decode attention */
 

@@ -188,6 +188,13 @@ def _onebit_device_checks(x, weight, scale_g, scale_h):
             _check(s.dim() == 1, f"{name} must be 1-D")
 
 
+def _split_workspace(device, nbytes):
+    """Scratch for the GEMM's split-K partial sums (None when the shape does not split)."""
+    if nbytes == 0:
+        return None
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+
 def marlin_onebit_forward_cuda(x, weight, scale_g, scale_h, workspace):
     """Device implementation of ``marlin_onebit_forward`` (gemm.cpp:59-98)."""
     prob_m, prob_n, prob_k = _onebit_check_and_shape(x, weight, scale_g, scale_h, workspace)
@@ -196,10 +203,13 @@ def marlin_onebit_forward_cuda(x, weight, scale_g, scale_h, workspace):
     if prob_m == 0 or prob_n == 0:
         return C
     lib = _lib.load()
+    # fp32 partial sums when the library splits K across blocks (small grids); the caching
+    # allocator makes this stream-ordered scratch
+    split = _split_workspace(x.device, lib.nq_gemm_onebit_workspace_bytes(prob_m, prob_k, prob_n))
     with torch.cuda.device(x.device):
         status = lib.nq_gemm_onebit(_lib.dtype_code(x.dtype), x.data_ptr(), weight.data_ptr(), _lib.ptr(scale_g),
-                                    _lib.ptr(scale_h), C.data_ptr(), prob_m, prob_k, prob_n,
-                                    _lib.stream_of(x.device))
+                                    _lib.ptr(scale_h), C.data_ptr(), prob_m, prob_k, prob_n, _lib.ptr(split),
+                                    0 if split is None else split.numel(), _lib.stream_of(x.device))
     _lib.check(status, "marlin_onebit_forward")
     return C
 
@@ -226,10 +236,12 @@ def marlin_nanoquant_forward_cuda(x, weight_u, weight_v, scale_g, scale_l, scale
     if prob_m == 0 or m == 0:
         return y
     lib = _lib.load()
+    split = _split_workspace(x.device, lib.nq_gemm_nanoquant_workspace_bytes(prob_m, n, r_pad, m))
     with torch.cuda.device(x.device):
         status = lib.nq_gemm_nanoquant(_lib.dtype_code(x.dtype), x.data_ptr(), weight_u.data_ptr(),
                                        weight_v.data_ptr(), _lib.ptr(scale_g), _lib.ptr(scale_l),
                                        _lib.ptr(scale_h), imm.data_ptr(), y.data_ptr(), prob_m, n, r_pad, m,
+                                       _lib.ptr(split), 0 if split is None else split.numel(),
                                        _lib.stream_of(x.device))
     _lib.check(status, "marlin_nanoquant_forward")
     return y

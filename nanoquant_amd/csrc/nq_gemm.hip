@@ -18,6 +18,8 @@
 // 16t + 8 + 4g' + {0..3}: two 8-byte LDS reads.
 //
 // Block tile 128 x 128, 4 waves (2 x 2), wave tile 64 x 64 = 4 x 4 MFMA tiles, K step 32.
+#include <algorithm>
+
 #include "nq_common.h"
 
 namespace nq {
@@ -199,7 +201,9 @@ int launch_onebit(const void* A, const uint32_t* W, const void* s_in, const void
 // that ends a step each wave waits for its own DMAs of the next step.
 // With KS = 2 the block holds two groups of waves with buffers of their own, each over half of
 // the k steps (for outputs too few to give every SIMD two waves); group 1 hands its accumulators
-// to group 0 through LDS at the end.
+// to group 0 through LDS at the end. With kSplit the grid repeats the tiles once per k range of
+// split_steps steps, and each block stores its raw fp32 sums to its plane of `part`
+// [splits][M][N]; gemm_split_finish_kernel adds the planes in order and applies the epilogue.
 template <int N>
 __device__ inline void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt has 6 bits");
@@ -217,11 +221,12 @@ __device__ inline void dma_to_lds4(const void* src, void* lds) {
                                      (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
 }
 
-template <typename T, bool kSin, bool kSout, int BP, int BQ, int WP, int WQ, int WPE, int KS>
+template <typename T, bool kSin, bool kSout, int BP, int BQ, int WP, int WQ, int WPE, int KS, bool kSplit>
 __global__ __launch_bounds__((BP / WP) * (BQ / WQ) * 64 * KS) __attribute__((amdgpu_waves_per_eu(WPE)))
 void gemm_dm_kernel(
     const uint16_t* __restrict__ A, const uint32_t* __restrict__ W, const uint16_t* __restrict__ s_in,
-    const uint16_t* __restrict__ s_out, uint16_t* __restrict__ C, int M, int K, int N, int q_tiles) {
+    const uint16_t* __restrict__ s_out, uint16_t* __restrict__ C, int M, int K, int N, int q_tiles, int p_tiles,
+    float* __restrict__ part, int split_steps) {
     constexpr int BKK = 64;
     constexpr int NWP = BP / WP;
     constexpr int NWQ = BQ / WQ;
@@ -241,6 +246,7 @@ void gemm_dm_kernel(
     static_assert(XCH % NTG == 0 && WWORDS % NTG == 0, "tile pieces must divide evenly");
     static_assert(WP % 64 == 0 && BP % 64 == 0, "features come in whole 64-feature word groups");
     static_assert(KS == 1 || KS == 2, "one or two k groups");
+    static_assert(!kSplit || (KS == 1 && !kSout), "a k range of the grid is one wave group, scaled later");
     __shared__ __attribute__((aligned(16))) uint16_t xs0[KS][BQ * BKK], xs1[KS][BQ * BKK], xs2[KS][BQ * BKK];
     __shared__ __attribute__((aligned(16))) uint32_t ws0[KS][WWORDS], ws1[KS][WWORDS], ws2[KS][WWORDS];
     __shared__ __attribute__((aligned(16))) uint32_t ss0[kSin ? NT : 4], ss1[kSin ? NT : 4], ss2[kSin ? NT : 4];
@@ -257,13 +263,17 @@ void gemm_dm_kernel(
     const int kg = lane >> 5;
     const int wp = gw % NWP;
     const int wq = gw / NWP;
-    const int qt = blockIdx.x % q_tiles;
-    const int pt = blockIdx.x / q_tiles;
+    const int split = kSplit ? static_cast<int>(blockIdx.x) / (q_tiles * p_tiles) : 0;
+    const int tile = static_cast<int>(blockIdx.x) - split * (q_tiles * p_tiles);
+    const int qt = tile % q_tiles;
+    const int pt = tile / q_tiles;
     const int q0 = qt * BQ;
     const int p0 = pt * BP;
     const uint32_t half_n = static_cast<uint32_t>(N) >> 1;
-    const int k_iters = K / BKK / KS;  // steps of each k group (the host makes K / 64 divide by KS)
-    const int k_first = grp * k_iters;
+    // steps of this block's k group or k range (the host makes K / 64 divide by KS and leaves no
+    // k range empty), and the first of them
+    const int k_iters = kSplit ? min(split_steps, K / BKK - split * split_steps) : K / BKK / KS;
+    const int k_first = kSplit ? split * split_steps : grp * k_iters;
 
     // lane constants: the first of the four words of its feature per 64-feature group, the shift
     // per 32-feature tile, its A-tile rows and the swizzled chunk of its 8 k per k tile
@@ -404,6 +414,24 @@ void gemm_dm_kernel(
                 for (int i = 0; i < 16; ++i) acc[tp][tq][i] += red[((tp * TQ + tq) * 16 + i) * NTG + tg];
     }
 
+    if (kSplit) {  // raw sums of this k range, four consecutive features per 16-byte store
+        float* plane = part + static_cast<size_t>(split) * static_cast<size_t>(M) * static_cast<size_t>(N);
+#pragma unroll
+        for (int tp = 0; tp < TP; ++tp)
+#pragma unroll
+            for (int tq = 0; tq < TQ; ++tq) {
+                const int q = q0 + wq * WQ + 32 * tq + c;
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4) {
+                    const int o = p0 + wp * WP + 32 * tp + 8 * g4 + 4 * kg;
+                    if (q < M && o < N)
+                        *reinterpret_cast<f32x4*>(plane + static_cast<size_t>(q) * N + o) =
+                            f32x4{acc[tp][tq][4 * g4], acc[tp][tq][4 * g4 + 1], acc[tp][tq][4 * g4 + 2],
+                                  acc[tp][tq][4 * g4 + 3]};
+                }
+            }
+        return;
+    }
     // epilogue: scale, saturate, four consecutive features per 8-byte store
 #pragma unroll
     for (int tp = 0; tp < TP; ++tp)
@@ -443,34 +471,141 @@ void launch_dm(const void* A, const uint32_t* W, const void* s_in, const void* s
     auto* c = static_cast<uint16_t*>(C);
     const int m = static_cast<int>(M), k = static_cast<int>(K), n = static_cast<int>(N);
     if (s_in && s_out)
-        gemm_dm_kernel<T, true, true, BP, BQ, WP, WQ, WPE, KS><<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles);
+        gemm_dm_kernel<T, true, true, BP, BQ, WP, WQ, WPE, KS, false>
+            <<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles, p_tiles, nullptr, 0);
     else if (s_in)
-        gemm_dm_kernel<T, true, false, BP, BQ, WP, WQ, WPE, KS><<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles);
+        gemm_dm_kernel<T, true, false, BP, BQ, WP, WQ, WPE, KS, false>
+            <<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles, p_tiles, nullptr, 0);
     else if (s_out)
-        gemm_dm_kernel<T, false, true, BP, BQ, WP, WQ, WPE, KS><<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles);
+        gemm_dm_kernel<T, false, true, BP, BQ, WP, WQ, WPE, KS, false>
+            <<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles, p_tiles, nullptr, 0);
     else
-        gemm_dm_kernel<T, false, false, BP, BQ, WP, WQ, WPE, KS><<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n,
-                                                                                       q_tiles);
+        gemm_dm_kernel<T, false, false, BP, BQ, WP, WQ, WPE, KS, false>
+            <<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles, p_tiles, nullptr, 0);
 }
 
-// The 32x32x16 kernel needs whole 64-k iterations, 8-byte output stores and 32-bit element
-// offsets into A and the words; anything else runs on the 16x16x32 kernel. Block tile 256
-// features x 64 rows, four waves of 64 x 64: at B = 2048 on the Llama-2-7B shapes this beat
-// 128 x 128, 256 x 128 (waves of 64 x 128 or 128 x 64) and 256 x 128 with one 128 x 128 wave per
-// SIMD, whose 1376 wave tiles leave a third of the second round of the chip idle. A grid of
-// fewer than two blocks per CU (e.g. the rank-wide first stage, N = r) splits K over two wave
-// groups per block instead (B = 2048, K = 4096, N = 1792: 46 -> 38 us).
+// C[q, o] = sat(s_out[o] * sum_s part[s][q][o]) (the planes added in order); one thread per four
+// consecutive outputs.
+template <typename T, bool kSout>
+__global__ __launch_bounds__(256) void gemm_split_finish_kernel(const float* __restrict__ part,
+                                                                const uint16_t* __restrict__ s_out,
+                                                                uint16_t* __restrict__ C, int M, int N, int splits) {
+    const int64_t quads = static_cast<int64_t>(M) * (N / 4);
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= quads) return;
+    const int64_t q = i / (N / 4);
+    const int o = static_cast<int>(i - q * (N / 4)) * 4;
+    const size_t plane = static_cast<size_t>(M) * static_cast<size_t>(N);
+    const float* src = part + static_cast<size_t>(q) * N + o;
+    f32x4 sum = *reinterpret_cast<const f32x4*>(src);
+    for (int s = 1; s < splits; ++s) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(src + s * plane);
+        sum = f32x4{sum[0] + v[0], sum[1] + v[1], sum[2] + v[2], sum[3] + v[3]};
+    }
+    uint16_t h[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float sc = kSout ? T::to_float(s_out[perm_out(o + e)]) : 1.0f;
+        h[e] = saturate_to<T>(sum[e] * sc, T::SAT_GEMM);
+    }
+    uint2 v;
+    v.x = static_cast<uint32_t>(h[0]) | (static_cast<uint32_t>(h[1]) << 16);
+    v.y = static_cast<uint32_t>(h[2]) | (static_cast<uint32_t>(h[3]) << 16);
+    *reinterpret_cast<uint2*>(C + static_cast<size_t>(q) * N + o) = v;
+}
+
+// K split over `splits` ranges of the grid: the ranges' raw sums into part [splits][M][N] fp32,
+// then the finishing launch.
+template <typename T, int BP, int BQ, int WP, int WQ, int WPE>
+void launch_dm_split(const void* A, const uint32_t* W, const void* s_in, const void* s_out, void* C, int64_t M,
+                     int64_t K, int64_t N, float* part, int splits, int split_steps, hipStream_t stream) {
+    const int q_tiles = static_cast<int>(ceil_div(M, BQ));
+    const int p_tiles = static_cast<int>(ceil_div(N, BP));
+    const dim3 grid(static_cast<unsigned>(q_tiles * p_tiles * splits));
+    constexpr int NT = (BP / WP) * (BQ / WQ) * 64;
+    const auto* a = static_cast<const uint16_t*>(A);
+    const auto* si = static_cast<const uint16_t*>(s_in);
+    const auto* so = static_cast<const uint16_t*>(s_out);
+    auto* c = static_cast<uint16_t*>(C);
+    const int m = static_cast<int>(M), k = static_cast<int>(K), n = static_cast<int>(N);
+    if (s_in)
+        gemm_dm_kernel<T, true, false, BP, BQ, WP, WQ, WPE, 1, true>
+            <<<grid, NT, 0, stream>>>(a, W, si, nullptr, c, m, k, n, q_tiles, p_tiles, part, split_steps);
+    else
+        gemm_dm_kernel<T, false, false, BP, BQ, WP, WQ, WPE, 1, true>
+            <<<grid, NT, 0, stream>>>(a, W, nullptr, nullptr, c, m, k, n, q_tiles, p_tiles, part, split_steps);
+    const int64_t quads = M * (N / 4);
+    const dim3 fgrid(static_cast<unsigned>(ceil_div(quads, 256)));
+    if (s_out)
+        gemm_split_finish_kernel<T, true><<<fgrid, 256, 0, stream>>>(part, so, c, m, n, splits);
+    else
+        gemm_split_finish_kernel<T, false><<<fgrid, 256, 0, stream>>>(part, so, c, m, n, splits);
+}
+
+// How one GEMM is launched. The 32x32x16 kernel needs whole 64-k steps, 8-byte output stores
+// and 32-bit element offsets into A and the words; anything else runs on the 16x16x32 kernel.
+// Block tile 256 features x 64 rows, four waves of 64 x 64: at B = 2048 on the Llama-2-7B shapes
+// this beat 128 x 128, 256 x 128 (waves of 64 x 128 or 128 x 64) and 256 x 128 with one 128 x 128
+// wave per SIMD, whose 1376 wave tiles leave a third of the second round of the chip idle. The
+// grid decides the rest:
+//   >= 512 tiles (two per CU): one block per tile;
+//   128-511 tiles: K split over two wave groups inside each block (B = 2048, K = 4096,
+//     N = 1792: 46 -> 38 us);
+//   fewer (B = 256 and the rank-wide stages): K split over up to 512 / tiles ranges of at least
+//     8 steps across the grid, fp32 sums into the caller's workspace, then a finishing launch;
+//     without that workspace, as above. (Against 512 / 4 and 256 / 8 over the B = 256 shapes of
+//     Llama-2-7B and Llama-3-70B, 512 / 8 was best or within 3% everywhere; 7B down at 0.55 bpw:
+//     97 us unsplit, 48 us split.)
+constexpr int64_t kSplitTarget = 512;  // blocks a split grid aims at (two per CU)
+constexpr int64_t kSplitMinSteps = 8;  // 64-k steps of the shortest range
+enum GemmMode { kModeOnebit, kModeTile, kModeGroups, kModeSplit };
+struct GemmPlan {
+    GemmMode mode = kModeOnebit;
+    int splits = 1;
+    int split_steps = 0;
+    size_t workspace_bytes = 0;  // needed by kModeSplit
+};
+
+GemmPlan plan_gemm(int64_t M, int64_t K, int64_t N) {
+    GemmPlan p;
+    if (K % 64 || K <= 0 || M * K >= ((int64_t)1 << 31) || (K / 16) * (N / 2) >= ((int64_t)1 << 31)) return p;
+    const int64_t tiles = ceil_div(M, 64) * ceil_div(N, 256);
+    const int64_t steps = K / 64;
+    p.mode = kModeTile;
+    if (tiles >= 2 * 256) return p;
+    if (steps % 2 == 0) p.mode = kModeGroups;
+    if (tiles >= 128) return p;
+    const int64_t want = std::min<int64_t>(ceil_div(kSplitTarget, tiles), steps / kSplitMinSteps);
+    if (want < 2) return p;
+    p.split_steps = static_cast<int>(ceil_div(steps, want));
+    p.splits = static_cast<int>(ceil_div(steps, p.split_steps));  // every range non-empty
+    if (p.splits < 2) return p;
+    p.mode = kModeSplit;
+    p.workspace_bytes = static_cast<size_t>(p.splits) * static_cast<size_t>(M) * static_cast<size_t>(N) * 4;
+    return p;
+}
+
 template <typename T>
 int launch_gemm(const char* name, const void* A, const uint32_t* W, const void* s_in, const void* s_out, void* C,
-                int64_t M, int64_t K, int64_t N, hipStream_t stream) {
-    const bool dm = K % 64 == 0 && K > 0 && aligned(C, 8) && M * K < ((int64_t)1 << 31) &&
-                    (K / 16) * (N / 2) < ((int64_t)1 << 31);
-    if (!dm) return launch_onebit<T>(A, W, s_in, s_out, C, M, K, N, stream);
-    const int64_t blocks = ceil_div(M, 64) * ceil_div(N, 256);
-    if (blocks < 2 * 256 && (K / 64) % 2 == 0)
-        launch_dm<T, 256, 64, 64, 64, 2, 2>(A, W, s_in, s_out, C, M, K, N, stream);
-    else
-        launch_dm<T, 256, 64, 64, 64, 2, 1>(A, W, s_in, s_out, C, M, K, N, stream);
+                int64_t M, int64_t K, int64_t N, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    GemmPlan p = plan_gemm(M, K, N);
+    if (p.mode != kModeOnebit && !aligned(C, 8)) p.mode = kModeOnebit;
+    if (p.mode == kModeSplit && (!workspace || workspace_bytes < p.workspace_bytes || !aligned(workspace, 16)))
+        p.mode = (K / 64) % 2 == 0 ? kModeGroups : kModeTile;
+    switch (p.mode) {
+        case kModeOnebit:
+            return launch_onebit<T>(A, W, s_in, s_out, C, M, K, N, stream);
+        case kModeTile:
+            launch_dm<T, 256, 64, 64, 64, 2, 1>(A, W, s_in, s_out, C, M, K, N, stream);
+            break;
+        case kModeGroups:
+            launch_dm<T, 256, 64, 64, 64, 2, 2>(A, W, s_in, s_out, C, M, K, N, stream);
+            break;
+        case kModeSplit:
+            launch_dm_split<T, 256, 64, 64, 64, 2>(A, W, s_in, s_out, C, M, K, N, static_cast<float*>(workspace),
+                                                   p.splits, p.split_steps, stream);
+            break;
+    }
     return check_launch(name);
 }
 
@@ -498,30 +633,45 @@ using namespace nq;
 
 extern "C" {
 
+size_t nq_gemm_onebit_workspace_bytes(int64_t M, int64_t K, int64_t N) {
+    if (M <= 0 || K <= 0 || N <= 0) return 0;
+    return plan_gemm(M, K, N).workspace_bytes;
+}
+
 int nq_gemm_onebit(int dtype, const void* A, const uint32_t* w_bits, const void* s_in, const void* s_out, void* C,
-                   int64_t M, int64_t K, int64_t N, nq_stream_t stream) {
+                   int64_t M, int64_t K, int64_t N, void* workspace, size_t workspace_bytes, nq_stream_t stream) {
     if (int s = check_onebit("nq_gemm_onebit", dtype, A, w_bits, s_in, s_out, C, M, K, N)) return s;
     if (M == 0 || N == 0) return NQ_OK;
     hipStream_t st = as_stream(stream);
-    if (dtype == NQ_F16) return launch_gemm<F16>("nq_gemm_onebit", A, w_bits, s_in, s_out, C, M, K, N, st);
-    return launch_gemm<BF16>("nq_gemm_onebit", A, w_bits, s_in, s_out, C, M, K, N, st);
+    if (dtype == NQ_F16)
+        return launch_gemm<F16>("nq_gemm_onebit", A, w_bits, s_in, s_out, C, M, K, N, workspace, workspace_bytes, st);
+    return launch_gemm<BF16>("nq_gemm_onebit", A, w_bits, s_in, s_out, C, M, K, N, workspace, workspace_bytes, st);
+}
+
+size_t nq_gemm_nanoquant_workspace_bytes(int64_t M, int64_t n, int64_t r_pad, int64_t m) {
+    if (M <= 0 || n <= 0 || r_pad <= 0 || m <= 0) return 0;
+    return std::max(plan_gemm(M, n, r_pad).workspace_bytes, plan_gemm(M, r_pad, m).workspace_bytes);
 }
 
 int nq_gemm_nanoquant(int dtype, const void* A, const uint32_t* v_bits, const uint32_t* u_bits, const void* s_g,
                       const void* s_l, const void* s_h, void* imm, void* C, int64_t M, int64_t n, int64_t r_pad,
-                      int64_t m, nq_stream_t stream) {
+                      int64_t m, void* workspace, size_t workspace_bytes, nq_stream_t stream) {
     if (int s = check_onebit("nq_gemm_nanoquant stage 1", dtype, A, v_bits, s_g, s_l, imm, M, n, r_pad)) return s;
     if (int s = check_onebit("nq_gemm_nanoquant stage 2", dtype, imm, u_bits, nullptr, s_h, C, M, r_pad, m)) return s;
     if (M == 0 || m == 0) return NQ_OK;
     hipStream_t st = as_stream(stream);
+    const char* n1 = "nq_gemm_nanoquant stage 1";
+    const char* n2 = "nq_gemm_nanoquant stage 2";
     if (r_pad > 0) {
         const int s1 = dtype == NQ_F16
-                           ? launch_gemm<F16>("nq_gemm_nanoquant stage 1", A, v_bits, s_g, s_l, imm, M, n, r_pad, st)
-                           : launch_gemm<BF16>("nq_gemm_nanoquant stage 1", A, v_bits, s_g, s_l, imm, M, n, r_pad, st);
+                           ? launch_gemm<F16>(n1, A, v_bits, s_g, s_l, imm, M, n, r_pad, workspace, workspace_bytes, st)
+                           : launch_gemm<BF16>(n1, A, v_bits, s_g, s_l, imm, M, n, r_pad, workspace, workspace_bytes, st);
         if (s1) return s1;
     }
-    return dtype == NQ_F16 ? launch_gemm<F16>("nq_gemm_nanoquant stage 2", imm, u_bits, nullptr, s_h, C, M, r_pad, m, st)
-                           : launch_gemm<BF16>("nq_gemm_nanoquant stage 2", imm, u_bits, nullptr, s_h, C, M, r_pad, m, st);
+    // stage 2 reuses the workspace: the finishing launch of stage 1 has read it by then (same stream)
+    return dtype == NQ_F16
+               ? launch_gemm<F16>(n2, imm, u_bits, nullptr, s_h, C, M, r_pad, m, workspace, workspace_bytes, st)
+               : launch_gemm<BF16>(n2, imm, u_bits, nullptr, s_h, C, M, r_pad, m, workspace, workspace_bytes, st);
 }
 
 }  // extern "C"

@@ -316,6 +316,35 @@ def test_gemm_onebit_scale_variants(nq, scales, K):
     assert err <= 1e-3, err
 
 
+@pytest.mark.parametrize("B,K,N", [(256, 4096, 1280), (100, 11008, 512)], ids=["b256_k4096", "b100_k11008"])
+def test_gemm_split_k(nq, B, K, N):
+    """Small grids split K across blocks (fp32 planes in the workspace the op allocates, added
+    by a finishing launch); the same call through the C ABI without a workspace runs unsplit.
+    Both within 1e-3 of float64."""
+    from nanoquant_amd import _lib
+    lib = _lib.load()
+    announce("gemm split-k", B, K, N, lib.nq_gemm_onebit_workspace_bytes(B, K, N))
+    assert lib.nq_gemm_onebit_workspace_bytes(B, K, N) > 0
+    rng = np.random.default_rng(9)
+    w = np.where(rng.random((N, K)) < 0.5, -1, 1).astype(np.int8)
+    s_in = np.abs(rng.normal(1, 0.2, K)).astype(np.float16)
+    s_out = (np.abs(rng.normal(1, 0.2, N)) / 16).astype(np.float16)
+    x = rng.normal(size=(B, K)).astype(np.float16)
+    words, p_in, p_out, ws_size = nq.pack_binary_marlin(dev_t(w), dev_t(s_in), dev_t(s_out))
+    ws = torch.zeros(max(ws_size, 32), dtype=torch.int32, device="cuda")
+    xd = dev_t(x)
+    y_split = torch.ops.binary_kernels.marlin_onebit_forward(xd, words, p_in, p_out, ws)
+    y_plain = torch.empty_like(y_split)
+    status = lib.nq_gemm_onebit(_lib.NQ_F16, xd.data_ptr(), words.data_ptr(), p_in.data_ptr(), p_out.data_ptr(),
+                                y_plain.data_ptr(), B, K, N, None, 0, _lib.stream_of(xd.device))
+    assert status == 0
+    torch.cuda.synchronize()
+    y64 = ((x.astype(np.float64) * s_in.astype(np.float64)) @ w.T.astype(np.float64)) * s_out.astype(np.float64)
+    for y in (y_split, y_plain):
+        err, _ = rel_err(y, y64, "gemm", torch.float16)
+        assert err <= 1e-3, err
+
+
 # --------------------------------------------------------------------------- Llama-3-70B shapes
 
 def mixed_rank(base: int, seed: int) -> int:

@@ -44,8 +44,8 @@ def test_c_abi_argument_errors_need_no_gpu():
     # rejected before any launch: unknown bit order, bad shapes, bad dtype
     assert lib.nq_pack_signs(None, None, 4, 32, 7, None) == _lib.NQ_ERR_INVALID_ARGUMENT
     assert lib.nq_pack_marlin(None, None, 63, 16, None) == _lib.NQ_ERR_SHAPE
-    assert lib.nq_gemm_onebit(9, None, None, None, None, None, 1, 16, 64, None) == _lib.NQ_ERR_DTYPE
-    assert lib.nq_gemm_onebit(0, None, None, None, None, None, 1, 24, 64, None) == _lib.NQ_ERR_SHAPE
+    assert lib.nq_gemm_onebit(9, None, None, None, None, None, 1, 16, 64, None, 0, None) == _lib.NQ_ERR_DTYPE
+    assert lib.nq_gemm_onebit(0, None, None, None, None, None, 1, 24, 64, None, 0, None) == _lib.NQ_ERR_SHAPE
     assert lib.nq_gemv(0, None, None, None, None, None, None, None, 1, 64, 32, 64, None, 0, None) == \
         _lib.NQ_ERR_INVALID_ARGUMENT
     assert b"null pointer" in lib.nq_last_error_message()
@@ -212,3 +212,23 @@ def test_module_inference_init_and_gemlite_refusal():
 def test_package_exports():
     assert nanoquant_amd.binary_packer is ku.pack_binary_gemv
     assert nanoquant_amd.marlin_nanoquant_packer is ku.pack_binary_marlin_fused
+
+
+def test_gemm_split_workspace_sizes():
+    """The GEMM asks for split-K scratch only where its grid is small, and then for one fp32
+    plane of the output per k range, each range at least 8 of the 64-k steps."""
+    lib = _lib.load()
+    # large grids and K % 64 != 0 never split
+    assert lib.nq_gemm_onebit_workspace_bytes(2048, 1792, 11008) == 0
+    assert lib.nq_gemm_onebit_workspace_bytes(2048, 4096, 1792) == 0
+    assert lib.nq_gemm_onebit_workspace_bytes(256, 4096 + 16, 1280) == 0
+    assert lib.nq_gemm_onebit_workspace_bytes(0, 4096, 1280) == 0
+    # B=256, K=4096, N=1280: 20 tiles of 64 x 256, 64 steps -> 8 ranges of 8 steps
+    assert lib.nq_gemm_onebit_workspace_bytes(256, 4096, 1280) == 8 * 256 * 1280 * 4
+    # B=256, K=11008 (172 steps), N=1792: 28 tiles -> ceil(512 / 28) = 19 ranges of ceil(172 / 19) = 10 steps,
+    # so 18 ranges cover the steps
+    assert lib.nq_gemm_onebit_workspace_bytes(256, 11008, 1792) == 18 * 256 * 1792 * 4
+    # two stages share the workspace: the larger need
+    s1 = lib.nq_gemm_onebit_workspace_bytes(256, 11008, 1792)
+    s2 = lib.nq_gemm_onebit_workspace_bytes(256, 1792, 4096)
+    assert lib.nq_gemm_nanoquant_workspace_bytes(256, 11008, 1792, 4096) == max(s1, s2) > 0
