@@ -81,6 +81,16 @@ int nq_pack_marlin(const int8_t* weight, uint32_t* dst, int64_t O, int64_t K, nq
  * counterpart, used to check and to read packed GEMM weights back). */
 int nq_unpack_marlin(const uint32_t* words, int8_t* weight, int64_t O, int64_t K, nq_stream_t stream);
 
+/* Sign words of a {-1,+1} [O, K] matrix (`method` order, ceil(K/32) words a row, as a
+ * checkpoint stores V [r, n] and U [m, r]) -> Marlin words uint32 [K_pad/16, O_pad/2] of the
+ * matrix padded with +1 to [O_pad, K_pad] (O_pad % 64 == 0, K_pad % 16 == 0); bits past K in
+ * `src` are ignored. No reference counterpart as one call: replaces binary_unpacker at load
+ * (utils/load_utils.py:392) followed by the sign part of pack_binary_marlin_fused
+ * (src/nanoquant/kernel/utils.py:262-277, rank padding included) in _prepare_kernel
+ * (modules/linear.py:226-232). */
+int nq_repack_marlin(const uint32_t* src, int64_t O, int64_t K, int method, uint32_t* dst, int64_t O_pad,
+                     int64_t K_pad, nq_stream_t stream);
+
 /* Scale permutations of pack_binary_marlin (src/nanoquant/kernel/utils.py:206-209), on
  * 16-bit elements: in  [K] -> out [K], natural 16c+8a+2b+d -> 16c+4b+2a+d (K % 16 == 0);
  *                  out [O] -> out [O], natural 32c+8a+2b+d -> 32c+8b+2a+d (O % 32 == 0).

@@ -60,6 +60,7 @@ SIGNATURES = {
     "nq_repack_signs": (_int, [_vp, _vp, _i64, _i64, _int, _int, _vp]),
     "nq_pack_marlin": (_int, [_vp, _vp, _i64, _i64, _vp]),
     "nq_unpack_marlin": (_int, [_vp, _vp, _i64, _i64, _vp]),
+    "nq_repack_marlin": (_int, [_vp, _i64, _i64, _int, _vp, _i64, _i64, _vp]),
     "nq_permute_marlin_scales": (_int, [_vp, _vp, _i64, _vp, _vp, _i64, _vp]),
     "nq_gemv_workspace_bytes": (_size, [_i64, _i64, _i64, _i64]),
     "nq_gemv": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _size, _vp]),

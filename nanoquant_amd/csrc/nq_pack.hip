@@ -162,6 +162,48 @@ __global__ __launch_bounds__(kThreads) void pack_marlin_kernel(const int8_t* __r
     dst[t] = word;
 }
 
+// Marlin words [K_pad/16, O_pad/2] straight from the sign words of a [O, K] matrix (lsb_first
+// or half2, ceil(K/32) words a row), as a checkpoint stores V [r, n] and U [m, r]; elements past
+// O or K are +1 (bit 0). Each output word's four k lie in one 16-k group, so in one source word
+// per row.
+__global__ __launch_bounds__(kThreads) void repack_marlin_kernel(const uint32_t* __restrict__ src, int64_t O,
+                                                                 int64_t K, int64_t words, int method,
+                                                                 uint32_t* __restrict__ dst, int64_t O_pad,
+                                                                 int64_t K_pad) {
+    const int64_t half_o = O_pad / 2;
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (t >= (K_pad / 16) * half_o) return;
+    const int64_t tr = t / half_o;
+    const int64_t col = t - tr * half_o;
+    const int64_t tile_out = col / 32;
+    const int o1 = static_cast<int>((col % 32) / 4);
+    const int r2 = static_cast<int>(col % 4);
+    const int64_t k0 = tr * 16 + r2 * 2;  // the word's k: k0 + 8*r8 + r1
+    uint32_t word = 0;
+    if (k0 < K) {
+        const int64_t kw = k0 / 32;
+#pragma unroll
+        for (int o16 = 0; o16 < 4; ++o16) {
+#pragma unroll
+            for (int o8 = 0; o8 < 2; ++o8) {
+                const int64_t o = tile_out * 64 + o16 * 16 + o8 * 8 + o1;
+                if (o >= O) continue;
+                const uint32_t L = from_method(src[o * words + kw], method);
+#pragma unroll
+                for (int r8 = 0; r8 < 2; ++r8) {
+#pragma unroll
+                    for (int r1 = 0; r1 < 2; ++r1) {
+                        const int64_t k = k0 + 8 * r8 + r1;
+                        const uint32_t neg = k < K ? (L >> (k % 32)) & 1u : 0u;
+                        word |= neg << (15 - (2 * o8 + r8) - 4 * o16 + 16 * r1);
+                    }
+                }
+            }
+        }
+    }
+    dst[t] = word;
+}
+
 __global__ __launch_bounds__(kThreads) void unpack_marlin_kernel(const uint32_t* __restrict__ src,
                                                                  int8_t* __restrict__ w, int64_t O, int64_t K) {
     const int64_t half_o = O / 2;
@@ -274,6 +316,21 @@ int nq_pack_marlin(const int8_t* weight, uint32_t* dst, int64_t O, int64_t K, nq
     if (!aligned(weight, 2)) return fail(NQ_ERR_ALIGNMENT, "nq_pack_marlin: weight must be 2-byte aligned");
     pack_marlin_kernel<<<grid_for((K / 16) * (O / 2)), kThreads, 0, as_stream(stream)>>>(weight, dst, O, K);
     return check_launch("nq_pack_marlin");
+}
+
+int nq_repack_marlin(const uint32_t* src, int64_t O, int64_t K, int method, uint32_t* dst, int64_t O_pad,
+                     int64_t K_pad, nq_stream_t stream) {
+    if (int s = check_method(method, "nq_repack_marlin")) return s;
+    if (O < 0 || K < 0 || O_pad < O || K_pad < K)
+        return fail(NQ_ERR_INVALID_ARGUMENT, "nq_repack_marlin: need 0 <= O <= O_pad and 0 <= K <= K_pad");
+    if (O_pad % 64 || K_pad % 16)
+        return fail(NQ_ERR_SHAPE, "nq_repack_marlin: need O_pad %% 64 == 0 and K_pad %% 16 == 0, got O_pad=%lld K_pad=%lld",
+                    (long long)O_pad, (long long)K_pad);
+    if (O_pad == 0 || K_pad == 0) return NQ_OK;
+    if (!dst || (O > 0 && K > 0 && !src)) return fail(NQ_ERR_INVALID_ARGUMENT, "nq_repack_marlin: null pointer");
+    repack_marlin_kernel<<<grid_for((K_pad / 16) * (O_pad / 2)), kThreads, 0, as_stream(stream)>>>(
+        src, O, K, ceil_div(K, 32), method, dst, O_pad, K_pad);
+    return check_launch("nq_repack_marlin");
 }
 
 int nq_unpack_marlin(const uint32_t* words, int8_t* weight, int64_t O, int64_t K, nq_stream_t stream) {

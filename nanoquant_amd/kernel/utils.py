@@ -208,6 +208,79 @@ def pack_binary_marlin_fused(V_sign: torch.Tensor, U_sign: torch.Tensor, scale_g
     return V_bits.contiguous(), U_bits.contiguous(), scale_g_marlin, scale_l_marlin, scale_h_marlin, workspace
 
 
+def repack_binary_marlin(packed_tensor: torch.Tensor, original_shape: Tuple[int, int],
+                         padded_shape: Tuple[int, int] | None = None, src_method: str = "lsb_first") -> torch.Tensor:
+    """Marlin words of a {-1,+1} [O, K] matrix given as its packed sign words.
+
+    ``packed_tensor`` holds ``original_shape`` = (O, K) in ``src_method`` order, (O, ceil(K/32))
+    words, as a checkpoint stores V [r, n] and U [m, r] (linear.py:359-376). The matrix is padded
+    with +1 to ``padded_shape`` (default: unpadded; O_pad % 64 == 0, K_pad % 16 == 0) and returned
+    as int32 words [K_pad/16, O_pad/2], the words ``pack_binary_marlin`` makes from the dense
+    padded matrix, in one pass on the GPU.
+    """
+    if packed_tensor.dim() != 2:
+        raise ValueError(f"Unsupported packed tensor format. Expected 2D tensor, got {packed_tensor.dim()} dimensions.")
+    O, K = (int(s) for s in original_shape)
+    O_pad, K_pad = (O, K) if padded_shape is None else (int(s) for s in padded_shape)
+    if tuple(packed_tensor.shape) != (O, (K + 31) // 32):
+        raise ValueError(f"Unsupported packed tensor shape. Expected ({O}, {(K + 31) // 32}), "
+                         f"got {packed_tensor.shape}.")
+    if packed_tensor.dtype not in (torch.int32, torch.uint32):
+        raise TypeError(f"packed words must be int32, got {packed_tensor.dtype}")
+    if O_pad < O or K_pad < K or O_pad % 64 or K_pad % 16:
+        raise RuntimeError(f"padded shape ({O_pad}, {K_pad}) must cover ({O}, {K}) with O % 64 == 0 and K % 16 == 0")
+    code = _method_code(src_method)
+    src = _on_gpu(packed_tensor)
+    words = torch.empty((K_pad // 16, O_pad // 2), dtype=torch.int32, device=src.device)
+    if words.numel():
+        lib = _lib.load()
+        with torch.cuda.device(src.device):
+            status = lib.nq_repack_marlin(src.data_ptr(), O, K, code, words.data_ptr(), O_pad, K_pad,
+                                          _lib.stream_of(src.device))
+        _lib.check(status, "repack_binary_marlin")
+    return words if packed_tensor.is_cuda else words.to(packed_tensor.device)
+
+
+def marlin_rank(rank: int) -> int:
+    """The rank the fused Marlin packer pads to: a multiple of 32, then of 256 (kernel/utils.py:251-271)."""
+    rank = (rank + 31) // 32 * 32
+    return (rank + 255) // 256 * 256
+
+
+def pack_binary_marlin_fused_from_packed(V_packed: torch.Tensor, V_shape: Tuple[int, int], U_packed: torch.Tensor,
+                                         U_shape: Tuple[int, int], scale_g: torch.Tensor, scale_l: torch.Tensor,
+                                         scale_h: torch.Tensor, src_method: str = "lsb_first"):
+    """``pack_binary_marlin_fused(V.T, U.T, ...)`` from a checkpoint's sign words of V [r, n] and U [m, r].
+
+    Returns the same (V_bits, U_bits, scale_g', scale_l', scale_h', workspace) as the fused
+    packer given the dense factors (kernel/utils.py:217-284, as ``_prepare_kernel`` calls it,
+    linear.py:226-232), without expanding either factor: the words are repacked on the GPU
+    with the rank padding (+1 signs, zero ``scale_l``) folded in.
+    """
+    if scale_l is None:
+        raise ValueError("pack_binary_marlin_fused needs scale_l (use ones when the layer has none)")
+    r, n = (int(s) for s in V_shape)
+    m, r_u = (int(s) for s in U_shape)
+    if r_u != r or scale_l.shape[0] != r or scale_g.shape[0] != n or scale_h.shape[0] != m:
+        raise ValueError(f"factor shapes disagree: V {tuple(V_shape)}, U {tuple(U_shape)}, scales "
+                         f"{scale_g.shape[0]}, {scale_l.shape[0]}, {scale_h.shape[0]}")
+    r_pad = marlin_rank(r)
+    V_bits = repack_binary_marlin(V_packed, (r, n), (r_pad, n), src_method)
+    U_bits = repack_binary_marlin(U_packed, (m, r), (m, r_pad), src_method)
+    if r_pad > r:
+        scale_l = torch.cat([scale_l, torch.zeros(r_pad - r, device=scale_l.device, dtype=scale_l.dtype)], dim=0)
+    scale_g_marlin, scale_l_marlin = _permute_scales(scale_g, scale_l)
+    _, scale_h_marlin = _permute_scales(scale_l, scale_h)
+    workspace_size = max(scale_l_marlin.numel(), scale_h_marlin.numel()) // 128 * MARLIN_MIN_MAX_PAR
+    workspace = torch.zeros(workspace_size, device=V_bits.device, dtype=torch.int32)
+    dev = V_packed.device
+    outs = (V_bits, U_bits, scale_g_marlin, scale_l_marlin, scale_h_marlin)
+    if dev.type != "cuda":
+        outs = tuple(t.to(dev) for t in outs)
+        workspace = workspace.to(dev)
+    return (*outs, workspace)
+
+
 # Aliases of the reference (kernel/utils.py:503-506)
 binary_packer = pack_binary_gemv
 binary_unpacker = unpack_binary_gemv

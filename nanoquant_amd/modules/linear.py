@@ -17,7 +17,21 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from ..kernel.utils import binary_packer, binary_unpacker, get_kernel_function, marlin_nanoquant_packer
+from ..kernel.utils import (binary_packer, binary_unpacker, get_kernel_function, marlin_nanoquant_packer,
+                            pack_binary_marlin_fused_from_packed, repack_binary_gemv)
+
+# The GEMV tuning ints _prepare_kernel fixes (linear.py:210-219); the kernels here accept and
+# validate them but pick their own launch shapes.
+_GEMV_KWARGS = {
+    "num_thread_stage1": 128,
+    "num_thread_stage2": 128,
+    "num_row_per_warp_stage1": 2,
+    "num_row_per_warp_stage2": 2,
+    "num_acc_stage1": 1,
+    "num_acc_stage2": 1,
+    "num_pipeline_stage1": 8,
+    "num_pipeline_stage2": 8,
+}
 
 
 class _BinarySignSTE(torch.autograd.Function):
@@ -158,16 +172,7 @@ class NanoQuantLinear(nn.Module):
             delattr(self, "U")
             delattr(self, "V")
             self.kernel_forward = get_kernel_function("nanoquant", dtype, kernel_type="dynamic")
-            self.kernel_kwargs = {
-                "num_thread_stage1": 128,
-                "num_thread_stage2": 128,
-                "num_row_per_warp_stage1": 2,
-                "num_row_per_warp_stage2": 2,
-                "num_acc_stage1": 1,
-                "num_acc_stage2": 1,
-                "num_pipeline_stage1": 8,
-                "num_pipeline_stage2": 8,
-            }
+            self.kernel_kwargs = dict(_GEMV_KWARGS)
         elif kernel_type == "gemm":
             if self.scale_mid is None:
                 self.scale_mid = nn.Parameter(
@@ -184,6 +189,56 @@ class NanoQuantLinear(nn.Module):
             self.kernel_forward = get_kernel_function("marlin_nanoquant", dtype, kernel_type="fixed")
         else:
             raise ValueError("kernel_type must be one of ['gemv', 'gemm', 'gemlite'].")
+
+    def _prepare_kernel_from_packed(self, V_packed, V_shape, U_packed, U_shape, kernel_type="gemv",
+                                    dtype=torch.float16, method="lsb_first"):
+        """``_prepare_kernel`` from the factors' packed sign words instead of dense V/U.
+
+        ``V_packed``/``U_packed`` are the words of V [rank, in] and U [out, rank] in ``method``
+        order (a checkpoint's ``{name}_packed`` entries, lsb_first, linear.py:359-376). The kernel
+        words are made from them on the GPU (half2 for gemv; Marlin, rank padding included, for
+        gemm) and are bit-identical to what ``_prepare_kernel`` makes from the dense factors;
+        the dense factors are never built (the reference unpacks them at load,
+        load_utils.py:392, and packs them again here, linear.py:205-206,226-232).
+        """
+        if kernel_type == "gemlite":
+            raise NotImplementedError("the gemlite kernel is not part of nanoquant_amd; use 'gemv' or 'gemm'")
+        if kernel_type not in ("gemv", "gemm"):
+            raise ValueError("kernel_type must be one of ['gemv', 'gemm', 'gemlite'].")
+        V_shape = tuple(int(s) for s in V_shape)
+        U_shape = tuple(int(s) for s in U_shape)
+        if V_shape != (self.rank, self.in_features) or U_shape != (self.out_features, self.rank):
+            raise ValueError(f"packed factor shapes {V_shape}, {U_shape} do not match rank {self.rank}, "
+                             f"in {self.in_features}, out {self.out_features}")
+        device = self.scale_pre.device
+        V_packed = V_packed.to(device)
+        U_packed = U_packed.to(device)
+        for name in ("U", "V"):
+            if name in self._parameters:
+                del self._parameters[name]
+        self.do_kernel_inference = True
+        self.kernel_type = kernel_type
+        self.dtype = dtype
+        self.scale_pre = nn.Parameter(self.scale_pre.to(dtype).squeeze(0), requires_grad=False)
+        self.scale_post = nn.Parameter(self.scale_post.to(dtype).squeeze(0), requires_grad=False)
+        self.scale_mid = getattr(self, "scale_mid", None)
+        if self.scale_mid is not None:
+            self.scale_mid = nn.Parameter(self.scale_mid.to(dtype).squeeze(0), requires_grad=False)
+
+        if kernel_type == "gemv":
+            self.U_int8 = repack_binary_gemv(U_packed, U_shape, method, "half2")
+            self.V_int8 = repack_binary_gemv(V_packed, V_shape, method, "half2")
+            self.kernel_forward = get_kernel_function("nanoquant", dtype, kernel_type="dynamic")
+            self.kernel_kwargs = dict(_GEMV_KWARGS)
+        else:
+            if self.scale_mid is None:
+                self.scale_mid = nn.Parameter(torch.ones(self.rank, device=device, dtype=dtype), requires_grad=False)
+            (self.V_int8, self.U_int8, self.s1, self.s2, self.s3, self.workspace) = \
+                pack_binary_marlin_fused_from_packed(V_packed, V_shape, U_packed, U_shape, self.scale_pre,
+                                                     self.scale_mid, self.scale_post, method)
+            for key in ["scale_pre", "scale_mid", "scale_post"]:
+                delattr(self, key)
+            self.kernel_forward = get_kernel_function("marlin_nanoquant", dtype, kernel_type="fixed")
 
     # ------------------------------------------------------------------ packed state dict
 
@@ -236,3 +291,38 @@ class NanoQuantLinear(nn.Module):
         unpack_param("U")
         super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys,
                                       error_msgs)
+
+
+def load_packed_for_kernels(model: nn.Module, state_dict: dict, kernel_type: str = "gemv",
+                            dtype: torch.dtype = torch.float16, method: str = "lsb_first"):
+    """Load a packed NanoQuant state dict with every ``NanoQuantLinear`` made ready for a kernel.
+
+    ``state_dict`` is what ``model.state_dict()`` saves: ``{name}_packed`` sign words and
+    ``{name}_shape`` for V and U (linear.py:359-394), scales and every other parameter as is.
+    The other entries load as usual; each NanoQuantLinear then takes the kernel words straight
+    from its packed entries (``_prepare_kernel_from_packed``), so no dense +-1 factor is ever
+    built, on the host or the GPU. The reference's route is ``load_state_dict`` (unpacking the
+    words to dense factors, load_utils.py:392, linear.py:396-433) then ``_prepare_kernel``.
+    Returns ``load_state_dict``'s result for the remaining entries; a missing packed entry raises
+    KeyError.
+    """
+    state = dict(state_dict)
+    layers = []
+    for name, mod in model.named_modules():
+        if not isinstance(mod, NanoQuantLinear):
+            continue
+        prefix = f"{name}." if name else ""
+        words = {}
+        for p in ("V", "U"):
+            pk, sk = f"{prefix}{p}_packed", f"{prefix}{p}_shape"
+            if pk not in state or sk not in state:
+                raise KeyError(f"missing {pk} or {sk} in the packed state dict")
+            words[p] = (state.pop(pk), tuple(int(s) for s in state.pop(sk).tolist()))
+        for p in ("V", "U"):  # never loaded densely
+            if p in mod._parameters:
+                del mod._parameters[p]
+        layers.append((mod, words))
+    result = model.load_state_dict(state, strict=False)
+    for mod, words in layers:
+        mod._prepare_kernel_from_packed(*words["V"], *words["U"], kernel_type=kernel_type, dtype=dtype, method=method)
+    return result

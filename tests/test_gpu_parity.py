@@ -415,3 +415,80 @@ def test_state_dict_round_trip_on_gpu(nq):
     other.load_state_dict(state, strict=True)
     torch.testing.assert_close(other.V, lin.V)
     torch.testing.assert_close(other.U, lin.U)
+
+
+# --------------------------------------------------------------------------- checkpoint words -> kernel words
+
+@pytest.mark.parametrize("method", ["lsb_first", "half2"])
+@pytest.mark.parametrize("OK,pad", [((64, 16), (64, 16)), ((100, 80), (128, 96)), ((1632, 4096), (1792, 4096)),
+                                    ((4096, 1632), (4096, 1792)), ((5, 40), (256, 48))],
+                         ids=["exact", "ragged", "v_gate_055", "u_down_055", "tiny"])
+def test_repack_to_marlin_matches_dense_packing(nq, OK, pad, method):
+    """Marlin words straight from sign words equal the oracle's Marlin packing of the dense
+    matrix padded with +1."""
+    announce("repack marlin", OK, pad, method)
+    (O_, K_), (Op, Kp) = OK, pad
+    rng = np.random.default_rng(O_ * 7 + K_)
+    w = np.where(rng.random((O_, K_)) < 0.5, -1, 1).astype(np.int8)
+    words_in = O.pack_binary_gemv(w, method)
+    padded = np.ones((Op, Kp), np.int8)
+    padded[:O_, :K_] = w
+    exp, _, _, _ = O.pack_binary_marlin(padded, np.ones(Kp, np.float16), np.ones(Op, np.float16))
+    got = nq.repack_binary_marlin(torch.from_numpy(words_in.view(np.int32)).cuda(), (O_, K_), (Op, Kp), method)
+    np.testing.assert_array_equal(as_words(got), exp)
+
+
+@pytest.mark.parametrize("nrm", [(256, 288, 192), (4096, 1632, 11008)], ids=["rank_pad_288", "gate_055"])
+def test_fused_marlin_from_packed_matches_fused_packer(nq, nrm):
+    """pack_binary_marlin_fused_from_packed on lsb_first checkpoint words equals
+    pack_binary_marlin_fused on the dense factors, every output bit for bit."""
+    n, r, m = nrm
+    announce("fused from packed", nrm)
+    c = O.random_case(17, m, n, r, 1, with_mid=True)
+    s_g, s_l, s_h = dev_t(c["s_in"]), dev_t(c["s_mid"]), dev_t(c["s_out"])
+    ref = nq.pack_binary_marlin_fused(dev_t(c["V"].T), dev_t(c["U"].T), s_g, s_l, s_h)
+    Vw = torch.from_numpy(O.pack_binary_gemv(c["V"], "lsb_first").view(np.int32)).cuda()
+    Uw = torch.from_numpy(O.pack_binary_gemv(c["U"], "lsb_first").view(np.int32)).cuda()
+    got = nq.pack_binary_marlin_fused_from_packed(Vw, (r, n), Uw, (m, r), s_g, s_l, s_h)
+    for name, a, b in zip(["V_bits", "U_bits", "s_g", "s_l", "s_h", "workspace"], got, ref):
+        assert a.shape == b.shape and a.dtype == b.dtype, name
+        assert torch.equal(a, b), name
+
+
+@pytest.mark.parametrize("kernel", ["gemv", "gemm"])
+def test_load_packed_for_kernels_matches_dense_route(nq, kernel):
+    """A model loaded from its packed state dict with load_packed_for_kernels has the kernel
+    words and outputs of the reference route (load_state_dict, which unpacks to dense factors,
+    then _prepare_kernel), and no dense factor."""
+    announce("packed loader", kernel)
+    import torch.nn as nn
+    from tests.test_host import make_layer
+
+    def model(seed):
+        a, _ = make_layer(256, 320, 96, seed=seed, with_mid=True, device="cuda")
+        b, _ = make_layer(320, 128, 64, seed=seed + 1, device="cuda")
+        return nn.Sequential(a, nn.ReLU(), b)
+
+    src = model(3)
+    state = {k: v.clone() for k, v in src.state_dict().items()}
+    dense_route = model(50)
+    dense_route.load_state_dict(state, strict=True)
+    for lin in (dense_route[0], dense_route[2]):
+        lin._prepare_kernel(kernel, torch.float16)
+    packed_route = model(70)
+    res = nq.load_packed_for_kernels(packed_route, state, kernel, torch.float16)
+    assert not res.unexpected_keys
+    x = torch.from_numpy(np.random.default_rng(2).normal(size=(3, 256)).astype(np.float32)).cuda()
+    for a, b in ((dense_route[0], packed_route[0]), (dense_route[2], packed_route[2])):
+        assert not hasattr(b, "V") and not hasattr(b, "U")
+        names = ["V_int8", "U_int8"] + (["s1", "s2", "s3"] if kernel == "gemm" else
+                                        ["scale_pre", "scale_mid", "scale_post"])
+        for name in names:
+            ta, tb = getattr(a, name), getattr(b, name)
+            if ta is None:
+                assert tb is None, name
+                continue
+            assert torch.equal(ta, tb), name
+    ya, yb = dense_route(x), packed_route(x)
+    torch.cuda.synchronize()
+    assert torch.equal(ya, yb)

@@ -232,3 +232,18 @@ def test_gemm_split_workspace_sizes():
     s1 = lib.nq_gemm_onebit_workspace_bytes(256, 11008, 1792)
     s2 = lib.nq_gemm_onebit_workspace_bytes(256, 1792, 4096)
     assert lib.nq_gemm_nanoquant_workspace_bytes(256, 11008, 1792, 4096) == max(s1, s2) > 0
+
+
+def test_repack_marlin_argument_errors_need_no_gpu():
+    lib = _lib.load()
+    # padded shape smaller than the matrix, padding not a whole Marlin tile, unknown bit order
+    assert lib.nq_repack_marlin(None, 65, 16, 0, None, 64, 16, None) == _lib.NQ_ERR_INVALID_ARGUMENT
+    assert lib.nq_repack_marlin(None, 64, 16, 0, None, 96, 16, None) == _lib.NQ_ERR_SHAPE
+    assert lib.nq_repack_marlin(None, 64, 16, 0, None, 64, 24, None) == _lib.NQ_ERR_SHAPE
+    assert lib.nq_repack_marlin(None, 64, 16, 7, None, 64, 16, None) == _lib.NQ_ERR_INVALID_ARGUMENT
+    assert lib.nq_repack_marlin(None, 64, 16, 0, None, 64, 16, None) == _lib.NQ_ERR_INVALID_ARGUMENT  # null dst
+    assert lib.nq_repack_marlin(None, 0, 0, 0, None, 0, 0, None) == 0  # empty
+    with pytest.raises(RuntimeError, match="must cover"):
+        ku.repack_binary_marlin(torch.zeros(64, 1, dtype=torch.int32), (64, 16), (64, 8))
+    with pytest.raises(ValueError, match="Expected"):
+        ku.repack_binary_marlin(torch.zeros(64, 2, dtype=torch.int32), (64, 16))
