@@ -28,6 +28,8 @@ The same JSON line carries:
 * ``parity``: relative error of one GEMV and one GEMM against the float64 oracle on the
   same inputs, computed in the CPU leg (null with ``--skip-cpu``).
 
+``--batch-sweep`` prints the GEMV and the GEMM at batch 1..256 on the 7B gate and down shapes.
+
 ``--sweep`` instead prints one line per config shape: the GEMV at batch 1, 4, 16 and
 the GEMM at batch 256 and 2048 on Llama-2-7B (1.0 and 0.55 bpw) and Llama-3-70B
 (0.55 bpw, uniform and mixture-of-rank) linears.
@@ -411,6 +413,52 @@ def run_sweep(args, dev):
         torch.cuda.empty_cache()
 
 
+def run_batch_sweep(args, dev):
+    """One JSON line per (shape, batch, kind): the GEMV and the GEMM at batch 1, 2, 4, 8, 16, 32, 64, 128, 256 on
+    the Llama-2-7B gate and down shapes at 0.55 bpw, both over the same rotating copies (more than 512 MB of packed
+    weights in all, so both stream from HBM). This is where one kernel should hand over to the other."""
+    from nanoquant_amd.decode import rank_for_bpw
+
+    op_gemv = torch.ops.binary_kernels.nanoquant_dyn_forward
+    op_gemm = torch.ops.binary_kernels.marlin_nanoquant_forward
+    kw = gemv_kwargs()
+    gen = torch.Generator(device=dev).manual_seed(12)
+    stream = torch.cuda.Stream(device=dev)
+    words = lambda *shape: torch.randint(-2**31, 2**31 - 1, shape, dtype=torch.int32, device=dev,  # noqa: E731
+                                         generator=gen)
+    scales = lambda k: (torch.rand(k, device=dev, generator=gen) * 0.4 + 0.8).half()  # noqa: E731
+    for name, m, n in [("gate,up", 11008, 4096), ("down", 4096, 11008)]:
+        r = rank_for_bpw(m, n, 0.55)
+        r_pad = -(-r // 256) * 256
+        pb = packed_bytes(m, n, r)
+        copies = int(min(128, max(8, -(-(512 << 20) // pb))))
+        Vs = [words(r, (n + 31) // 32) for _ in range(copies)]
+        Us = [words(m, (r + 31) // 32) for _ in range(copies)]
+        Wv = [words(n // 16, r_pad // 2) for _ in range(copies)]
+        Wu = [words(r_pad // 16, m // 2) for _ in range(copies)]
+        s_in, s_out, s_l = scales(n), scales(m), scales(r_pad)
+        ws = torch.zeros(m // 128 * 32, dtype=torch.int32, device=dev)
+        for B in (1, 2, 4, 8, 16, 32, 64, 128, 256):
+            x = torch.randn(B, n, device=dev, generator=gen).half()
+            reps = max(1, 512 // copies)
+
+            def gemv_steps():
+                return [op_gemv(x, s_in, Vs[i], None, Us[i], s_out, **kw) for i in range(copies)]
+
+            def gemm_steps():
+                return [op_gemm(x, Wv[i], Wu[i], s_in, s_l, s_out, ws) for i in range(copies)]
+
+            for kind, fn in (("gemv", gemv_steps), ("gemm", gemm_steps)):
+                ms, graph, _ = time_graph(fn, copies, reps, 1, stream)
+                del graph
+                print(json.dumps({"kind": kind, "linear": name, "m": m, "n": n, "r": r, "batch": B,
+                                  "us": round(ms * 1e3, 3),
+                                  "packed_gbs": round(pb / (ms * 1e-3) / 1e9, 1),
+                                  "tflops": round(2.0 * B * r * (n + m) / (ms * 1e-3) / 1e12, 2)}), flush=True)
+        del Vs, Us, Wv, Wu
+        torch.cuda.empty_cache()
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -427,6 +475,8 @@ def main():
     ap.add_argument("--skip-decode", action="store_true", help="skip the end-to-end decode measurement")
     ap.add_argument("--sweep", action="store_true",
                     help="measure GEMV (batch 1/4/16) and GEMM (batch 256/2048) on every config shape instead")
+    ap.add_argument("--batch-sweep", action="store_true",
+                    help="measure GEMV and GEMM at batch 1..256 on the 7B gate and down shapes instead")
     ap.add_argument("--decode-only", action="store_true",
                     help="run only the end-to-end decode and print its result alone (for kernel traces)")
     ap.add_argument("--e2e-batch", type=int, default=1)
@@ -454,6 +504,10 @@ def main():
     if args.sweep:  # every config shape, one JSON line each (not the headline line)
         import nanoquant_amd  # noqa: F401
         run_sweep(args, dev)
+        return 0
+
+    if args.batch_sweep:  # the hand-over between the GEMV and the GEMM, one JSON line each
+        run_batch_sweep(args, dev)
         return 0
 
     if args.decode_only:  # profiling aid: only the end-to-end decode, reported on its own line

@@ -20,6 +20,11 @@ import torch.nn.functional as F
 from ..kernel.utils import (binary_packer, binary_unpacker, get_kernel_function, marlin_nanoquant_packer,
                             pack_binary_marlin_fused_from_packed, repack_binary_gemv)
 
+# Rows up to which kernel_type "auto" runs the GEMV; more rows run the GEMM. Measured on the
+# Llama-2-7B gate and down shapes at 0.55 bpw (bench.py --batch-sweep): at 32 rows the GEMV takes
+# 28 and 25 us against the GEMM's 30 and 34 us, at 64 rows 49 and 43 us against 35 and 38 us.
+AUTO_GEMV_MAX_ROWS = 32
+
 # The GEMV tuning ints _prepare_kernel fixes (linear.py:210-219); the kernels here accept and
 # validate them but pick their own launch shapes.
 _GEMV_KWARGS = {
@@ -122,11 +127,13 @@ class NanoQuantLinear(nn.Module):
             else:
                 raise ValueError(f"Expected 2D or 3D input tensor, got {x.ndim}D")
 
-            if self.kernel_type == "gemv":
+            if self.kernel_type == "gemv" or (self.kernel_type == "auto" and x.size(0) <= AUTO_GEMV_MAX_ROWS):
                 y = self.kernel_forward(x, self.scale_pre, self.V_int8, self.scale_mid, self.U_int8,
                                         self.scale_post, **self.kernel_kwargs)
             elif self.kernel_type == "gemm":
                 y = self.kernel_forward(x, self.V_int8, self.U_int8, self.s1, self.s2, self.s3, self.workspace)
+            elif self.kernel_type == "auto":
+                y = self.gemm_forward(x, self.V_marlin, self.U_marlin, self.s1, self.s2, self.s3, self.workspace)
             else:
                 raise ValueError(f"Unknown kernel_type: {self.kernel_type}")
 
@@ -152,7 +159,12 @@ class NanoQuantLinear(nn.Module):
         return y * scale_post
 
     def _prepare_kernel(self, kernel_type="gemv", dtype=torch.float16):
-        """Pack the factors for a kernel and switch the forward to it (linear.py:186-238)."""
+        """Pack the factors for a kernel and switch the forward to it (linear.py:186-238).
+
+        Besides the reference's "gemv" and "gemm", "auto" keeps both layouts (V_int8/U_int8 in
+        half2 order for the GEMV, V_marlin/U_marlin with s1..s3 and the workspace for the GEMM)
+        and runs each call on the GEMV up to AUTO_GEMV_MAX_ROWS rows, on the GEMM beyond.
+        """
         self.do_kernel_inference = True
         self.kernel_type = kernel_type
         self.dtype = dtype
@@ -187,8 +199,25 @@ class NanoQuantLinear(nn.Module):
             for key in ["U", "V", "scale_pre", "scale_mid", "scale_post"]:
                 delattr(self, key)
             self.kernel_forward = get_kernel_function("marlin_nanoquant", dtype, kernel_type="fixed")
+        elif kernel_type == "auto":
+            U8, V8 = self.U.to(torch.int8), self.V.to(torch.int8)
+            self.U_int8 = binary_packer(U8, method="half2")
+            self.V_int8 = binary_packer(V8, method="half2")
+            s_mid = self.scale_mid
+            if s_mid is None:
+                s_mid = torch.ones(self.rank, device=self.scale_pre.device, dtype=dtype)
+            (self.V_marlin, self.U_marlin, self.s1, self.s2, self.s3, self.workspace) = marlin_nanoquant_packer(
+                V8.T, U8.T, self.scale_pre, s_mid, self.scale_post)
+            delattr(self, "U")
+            delattr(self, "V")
+            self._set_auto_forwards(dtype)
         else:
-            raise ValueError("kernel_type must be one of ['gemv', 'gemm', 'gemlite'].")
+            raise ValueError("kernel_type must be one of ['gemv', 'gemm', 'gemlite', 'auto'].")
+
+    def _set_auto_forwards(self, dtype):
+        self.kernel_forward = get_kernel_function("nanoquant", dtype, kernel_type="dynamic")
+        self.kernel_kwargs = dict(_GEMV_KWARGS)
+        self.gemm_forward = get_kernel_function("marlin_nanoquant", dtype, kernel_type="fixed")
 
     def _prepare_kernel_from_packed(self, V_packed, V_shape, U_packed, U_shape, kernel_type="gemv",
                                     dtype=torch.float16, method="lsb_first"):
@@ -203,8 +232,8 @@ class NanoQuantLinear(nn.Module):
         """
         if kernel_type == "gemlite":
             raise NotImplementedError("the gemlite kernel is not part of nanoquant_amd; use 'gemv' or 'gemm'")
-        if kernel_type not in ("gemv", "gemm"):
-            raise ValueError("kernel_type must be one of ['gemv', 'gemm', 'gemlite'].")
+        if kernel_type not in ("gemv", "gemm", "auto"):
+            raise ValueError("kernel_type must be one of ['gemv', 'gemm', 'gemlite', 'auto'].")
         V_shape = tuple(int(s) for s in V_shape)
         U_shape = tuple(int(s) for s in U_shape)
         if V_shape != (self.rank, self.in_features) or U_shape != (self.out_features, self.rank):
@@ -225,12 +254,20 @@ class NanoQuantLinear(nn.Module):
         if self.scale_mid is not None:
             self.scale_mid = nn.Parameter(self.scale_mid.to(dtype).squeeze(0), requires_grad=False)
 
-        if kernel_type == "gemv":
+        if kernel_type in ("gemv", "auto"):
             self.U_int8 = repack_binary_gemv(U_packed, U_shape, method, "half2")
             self.V_int8 = repack_binary_gemv(V_packed, V_shape, method, "half2")
             self.kernel_forward = get_kernel_function("nanoquant", dtype, kernel_type="dynamic")
             self.kernel_kwargs = dict(_GEMV_KWARGS)
-        else:
+        if kernel_type == "auto":
+            s_mid = self.scale_mid
+            if s_mid is None:
+                s_mid = torch.ones(self.rank, device=device, dtype=dtype)
+            (self.V_marlin, self.U_marlin, self.s1, self.s2, self.s3, self.workspace) = \
+                pack_binary_marlin_fused_from_packed(V_packed, V_shape, U_packed, U_shape, self.scale_pre, s_mid,
+                                                     self.scale_post, method)
+            self._set_auto_forwards(dtype)
+        elif kernel_type == "gemm":
             if self.scale_mid is None:
                 self.scale_mid = nn.Parameter(torch.ones(self.rank, device=device, dtype=dtype), requires_grad=False)
             (self.V_int8, self.U_int8, self.s1, self.s2, self.s3, self.workspace) = \

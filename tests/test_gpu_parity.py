@@ -492,3 +492,34 @@ def test_load_packed_for_kernels_matches_dense_route(nq, kernel):
     ya, yb = dense_route(x), packed_route(x)
     torch.cuda.synchronize()
     assert torch.equal(ya, yb)
+
+
+def test_auto_kernel_routes_by_rows(nq):
+    """kernel_type "auto" runs the GEMV up to AUTO_GEMV_MAX_ROWS rows and the GEMM beyond: its
+    outputs equal those of the layer prepared for that kernel, bit for bit, from the dense
+    factors and from the packed state dict alike."""
+    announce("auto kernel")
+    import copy
+    from nanoquant_amd.modules.linear import AUTO_GEMV_MAX_ROWS
+    from tests.test_host import make_layer
+    base, c = make_layer(256, 320, 96, seed=12, with_mid=True, device="cuda")
+    state = {k: v.clone() for k, v in base.state_dict().items()}
+    layers = {}
+    for kt in ("gemv", "gemm", "auto"):
+        layers[kt] = copy.deepcopy(base)
+        layers[kt]._prepare_kernel(kt, torch.float16)
+    packed_auto, _ = make_layer(256, 320, 96, seed=99, with_mid=True, device="cuda")
+    nq.load_packed_for_kernels(packed_auto, state, "auto", torch.float16)
+    rng = np.random.default_rng(4)
+    f = lambda t: t.detach().double().cpu().numpy().reshape(-1)  # noqa: E731
+    for rows, kernel in ((1, "gemv"), (AUTO_GEMV_MAX_ROWS, "gemv"), (AUTO_GEMV_MAX_ROWS + 1, "gemm"), (100, "gemm")):
+        x = torch.from_numpy(rng.normal(size=(rows, 256)).astype(np.float16)).cuda()
+        want = layers[kernel](x)
+        for got in (layers["auto"](x), packed_auto(x)):
+            assert torch.equal(got, want), (rows, kernel)
+        y64 = O.nanoquant_forward_f64(x.double().cpu().numpy(), f(base.scale_pre), c["V"], f(base.scale_mid), c["U"],
+                                      f(base.scale_post))
+        err = np.abs(want.double().cpu().numpy() - y64).max() / np.abs(y64).max()
+        assert err <= 1e-3, (rows, err)
+    x3 = torch.from_numpy(rng.normal(size=(2, 40, 256)).astype(np.float16)).cuda()  # 80 rows: the GEMM
+    assert torch.equal(layers["auto"](x3), layers["gemm"](x3))
