@@ -349,6 +349,7 @@ __global__ __launch_bounds__(256) void s1w_kernel(const S1Table tab, const uint1
             }
         }
 
+    NQ_STAMP(1);
     // Even and odd pairs accumulate separately and rows are innermost, so consecutive dot2
     // instructions do not wait on each other.
     float acc[2][R][NB];
@@ -368,6 +369,7 @@ __global__ __launch_bounds__(256) void s1w_kernel(const S1Table tab, const uint1
 #pragma unroll
                 for (int b = 0; b < NB; ++b) acc[pp & 1][k][b] = T::dot2(a, xp[w][b][pp], acc[pp & 1][k][b]);
             }
+    NQ_STAMP(2);
     // sum of squares of x (a sign flip does not change a square; zeroed slots add nothing)
     float ss[2][NB];
 #pragma unroll
@@ -625,6 +627,21 @@ __global__ __launch_bounds__(256) void s2t_kernel(const S2Table tab, int batch) 
     uint32_t tail_word[P];
     u32x4 zv[P][kZPieces];
     uint16_t so[P][4];  // raw until the epilogue
+    // the output scales and the residual first: loads return in issue order, so what is issued
+    // last is waited for last, and these are needed before the MFMAs (in the wait the compiler
+    // places there), while the words of U come from HBM
+#pragma unroll
+    for (int pi = 0; pi < P; ++pi)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) so[pi][i] = its[pi].s_out[min(i0 + 4 * g + i, m - 1)];
+    // the residual of this lane's outputs (batch row b0 + c/2, rows i0 + 4g + i)
+    uint16_t res[4] = {0, 0, 0, 0};
+    if (EPI == kEpiResidual) {
+        const uint32_t rb = static_cast<uint32_t>(min(b0 + min(c >> 1, NB - 1), batch - 1));
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            res[i] = its[0].resid[rb * static_cast<uint32_t>(its[0].ystride) + min(i0 + 4 * g + i, m - 1)];
+    }
 #pragma unroll
     for (int pi = 0; pi < P; ++pi) {
         const S2Item& it = its[pi];
@@ -645,16 +662,6 @@ __global__ __launch_bounds__(256) void s2t_kernel(const S2Table tab, int batch) 
                                                             static_cast<uint32_t>(it.zpitch) +
                                                         off);
         }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) so[pi][i] = it.s_out[min(i0 + 4 * g + i, m - 1)];
-    }
-    // the residual of this lane's outputs (batch row b0 + c/2, rows i0 + 4g + i)
-    uint16_t res[4] = {0, 0, 0, 0};
-    if (EPI == kEpiResidual) {
-        const uint32_t rb = static_cast<uint32_t>(min(b0 + min(c >> 1, NB - 1), batch - 1));
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            res[i] = its[0].resid[rb * static_cast<uint32_t>(its[0].ystride) + min(i0 + 4 * g + i, m - 1)];
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -681,25 +688,46 @@ __global__ __launch_bounds__(256) void s2t_kernel(const S2Table tab, int batch) 
         }
     }
     __syncthreads();
+    NQ_STAMP(1);
 
     // 3. MFMAs
     const uint32_t mask = kSignPair, one = kBf16OnePair;
     const int sh = 4 * g;
     const int bcol = c >> 1;
+    // The LDS operands of step s + CH are read right after step s's MFMA is issued, so each read
+    // has CH steps to land; the fences keep the scheduler from sinking the reads next to their
+    // uses (which made every step wait out an LDS round trip: ~1 us for 14 steps).
+    constexpr int CH = QW < 8 ? QW : 8;
 #pragma unroll
     for (int pi = 0; pi < P; ++pi) {
         f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
         const uint16_t* hsrc = &hz[pi][(c & 1) * NB + min(bcol, NB - 1)][8 * g];
         const uint32_t* trow = tile[pi] + min(c, rows - 1) * wr;
+        u32x4 bq[CH];
+        uint32_t wq[CH];
+#pragma unroll
+        for (int s = 0; s < CH; ++s) {
+            const int q = wave + NW * s;
+            bq[s] = *reinterpret_cast<const u32x4*>(hsrc + 32 * q);
+            wq[s] = trow[min(q, wr - 1)];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        NQ_STAMP(4);
 #pragma unroll
         for (int s = 0; s < QW; ++s) {
-            const int q = wave + NW * s;
-            const u32x4 b = *reinterpret_cast<const u32x4*>(hsrc + 32 * q);
-            const uint32_t w = trow[min(q, wr - 1)] << sh;
+            const int j = s % CH;
+            const uint32_t w = wq[j] << sh;
             const u32x4 a = u32x4{and_or(w, mask, one), and_or(w << 1, mask, one), and_or(w << 2, mask, one),
                                   and_or(w << 3, mask, one)};
-            acc[s & 1] = mfma16x16x32<BF16>(a, b, acc[s & 1]);
+            acc[s & 1] = mfma16x16x32<BF16>(a, bq[j], acc[s & 1]);
+            if (s + CH < QW) {
+                const int q = wave + NW * (s + CH);
+                bq[j] = *reinterpret_cast<const u32x4*>(hsrc + 32 * q);
+                wq[j] = trow[min(q, wr - 1)];
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
+        NQ_STAMP(5);
         red[pi][wave][lane] =
             f32x4{acc[0].x + acc[1].x, acc[0].y + acc[1].y, acc[0].z + acc[1].z, acc[0].w + acc[1].w};
     }
