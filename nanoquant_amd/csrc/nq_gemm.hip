@@ -221,13 +221,15 @@ __device__ inline void dma_to_lds4(const void* src, void* lds) {
                                      (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
 }
 
-template <typename T, bool kSin, bool kSout, int BP, int BQ, int WP, int WQ, int WPE, int KS, bool kSplit>
+template <typename T, bool kSin, bool kSout, int BP, int BQ, int WP, int WQ, int WPE, int KS, bool kSplit,
+          int BKK = 64>
 __global__ __launch_bounds__((BP / WP) * (BQ / WQ) * 64 * KS) __attribute__((amdgpu_waves_per_eu(WPE)))
 void gemm_dm_kernel(
     const uint16_t* __restrict__ A, const uint32_t* __restrict__ W, const uint16_t* __restrict__ s_in,
     const uint16_t* __restrict__ s_out, uint16_t* __restrict__ C, int M, int K, int N, int q_tiles, int p_tiles,
     float* __restrict__ part, int split_steps) {
-    constexpr int BKK = 64;
+    static_assert(BKK == 64 || BKK == 128, "64 or 128 k per step");
+    constexpr int CPR = BKK / 8;       // 16-byte chunks per A-tile row
     constexpr int NWP = BP / WP;
     constexpr int NWQ = BQ / WQ;
     constexpr int NTG = NWP * NWQ * 64;  // threads of one k group
@@ -291,8 +293,8 @@ void gemm_dm_kernel(
 #pragma unroll
     for (int j = 0; j < XPT; ++j) {
         const int ci = j * NTG + tg;
-        const int r = ci >> 3;
-        xoff[j] = static_cast<uint32_t>(min(q0 + r, M - 1)) * static_cast<uint32_t>(K) + 8 * ((ci & 7) ^ (r & 7));
+        const int r = ci / CPR;
+        xoff[j] = static_cast<uint32_t>(min(q0 + r, M - 1)) * static_cast<uint32_t>(K) + 8 * ((ci % CPR) ^ (r & 7));
     }
     uint32_t wsrc[WPT];
 #pragma unroll
@@ -303,7 +305,7 @@ void gemm_dm_kernel(
     }
     // s_in comes permuted: dword 8tr + 2r2 + r8 holds the pair k = 16tr + 8r8 + 2r2 + {0, 1}; LDS
     // slot 8tr + 4r8 + r2 of the wave's copy takes it, so the pairs r2 = 0..3 of one r8 are adjacent
-    const int sl = lane & 31;
+    const int sl = lane & (BKK / 2 - 1);
     const int sidx = (sl & ~7) | ((sl & 3) << 1) | ((sl >> 2) & 1);
     for (int e = t; e < BP; e += NT) sos[e] = kSout ? s_out[perm_out(min(p0 + e, N - 1))] : uint16_t(0);
 
@@ -360,15 +362,13 @@ void gemm_dm_kernel(
     auto step = [&](const uint16_t* xc, const uint32_t* wc, const uint32_t* sc, uint16_t* xf, uint32_t* wf,
                     uint32_t* sf, int it) {
         issue(min(it + 2, k_iters - 1), xf, wf, sf);
-        Frag f0, f1;
-        read_kt(f0, xc, wc, sc, 0);
-        read_kt(f1, xc, wc, sc, 1);
-        compute_kt(f0);
-        read_kt(f0, xc, wc, sc, 2);
-        compute_kt(f1);
-        read_kt(f1, xc, wc, sc, 3);
-        compute_kt(f0);
-        compute_kt(f1);
+        Frag f[2];
+        read_kt(f[0], xc, wc, sc, 0);
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) {
+            if (kt + 1 < KT) read_kt(f[(kt + 1) & 1], xc, wc, sc, kt + 1);
+            compute_kt(f[kt & 1]);
+        }
         wait_vmcnt<kIssued>();
         __syncthreads();
     };
