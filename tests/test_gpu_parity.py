@@ -147,6 +147,11 @@ GEMV_CASES = [
     ("llama7b_gate_055_b4", 11008, 4096, 1632, 4, False),
     ("llama7b_down_055_b16", 4096, 11008, 1632, 16, False),
     ("llama7b_gate_10_b1", 11008, 4096, 2976, 1, False),
+    # a stage-2 grid of 1283 blocks of 16 rows (more than one round of resident blocks), the last
+    # one ragged: 20520 = 1282 * 16 + 8
+    ("tall_ragged_b1", 20520, 256, 96, 1, False),
+    # 688 row tiles x two passes of 8 batch rows, with s_mid
+    ("tall_b16_mid", 11008, 512, 64, 16, True),
 ]
 
 
