@@ -856,11 +856,15 @@ void launch_stage2_generic(const GemvArgs& a) {
 // Rows of V per block of the stage-1 configuration used for wn words per row (0: none).
 // Shapes measured on MI355X (graph-replayed, cold weights): n = 4096 is fastest with two waves
 // per row and one word per lane, two rows per group (3.3 us against 3.6-4.3 for the other
-// splits); n = 11008 with four waves per row, two words per lane, four rows per group.
+// splits). Wider rows gain from more rows per block, since every block reads all of x and s_in
+// once: n = 8192, r = 3520 takes 5.8 us with four rows per group (6.9 with two, 6.2 with eight);
+// n = 11008 takes 5.3 us with three words per lane over two waves (384 words for 344) and four
+// rows per group (6.2 with two words over four waves, 6.5 and 7.7 with six and eight rows).
 inline int s1w_rows_per_block(int wn) {
     if (wn <= 64) return 4 * 2;      // <WPL 1, WR 1, R 2>
     if (wn <= 128) return 2 * 2;     // <1, 2, 2>
-    if (wn <= 256) return 2 * 2;     // <2, 2, 2>
+    if (wn <= 256) return 2 * 4;     // <2, 2, 4>
+    if (wn <= 384) return 2 * 4;     // <3, 2, 4>
     if (wn <= 512) return 1 * 4;     // <2, 4, 4>
     return 0;
 }
@@ -871,7 +875,8 @@ void launch_s1w_cfg(const S1Table& tab, int blocks, const uint16_t* x, int batch
     const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(ceil_div(batch, NB)));
     if (wn <= 64) s1w_kernel<T, NB, 1, 1, 2, kNorm, kOne><<<grid, 256, 0, st>>>(tab, x, batch, n, wn, eps);
     else if (wn <= 128) s1w_kernel<T, NB, 1, 2, 2, kNorm, kOne><<<grid, 256, 0, st>>>(tab, x, batch, n, wn, eps);
-    else if (wn <= 256) s1w_kernel<T, NB, 2, 2, 2, kNorm, kOne><<<grid, 256, 0, st>>>(tab, x, batch, n, wn, eps);
+    else if (wn <= 256) s1w_kernel<T, NB, 2, 2, 4, kNorm, kOne><<<grid, 256, 0, st>>>(tab, x, batch, n, wn, eps);
+    else if (wn <= 384) s1w_kernel<T, NB, 3, 2, 4, kNorm, kOne><<<grid, 256, 0, st>>>(tab, x, batch, n, wn, eps);
     else s1w_kernel<T, NB, 2, 4, 4, kNorm, kOne><<<grid, 256, 0, st>>>(tab, x, batch, n, wn, eps);
 }
 

@@ -147,6 +147,11 @@ GEMV_CASES = [
     ("llama7b_gate_055_b4", 11008, 4096, 1632, 4, False),
     ("llama7b_down_055_b16", 4096, 11008, 1632, 16, False),
     ("llama7b_gate_10_b1", 11008, 4096, 2976, 1, False),
+    # the VALU stage 1 on wide rows: three words per lane over two waves (n = 11008; n = 10000
+    # ends in a half-filled word), two words over two waves at n = 8192; four rows per group
+    ("llama7b_down_055_b1", 4096, 11008, 1632, 1, False),
+    ("ragged_word_10000_b1", 300, 10000, 100, 1, True),
+    ("wide_8192_b2", 600, 8192, 200, 2, True),
     # a stage-2 grid of 1283 blocks of 16 rows (more than one round of resident blocks), the last
     # one ragged: 20520 = 1282 * 16 + 8
     ("tall_ragged_b1", 20520, 256, 96, 1, False),
