@@ -31,6 +31,7 @@
 //
 // Generic kernels (one wave per output row) cover the shapes the fast ones do not.
 #include <algorithm>
+#include <cstdint>
 
 #include "nq_common.h"
 
@@ -451,12 +452,14 @@ __global__ __launch_bounds__(256) void s1w_kernel(const S1Table tab, const uint1
 // of the rows and add their tiles in LDS. Each wave issues the loads of CH words before their
 // MFMAs. kNorm sums x^2 of each batch row on the way (the B fragments of the block's lanes cover
 // every k of a batch row once) and scales h by rsqrt(mean(x^2) + eps).
-template <typename T, int NW, bool kNorm, bool kOne, bool kSinLds>
+template <typename T, int NW, bool kNorm, bool kOne, bool kSinLds, int kLoads>
 __global__ __launch_bounds__(NW * 64) void s1m_kernel(const S1Table tab, const uint16_t* __restrict__ x, int batch,
                                                       int n, int wn, float eps) {
     constexpr int CH = 8;
     constexpr int NT = NW * 64;
-    constexpr int kMaxLoads = 16;  // dwords per thread staged (the host checks the staged words fit)
+    // dwords per thread staged: the host picks the smallest of 4, 8, 12, 16 that covers the block's
+    // words (a fixed 16 issued up to three quarters of redundant, clamped loads at n = 4096)
+    constexpr int kMaxLoads = kLoads;
     // [16][wn] sign words, then (kSinLds) s_in as [n / 2] pairs; wider rows read s_in from global
     // (after the MFMAs the same memory holds the waves' partial tiles)
     extern __shared__ uint32_t lds[];
@@ -585,24 +588,31 @@ __global__ __launch_bounds__(NW * 64) void s1m_kernel(const S1Table tab, const u
 //
 // With the gated epilogue a block runs two items (gate, up) over the same 16 rows, each with
 // its own U tile and intermediate, and stores silu(gate) * up.
+//
+// RT row tiles per block: the block stages 16 * RT rows of U, and each step's B fragment serves
+// RT MFMAs, one per tile; wave t < RT runs tile t's epilogue. With several batch rows per pass
+// the staged intermediate (2 * NB rows of up to 128 * QW columns) outweighs the block's words of
+// U many times over, and more rows per block stage it fewer times.
 template <typename T>
 __device__ inline float silu_of(float g) {
     return g / (1.0f + expf(-g));
 }
 
-template <typename T, int QW, int NB, int EPI>
+template <typename T, int QW, int NB, int EPI, int RT>
 __global__ __launch_bounds__(256) void s2t_kernel(const S2Table tab, int batch) {
     constexpr int NW = 4;
     constexpr int kThr = 256;
     constexpr int P = EPI == kEpiGated ? 2 : 1;  // items per block
-    constexpr int kWords = 16 * NW * QW;  // tile words (wr <= NW * QW)
+    constexpr int kRows = 16 * RT;               // rows of U per block
+    static_assert(RT >= 1 && RT <= NW, "one epilogue wave per row tile");
+    constexpr int kWords = kRows * NW * QW;  // tile words (wr <= NW * QW)
     constexpr int kUPieces = (kWords / 4 + kThr - 1) / kThr;
     constexpr int kCols = 32 * NW * QW;  // h columns used per batch row (<= zpitch)
     constexpr int kRowPieces = kCols / 8;
     constexpr int kZPieces = (2 * NB * kRowPieces + kThr - 1) / kThr;
     __shared__ __attribute__((aligned(16))) uint32_t tile[P][kWords + 4];
     __shared__ __attribute__((aligned(16))) uint16_t hz[P][2 * NB][kCols];  // [hi rows, then lo rows][column]
-    __shared__ f32x4 red[P][NW][64];
+    __shared__ f32x4 red[P][RT][NW][64];
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
@@ -613,15 +623,16 @@ __global__ __launch_bounds__(256) void s2t_kernel(const S2Table tab, int batch) 
     if (P == 2) its[P - 1] = tab.item[1];
     const int m = its[0].m;
     const int wr = its[0].wr;  // gated items share m and wr
-    const int i0 = (static_cast<int>(blockIdx.x) - its[0].block_begin) * 16;
+    const int i0 = (static_cast<int>(blockIdx.x) - its[0].block_begin) * kRows;
     const int b0 = blockIdx.y * NB;
+    const int ie = i0 + 16 * min(wave, RT - 1);  // first row of the tile whose epilogue this wave may run
     NQ_STAMP(0);
 
     // 1. every global load: the tiles' words as 16-byte pieces, h, the output scales
     const uint32_t total = static_cast<uint32_t>(m) * static_cast<uint32_t>(wr);
     const uint32_t vec_end = total & ~3u;  // the host guarantees total >= 4
     const uint32_t base = static_cast<uint32_t>(i0) * static_cast<uint32_t>(wr);  // a multiple of 16
-    const int rows = min(16, m - i0);
+    const int rows = min(kRows, m - i0);
     const int nwords = rows * wr;
     u32x4 pv[P][kUPieces];
     uint32_t tail_word[P];
@@ -633,14 +644,14 @@ __global__ __launch_bounds__(256) void s2t_kernel(const S2Table tab, int batch) 
 #pragma unroll
     for (int pi = 0; pi < P; ++pi)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) so[pi][i] = its[pi].s_out[min(i0 + 4 * g + i, m - 1)];
+        for (int i = 0; i < 4; ++i) so[pi][i] = its[pi].s_out[min(ie + 4 * g + i, m - 1)];
     // the residual of this lane's outputs (batch row b0 + c/2, rows i0 + 4g + i)
     uint16_t res[4] = {0, 0, 0, 0};
     if (EPI == kEpiResidual) {
         const uint32_t rb = static_cast<uint32_t>(min(b0 + min(c >> 1, NB - 1), batch - 1));
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            res[i] = its[0].resid[rb * static_cast<uint32_t>(its[0].ystride) + min(i0 + 4 * g + i, m - 1)];
+            res[i] = its[0].resid[rb * static_cast<uint32_t>(its[0].ystride) + min(ie + 4 * g + i, m - 1)];
     }
 #pragma unroll
     for (int pi = 0; pi < P; ++pi) {
@@ -700,49 +711,61 @@ __global__ __launch_bounds__(256) void s2t_kernel(const S2Table tab, int batch) 
     constexpr int CH = QW < 8 ? QW : 8;
 #pragma unroll
     for (int pi = 0; pi < P; ++pi) {
-        f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+        f32x4 acc[RT][2];
+        const uint32_t* trow[RT];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            acc[rt][0] = acc[rt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+            trow[rt] = tile[pi] + min(16 * rt + c, rows - 1) * wr;
+        }
         const uint16_t* hsrc = &hz[pi][(c & 1) * NB + min(bcol, NB - 1)][8 * g];
-        const uint32_t* trow = tile[pi] + min(c, rows - 1) * wr;
         u32x4 bq[CH];
-        uint32_t wq[CH];
+        uint32_t wq[RT][CH];
 #pragma unroll
         for (int s = 0; s < CH; ++s) {
             const int q = wave + NW * s;
             bq[s] = *reinterpret_cast<const u32x4*>(hsrc + 32 * q);
-            wq[s] = trow[min(q, wr - 1)];
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) wq[rt][s] = trow[rt][min(q, wr - 1)];
         }
         __builtin_amdgcn_sched_barrier(0);
         NQ_STAMP(4);
 #pragma unroll
         for (int s = 0; s < QW; ++s) {
             const int j = s % CH;
-            const uint32_t w = wq[j] << sh;
-            const u32x4 a = u32x4{and_or(w, mask, one), and_or(w << 1, mask, one), and_or(w << 2, mask, one),
-                                  and_or(w << 3, mask, one)};
-            acc[s & 1] = mfma16x16x32<BF16>(a, bq[j], acc[s & 1]);
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                const uint32_t w = wq[rt][j] << sh;
+                const u32x4 a = u32x4{and_or(w, mask, one), and_or(w << 1, mask, one), and_or(w << 2, mask, one),
+                                      and_or(w << 3, mask, one)};
+                acc[rt][s & 1] = mfma16x16x32<BF16>(a, bq[j], acc[rt][s & 1]);
+            }
             if (s + CH < QW) {
                 const int q = wave + NW * (s + CH);
                 bq[j] = *reinterpret_cast<const u32x4*>(hsrc + 32 * q);
-                wq[j] = trow[min(q, wr - 1)];
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) wq[rt][j] = trow[rt][min(q, wr - 1)];
             }
             __builtin_amdgcn_sched_barrier(0);
         }
         NQ_STAMP(5);
-        red[pi][wave][lane] =
-            f32x4{acc[0].x + acc[1].x, acc[0].y + acc[1].y, acc[0].z + acc[1].z, acc[0].w + acc[1].w};
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+            red[pi][rt][wave][lane] = f32x4{acc[rt][0].x + acc[rt][1].x, acc[rt][0].y + acc[rt][1].y,
+                                            acc[rt][0].z + acc[rt][1].z, acc[rt][0].w + acc[rt][1].w};
     }
     __syncthreads();
     NQ_STAMP(2);
 
-    // 4. sum the waves' tiles, add hi and lo, scale, store
-    if (wave == 0) {
+    // 4. sum the waves' partial tiles, add hi and lo, scale, store (wave t: row tile t)
+    if (wave < RT) {
         float v[P][4];
 #pragma unroll
         for (int pi = 0; pi < P; ++pi) {
-            f32x4 sum = red[pi][0][lane];
+            f32x4 sum = red[pi][wave][0][lane];
 #pragma unroll
             for (int w = 1; w < NW; ++w) {
-                const f32x4 pr = red[pi][w][lane];
+                const f32x4 pr = red[pi][wave][w][lane];
                 sum = f32x4{sum.x + pr.x, sum.y + pr.y, sum.z + pr.z, sum.w + pr.w};
             }
             v[pi][0] = sum.x;
@@ -760,7 +783,7 @@ __global__ __launch_bounds__(256) void s2t_kernel(const S2Table tab, int batch) 
                 const float lo = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v[pi][i]), 0xB1, 0xF, 0xF, false));
                 out[pi] = (v[pi][i] + lo) * T::to_float(so[pi][i]);
             }
-            const int row = i0 + 4 * g + i;
+            const int row = ie + 4 * g + i;
             if (b_ok && row < m) {
                 uint16_t val = saturate_to<T>(out[0], T::SAT);
                 if (EPI == kEpiResidual) {
@@ -923,14 +946,14 @@ inline bool s1m_fits(int n, int wn) {
     return 16 * wn <= kS1mMaxStaged;
 }
 
-template <typename T, int NW>
-void launch_s1m_nw(const S1Table& tab, dim3 grid, const uint16_t* x, int batch, int n, int wn, bool norm, float eps,
-                   hipStream_t st) {
+template <typename T, int NW, int LD>
+void launch_s1m_loads(const S1Table& tab, dim3 grid, const uint16_t* x, int batch, int n, int wn, bool norm, float eps,
+                      hipStream_t st) {
     const size_t lds = s1m_lds_bytes(n, wn);
     const bool sl = s1m_sin_lds(n, wn);
-#define NQ_S1M(NORM, ONE)                                                                              \
-    (sl ? (s1m_kernel<T, NW, NORM, ONE, true><<<grid, NW * 64, lds, st>>>(tab, x, batch, n, wn, eps)) \
-        : (s1m_kernel<T, NW, NORM, ONE, false><<<grid, NW * 64, lds, st>>>(tab, x, batch, n, wn, eps)))
+#define NQ_S1M(NORM, ONE)                                                                                  \
+    (sl ? (s1m_kernel<T, NW, NORM, ONE, true, LD><<<grid, NW * 64, lds, st>>>(tab, x, batch, n, wn, eps)) \
+        : (s1m_kernel<T, NW, NORM, ONE, false, LD><<<grid, NW * 64, lds, st>>>(tab, x, batch, n, wn, eps)))
     if (tab.count == 1) {
         if (norm) NQ_S1M(true, true);
         else NQ_S1M(false, true);
@@ -939,6 +962,17 @@ void launch_s1m_nw(const S1Table& tab, dim3 grid, const uint16_t* x, int batch, 
         else NQ_S1M(false, false);
     }
 #undef NQ_S1M
+}
+template <typename T, int NW>
+void launch_s1m_nw(const S1Table& tab, dim3 grid, const uint16_t* x, int batch, int n, int wn, bool norm, float eps,
+                   hipStream_t st) {
+    const bool sl = s1m_sin_lds(n, wn);
+    const int staged = 16 * wn + (sl ? n / 2 : 0);
+    const int per_thread = static_cast<int>(ceil_div(staged, NW * 64));
+    if (per_thread <= 4) launch_s1m_loads<T, NW, 4>(tab, grid, x, batch, n, wn, norm, eps, st);
+    else if (per_thread <= 8) launch_s1m_loads<T, NW, 8>(tab, grid, x, batch, n, wn, norm, eps, st);
+    else if (per_thread <= 12) launch_s1m_loads<T, NW, 12>(tab, grid, x, batch, n, wn, norm, eps, st);
+    else launch_s1m_loads<T, NW, 16>(tab, grid, x, batch, n, wn, norm, eps, st);
 }
 
 // The MFMA stage 1 over every item of `tab` (16 rows per block, 16 batch rows per grid row).
@@ -1000,10 +1034,44 @@ void launch_stage1(const GemvArgs& a) {
 }
 
 // Only the batch splits that fit in LDS are instantiated (the host never picks the others).
-template <typename T, int QW, int NB, int EPI>
+template <typename T, int QW, int NB, int EPI, int RT>
 void launch_s2t_nb(const S2Table& tab, dim3 grid, int batch, hipStream_t st) {
     if constexpr (NB == 1 || (EPI == kEpiGated ? 2 : 1) * NB * QW <= 128)
-        s2t_kernel<T, QW, NB, EPI><<<grid, 256, 0, st>>>(tab, batch);
+        s2t_kernel<T, QW, NB, EPI, RT><<<grid, 256, 0, st>>>(tab, batch);
+}
+
+// Static LDS of s2t_kernel<QW, NB, one item, RT> (tile, intermediate, partial tiles).
+inline int64_t s2t_lds_bytes(int nb, int qw, int rt) {
+    return (16LL * rt * kS2Waves * qw + 4) * 4 + 2LL * nb * 32 * kS2Waves * qw * 2 + 16LL * rt * kS2Waves * 64;
+}
+// Row tiles per block of the MFMA stage 2 for nb batch rows per pass over `tiles` 16-row tiles and
+// `passes` passes. One or two batch rows: one tile (measured: two tiles gain nothing). From four:
+// the most tiles per block (4, 2, 1) whose grid still has at least 160 blocks and fits one round
+// of blocks resident by LDS; if none fits, the fewest rounds, ties to fewer tiles. Measured
+// (11008 x 1632, us at batch 4 / 8 / 16, tiles 1 - 2 - 4): 5.55-5.03-4.87, 7.37-6.26-5.49,
+// 11.37-8.40-9.74; at 4096 x 1632, batch 8 / 16: 3.89-4.30-5.33, 5.41-4.46-5.45.
+inline int s2t_row_tiles(int nb, int qw, int64_t tiles, int64_t passes) {
+    if (nb < 4) return 1;
+    int best = 1;
+    int64_t best_rounds = INT64_MAX;
+    for (int rt : {4, 2, 1}) {
+        const int64_t blocks = ceil_div(tiles, rt) * passes;
+        const int64_t per_cu = std::min<int64_t>(8, (160 * 1024) / s2t_lds_bytes(nb, qw, rt));
+        const int64_t rounds = ceil_div(blocks, std::max<int64_t>(1, per_cu) * 256);
+        if (rounds == 1 && blocks >= 160) return rt;
+        if (rounds <= best_rounds) {  // <= : ties go to the fewer tiles tried later
+            best_rounds = rounds;
+            best = rt;
+        }
+    }
+    return best;
+}
+
+template <typename T, int QW, int NB, int EPI>
+void launch_s2t_rt(const S2Table& tab, dim3 grid, int batch, int rt, hipStream_t st) {
+    if (rt == 4) launch_s2t_nb<T, QW, NB, EPI, 4>(tab, grid, batch, st);
+    else if (rt == 2) launch_s2t_nb<T, QW, NB, EPI, 2>(tab, grid, batch, st);
+    else launch_s2t_nb<T, QW, NB, EPI, 1>(tab, grid, batch, st);
 }
 
 // NB batch rows of h per block (LDS holds P * 2 * NB * 128 * QW halves: P * NB * QW <= 128
@@ -1014,17 +1082,27 @@ void launch_s2t_table(S2Table& tab, int batch, hipStream_t st) {
     const int want = std::min(batch, 8);
     int nb = want <= 1 ? 1 : (want <= 2 ? 2 : (want <= 4 ? 4 : 8));
     while (nb > 1 && P * nb * QW > 128) nb >>= 1;
+    // row tiles per block (the gated pair stays at one: it runs two items already)
+    int64_t tiles = 0;
+    for (int k = 0; k < (EPI == kEpiGated ? 1 : tab.count); ++k) tiles += ceil_div(tab.item[k].m, 16);
+    const int rt = EPI == kEpiGated ? 1 : s2t_row_tiles(nb, QW, tiles, ceil_div(batch, nb));
     int blocks = 0;
     const int items = EPI == kEpiGated ? 1 : tab.count;  // a gated pair runs item 1 inside item 0's blocks
     for (int k = 0; k < items; ++k) {
         tab.item[k].block_begin = blocks;
-        blocks += static_cast<int>(ceil_div(tab.item[k].m, 16));
+        blocks += static_cast<int>(ceil_div(tab.item[k].m, 16 * rt));
     }
     const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(ceil_div(batch, nb)));
-    if (nb == 1) launch_s2t_nb<T, QW, 1, EPI>(tab, grid, batch, st);
-    else if (nb == 2) launch_s2t_nb<T, QW, 2, EPI>(tab, grid, batch, st);
-    else if (nb == 4) launch_s2t_nb<T, QW, 4, EPI>(tab, grid, batch, st);
-    else launch_s2t_nb<T, QW, 8, EPI>(tab, grid, batch, st);
+    if (nb == 1) launch_s2t_nb<T, QW, 1, EPI, 1>(tab, grid, batch, st);
+    else if constexpr (EPI == kEpiGated) {
+        if (nb == 2) launch_s2t_nb<T, QW, 2, EPI, 1>(tab, grid, batch, st);
+        else if (nb == 4) launch_s2t_nb<T, QW, 4, EPI, 1>(tab, grid, batch, st);
+        else launch_s2t_nb<T, QW, 8, EPI, 1>(tab, grid, batch, st);
+    } else {
+        if (nb == 2) launch_s2t_rt<T, QW, 2, EPI>(tab, grid, batch, rt, st);
+        else if (nb == 4) launch_s2t_rt<T, QW, 4, EPI>(tab, grid, batch, rt, st);
+        else launch_s2t_rt<T, QW, 8, EPI>(tab, grid, batch, rt, st);
+    }
 }
 
 // Launches the MFMA stage 2 for words-per-wave choice qw; false when qw is not one of them.
