@@ -275,6 +275,8 @@ GEMM_CASES = [
     ("llama7b_gate_055_b256", 256, 4096, 1632, 11008, False),
     ("llama7b_down_055_b256", 256, 11008, 1632, 4096, False),
     ("llama7b_gate_055_b2048", 2048, 4096, 1632, 11008, False),
+    # stage 2 on 1024 blocks of 64 rows x 256 features, the last row block ragged: 1000 = 15 * 64 + 40
+    ("wide_ragged_rows", 1000, 256, 128, 16384, True),
 ]
 
 
