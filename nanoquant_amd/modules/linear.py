@@ -21,9 +21,9 @@ from ..kernel.utils import (binary_packer, binary_unpacker, get_kernel_function,
                             pack_binary_marlin_fused_from_packed, repack_binary_gemv)
 
 # Rows up to which kernel_type "auto" runs the GEMV; more rows run the GEMM. Measured on the
-# Llama-2-7B gate and down shapes at 0.55 bpw (bench.py --batch-sweep): at 32 rows the GEMV takes
-# 28 and 25 us against the GEMM's 30 and 34 us, at 64 rows 49 and 43 us against 35 and 38 us.
-AUTO_GEMV_MAX_ROWS = 32
+# Llama-2-7B gate and down shapes at 0.55 bpw (bench.py --batch-sweep): at 64 rows the GEMV takes
+# 34.4 and 37.5 us against the GEMM's 35.3 and 38.5 us, at 128 rows 63 and 69 us against 41 and 45 us.
+AUTO_GEMV_MAX_ROWS = 64
 
 # The GEMV tuning ints _prepare_kernel fixes (linear.py:210-219); the kernels here accept and
 # validate them but pick their own launch shapes.
