@@ -803,7 +803,8 @@ __global__ __launch_bounds__(256) void s2t_kernel(const S2Table tab, int batch) 
 // --------------------------------------------------------------------------- plan and dispatch
 
 constexpr int kS2Waves = 4;
-constexpr int kS2QwChoices[] = {2, 4, 6, 8, 10, 12, 14, 16, 20, 24, 28, 32, 36};
+// 9, 13 and 18 fit the ranks 1120, 1632 and 2240 (35, 51 and 70 words) with one or two fewer steps per wave
+constexpr int kS2QwChoices[] = {2, 4, 6, 8, 9, 10, 12, 13, 14, 16, 18, 20, 24, 28, 32, 36};
 constexpr int kS2MaxWr = kS2Waves * 36;
 
 struct Plan {
@@ -1116,10 +1117,13 @@ bool launch_s2t_qw(S2Table& tab, int qw, int batch, hipStream_t st) {
         case 4: launch_s2t_table<T, 4, EPI>(tab, batch, st); return true;
         case 6: launch_s2t_table<T, 6, EPI>(tab, batch, st); return true;
         case 8: launch_s2t_table<T, 8, EPI>(tab, batch, st); return true;
+        case 9: launch_s2t_table<T, 9, EPI>(tab, batch, st); return true;
         case 10: launch_s2t_table<T, 10, EPI>(tab, batch, st); return true;
         case 12: launch_s2t_table<T, 12, EPI>(tab, batch, st); return true;
+        case 13: launch_s2t_table<T, 13, EPI>(tab, batch, st); return true;
         case 14: launch_s2t_table<T, 14, EPI>(tab, batch, st); return true;
         case 16: launch_s2t_table<T, 16, EPI>(tab, batch, st); return true;
+        case 18: launch_s2t_table<T, 18, EPI>(tab, batch, st); return true;
         case 20: launch_s2t_table<T, 20, EPI>(tab, batch, st); return true;
         case 24: launch_s2t_table<T, 24, EPI>(tab, batch, st); return true;
         case 28: launch_s2t_table<T, 28, EPI>(tab, batch, st); return true;
