@@ -638,9 +638,27 @@ __global__ __launch_bounds__(256) void s2t_kernel(const S2Table tab, int batch) 
     uint32_t tail_word[P];
     u32x4 zv[P][kZPieces];
     uint16_t so[P][4];  // raw until the epilogue
-    // the output scales and the residual first: loads return in issue order, so what is issued
-    // last is waited for last, and these are needed before the MFMAs (in the wait the compiler
-    // places there), while the words of U come from HBM
+    // The intermediate's pieces first: they come from L2, and loads return in issue order, so the
+    // block can put them in LDS and read its first fragments while U's words (issued after them)
+    // are still on their way from HBM.
+#pragma unroll
+    for (int pi = 0; pi < P; ++pi) {
+        const S2Item& it = its[pi];
+#pragma unroll
+        for (int k = 0; k < kZPieces; ++k) {
+            const int pc = min(t + k * kThr, 2 * NB * kRowPieces - 1);
+            const int arr = pc / (NB * kRowPieces);
+            const int rem = pc - arr * (NB * kRowPieces);
+            const int b = rem / kRowPieces;
+            const int off = (rem - b * kRowPieces) * 8;
+            zv[pi][k] = *reinterpret_cast<const u32x4*>((arr ? it.z_lo : it.z_hi) +
+                                                        static_cast<uint32_t>(min(b0 + b, batch - 1)) *
+                                                            static_cast<uint32_t>(it.zpitch) +
+                                                        off);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // then the output scales and the residual (needed only by the epilogue) and U's words
 #pragma unroll
     for (int pi = 0; pi < P; ++pi)
 #pragma unroll
@@ -661,22 +679,35 @@ __global__ __launch_bounds__(256) void s2t_kernel(const S2Table tab, int batch) 
             pv[pi][k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
                 it.u_bits + min(base + 4u * static_cast<uint32_t>(t + k * kThr), vec_end - 4u)));
         tail_word[pi] = it.u_bits[min(vec_end + static_cast<uint32_t>(t), total - 1u)];  // words past vec_end
-#pragma unroll
-        for (int k = 0; k < kZPieces; ++k) {
-            const int pc = min(t + k * kThr, 2 * NB * kRowPieces - 1);
-            const int arr = pc / (NB * kRowPieces);
-            const int rem = pc - arr * (NB * kRowPieces);
-            const int b = rem / kRowPieces;
-            const int off = (rem - b * kRowPieces) * 8;
-            zv[pi][k] = *reinterpret_cast<const u32x4*>((arr ? it.z_lo : it.z_hi) +
-                                                        static_cast<uint32_t>(min(b0 + b, batch - 1)) *
-                                                            static_cast<uint32_t>(it.zpitch) +
-                                                        off);
-        }
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    // 2. into LDS; vec_end and base + e4 are multiples of 4, so a piece lies wholly below
+    // 2. the intermediate into LDS, then each wave's first CH fragments of it
+#pragma unroll
+    for (int pi = 0; pi < P; ++pi) {
+#pragma unroll
+        for (int k = 0; k < kZPieces; ++k) {
+            const int pc = t + k * kThr;
+            if (pc < 2 * NB * kRowPieces) {
+                const int row = pc / kRowPieces;  // arr * NB + b
+                *reinterpret_cast<u32x4*>(&hz[pi][row][(pc - row * kRowPieces) * 8]) = zv[pi][k];
+            }
+        }
+    }
+    __syncthreads();
+    const uint32_t mask = kSignPair, one = kBf16OnePair;
+    const int sh = 4 * g;
+    const int bcol = c >> 1;
+    constexpr int CH = QW < 4 ? QW : 4;
+    u32x4 bq0[P][CH];
+#pragma unroll
+    for (int pi = 0; pi < P; ++pi) {
+        const uint16_t* hsrc = &hz[pi][(c & 1) * NB + min(bcol, NB - 1)][8 * g];
+#pragma unroll
+        for (int s = 0; s < CH; ++s) bq0[pi][s] = *reinterpret_cast<const u32x4*>(hsrc + 32 * (wave + NW * s));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    //    then U's words; vec_end and base + e4 are multiples of 4, so a piece lies wholly below
     //    vec_end or wholly past it, and words past it come from tail_word
 #pragma unroll
     for (int pi = 0; pi < P; ++pi) {
@@ -689,27 +720,15 @@ __global__ __launch_bounds__(256) void s2t_kernel(const S2Table tab, int batch) 
             const uint32_t w = vec_end + t;
             if (w < total && w >= base && w < base + nwords) tile[pi][w - base] = tail_word[pi];
         }
-#pragma unroll
-        for (int k = 0; k < kZPieces; ++k) {
-            const int pc = t + k * kThr;
-            if (pc < 2 * NB * kRowPieces) {
-                const int row = pc / kRowPieces;  // arr * NB + b
-                *reinterpret_cast<u32x4*>(&hz[pi][row][(pc - row * kRowPieces) * 8]) = zv[pi][k];
-            }
-        }
     }
     __syncthreads();
     NQ_STAMP(1);
 
     // 3. MFMAs
-    const uint32_t mask = kSignPair, one = kBf16OnePair;
-    const int sh = 4 * g;
-    const int bcol = c >> 1;
     // The LDS operands of step s + CH are read right after step s's MFMA is issued, so each read
     // has CH steps to land; the fences keep the scheduler from sinking the reads next to their
     // uses (which made every step wait out an LDS round trip: ~1 us for 14 steps).
     // (4 steps ahead measured 3.96 us on the 11008 x 1632 shape against 4.03-4.05 for 8 and 4.05 for all 13)
-    constexpr int CH = QW < 4 ? QW : 4;
 #pragma unroll
     for (int pi = 0; pi < P; ++pi) {
         f32x4 acc[RT][2];
@@ -725,7 +744,7 @@ __global__ __launch_bounds__(256) void s2t_kernel(const S2Table tab, int batch) 
 #pragma unroll
         for (int s = 0; s < CH; ++s) {
             const int q = wave + NW * s;
-            bq[s] = *reinterpret_cast<const u32x4*>(hsrc + 32 * q);
+            bq[s] = bq0[pi][s];
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt) wq[rt][s] = trow[rt][min(q, wr - 1)];
         }
