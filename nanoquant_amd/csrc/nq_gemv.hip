@@ -295,12 +295,6 @@ __global__ __launch_bounds__(256) void s1w_kernel(const S1Table tab, const uint1
 #pragma unroll
     for (int w = 0; w < WPL; ++w) qc[w] = min(p + 64 * WR * w, wn - 1);
     uint32_t vb[R][WPL];
-#pragma unroll
-    for (int k = 0; k < R; ++k) {
-        const uint32_t* row = it.v_bits + static_cast<uint32_t>(min(j0 + k, r - 1)) * static_cast<uint32_t>(wn);
-#pragma unroll
-        for (int w = 0; w < WPL; ++w) vb[k][w] = row[qc[w]];
-    }
     // the mid scales, raw until the end; without s_mid the (unused) loads read s_in
     const uint16_t* msrc = it.s_mid != nullptr ? it.s_mid : it.s_in;
     const int mlim = (it.s_mid != nullptr ? r : n) - 1;
@@ -329,6 +323,15 @@ __global__ __launch_bounds__(256) void s1w_kernel(const S1Table tab, const uint1
                 xp[w][b][4 * v + 3] = xv.w;
             }
         }
+    // V's words after x and s_in: loads return in issue order, so the sign fix-up below waits only
+    // for x and s_in (from L2) and runs while V's words come from HBM
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+        const uint32_t* row = it.v_bits + static_cast<uint32_t>(min(j0 + k, r - 1)) * static_cast<uint32_t>(wn);
+#pragma unroll
+        for (int w = 0; w < WPL; ++w) vb[k][w] = row[qc[w]];
+    }
     __builtin_amdgcn_sched_barrier(0);
 
     // zero what lies past the row or the batch; move s_in's sign onto x
