@@ -75,23 +75,18 @@ def _check_tuning(th1, th2, rpw1, rpw2, acc1, acc2, pipe1, pipe2) -> None:
             raise ValueError(f"{name} should be one of [{', '.join(str(c) for c in choices)}], but {value} was given")
 
 
-# --------------------------------------------------------------------------- workspace cache
-# The GEMV workspace holds the fp32 intermediate and words that must start zeroed
-# once; it is kept per (device, stream) and grown on demand, so steady-state calls
-# allocate nothing but the output.
-_workspaces: dict = {}
+# --------------------------------------------------------------------------- GEMV workspace
+# The GEMV workspace is a 256-byte reserved header followed by the intermediate h as two
+# bf16 arrays (hi, then lo), each [batch][zpitch]; stage 1 rewrites every element of both
+# on each call, so the buffer needs no initial contents. It is taken from torch's caching
+# allocator per call, as the reference allocates its intermediate per call
+# (gemv_kernel.cu:345-346): the allocator orders reuse by stream, and under graph capture
+# the block comes from the graph's private pool and stays reserved for its replays, so no
+# captured graph can be left pointing at memory that was handed to another tensor.
 
 
-def gemv_workspace(device: torch.device, stream_handle: int, nbytes: int) -> torch.Tensor:
-    key = (device.index, stream_handle)
-    ws = _workspaces.get(key)
-    if ws is None or ws.numel() < nbytes:
-        size = max(nbytes, 1 << 20)
-        if ws is not None:
-            size = max(size, 2 * ws.numel())
-        ws = torch.zeros(size, dtype=torch.uint8, device=device)
-        _workspaces[key] = ws
-    return ws
+def gemv_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
 
 
 # --------------------------------------------------------------------------- nanoquant_dyn_forward
@@ -141,8 +136,7 @@ def nanoquant_dyn_forward_cuda(x, scale_g, Ubits, scale_l, Vbits, scale_h, num_t
     lib = _lib.load()
     with torch.cuda.device(x.device):
         stream = _lib.stream_of(x.device)
-        need = lib.nq_gemv_workspace_bytes(batch, n, r, m)
-        ws = gemv_workspace(x.device, stream, need)
+        ws = gemv_workspace(x.device, lib.nq_gemv_workspace_bytes(batch, n, r, m))
         status = lib.nq_gemv(_lib.dtype_code(x.dtype), x.data_ptr(), scale_g.data_ptr(), Ubits.data_ptr(),
                              _lib.ptr(scale_l), Vbits.data_ptr(), scale_h.data_ptr(), y.data_ptr(), batch, n, r, m,
                              ws.data_ptr(), ws.numel(), stream)

@@ -220,6 +220,72 @@ def test_gemv_stage_entry_points_match_nq_gemv(nq, shape):
     assert torch.equal(y2.view(torch.int16), y.view(torch.int16))
 
 
+GENERIC_STAGE1_CASES = [
+    # name, m, n, r, batch, with_mid, x offset in elements: n % 8 != 0 or an x that is not 16-byte
+    # aligned sends stage 1 to the one-wave-per-row kernel (vector loads only when n % 8 == 0 and
+    # both x and s_in are 16-byte aligned)
+    ("n70_b1", 72, 70, 24, 1, False, 0),
+    ("n70_b3_mid", 72, 70, 24, 3, True, 0),
+    ("n4095_b2", 256, 4095, 160, 2, False, 0),
+    ("x_offset2_b1", 300, 512, 96, 1, False, 1),
+    ("x_offset2_b5_mid", 130, 1024, 64, 5, True, 1),
+    ("n5_b1", 40, 5, 3, 1, False, 0),
+]
+
+
+@pytest.mark.parametrize("case", GENERIC_STAGE1_CASES, ids=[c[0] for c in GENERIC_STAGE1_CASES])
+def test_gemv_generic_stage1(nq, case):
+    name, m, n, r, B, mid, off = case
+    announce("gemv generic stage 1", name, (m, n, r, B, off))
+    c = O.random_case(16, m, n, r, B, with_mid=mid)
+    U_bits = nq.pack_binary_gemv(dev_t(c["U"]), method="half2")
+    V_bits = nq.pack_binary_gemv(dev_t(c["V"]), method="half2")
+    buf = torch.zeros(off + B * n + 8, dtype=torch.float16, device="cuda")
+    buf[off:off + B * n] = dev_t(c["x"]).reshape(-1)
+    x = buf[off:off + B * n].view(B, n)
+    assert x.is_contiguous() and (x.data_ptr() % 16 == 0) == (off == 0)
+    s_mid = None if c["s_mid"] is None else dev_t(c["s_mid"])
+    y = torch.ops.binary_kernels.nanoquant_dyn_forward(
+        x, dev_t(c["s_in"]), V_bits, s_mid, U_bits, dev_t(c["s_out"]), num_acc_stage1=1, num_acc_stage2=1)
+    torch.cuda.synchronize()
+    y64 = O.nanoquant_forward_f64(c["x"], c["s_in"], c["V"], c["s_mid"], c["U"], c["s_out"])
+    err, _ = rel_err(y, y64, "gemv", torch.float16)
+    print(f"[gemv generic] {name} rel_err={err:.3e}", flush=True)
+    assert err <= 1e-3, err
+
+
+def test_gemv_workspace_survives_graph_capture(nq):
+    """A GEMV captured at batch 1, then an eager call that needs a larger workspace on the same
+    stream, then a new allocation, then a replay: the replay still gives the eager result and the
+    new tensor is left alone (a workspace freed under a captured graph would be overwritten)."""
+    announce("gemv workspace under capture")
+    # batch 128 at r = 4096 needs a 4 MiB workspace, more than a batch-1 call asks for
+    m, n, r = 512, 512, 4096
+    c = O.random_case(18, m, n, r, 128)
+    U_bits = nq.pack_binary_gemv(dev_t(c["U"]), method="half2")
+    V_bits = nq.pack_binary_gemv(dev_t(c["V"]), method="half2")
+    s_in, s_out = dev_t(c["s_in"]), dev_t(c["s_out"])
+    x1, xb = dev_t(c["x"][:1]), dev_t(c["x"])
+    kw = dict(num_acc_stage1=1, num_acc_stage2=1)
+    op = torch.ops.binary_kernels.nanoquant_dyn_forward
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        want1 = op(x1, s_in, V_bits, None, U_bits, s_out, **kw)
+    stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        y1 = op(x1, s_in, V_bits, None, U_bits, s_out, **kw)
+    with torch.cuda.stream(stream):
+        yb = op(xb, s_in, V_bits, None, U_bits, s_out, **kw)
+        sentinel = torch.full((1 << 20,), 7, dtype=torch.int32, device="cuda")
+        del yb
+        for _ in range(3):
+            graph.replay()
+    stream.synchronize()
+    assert torch.equal(y1, want1)
+    assert bool((sentinel == 7).all())
+
+
 def test_gemv_1d_and_3d_inputs(nq):
     announce("gemv shapes")
     c = O.random_case(12, 96, 64, 32, 6)

@@ -73,12 +73,32 @@ def test_c_abi_argument_errors_need_no_gpu():
     assert lib.nq_attention_decode_workspace_bytes(1, 32, 32, 64, 384) == 0
 
 
-def test_schemas_are_the_reference_schemas():
-    # pybind.cpp:85-104
-    assert str(torch.ops.binary_kernels.nanoquant_dyn_forward.default._schema) == "binary_kernels::" + bk.GEMV_SCHEMA
-    assert str(torch.ops.binary_kernels.marlin_onebit_forward.default._schema) == "binary_kernels::" + bk.ONEBIT_SCHEMA
-    assert str(torch.ops.binary_kernels.marlin_nanoquant_forward.default._schema) == \
-        "binary_kernels::" + bk.NANOQUANT_SCHEMA
+# The schema strings of the reference extension (kernel/pybind.cpp:85-104), written out here as
+# the concatenation of its C string literals, independently of the package's own constants.
+REFERENCE_SCHEMAS = {
+    "nanoquant_dyn_forward":
+        "nanoquant_dyn_forward(Tensor x, Tensor scale_g, Tensor Ubits, Tensor? scale_l, Tensor Vbits, "
+        "Tensor scale_h, int num_thread_stage1=128, int num_thread_stage2=128, int num_row_per_warp_stage1=2, "
+        "int num_row_per_warp_stage2=2, int num_acc_stage1=4, int num_acc_stage2=4, int num_pipeline_stage1=2, "
+        "int num_pipeline_stage2=2) -> Tensor",
+    "marlin_onebit_forward":
+        "marlin_onebit_forward(Tensor x, Tensor weight, Tensor? scale_g, Tensor? scale_h, Tensor(a!) workspace) "
+        "-> Tensor",
+    "marlin_nanoquant_forward":
+        "marlin_nanoquant_forward(Tensor x, Tensor weight_u, Tensor weight_v, Tensor? scale_g, Tensor? scale_l, "
+        "Tensor? scale_h, Tensor(a!) workspace) -> Tensor",
+}
+
+
+@pytest.mark.parametrize("name", sorted(REFERENCE_SCHEMAS))
+def test_schemas_are_the_reference_schemas(name):
+    registered = str(getattr(torch.ops.binary_kernels, name).default._schema)
+    want = str(torch._C.parse_schema("binary_kernels::" + REFERENCE_SCHEMAS[name]))
+    assert registered == want
+    # and the package's constants are those strings
+    const = {"nanoquant_dyn_forward": bk.GEMV_SCHEMA, "marlin_onebit_forward": bk.ONEBIT_SCHEMA,
+             "marlin_nanoquant_forward": bk.NANOQUANT_SCHEMA}[name]
+    assert const == REFERENCE_SCHEMAS[name]
 
 
 def meta(*shape, dtype=torch.float16):
