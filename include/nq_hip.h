@@ -5,8 +5,9 @@
  * HIP device of the calling thread, every call is enqueued on `stream` (a
  * hipStream_t passed as void*, NULL = the null stream) and never synchronises.
  * No entry point allocates: scratch comes from caller buffers whose sizes the
- * *_workspace_bytes queries give. Calls are thread-safe except that two calls
- * sharing one workspace must not overlap.
+ * *_workspace_bytes queries give, except for nq_gemv_noalloc, whose scratch is a
+ * static device array of the library. Calls are thread-safe except that two calls
+ * sharing one workspace (or, for nq_gemv_noalloc, one GPU) must not overlap.
  *
  * Every entry point returns an nq_status; nq_status_string() names it and
  * nq_last_error_message() gives the detail of the last failure on this thread.
@@ -129,6 +130,22 @@ int nq_gemv_stage1(int dtype, const void* x, const void* s_in, const uint32_t* v
                    nq_stream_t stream);
 int nq_gemv_stage2(int dtype, const uint32_t* u_bits, const void* s_out, void* y, int64_t batch, int64_t n,
                    int64_t r, int64_t m, void* workspace, size_t workspace_bytes, nq_stream_t stream);
+
+/* Bytes of the library's static GEMV scratch buffer on each GPU (4 MiB). */
+#define NQ_GEMV_NOALLOC_SCRATCH_BYTES (4u << 20)
+
+/* nq_gemv with no workspace argument and no allocation of any kind: the intermediate lives in
+ * a static device array of NQ_GEMV_NOALLOC_SCRATCH_BYTES that each GPU holds until the process
+ * ends. Same arguments (minus the workspace), kernels and results as nq_gemv, bit for bit.
+ * Returns NQ_ERR_WORKSPACE, launching nothing, when nq_gemv_workspace_bytes(batch, n, r, m)
+ * exceeds that size (batch > 630 at r = 1632, batch > 227 at r = 4608). Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (concurrent streams or threads) race,
+ * so order them on one stream. The first call on a device looks up the array's address there.
+ * No counterpart in the reference: for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). */
+int nq_gemv_noalloc(int dtype, const void* x, const void* s_in, const uint32_t* v_bits, const void* s_mid,
+                    const uint32_t* u_bits, const void* s_out, void* y, int64_t batch, int64_t n, int64_t r,
+                    int64_t m, nq_stream_t stream);
 
 /* ---------------------------------------------------------------- grouped decode GEMV
  *

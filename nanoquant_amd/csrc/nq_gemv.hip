@@ -32,6 +32,7 @@
 // Generic kernels (one wave per output row) cover the shapes the fast ones do not.
 #include <algorithm>
 #include <cstdint>
+#include <mutex>
 
 #include "nq_common.h"
 
@@ -1302,6 +1303,70 @@ int nq_gemv_stage2(int dtype, const uint32_t* u_bits, const void* s_out, void* y
                              batch, n, r, m, workspace, workspace_bytes, stream, a);
     if (s != NQ_OK) return s < 0 ? NQ_OK : s;
     return dtype == NQ_F16 ? run_stage2<F16>(a) : run_stage2<BF16>(a);
+}
+
+}  // extern "C"
+
+// --------------------------------------------------------------------------- GEMV without allocation
+//
+// nq_gemv_noalloc runs nq_gemv's two launches with the workspace in `scratch`, a file-scope
+// device array each GPU holds for the life of the process. In host code `scratch` names a
+// host-side stand-in, not device memory: the device address is fetched once per device with
+// hipGetSymbolAddress (with that device current) and only that address is ever passed on.
+// Every call on one GPU shares that GPU's array; stage 1 rewrites every element stage 2 reads
+// on each call, so nothing is cleared between calls. Calls that overlap on one GPU race.
+static __device__ __align__(256) unsigned char scratch[NQ_GEMV_NOALLOC_SCRATCH_BYTES];
+
+namespace nq {
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// The current device's address of `scratch` (looked up on the first call on that device).
+int scratch_of_current_device(const char* name, void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(NQ_ERR_HIP, "%s: hipGetDevice: %s", name, hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxScratchDevices)
+        return fail(NQ_ERR_UNSUPPORTED, "%s: device %d is beyond the %d this build tracks", name, dev,
+                    kMaxScratchDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr)
+            return fail(NQ_ERR_HIP, "%s: hipGetSymbolAddress(scratch) on device %d: %s", name, dev,
+                        hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return NQ_OK;
+}
+
+}  // namespace
+}  // namespace nq
+
+extern "C" {
+
+int nq_gemv_noalloc(int dtype, const void* x, const void* s_in, const uint32_t* v_bits, const void* s_mid,
+                    const uint32_t* u_bits, const void* s_out, void* y, int64_t batch, int64_t n, int64_t r,
+                    int64_t m, nq_stream_t stream) {
+    const char* name = "nq_gemv_noalloc";
+    if (batch < 0 || n < 0 || r < 0 || m < 0) return fail(NQ_ERR_INVALID_ARGUMENT, "%s: negative size", name);
+    const size_t need = nq_gemv_workspace_bytes(batch, n, r, m);
+    if (need > static_cast<size_t>(NQ_GEMV_NOALLOC_SCRATCH_BYTES))
+        return fail(NQ_ERR_WORKSPACE, "%s: batch %lld at rank %lld needs %zu bytes of scratch, the static buffer "
+                    "holds %zu", name, (long long)batch, (long long)r, need,
+                    static_cast<size_t>(NQ_GEMV_NOALLOC_SCRATCH_BYTES));
+    void* ws = nullptr;
+    if (int s = scratch_of_current_device(name, &ws)) return s;
+    GemvArgs a;
+    const int s = setup_gemv(name, kBoth, dtype, x, s_in, v_bits, s_mid, u_bits, s_out, y, batch, n, r, m, ws,
+                             NQ_GEMV_NOALLOC_SCRATCH_BYTES, stream, a);
+    if (s != NQ_OK) return s < 0 ? NQ_OK : s;
+    return dtype == NQ_F16 ? run_gemv<F16>(a) : run_gemv<BF16>(a);
 }
 
 }  // extern "C"
