@@ -1,39 +1,37 @@
 """Benchmark of the NanoQuant inference path on one MI355X.
 
-One step = one decode GEMV (``torch.ops.binary_kernels.nanoquant_dyn_forward``) of the
-Llama-2-7B gate_proj shape at 0.55 bpw (m=11008, n=4096, r=1632), batch 1, fp16, on a
-weight copy that differs from the previous step's: a pool of ``--copies`` packed
-copies (default 128, 394 MB) is larger than the 256 MB Infinity Cache, so every
-step streams its weights from HBM. Steps are captured in a HIP graph and replayed;
-the timed region is bracketed by a device synchronisation on both sides and timed
-with HIP events on the capture stream.
+A step is one decode GEMV (``torch.ops.binary_kernels.nanoquant_dyn_forward``: both launches)
+of the Llama-2-7B down_proj shape at 0.55 bpw (m=4096, n=11008, r=1632; the 4096x11008
+0.55-bpw GEMV), batch 1, fp16, on a weight copy that differs from the previous step's: step i
+uses copy i mod ``--copies`` of a pool (128 copies, 394 MB) larger than the 256 MB Infinity
+Cache, so every step streams its weights from HBM. ``--warmup`` untimed steps, then exactly
+``--steps`` timed steps, each set recorded as one HIP graph and replayed; the timed replay is
+bracketed by device synchronisation and timed with HIP events on the replay stream (a spin
+kernel ahead of it keeps the GPU busy while the host enqueues, so no launch gap is timed).
 
-The same JSON line carries:
-* ``value``: packed bytes per GEMV / measured time per GEMV (both launches), GB/s;
-* ``roofline``: the dominant kernel, stage 2 (U's sign words, 2.25 of the 3.08 MB),
-  timed on its own through ``nq_gemv_stage2`` in the same way: its packed bytes /
-  its time per launch against 8 TB/s; ``traffic`` is the HBM bytes per launch that
-  ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE`` measured for it, scaled by what the
-  same counters read for a copy of known size (``profiles/pmc_traffic.json``), when
-  that file describes this workload, else null;
-* ``gemm``: the prefill GEMM (``marlin_nanoquant_forward``) at B=2048 on the same
-  shape, algorithmic TFLOP/s = 2*B*r*(n+m) / time, against 2.5 PFLOP/s dense fp16;
-* ``decode_e2e``: greedy decode of a random-init Llama-2-7B-architecture model with
-  every linear NanoQuant-factorised at 0.55 bpw (prompt 128, 256 new tokens, batch 1),
-  tokens/s as the reference's decode harness reports it, with the bytes one step must
-  read against 8 TB/s;
-* ``cpu_baseline``: the reference's dense dequantize-and-matmul forward (two
-  ``F.linear`` on dense +-1 bf16 factors, modules/linear.py:282-291) on the host
-  cores, batch 1, on a bounded sample, in the same unit;
-* ``parity``: relative error of one GEMV and one GEMM against the float64 oracle on the
-  same inputs, computed in the CPU leg (null with ``--skip-cpu``).
+The JSON line carries:
+* ``value``: packed bytes per GEMV / time per GEMV, GB/s (``ms_per_step`` the time);
+* ``roofline``: the whole GEMV (its two launches) against 8 TB/s on the packed bytes of both
+  factors, with each launch's own figure (stage 1 over V's words, stage 2 over U's) timed
+  through ``nq_gemv_stage1`` / ``nq_gemv_stage2`` in the same rotation; ``traffic`` is the HBM
+  bytes per GEMV from ``rocprofv3 --pmc`` runs on these kernels (``profiles/pmc_traffic.json``)
+  when that file describes this workload, else null;
+* ``gemv``: the down and gate shapes at batch 1, each timed over 2048 steps at steady state;
+* ``gemm``: the prefill GEMM (``marlin_nanoquant_forward``) at B=2048 on the gate and down
+  shapes, TFLOP/s = 2*B*r*(n+m) / time against 2.5 PFLOP/s dense fp16;
+* ``pack``: sign packing, unpacking, reordering and Marlin packing of the down factors, GB/s of
+  bytes read plus written against 8 TB/s;
+* ``decode_e2e``: greedy decode of a random-init Llama-2-7B-architecture model with every linear
+  NanoQuant-factorised at 0.55 bpw (prompt 128, 256 new tokens, batch 1): the fused-linears step
+  with attention in torch (the headline), the unfused step, and the step with the HIP attention;
+* ``cpu_baseline``: the reference's dense dequantize-and-matmul forward (two ``F.linear`` on
+  dense +-1 factors, modules/linear.py:282-291) on the host cores at batch 1 in bf16 (the
+  reference's module dtype; ``value``) and fp32, and its packers in eager torch;
+* ``parity``: relative error of the GEMVs and GEMMs against the float64 oracle on the same
+  inputs (the CPU leg; null with ``--skip-cpu``).
 
-``--batch-sweep`` prints the GEMV and the GEMM at batch 1..256 on the 7B gate and down shapes.
-
-``--sweep`` instead prints one line per config shape: the GEMV at batch 1, 4, 16 and
-the GEMM at batch 256 and 2048 on Llama-2-7B (1.0 and 0.55 bpw) and Llama-3-70B
-(0.55 bpw, uniform and mixture-of-rank) linears.
-
+``--sweep`` prints one line per config shape (GEMV at batch 1/4/16, GEMM at 256/2048);
+``--batch-sweep`` the GEMV and the GEMM at batch 1..256 on the 7B gate and down shapes.
 Multi-GPU runs are not part of this build: ``--gpus`` above 1 exits with a message.
 """
 from __future__ import annotations
@@ -54,8 +52,11 @@ if ROOT not in sys.path:
 METRIC = "decode GEMV µs + % HBM roofline; prefill GEMM TFLOP/s (Llama-7B shapes)"
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
-M, N, R = 11008, 4096, 1632  # Llama-2-7B gate_proj at 0.55 bpw: r = round32(0.55*m*n/(m+n))
+R_055 = 1632  # round32(0.55 * m * n / (m + n)) for 4096 x 11008 and 11008 x 4096
+SHAPES = {"down": (4096, 11008, R_055), "gate": (11008, 4096, R_055)}  # (m, n, r)
+HEADLINE = "down"
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "pmc_traffic.json")
+SPIN_CYCLES = 2_000_000  # about 1 ms of GPU clock ahead of each timed replay
 
 
 def log(*a):
@@ -84,26 +85,46 @@ def gemv_kwargs():
                 num_acc_stage1=1, num_acc_stage2=1, num_pipeline_stage1=8, num_pipeline_stage2=8)
 
 
-def time_graph(fn_steps, n_steps, replays, warmup_replays, stream):
-    """Capture ``fn_steps`` (which enqueues n_steps steps) in a graph; return ms per step."""
-    with torch.cuda.stream(stream):
-        fn_steps()  # eager warm-up on the capture stream (workspaces, allocator)
-    stream.synchronize()
+def capture(fn, stream, eager_first=True):
+    """Record ``fn`` into a graph on ``stream``, after one eager run of it (allocator warm-up)
+    unless ``eager_first`` is False."""
+    if eager_first:
+        with torch.cuda.stream(stream):
+            fn()
+        stream.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
-        outs = fn_steps()
-    for _ in range(warmup_replays):
-        graph.replay()
+        outs = fn()
+    return graph, outs
+
+
+def timed_replay(graph, stream, replays=1, before=None):
+    """Milliseconds of ``replays`` back-to-back replays of ``graph`` on ``stream``: ``before``
+    (an untimed graph, e.g. the warm-up steps) and a spin kernel run first, the events bracket
+    only the timed replays, and the device is synchronised on both sides."""
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
+        if before is not None:
+            before.replay()
+        torch.cuda._sleep(SPIN_CYCLES)
         start.record(stream)
         for _ in range(replays):
             graph.replay()
         end.record(stream)
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / (replays * n_steps), graph, outs
+    return start.elapsed_time(end)
+
+
+def steady_ms(fn_steps, n_steps, stream, replays=8, warm_replays=2):
+    """ms per step of a graph of ``n_steps`` steps replayed ``replays`` times after warm-up."""
+    graph, outs = capture(fn_steps, stream)
+    for _ in range(warm_replays):
+        with torch.cuda.stream(stream):
+            graph.replay()
+    ms = timed_replay(graph, stream, replays) / (replays * n_steps)
+    return ms, graph, outs
 
 
 def make_case(seed, m, n, r, batch):
@@ -118,154 +139,248 @@ def make_case(seed, m, n, r, batch):
     return dict(U=U, V=V, s_in=s_in, s_out=s_out, x=x)
 
 
-def bench_gemv(args, dev):
-    import nanoquant_amd as nq
-    from nanoquant_amd import _lib
+def dev_t(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
 
-    batch = args.batch
-    c = make_case(2024, M, N, R, batch)
-    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
-    # copy 0 is packed from known signs (parity); the others are random words, which are
-    # valid half2 words of random signs (the padding-free shape leaves no unused bits)
-    U0 = nq.pack_binary_gemv(t(c["U"]), method="half2")
-    V0 = nq.pack_binary_gemv(t(c["V"]), method="half2")
-    gen = torch.Generator(device=dev).manual_seed(7)
-    Us = [U0] + [torch.randint(-2**31, 2**31 - 1, U0.shape, dtype=torch.int32, device=dev, generator=gen)
-                 for _ in range(args.copies - 1)]
-    Vs = [V0] + [torch.randint(-2**31, 2**31 - 1, V0.shape, dtype=torch.int32, device=dev, generator=gen)
-                 for _ in range(args.copies - 1)]
-    x, s_in, s_out = t(c["x"]), t(c["s_in"]), t(c["s_out"])
+
+class GemvPool:
+    """Packed copies of one linear: copy 0 from known signs (checked against the oracle), the
+    others random words (valid half2 words of random signs: these shapes leave no padding bits)."""
+
+    def __init__(self, name, copies, batch, dev, seed):
+        import nanoquant_amd as nq
+
+        self.name = name
+        self.m, self.n, self.r = SHAPES[name]
+        self.batch, self.copies = batch, copies
+        self.case = make_case(seed, self.m, self.n, self.r, batch)
+        c = self.case
+        U0 = nq.pack_binary_gemv(dev_t(c["U"], dev), method="half2")
+        V0 = nq.pack_binary_gemv(dev_t(c["V"], dev), method="half2")
+        gen = torch.Generator(device=dev).manual_seed(seed + 1)
+        rand = lambda like: torch.randint(-2**31, 2**31 - 1, like.shape, dtype=torch.int32, device=dev,  # noqa: E731
+                                          generator=gen)
+        self.Us = [U0] + [rand(U0) for _ in range(copies - 1)]
+        self.Vs = [V0] + [rand(V0) for _ in range(copies - 1)]
+        self.x, self.s_in, self.s_out = dev_t(c["x"], dev), dev_t(c["s_in"], dev), dev_t(c["s_out"], dev)
+
+    def op_steps(self, count, first=0):
+        op = torch.ops.binary_kernels.nanoquant_dyn_forward
+        kw = gemv_kwargs()
+
+        def fn():
+            return [op(self.x, self.s_in, self.Vs[(first + i) % self.copies], None,
+                       self.Us[(first + i) % self.copies], self.s_out, **kw) for i in range(count)]
+        return fn
+
+    def stage_steps(self, stage, count, ws, y):
+        from nanoquant_amd import _lib
+        lib = _lib.load()
+        b, n, r, m = self.batch, self.n, self.r, self.m
+
+        def fn():
+            st = torch.cuda.current_stream().cuda_stream
+            for i in range(count):
+                k = i % self.copies
+                if stage == 1:
+                    s = lib.nq_gemv_stage1(_lib.NQ_F16, self.x.data_ptr(), self.s_in.data_ptr(), self.Vs[k].data_ptr(),
+                                           None, b, n, r, m, ws.data_ptr(), ws.numel(), st)
+                else:
+                    s = lib.nq_gemv_stage2(_lib.NQ_F16, self.Us[k].data_ptr(), self.s_out.data_ptr(), y.data_ptr(),
+                                           b, n, r, m, ws.data_ptr(), ws.numel(), st)
+                _lib.check(s, f"stage {stage}")
+        return fn
+
+
+def bench_gemv_headline(args, dev):
+    """``--warmup`` untimed then exactly ``--steps`` timed GEMVs of the headline shape."""
+    pool = GemvPool(HEADLINE, args.copies, args.batch, dev, seed=2024)
     op = torch.ops.binary_kernels.nanoquant_dyn_forward
     kw = gemv_kwargs()
-
-    y_eager = op(x, s_in, V0, None, U0, s_out, **kw)
+    # copy 0 (known signs, for parity) and the copy of the first timed step, eagerly: this also
+    # loads both kernels before any capture
+    y_eager = op(pool.x, pool.s_in, pool.Vs[0], None, pool.Us[0], pool.s_out, **kw)
+    k0 = args.warmup % pool.copies
+    y_first = op(pool.x, pool.s_in, pool.Vs[k0], None, pool.Us[k0], pool.s_out, **kw)
     torch.cuda.synchronize()
-
-    n_steps = args.copies
-    replays = max(1, args.steps // n_steps)
-    warm = max(1, args.warmup // n_steps)
-
-    def steps():
-        return [op(x, s_in, Vs[i], None, Us[i], s_out, **kw) for i in range(n_steps)]
-
     stream = torch.cuda.Stream(device=dev)
-    ms, graph, outs = time_graph(steps, n_steps, replays, warm, stream)
-    graph_ok = bool(torch.equal(outs[0], y_eager))
-    del graph, outs
+    warm_graph = capture(pool.op_steps(args.warmup), stream, eager_first=False)[0] if args.warmup > 0 else None
+    # the timed steps continue the rotation where the warm-up stopped
+    timed_graph, outs = capture(pool.op_steps(args.steps, first=args.warmup), stream, eager_first=False)
+    ms = timed_replay(timed_graph, stream, 1, before=warm_graph) / args.steps
+    graph_ok = bool(torch.equal(outs[0], y_first))
+    del warm_graph, timed_graph, outs
+    return pool, ms, y_eager, graph_ok
 
-    # each launch on its own, through the stage entry points, same rotation
+
+def bench_gemv_shape(pool, dev, steps=2048):
+    """Steady-state ms per GEMV and per launch (stage entry points, same rotation)."""
+    from nanoquant_amd import _lib
     lib = _lib.load()
-    ws = torch.zeros(lib.nq_gemv_workspace_bytes(batch, N, R, M), dtype=torch.uint8, device=dev)
-    y = torch.empty(batch, M, dtype=torch.float16, device=dev)
-
-    def stage1_steps():
-        st = torch.cuda.current_stream(dev).cuda_stream
-        for i in range(n_steps):
-            _lib.check(lib.nq_gemv_stage1(_lib.NQ_F16, x.data_ptr(), s_in.data_ptr(), Vs[i].data_ptr(), None, batch,
-                                          N, R, M, ws.data_ptr(), ws.numel(), st), "stage 1")
-
-    def stage2_steps():
-        st = torch.cuda.current_stream(dev).cuda_stream
-        for i in range(n_steps):
-            _lib.check(lib.nq_gemv_stage2(_lib.NQ_F16, Us[i].data_ptr(), s_out.data_ptr(), y.data_ptr(), batch, N,
-                                          R, M, ws.data_ptr(), ws.numel(), st), "stage 2")
-
-    ms1, g1, _ = time_graph(stage1_steps, n_steps, replays, warm, stream)
-    ms2, g2, _ = time_graph(stage2_steps, n_steps, replays, warm, stream)
+    stream = torch.cuda.Stream(device=dev)
+    n_steps = pool.copies
+    replays = max(1, steps // n_steps)
+    ms, g, _ = steady_ms(pool.op_steps(n_steps), n_steps, stream, replays)
+    del g
+    ws = torch.empty(lib.nq_gemv_workspace_bytes(pool.batch, pool.n, pool.r, pool.m), dtype=torch.uint8, device=dev)
+    y = torch.empty(pool.batch, pool.m, dtype=torch.float16, device=dev)
+    ms1, g1, _ = steady_ms(pool.stage_steps(1, n_steps, ws, y), n_steps, stream, replays)
+    ms2, g2, _ = steady_ms(pool.stage_steps(2, n_steps, ws, y), n_steps, stream, replays)
     del g1, g2
-    pb = packed_bytes(M, N, R)
-    return dict(ms=ms, ms1=ms1, ms2=ms2, steps=replays * n_steps, warmup=warm * n_steps, case=c,
-                y=y_eager.double().cpu().numpy(),
-                graph_matches_eager=graph_ok, packed_bytes=pb, total_bytes=gemv_total_bytes(M, N, R, batch),
-                pool_bytes=pb * args.copies)
+    m, n, r = pool.m, pool.n, pool.r
+    pb = packed_bytes(m, n, r)
+    kern = lambda b, t: {"us_per_launch": round(t * 1e3, 4), "bytes": b,  # noqa: E731
+                         "achieved": round(b / (t * 1e-3) / 1e9, 2), "frac": round(b / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    return {"m": m, "n": n, "r": r, "batch": pool.batch, "steps": replays * n_steps, "us": round(ms * 1e3, 4),
+            "packed_bytes": pb, "packed_gbs": round(pb / (ms * 1e-3) / 1e9, 2),
+            "frac_hbm": round(pb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "total_bytes_gbs": round(gemv_total_bytes(m, n, r, pool.batch) / (ms * 1e-3) / 1e9, 2),
+            "stage1": dict(kernel="s1w_kernel (V's sign words)", **kern(stage1_bytes(n, r), ms1)),
+            "stage2": dict(kernel="s2t_kernel (U's sign words)", **kern(stage2_bytes(m, r), ms2))}
 
 
-def bench_gemm(args, dev):
+def bench_gemm(name, args, dev):
     import nanoquant_amd as nq
 
-    dtype = torch.float16
+    m, n, r = SHAPES[name]
     B = args.gemm_batch
-    c = make_case(2025, M, N, R, B)
-    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
-    packed = nq.pack_binary_marlin_fused(t(c["V"].T), t(c["U"].T), t(c["s_in"]),
-                                         torch.ones(R, dtype=dtype, device=dev), t(c["s_out"]))
-    x = t(c["x"])
+    c = make_case(2025, m, n, r, B)
+    packed = nq.pack_binary_marlin_fused(dev_t(c["V"].T, dev), dev_t(c["U"].T, dev), dev_t(c["s_in"], dev),
+                                         torch.ones(r, dtype=torch.float16, device=dev), dev_t(c["s_out"], dev))
+    x = dev_t(c["x"], dev)
     op = torch.ops.binary_kernels.marlin_nanoquant_forward
     y = op(x, *packed)
     torch.cuda.synchronize()
     n_steps = 4
-
-    def steps():
-        return [op(x, *packed) for _ in range(n_steps)]
-
     stream = torch.cuda.Stream(device=dev)
-    # warm-up replays first: with 8 warm-up calls, 64 timed calls measured 138 us per call against 127 us at steady
-    # state (the clock ramps up under the first ~100 calls); every timed call still computes its full output
-    ms, _, _ = time_graph(steps, n_steps, max(1, args.gemm_steps // n_steps), max(2, args.gemm_warmup // n_steps),
-                          stream)
-    flops = 2.0 * B * R * (N + M)
+    # warm-up replays first: the clock ramps up under the first ~100 calls; every timed call
+    # still computes its full output
+    ms, _, _ = steady_ms(lambda: [op(x, *packed) for _ in range(n_steps)], n_steps, stream,
+                         max(1, args.gemm_steps // n_steps), max(2, args.gemm_warmup // n_steps))
+    flops = 2.0 * B * r * (n + m)
     tflops = flops / (ms * 1e-3) / 1e12
-    return dict(ms=ms, tflops=tflops, flops=flops, r_pad=packed[1].shape[0] * 16, case=c,
-                y=y.double().cpu().numpy())
+    return {"m": m, "n": n, "r": r, "r_pad": packed[1].shape[0] * 16, "batch": B, "us": round(ms * 1e3, 2),
+            "tflops": round(tflops, 2), "flops_per_call": flops,
+            "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_F16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+                         "traffic": measured_traffic(f"gemm_{name}", (m, n, r, B))[0]}}, c, y
+
+
+def bench_pack(dev):
+    """Packing work on the down linear's factors, each kind of launch over 16 rotating inputs (more
+    than the Infinity Cache holds), graph-replayed: GB/s of bytes read plus written."""
+    from nanoquant_amd import _lib
+    lib = _lib.load()
+    m, n, r = SHAPES[HEADLINE]
+    copies = 16
+    gen = torch.Generator(device=dev).manual_seed(5)
+    stream = torch.cuda.Stream(device=dev)
+    rows, cols = r, n  # V [r, n]: 18.0 MB of int8, 2.2 MB of words
+    wn = (cols + 31) // 32
+    signs = [torch.randint(0, 2, (rows, cols), dtype=torch.int8, device=dev, generator=gen).mul_(2).sub_(1)
+             for _ in range(copies)]
+    words = [torch.empty(rows, wn, dtype=torch.int32, device=dev) for _ in range(copies)]
+    back = [torch.empty(rows, cols, dtype=torch.int8, device=dev) for _ in range(copies)]
+    h2 = [torch.empty(rows, wn, dtype=torch.int32, device=dev) for _ in range(copies)]
+    r_pad = -(-r // 256) * 256  # Marlin: V^T padded to [r_pad, n] -> words [n / 16, r_pad / 2]
+    mar_src = [torch.randint(0, 2, (r_pad, cols), dtype=torch.int8, device=dev, generator=gen).mul_(2).sub_(1)
+               for _ in range(copies)]
+    mar = [torch.empty(cols // 16, r_pad // 2, dtype=torch.int32, device=dev) for _ in range(copies)]
+    st = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+    L, H2 = _lib.NQ_PACK_LSB_FIRST, _lib.NQ_PACK_HALF2
+    kinds = {
+        "pack_signs": (lambda i: lib.nq_pack_signs(signs[i].data_ptr(), words[i].data_ptr(), rows, cols, L, st()),
+                       rows * cols + 4 * rows * wn, "int8 V [1632, 11008] -> lsb_first words"),
+        "unpack_signs": (lambda i: lib.nq_unpack_signs(words[i].data_ptr(), back[i].data_ptr(), rows, cols, L, st()),
+                         rows * cols + 4 * rows * wn, "lsb_first words -> int8 V"),
+        "repack_signs": (lambda i: lib.nq_repack_signs(words[i].data_ptr(), h2[i].data_ptr(), rows, cols, L, H2, st()),
+                         8 * rows * wn, "lsb_first -> half2 words of V"),
+        "pack_marlin": (lambda i: lib.nq_pack_marlin(mar_src[i].data_ptr(), mar[i].data_ptr(), r_pad, cols, st()),
+                        r_pad * cols + 4 * (cols // 16) * (r_pad // 2), f"int8 V^T [{r_pad}, 11008] -> Marlin words"),
+    }
+    out = {}
+    for name, (call, nbytes, what) in kinds.items():
+        def fn(call=call, name=name):
+            for i in range(copies):
+                _lib.check(call(i), name)
+        ms, g, _ = steady_ms(fn, copies, stream, replays=8)
+        del g
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"what": what, "bytes_per_launch": nbytes, "us_per_launch": round(ms * 1e3, 3),
+                     "achieved": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    # the packers' output is the oracle's (a sample of the last copy)
+    import oracle as O
+    s0 = signs[0][:64].cpu().numpy()
+    out["checked_bits"] = bool((words[0][:64].cpu().numpy().view(np.uint32) == O.pack_binary_gemv(s0)).all()
+                               and torch.equal(back[0], signs[0]))
+    return out
 
 
 def check_parity(results):
     """Relative error of the GPU outputs against the float64 oracle on the same inputs (the CPU leg of the
-    bench: the oracle is the checker here, never the measured path). ``results`` maps a name to a dict with
-    ``case`` and ``y``."""
+    bench: the oracle is the checker here, never the measured path). ``results`` maps a name to (case, y)."""
     import oracle as O
 
     out = {}
-    for name, res in results.items():
-        c = res["case"]
+    for name, (c, y) in results.items():
         y64 = O.nanoquant_forward_f64(c["x"], c["s_in"], c["V"], None, c["U"], c["s_out"])
-        out[name] = float(np.abs(res["y"] - y64).max() / np.abs(y64).max())
+        out[name] = float(np.abs(y.double().cpu().numpy() - y64).max() / np.abs(y64).max())
     return out
 
 
+def _median_time(fn, seconds, min_reps=10, max_reps=2000):
+    fn()  # warm-up
+    times = []
+    deadline = time.perf_counter() + seconds
+    while (time.perf_counter() < deadline or len(times) < min_reps) and len(times) < max_reps:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), len(times)
+
+
 def cpu_baseline(args):
-    """The reference's dense path on the host cores (oracle.compute_forward_torch)."""
+    """The reference's dense path and its packers on the host cores (the oracle's restatements)."""
     import oracle as O
 
     cores = min(len(os.sched_getaffinity(0)), args.cpu_threads)
     torch.set_num_threads(cores)
-    c = make_case(2026, M, N, R, 1)
-    dt = torch.bfloat16  # the reference module dtype (modules/linear.py:57)
-    V = torch.from_numpy(c["V"].astype(np.float32)).to(dt)
-    U = torch.from_numpy(c["U"].astype(np.float32)).to(dt)
-    s_in = torch.from_numpy(c["s_in"].astype(np.float32)).to(dt)
-    s_out = torch.from_numpy(c["s_out"].astype(np.float32)).to(dt)
-    x = torch.from_numpy(c["x"].astype(np.float32)).to(dt)
-    O.compute_forward_torch(x, V, U, s_in, None, s_out)  # warm-up
-    times = []
-    deadline = time.perf_counter() + args.cpu_seconds
-    while time.perf_counter() < deadline or len(times) < 10:
-        t0 = time.perf_counter()
-        O.compute_forward_torch(x, V, U, s_in, None, s_out)
-        times.append(time.perf_counter() - t0)
-        if len(times) >= 2000:
-            break
-    med = float(np.median(times))
-    gbs = packed_bytes(M, N, R) / med / 1e9
-    return dict(value=round(gbs, 4), unit="GB/s", cores=cores, kind="port",
-                sample=f"oracle compute_forward_torch (reference dense path, linear.py:282-291), bf16, B=1, "
-                       f"m={M} n={N} r={R}; median of {len(times)} calls = {med * 1e6:.1f} us/GEMV, packed bytes "
-                       f"of the factorised layer per call")
+    m, n, r = SHAPES[HEADLINE]
+    c = make_case(2026, m, n, r, 1)
+    per = {}
+    for dt, secs in ((torch.bfloat16, args.cpu_seconds), (torch.float32, args.cpu_seconds)):
+        t = {k: torch.from_numpy(c[k].astype(np.float32)).to(dt) for k in ("V", "U", "s_in", "s_out", "x")}
+        med, reps = _median_time(lambda: O.compute_forward_torch(t["x"], t["V"], t["U"], t["s_in"], None, t["s_out"]),
+                                 secs)
+        per[str(dt).replace("torch.", "")] = {"us_per_gemv": round(med * 1e6, 1), "reps": reps,
+                                              "packed_gbs": round(packed_bytes(m, n, r) / med / 1e9, 4)}
+    V = torch.from_numpy(c["V"])
+    med_p, reps_p = _median_time(lambda: O.pack_signs_torch(V, "lsb_first"), args.cpu_pack_seconds)
+    words = O.pack_signs_torch(V, "lsb_first")
+    med_u, reps_u = _median_time(lambda: O.unpack_signs_torch(words, tuple(V.shape), "lsb_first"),
+                                 args.cpu_pack_seconds)
+    nbytes = V.numel() + 4 * words.numel()
+    pack = {"pack_signs": {"us": round(med_p * 1e6, 1), "gbs": round(nbytes / med_p / 1e9, 3), "reps": reps_p},
+            "unpack_signs": {"us": round(med_u * 1e6, 1), "gbs": round(nbytes / med_u / 1e9, 3), "reps": reps_u},
+            "sample": f"eager-torch restatement of kernel/utils.py:51-183 on V [{r}, {n}] int8, lsb_first"}
+    bf = per["bfloat16"]
+    return {"value": bf["packed_gbs"], "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": (f"oracle compute_forward_torch (reference dense path, linear.py:282-291), bf16, B=1, m={m} "
+                       f"n={n} r={r}: median of {bf['reps']} calls = {bf['us_per_gemv']} us/GEMV, packed bytes of the "
+                       f"factorised layer per call; {args.cpu_seconds:.0f} s bounded sample per dtype"),
+            "by_dtype": per, "pack": pack}
 
 
-def measured_traffic(batch):
-    """HBM bytes per launch of the stage-2 kernel from profiles/pmc_traffic.json, when it
-    describes this workload; else None."""
+def measured_traffic(kernel_key, workload):
+    """HBM bytes per launch of ``kernel_key`` from profiles/pmc_traffic.json when it was measured on
+    ``workload`` (m, n, r, batch); else (None, None)."""
     try:
         with open(TRAFFIC_FILE) as f:
             rec = json.load(f)
     except (OSError, ValueError):
         return None, None
-    w = rec.get("workload", {})
-    if (w.get("m"), w.get("n"), w.get("r"), w.get("batch")) != (M, N, R, batch):
-        return None, None
-    k = rec.get("kernels", {}).get("gemv_stage2")
-    if not k:
+    k = rec.get("kernels", {}).get(kernel_key)
+    if not k or tuple(k.get("workload", ())) != tuple(workload):
         return None, None
     return int(k["fetch_bytes"] + k["write_bytes"]), rec.get("source")
 
@@ -286,41 +401,51 @@ def bench_decode(args, dev):
     0.55 bpw on the GEMV kernel: prompt of ``--e2e-prompt`` uniform-random ids, then
     ``--e2e-new`` tokens, the one-token step replayed from a HIP graph.
     tokens/s = B * (new - 1) / decode wall time, as the reference's harness reports it."""
-    from nanoquant_amd.decode import LlamaShape, generate, random_llama
+    from nanoquant_amd.decode import FusedDecoder, GraphDecoder, LlamaShape, generate, random_llama
 
     shape = LlamaShape()
+    torch.cuda.reset_peak_memory_stats(dev)
     t0 = time.perf_counter()
     model = random_llama(shape, bpw=0.55, seed=0, device=dev, kernel_type="gemv", dtype=torch.float16)
     torch.cuda.synchronize(dev)
     build_s = time.perf_counter() - t0
+    model_bytes = torch.cuda.memory_allocated(dev)
     B, T, new = args.e2e_batch, args.e2e_prompt, args.e2e_new
     gen = torch.Generator(device=dev)
     gen.manual_seed(1)
     prompt = torch.randint(0, shape.vocab, (B, T), device=dev, generator=gen)
-    runs = {}  # (fused, steps per graph) -> (tokens/s, prof, ids)
-    variants = [(False, args.e2e_steps_per_graph)] + [(True, k) for k in sorted({1, args.e2e_steps_per_graph})]
-    for fused, spg in variants:
-        if (new - 1) % spg:
+    spg = args.e2e_steps_per_graph
+    variants = {  # name -> (fused, attention, steps per graph)
+        "fused_torch_attention": (True, "torch", spg),
+        "fused_torch_attention_spg1": (True, "torch", 1),
+        "unfused": (False, "torch", spg),
+        "fused_hip_attention": (True, "hip", spg),
+    }
+    runs = {}
+    for name, (fused, attention, k) in variants.items():
+        if (new - 1) % k:
             continue
-        generate(model, prompt, 1 + spg, steps_per_graph=spg, fused=fused)  # warm-up of kernels and allocator
-        ids, tps, prof = generate(model, prompt, new, steps_per_graph=spg, fused=fused)
-        runs[(fused, spg)] = (tps, prof, ids)
-        log(f"[bench] decode e2e B={B} fused={fused} steps/graph={spg}: {tps:.1f} tok/s, "
-            f"{prof['ms_per_token']:.3f} ms/token")
-    best = max((k for k in runs if k[0]), key=lambda k: runs[k][0])
-    tps, prof, ids = runs[best]
-    same = all(torch.equal(r[2], ids) for k, r in runs.items() if k[0])
-    # first decode step of both step kinds from the same prefix: the fused step rounds the folded
+        generate(model, prompt, 1 + k, steps_per_graph=k, fused=fused, attention=attention)  # warm-up
+        torch.cuda.reset_peak_memory_stats(dev)
+        ids, tps, prof = generate(model, prompt, new, steps_per_graph=k, fused=fused, attention=attention)
+        runs[name] = (tps, prof, ids, torch.cuda.max_memory_allocated(dev))
+        log(f"[bench] decode e2e {name}: {tps:.1f} tok/s, {prof['ms_per_token']:.3f} ms/token")
+    head = "fused_torch_attention"
+    tps, prof, ids, peak = runs[head]
+    same = all(torch.equal(r[2], ids) for k, r in runs.items() if k.startswith("fused_torch"))
+    # first decode step of each step kind from the same prefix: the fused step rounds the folded
     # norm and the epilogues differently, so its logits are compared, not its greedy tokens (a
     # random-init model's logits are nearly flat, so any rounding difference flips near-ties)
-    from nanoquant_amd.decode import FusedDecoder, GraphDecoder
-    first = []
-    for cls in (GraphDecoder, FusedDecoder):
-        dec = cls(model, B, T + 2, device=dev)
+    first = {}
+    for name, make in (("unfused", lambda: GraphDecoder(model, B, T + 2, device=dev)),
+                       ("fused_torch_attention", lambda: FusedDecoder(model, B, T + 2, device=dev)),
+                       ("fused_hip_attention", lambda: FusedDecoder(model, B, T + 2, device=dev, attention="hip"))):
+        dec = make()
         dec.prefill(prompt)
-        first.append(dec.decode(1, use_graph=False).double())
+        first[name] = dec.decode(1, use_graph=False).double()
         del dec
-    step_rel = float((first[1] - first[0]).abs().max() / first[0].abs().max())
+    rel = {k: float((v - first["unfused"]).abs().max() / first["unfused"].abs().max())
+           for k, v in first.items() if k != "unfused"}
     # bytes one step must read: packed sign words and scales of every linear, the fp16
     # lm_head, one embedding row, and the K/V cache up to the step's position (mean over steps)
     lin_bytes = 0
@@ -334,13 +459,15 @@ def bench_decode(args, dev):
     gbs = step_bytes / (prof["ms_per_token"] * 1e-3) / 1e9
     return {"model": "random-init Llama-2-7B architecture, 7 NanoQuant linears per layer at 0.55 bpw (GEMV kernel)",
             "batch": B, "prompt": T, "new_tokens": new, "tokens_per_s": round(tps, 2),
-            "ms_per_token": round(prof["ms_per_token"], 4), "step": "fused (9 launches per layer)",
-            "steps_per_graph": best[1],
-            "tokens_per_s_by_variant": {("fused" if k[0] else "unfused") + f"_spg{k[1]}": round(v[0], 2)
-                                        for k, v in runs.items()},
-            "same_tokens_across_graph_sizes": bool(same), "fused_vs_unfused_first_step_logits_rel": step_rel,
-            "prefill_s": round(prof["prefill_time_s_wall"], 4),
-            "model_build_s": round(build_s, 2),
+            "ms_per_token": round(prof["ms_per_token"], 4),
+            "step": ("fused linears (q/k/v and gate/up stage 1 each one launch with RMSNorm folded in, SiLU*mul "
+                     "and residual epilogues) with RoPE, KV write and attention in torch ops; HIP graph"),
+            "steps_per_graph": spg,
+            "tokens_per_s_by_variant": {k: round(v[0], 2) for k, v in runs.items()},
+            "peak_memory_bytes_by_variant": {k: int(v[3]) for k, v in runs.items()},
+            "model_bytes": int(model_bytes), "linear_bytes": int(lin_bytes),
+            "same_tokens_across_graph_sizes": bool(same), "first_step_logits_rel_vs_unfused": rel,
+            "prefill_s": round(prof["prefill_time_s_wall"], 4), "model_build_s": round(build_s, 2),
             "roofline": {"bound": "hbm", "bytes_per_step": int(step_bytes), "achieved": round(gbs, 2),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                          "tokens_per_s_at_peak": round(B * HBM_PEAK_GBS * 1e9 / step_bytes, 1)}}
@@ -365,6 +492,10 @@ def sweep_shapes():
     return out
 
 
+def _words(gen, dev):
+    return lambda *shape: torch.randint(-2**31, 2**31 - 1, shape, dtype=torch.int32, device=dev, generator=gen)
+
+
 def run_sweep(args, dev):
     """One JSON line per (shape, kind, batch): GEMV at batch 1, 4, 16 over rotating packed copies (more than 512 MB
     in total, so the weights stream from HBM), GEMM at batch 256 and 2048. Weights are random sign words."""
@@ -373,8 +504,7 @@ def run_sweep(args, dev):
     kw = gemv_kwargs()
     gen = torch.Generator(device=dev).manual_seed(11)
     stream = torch.cuda.Stream(device=dev)
-    words = lambda *shape: torch.randint(-2**31, 2**31 - 1, shape, dtype=torch.int32, device=dev,  # noqa: E731
-                                         generator=gen)
+    words = _words(gen, dev)
     scales = lambda k: (torch.rand(k, device=dev, generator=gen) * 0.4 + 0.8).half()  # noqa: E731
     for model, name, m, n, r in sweep_shapes():
         pb = packed_bytes(m, n, r)
@@ -384,11 +514,8 @@ def run_sweep(args, dev):
         s_in, s_out = scales(n), scales(m)
         for B in (1, 4, 16):
             x = torch.randn(B, n, device=dev, generator=gen).half()
-
-            def steps():
-                return [op_gemv(x, s_in, Vs[i], None, Us[i], s_out, **kw) for i in range(copies)]
-
-            ms, graph, _ = time_graph(steps, copies, max(1, 1024 // copies), 1, stream)
+            ms, graph, _ = steady_ms(lambda: [op_gemv(x, s_in, Vs[i], None, Us[i], s_out, **kw)
+                                              for i in range(copies)], copies, stream, max(1, 1024 // copies), 1)
             del graph
             print(json.dumps({"kind": "gemv", "model": model, "linear": name, "m": m, "n": n, "r": r, "batch": B,
                               "us": round(ms * 1e3, 3), "packed_gbs": round(pb / (ms * 1e-3) / 1e9, 1),
@@ -401,11 +528,8 @@ def run_sweep(args, dev):
         ws = torch.zeros(m // 128 * 32, dtype=torch.int32, device=dev)
         for B in (256, 2048):
             x = torch.randn(B, n, device=dev, generator=gen).half()
-
-            def gsteps():
-                return [op_gemm(x, wv, wu, s_g, s_l, s_h, ws) for _ in range(4)]
-
-            ms, graph, _ = time_graph(gsteps, 4, 32, 16, stream)  # 64 warm-up calls, as the default GEMM line
+            ms, graph, _ = steady_ms(lambda: [op_gemm(x, wv, wu, s_g, s_l, s_h, ws) for _ in range(4)], 4, stream,
+                                     32, 16)  # 64 warm-up calls, as the default GEMM line
             del graph
             flops = 2.0 * B * r * (n + m)
             print(json.dumps({"kind": "gemm", "model": model, "linear": name, "m": m, "n": n, "r": r, "r_pad": r_pad,
@@ -427,9 +551,9 @@ def run_batch_sweep(args, dev):
     kw = gemv_kwargs()
     gen = torch.Generator(device=dev).manual_seed(12)
     stream = torch.cuda.Stream(device=dev)
-    words = lambda *shape: torch.randint(-2**31, 2**31 - 1, shape, dtype=torch.int32, device=dev,  # noqa: E731
-                                         generator=gen)
+    words = _words(gen, dev)
     scales = lambda k: (torch.rand(k, device=dev, generator=gen) * 0.4 + 0.8).half()  # noqa: E731
+    batches = [int(b) for b in args.batches.split(",")]
     for name, m, n in [("gate,up", 11008, 4096), ("down", 4096, 11008)]:
         r = rank_for_bpw(m, n, 0.55)
         r_pad = -(-r // 256) * 256
@@ -441,18 +565,15 @@ def run_batch_sweep(args, dev):
         Wu = [words(r_pad // 16, m // 2) for _ in range(copies)]
         s_in, s_out, s_l = scales(n), scales(m), scales(r_pad)
         ws = torch.zeros(m // 128 * 32, dtype=torch.int32, device=dev)
-        for B in (1, 2, 4, 8, 16, 32, 64, 128, 256):
+        for B in batches:
             x = torch.randn(B, n, device=dev, generator=gen).half()
             reps = max(1, 512 // copies)
-
-            def gemv_steps():
-                return [op_gemv(x, s_in, Vs[i], None, Us[i], s_out, **kw) for i in range(copies)]
-
-            def gemm_steps():
-                return [op_gemm(x, Wv[i], Wu[i], s_in, s_l, s_out, ws) for i in range(copies)]
-
-            for kind, fn in (("gemv", gemv_steps), ("gemm", gemm_steps)):
-                ms, graph, _ = time_graph(fn, copies, reps, 1, stream)
+            for kind in ("gemv", "gemm"):
+                if kind == "gemv":
+                    fn = lambda: [op_gemv(x, s_in, Vs[i], None, Us[i], s_out, **kw) for i in range(copies)]  # noqa
+                else:
+                    fn = lambda: [op_gemm(x, Wv[i], Wu[i], s_in, s_l, s_out, ws) for i in range(copies)]  # noqa
+                ms, graph, _ = steady_ms(fn, copies, stream, reps, 1)
                 del graph
                 print(json.dumps({"kind": kind, "linear": name, "m": m, "n": n, "r": r, "batch": B,
                                   "us": round(ms * 1e3, 3),
@@ -465,24 +586,29 @@ def run_batch_sweep(args, dev):
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2048, help="timed GEMV steps (rounded to whole graph replays)")
-    ap.add_argument("--warmup", type=int, default=256, help="untimed GEMV steps before timing")
+    ap.add_argument("--steps", type=int, default=256, help="timed GEMV steps of the headline line")
+    ap.add_argument("--warmup", type=int, default=64, help="untimed GEMV steps before them")
     ap.add_argument("--copies", type=int, default=128, help="distinct weight copies rotated through")
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--gemm-batch", type=int, default=2048)
     ap.add_argument("--gemm-steps", type=int, default=256, help="timed GEMM calls")
     ap.add_argument("--gemm-warmup", type=int, default=64, help="untimed GEMM calls before timing")
     ap.add_argument("--skip-gemm", action="store_true")
+    ap.add_argument("--skip-pack", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-seconds", type=float, default=8.0, help="bounded CPU sample per dtype of the dense path")
+    ap.add_argument("--cpu-pack-seconds", type=float, default=3.0, help="bounded CPU sample per packer")
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--skip-decode", action="store_true", help="skip the end-to-end decode measurement")
     ap.add_argument("--sweep", action="store_true",
                     help="measure GEMV (batch 1/4/16) and GEMM (batch 256/2048) on every config shape instead")
     ap.add_argument("--batch-sweep", action="store_true",
-                    help="measure GEMV and GEMM at batch 1..256 on the 7B gate and down shapes instead")
+                    help="measure GEMV and GEMM at the --batches sizes on the 7B gate and down shapes instead")
+    ap.add_argument("--batches", default="1,2,4,8,16,32,64,128,256")
     ap.add_argument("--decode-only", action="store_true",
                     help="run only the end-to-end decode and print its result alone (for kernel traces)")
+    ap.add_argument("--gemv-only", action="store_true",
+                    help="run only the headline GEMV and the per-shape GEMV figures (for kernel traces)")
     ap.add_argument("--e2e-batch", type=int, default=1)
     ap.add_argument("--e2e-prompt", type=int, default=128)
     ap.add_argument("--e2e-new", type=int, default=256)
@@ -495,6 +621,9 @@ def main():
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the path has no "
               "multi-GPU collective to measure. Run with --gpus 1.", file=sys.stderr)
         return 2
+    if args.steps < 1 or args.warmup < 0:
+        print("bench.py: --steps must be >= 1 and --warmup >= 0", file=sys.stderr)
+        return 2
     if not torch.cuda.is_available():
         print("bench.py: no GPU available", file=sys.stderr)
         return 1
@@ -506,41 +635,60 @@ def main():
     torch.cuda.set_device(dev)
 
     if args.sweep:  # every config shape, one JSON line each (not the headline line)
-        import nanoquant_amd  # noqa: F401
         run_sweep(args, dev)
         return 0
-
     if args.batch_sweep:  # the hand-over between the GEMV and the GEMM, one JSON line each
         run_batch_sweep(args, dev)
         return 0
-
     if args.decode_only:  # profiling aid: only the end-to-end decode, reported on its own line
         log(f"[bench] decode e2e B={args.e2e_batch} prompt={args.e2e_prompt} new={args.e2e_new}")
         print(json.dumps({"decode_e2e": bench_decode(args, dev)}), flush=True)
         return 0
 
-    log(f"[bench] gemv m={M} n={N} r={R} B={args.batch} copies={args.copies}")
-    g = bench_gemv(args, dev)
-    gemv_us = g["ms"] * 1e3
-    achieved = g["packed_bytes"] / (g["ms"] * 1e-3) / 1e9
-    s1_gbs = stage1_bytes(N, R) / (g["ms1"] * 1e-3) / 1e9
-    s2_gbs = stage2_bytes(M, R) / (g["ms2"] * 1e-3) / 1e9
-    log(f"[bench] gemv {gemv_us:.3f} us/step, {achieved:.1f} GB/s packed; "
-        f"stage 1 {g['ms1'] * 1e3:.3f} us ({s1_gbs:.1f} GB/s), stage 2 {g['ms2'] * 1e3:.3f} us ({s2_gbs:.1f} GB/s)")
+    m, n, r = SHAPES[HEADLINE]
+    log(f"[bench] gemv {HEADLINE} m={m} n={n} r={r} B={args.batch} copies={args.copies} "
+        f"warmup={args.warmup} steps={args.steps}")
+    pool, ms, y_head, graph_ok = bench_gemv_headline(args, dev)
+    pb = packed_bytes(m, n, r)
+    achieved = pb / (ms * 1e-3) / 1e9
+    log(f"[bench] gemv {HEADLINE}: {ms * 1e3:.3f} us/step over {args.steps} steps, {achieved:.1f} GB/s packed")
+    shapes = {HEADLINE: bench_gemv_shape(pool, dev)}
+    other = "gate" if HEADLINE == "down" else "down"
+    pool_other = GemvPool(other, args.copies, args.batch, dev, seed=2023)
+    shapes[other] = bench_gemv_shape(pool_other, dev)
+    parity_cases = {f"gemv_{HEADLINE}": (pool.case, y_head)}
+    op = torch.ops.binary_kernels.nanoquant_dyn_forward
+    y_other = op(pool_other.x, pool_other.s_in, pool_other.Vs[0], None, pool_other.Us[0], pool_other.s_out,
+                 **gemv_kwargs())
+    parity_cases[f"gemv_{other}"] = (pool_other.case, y_other)
+    for k, v in shapes.items():
+        log(f"[bench] gemv {k} steady: {v['us']} us ({v['frac_hbm']} of HBM peak), stage 1 "
+            f"{v['stage1']['us_per_launch']} us, stage 2 {v['stage2']['us_per_launch']} us")
+    del pool_other
+    if args.gemv_only:
+        print(json.dumps({"gemv_headline_us": round(ms * 1e3, 4), "gemv": shapes}), flush=True)
+        return 0
 
     if args.calib_copy_mib > 0:
         calibration_copy(dev, args.calib_copy_mib)
 
     gemm = None
     if not args.skip_gemm:
-        log(f"[bench] gemm B={args.gemm_batch}")
-        gm = bench_gemm(args, dev)
-        gemm = {"batch": args.gemm_batch, "us": round(gm["ms"] * 1e3, 2), "tflops": round(gm["tflops"], 2),
-                "roofline": {"bound": "mfma", "achieved": round(gm["tflops"], 2), "peak": MFMA_F16_PEAK_TFLOPS,
-                             "unit": "TFLOP/s", "frac": round(gm["tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
-                             "traffic": None},
-                "flops_per_call": gm["flops"], "r_pad": gm["r_pad"]}
-        log(f"[bench] gemm {gm['ms'] * 1e3:.1f} us, {gm['tflops']:.1f} TFLOP/s")
+        gemm = {}
+        for name in ("gate", "down"):
+            log(f"[bench] gemm {name} B={args.gemm_batch}")
+            res, c, y = bench_gemm(name, args, dev)
+            gemm[name] = res
+            parity_cases[f"gemm_{name}"] = (c, y)
+            log(f"[bench] gemm {name}: {res['us']} us, {res['tflops']} TFLOP/s")
+        torch.cuda.empty_cache()
+
+    pack = None
+    if not args.skip_pack:
+        log("[bench] pack")
+        pack = bench_pack(dev)
+        log(f"[bench] pack {json.dumps(pack)}")
+        torch.cuda.empty_cache()
 
     decode = None
     if not args.skip_decode:
@@ -548,48 +696,45 @@ def main():
         decode = bench_decode(args, dev)
 
     cpu = None
-    parity = {"gemv_rel_err": None, "gemm_rel_err": None}
+    parity = {}
     if not args.skip_cpu:
         log("[bench] cpu baseline and parity check")
         cpu = cpu_baseline(args)
-        log(f"[bench] cpu {cpu['value']} GB/s ({cpu['sample']})")
-        checked = check_parity({"gemv": g} if gemm is None else {"gemv": g, "gemm": gm})
-        parity = {"gemv_rel_err": checked["gemv"], "gemm_rel_err": checked.get("gemm")}
+        log(f"[bench] cpu {json.dumps(cpu)}")
+        parity = {f"{k}_rel_err": v for k, v in check_parity(parity_cases).items()}
         log(f"[bench] parity {parity}")
 
-    traffic, traffic_src = measured_traffic(args.batch)
+    head = shapes[HEADLINE]
+    traffic, traffic_src = measured_traffic("gemv", (m, n, r, args.batch))
     line = {
         "metric": METRIC,
         "value": round(achieved, 2),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": g["steps"],
-        "warmup": g["warmup"],
-        "ms_per_step": round(g["ms"], 6),
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f16",
         "data": "synthetic",
-        "config": {"workload": f"decode GEMV, Llama-2-7B gate_proj at 0.55 bpw (m={M}, n={N}, r={R}), batch "
+        "config": {"workload": f"decode GEMV, Llama-2-7B down_proj at 0.55 bpw (m={m}, n={n}, r={r}), batch "
                                f"{args.batch}, fp16 in / fp32 accumulate, {args.copies} rotating packed weight copies "
-                               f"({g['pool_bytes'] / 1e6:.0f} MB) replayed in a HIP graph",
-                   "m": M, "n": N, "r": R, "batch": args.batch, "copies": args.copies},
-        "gemv_us": round(gemv_us, 4),
-        "roofline": {"bound": "hbm", "kernel": "GEMV stage 2 (s2t_kernel, U sign words)",
-                     "achieved": round(s2_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(s2_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "algorithmic_bytes": stage2_bytes(M, R), "us_per_launch": round(g["ms2"] * 1e3, 4),
-                     "traffic_source": traffic_src},
-        "gemv_stages": {"stage1_us": round(g["ms1"] * 1e3, 4), "stage1_gbs": round(s1_gbs, 2),
-                        "stage1_bytes": stage1_bytes(N, R), "stage2_us": round(g["ms2"] * 1e3, 4),
-                        "stage2_gbs": round(s2_gbs, 2), "stage2_bytes": stage2_bytes(M, R),
-                        "op_frac_of_hbm_peak": round(achieved / HBM_PEAK_GBS, 4)},
-        "gemv_total_bytes_gbs": round(g["total_bytes"] / (g["ms"] * 1e-3) / 1e9, 2),
+                               f"({pb * args.copies / 1e6:.0f} MB) replayed in a HIP graph",
+                   "m": m, "n": n, "r": r, "batch": args.batch, "copies": args.copies},
+        "gemv_us": round(ms * 1e3, 4),
+        "roofline": {"bound": "hbm", "kernel": "the GEMV's two launches (s1w_kernel, then s2t_kernel)",
+                     "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_src,
+                     "algorithmic_bytes": pb, "us_per_op": round(ms * 1e3, 4),
+                     "kernels": {"stage1": head["stage1"], "stage2": head["stage2"]}},
+        "gemv": shapes,
         "gemm": gemm,
+        "pack": pack,
         "decode_e2e": decode,
         "cpu_baseline": cpu,
-        "parity": {**parity, "gemv_graph_matches_eager": g["graph_matches_eager"], "bar": 1e-3},
+        "parity": {**parity, "gemv_graph_matches_eager": graph_ok, "bar": 1e-3},
     }
     print(json.dumps(line), flush=True)
     return 0

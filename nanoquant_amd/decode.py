@@ -130,33 +130,43 @@ class StaticKVCache:
         self.key_index = torch.arange(max_len, device=device)
 
 
+def rotary_attention(shape: LlamaShape, layer: int, q, k, v, cos, sin, positions, cache: StaticKVCache):
+    """Rotary embedding, KV-cache write at ``positions`` and causal attention over the cache, in
+    torch ops (Hugging Face's Llama attention on a static cache).
+
+    q [B, T, H*D], k and v [B, T, KV*D] (strided views are fine), cos and sin [T, D];
+    returns [B, T, H*D] in the cache dtype.
+    """
+    H, KV, D = shape.heads, shape.kv_heads, shape.head_dim
+    B, T = q.shape[0], q.shape[1]
+    G = H // KV
+    q = q.reshape(B, T, H, D).transpose(1, 2)
+    k = k.reshape(B, T, KV, D).transpose(1, 2)
+    v = v.reshape(B, T, KV, D).transpose(1, 2)
+    q = q * cos + _rotate_half(q) * sin
+    k = k * cos + _rotate_half(k) * sin
+    k_c, v_c = cache.k[layer], cache.v[layer]
+    k_c.index_copy_(2, positions, k.to(k_c.dtype))
+    v_c.index_copy_(2, positions, v.to(v_c.dtype))
+    # queries of one kv head side by side, scored as K [B, KV, L, D] @ Q^T [B, KV, D, G*T]: the
+    # right operand is a small contiguous copy, never a transposed view, and the cache is read
+    # in place
+    qg_t = q.reshape(B, KV, G * T, D).transpose(2, 3).contiguous()
+    scores = torch.matmul(k_c, qg_t).transpose(2, 3).float() * (D ** -0.5)  # [B, KV, G*T, L]
+    visible = cache.key_index.view(1, -1) <= positions.view(-1, 1)  # [T, L]
+    scores = scores.reshape(B, KV, G, T, -1).masked_fill(~visible, float("-inf"))
+    p = torch.softmax(scores, dim=-1).to(v_c.dtype).reshape(B, KV, G * T, -1)
+    return torch.matmul(p, v_c).view(B, H, T, D).transpose(1, 2).reshape(B, T, H * D)
+
+
 class LlamaAttention(nn.Module):
     def __init__(self, shape: LlamaShape, layer: int):
         super().__init__()
         self.shape, self.layer = shape, layer
-        self.scaling = shape.head_dim ** -0.5
 
     def forward(self, x, cos, sin, positions, cache: StaticKVCache):
-        s = self.shape
-        B, T, _ = x.shape
-        H, KV, D = s.heads, s.kv_heads, s.head_dim
-        G = H // KV
-        q = self.q_proj(x).view(B, T, H, D).transpose(1, 2)
-        k = self.k_proj(x).view(B, T, KV, D).transpose(1, 2)
-        v = self.v_proj(x).view(B, T, KV, D).transpose(1, 2)
-        q = q * cos + _rotate_half(q) * sin
-        k = k * cos + _rotate_half(k) * sin
-        k_c, v_c = cache.k[self.layer], cache.v[self.layer]
-        k_c.index_copy_(2, positions, k.to(k_c.dtype))
-        v_c.index_copy_(2, positions, v.to(v_c.dtype))
-        # queries of one kv head side by side: [B, KV, G*T, D] @ [B, KV, D, L] (a contiguous copy
-        # of K^T, so the batched product never takes a transposed operand)
-        qg = q.reshape(B, KV, G * T, D)
-        scores = torch.matmul(qg, k_c.transpose(2, 3).contiguous()).float() * self.scaling
-        visible = cache.key_index.view(1, -1) <= positions.view(-1, 1)  # [T, L]
-        scores = scores.view(B, KV, G, T, -1).masked_fill(~visible, float("-inf"))
-        p = torch.softmax(scores, dim=-1).to(v_c.dtype).view(B, KV, G * T, -1)
-        out = torch.matmul(p, v_c).view(B, H, T, D).transpose(1, 2).reshape(B, T, H * D)
+        out = rotary_attention(self.shape, self.layer, self.q_proj(x), self.k_proj(x), self.v_proj(x), cos, sin,
+                               positions, cache)
         return self.o_proj(out.to(x.dtype))
 
 
@@ -359,7 +369,9 @@ class FusedDecoder(GraphDecoder):
     1. q, k, v stage 1 in one launch, with input_layernorm folded in (its weight multiplied
        into each s_in, the rsqrt(mean(x^2) + eps) factor applied to h);
     2. q, k, v stage 2 in one launch, into one [B, (heads + 2 kv_heads) * head_dim] buffer;
-    3. rotary embedding, KV-cache write and attention (``nq_attention_decode``);
+    3. rotary embedding, KV-cache write and attention: in torch ops (``attention="torch"``, the
+       default, as the benchmark's end-to-end configuration keeps the non-linear ops in
+       PyTorch) or in one HIP launch pair (``attention="hip"``, ``nq_attention_decode``);
     4, 5. o_proj, its stage 2 adding the residual;
     6. gate and up stage 1 in one launch, post_attention_layernorm folded in;
     7. gate and up stage 2 in one launch storing silu(gate) * up;
@@ -370,9 +382,13 @@ class FusedDecoder(GraphDecoder):
     """
 
     def __init__(self, model: NanoQuantLlama, batch: int, max_len: int, steps_per_graph: int = 1,
-                 device="cuda"):
+                 device="cuda", attention: str = "torch"):
         super().__init__(model, batch, max_len, steps_per_graph, device)
         from . import _lib
+
+        if attention not in ("torch", "hip"):
+            raise ValueError(f"attention must be 'torch' or 'hip', got {attention!r}")
+        self.attention = attention
 
         self._lib = _lib
         self.lib = _lib.load()
@@ -380,8 +396,8 @@ class FusedDecoder(GraphDecoder):
         dt = model.dtype
         if dt not in (torch.float16, torch.bfloat16):
             raise ValueError(f"the fused decode step needs a float16 or bfloat16 model, got {dt}")
-        if s.head_dim != 128:
-            raise ValueError(f"the fused decode step needs head_dim 128, got {s.head_dim}")
+        if attention == "hip" and s.head_dim != 128:
+            raise ValueError(f"the HIP attention of the fused decode step needs head_dim 128, got {s.head_dim}")
         for lin in model.linears():
             if getattr(lin, "kernel_type", None) != "gemv":
                 raise ValueError("the fused decode step needs every linear prepared for the 'gemv' kernel")
@@ -403,11 +419,12 @@ class FusedDecoder(GraphDecoder):
             for items, count in (plan["qkv"], plan["o"], plan["gu"], plan["down"]):
                 need = max(need, self.lib.nq_gemv_group_workspace_bytes(count, items, batch))
         self.ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=dev)
-        # attention workspace: the partial results of the 64-position chunks
-        abytes = self.lib.nq_attention_decode_workspace_bytes(batch, H, KV, D, max_len)
-        if abytes == 0:
-            raise ValueError("nq_attention_decode does not take this head layout")
-        self.attn_ws = torch.zeros(abytes, dtype=torch.uint8, device=dev)
+        self.attn_ws = None
+        if attention == "hip":  # the partial results of the 64-position chunks
+            abytes = self.lib.nq_attention_decode_workspace_bytes(batch, H, KV, D, max_len)
+            if abytes == 0:
+                raise ValueError("nq_attention_decode does not take this head layout")
+            self.attn_ws = torch.zeros(abytes, dtype=torch.uint8, device=dev)
 
     def _scale_in(self, lin, norm_weight):
         s_in = lin.scale_pre
@@ -460,17 +477,26 @@ class FusedDecoder(GraphDecoder):
         st = self._lib.stream_of(self.device)
         tok = self.ids.index_select(1, self.pos).view(-1)
         torch.index_select(self.model.model.embed_tokens.weight, 0, tok, out=self.x)
+        if self.attention == "torch":
+            cos = self.rope_cos.index_select(0, self.pos)
+            sin = self.rope_sin.index_select(0, self.pos)
         x, h, qkv, attn, act = (t.data_ptr() for t in (self.x, self.h, self.qkv, self.attn, self.act))
         esz = self.qkv.element_size()
         for li, plan in enumerate(self.plans):
             items, n = plan["qkv"]
             self._check(lib.nq_gemv_group_stage1(dt, n, items, x, B, s.hidden, plan["eps1"], ws, wsb, st), "qkv 1")
             self._check(lib.nq_gemv_group_stage2(dt, n, items, B, self._lib.NQ_EPI_STORE, ws, wsb, st), "qkv 2")
-            self._check(lib.nq_attention_decode(
-                dt, qkv, qkv + H * D * esz, qkv + (H + KV) * D * esz, self.qkv_width,
-                self.cache.k[li].data_ptr(), self.cache.v[li].data_ptr(), self.rope_cos.data_ptr(),
-                self.rope_sin.data_ptr(), self.pos.data_ptr(), attn, B, H, KV, D, self.max_len,
-                D ** -0.5, self.attn_ws.data_ptr(), self.attn_ws.numel(), st), "attention")
+            if self.attention == "hip":
+                self._check(lib.nq_attention_decode(
+                    dt, qkv, qkv + H * D * esz, qkv + (H + KV) * D * esz, self.qkv_width,
+                    self.cache.k[li].data_ptr(), self.cache.v[li].data_ptr(), self.rope_cos.data_ptr(),
+                    self.rope_sin.data_ptr(), self.pos.data_ptr(), attn, B, H, KV, D, self.max_len,
+                    D ** -0.5, self.attn_ws.data_ptr(), self.attn_ws.numel(), st), "attention")
+            else:
+                q3 = self.qkv.view(B, 1, self.qkv_width)
+                out = rotary_attention(s, li, q3[..., :H * D], q3[..., H * D:(H + KV) * D],
+                                       q3[..., (H + KV) * D:], cos, sin, self.pos, self.cache)
+                self.attn.copy_(out.view(B, H * D))
             items, n = plan["o"]
             self._check(lib.nq_gemv_group_stage1(dt, n, items, attn, B, H * D, -1.0, ws, wsb, st), "o 1")
             self._check(lib.nq_gemv_group_stage2(dt, n, items, B, self._lib.NQ_EPI_RESIDUAL, ws, wsb, st), "o 2")
@@ -490,7 +516,8 @@ class FusedDecoder(GraphDecoder):
 
 @torch.no_grad()
 def generate(model: NanoQuantLlama, prompt: torch.Tensor, max_new_tokens: int, steps_per_graph: int = 1,
-             use_graph: bool = True, decoder: GraphDecoder | None = None, fused: bool = False):
+             use_graph: bool = True, decoder: GraphDecoder | None = None, fused: bool = False,
+             attention: str = "torch"):
     """Greedy generation with decode timing (test_decode.py:474-693, greedy instead of top-k sampling).
 
     Returns (ids [B, T + max_new_tokens], tokens_per_s, prof). Token 1 comes from the
@@ -499,8 +526,11 @@ def generate(model: NanoQuantLlama, prompt: torch.Tensor, max_new_tokens: int, s
     """
     B, T = prompt.shape
     if decoder is None:
-        cls = FusedDecoder if fused else GraphDecoder
-        decoder = cls(model, B, T + max_new_tokens, steps_per_graph, device=prompt.device)
+        if fused:
+            decoder = FusedDecoder(model, B, T + max_new_tokens, steps_per_graph, device=prompt.device,
+                                   attention=attention)
+        else:
+            decoder = GraphDecoder(model, B, T + max_new_tokens, steps_per_graph, device=prompt.device)
         if use_graph:
             decoder.capture()
     steps = max_new_tokens - 1

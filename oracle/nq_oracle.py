@@ -28,7 +28,7 @@ __all__ = [
     "pack_binary_marlin", "unpack_binary_marlin", "pack_binary_marlin_fused",
     "MARLIN_MIN_MAX_PAR", "nanoquant_forward_f64", "compute_forward_torch",
     "gemv_output_shape", "check_gemv_tuning", "GEMV_TUNING_CHOICES",
-    "marlin_onebit_output_shape", "round_rank", "random_case",
+    "marlin_onebit_output_shape", "round_rank", "random_case", "pack_signs_torch", "unpack_signs_torch",
 ]
 
 MARLIN_MIN_MAX_PAR = 32  # kernel/utils.py:21, gemm.cpp:33
@@ -257,6 +257,38 @@ def compute_forward_torch(x, V, U, scale_pre, scale_mid, scale_post):
         y = y * scale_mid
     y = F.linear(y, U)
     return y * scale_post
+
+
+def pack_signs_torch(signs, method: str = "lsb_first"):
+    """The packer of kernel/utils.py:51-113 as eager torch ops on the CPU (the timed CPU baseline
+    of packing; the reference decorates it with torch.compile, whose compile time the baseline
+    leaves out). Pad to 32 columns with +1 (:87-93), bits (1 - v) // 2 (:96), int32 weights 2^bit
+    in ``method`` order (:99-109), int32 sum with wraparound (:112). Checked against
+    :func:`pack_binary_gemv` in tests/test_oracle.py."""
+    import torch
+
+    rows, cols = signs.shape
+    words = (cols + 31) // 32
+    if words * 32 != cols:
+        signs = torch.cat([signs, torch.ones(rows, words * 32 - cols, dtype=signs.dtype)], dim=1)
+    bits = ((1 - signs) // 2).int().view(rows, words, 32)
+    weights = torch.from_numpy((np.uint64(1) << bit_position(method).astype(np.uint64)).astype(np.uint32)
+                               .view(np.int32).copy())
+    return (bits * weights).sum(dim=2, dtype=torch.int32).contiguous()
+
+
+def unpack_signs_torch(packed, shape, method: str = "lsb_first"):
+    """The unpacker of kernel/utils.py:116-183 as eager torch ops on the CPU (timed CPU baseline):
+    every bit extracted with a shift by its position and ``& 1`` (:172), trimmed to the original
+    columns (:178), 0 -> +1 and 1 -> -1 (:183). Checked against :func:`unpack_binary_gemv`."""
+    import torch
+
+    rows, cols = (int(v) for v in shape)
+    words = (cols + 31) // 32
+    shifts = torch.from_numpy(bit_position(method).astype(np.int32))
+    bits = (packed.unsqueeze(2) >> shifts) & 1
+    flat = bits.view(rows, words * 32).to(torch.int8)[:, :cols]
+    return (1 - 2 * flat).to(torch.int8)
 
 
 # ---------------------------------------------------------------------------

@@ -121,10 +121,10 @@ FUSED_SHAPES = {
 }
 
 
-def run_fused(model, prompt, new, use_graph, steps_per_graph=1):
+def run_fused(model, prompt, new, use_graph, steps_per_graph=1, attention="torch"):
     from nanoquant_amd.decode import FusedDecoder
     B, T = prompt.shape
-    dec = FusedDecoder(model, B, T + new, steps_per_graph=steps_per_graph)
+    dec = FusedDecoder(model, B, T + new, steps_per_graph=steps_per_graph, attention=attention)
     if use_graph:
         dec.capture()
     logits = [dec.prefill(prompt.cuda()).clone()]
@@ -139,10 +139,11 @@ def run_fused(model, prompt, new, use_graph, steps_per_graph=1):
     return dec.ids[:, :T + new].cpu(), [lg.cpu() for lg in logits]
 
 
+@pytest.mark.parametrize("attention", ["torch", "hip"])
 @pytest.mark.parametrize("name", list(FUSED_SHAPES))
-def test_fused_decode_matches_dense(name):
+def test_fused_decode_matches_dense(name, attention):
     shape = FUSED_SHAPES[name]
-    announce("fused decode", name, shape)
+    announce("fused decode", name, attention, shape)
     from nanoquant_amd import _lib
     _lib.load()
     dense = random_llama(shape, bpw=0.55, seed=13, device="cpu", with_mid=(name == "gqa"))
@@ -153,8 +154,8 @@ def test_fused_decode_matches_dense(name):
     model = kernel_model(dense, "gemv")
     prompt = torch.randint(0, shape.vocab, (2, 12), generator=torch.Generator().manual_seed(3))
     new = 9
-    ids_g, lg_g = run_fused(model, prompt, new, use_graph=True, steps_per_graph=2)
-    ids_e, lg_e = run_fused(model, prompt, new, use_graph=False)
+    ids_g, lg_g = run_fused(model, prompt, new, use_graph=True, steps_per_graph=2, attention=attention)
+    ids_e, lg_e = run_fused(model, prompt, new, use_graph=False, attention=attention)
     assert torch.equal(ids_g, ids_e)
     for j, (a, b) in enumerate(zip(lg_g, lg_e[::2])):
         assert torch.equal(a, b), j

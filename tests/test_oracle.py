@@ -195,3 +195,19 @@ def test_tuning_rules():
     assert name == "n_acc1" and msg == "n_acc1 should be one of [1, 2], but 4 was given"
     assert O.check_gemv_tuning(32, 128, 2, 2, 1, 1, 8, 8)[0] == "n_th1"
     assert O.check_gemv_tuning(128, 128, 2, 3, 1, 1, 8, 8)[0] == "n_rpw2"
+
+
+@pytest.mark.parametrize("method", ["lsb_first", "half2"])
+@pytest.mark.parametrize("shape", [(1, 1), (5, 33), (17, 100), (64, 4096)])
+def test_torch_eager_packers_match_the_numpy_oracle(method, shape):
+    """The eager-torch packers (the CPU baseline of packing) give the pinned numpy oracle's words,
+    including bit 31 (int32 wraparound) and the +1 padding of a partial word."""
+    import torch
+    rng = np.random.default_rng(shape[0] * 131 + shape[1])
+    s = np.where(rng.random(shape) < 0.5, -1, 1).astype(np.int8)
+    s[0, :min(32, shape[1])] = -1  # a word (or its valid part) of all -1, bit 31 set
+    words = O.pack_signs_torch(torch.from_numpy(s), method)
+    assert words.dtype == torch.int32
+    np.testing.assert_array_equal(words.numpy().view(np.uint32), O.pack_binary_gemv(s, method))
+    back = O.unpack_signs_torch(words, shape, method)
+    np.testing.assert_array_equal(back.numpy(), s)
