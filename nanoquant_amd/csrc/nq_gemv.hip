@@ -264,8 +264,8 @@ __device__ inline Item pick_item(const Table& tab) {
 
 // --------------------------------------------------------------------------- stage 1, VALU rows
 //
-// Block = 4 waves = 4/WR groups of WR waves; group gi owns rows j0 .. j0+R-1 (j0 = block row
-// base + gi*R) of its item. Lane p = (wave % WR)*64 + lane of a group holds words
+// Block = G groups of WR waves; group gi owns rows j0 .. j0+R-1 (j0 = block row base + gi*R) of
+// its item. Lane p = (wave % WR)*64 + lane of a group holds words
 // q_w = p + 64*WR*w (w < WPL) of those rows: consecutive lanes read consecutive words.
 // Requires n % 8 == 0 (an 8-column piece is wholly inside or outside a row) and 16-byte
 // aligned x and s_in.
@@ -273,10 +273,10 @@ __device__ inline Item pick_item(const Table& tab) {
 // kNorm folds an RMSNorm of x into the stage: every group also sums x^2 over the whole row
 // (the lanes hold all of x anyway) and h is multiplied by rsqrt(sum / n + eps); the norm's
 // weight is expected inside s_in.
-template <typename T, int NB, int WPL, int WR, int R, bool kNorm, bool kOne>
-__global__ __launch_bounds__(256) void s1w_kernel(const S1Table tab, const uint16_t* __restrict__ x, int batch, int n,
-                                                  int wn, float eps) {
-    constexpr int kGroups = 4 / WR;
+template <typename T, int NB, int WPL, int WR, int R, int G, bool kNorm, bool kOne>
+__global__ __launch_bounds__(G * WR * 64) void s1w_kernel(const S1Table tab, const uint16_t* __restrict__ x, int batch,
+                                                          int n, int wn, float eps) {
+    constexpr int kGroups = G;
     constexpr int kRows = kGroups * R;
     constexpr int kPartRows = R + (kNorm ? 1 : 0);
     __shared__ float part[kGroups * kPartRows * NB * WR];
@@ -910,36 +910,48 @@ void launch_stage2_generic(const GemvArgs& a) {
 // rows per group (6.2 with two words over four waves, 6.5 and 7.7 with six and eight rows).
 // A table of several items (the decode step's q/k/v and gate/up groups) at n = 4096 takes four
 // rows per group: 612.0 against 608.8 tokens/s end to end, repeatable.
-inline int s1w_rows_per_block(int wn, bool grouped) {
-    if (wn <= 64) return 4 * 2;      // <WPL 1, WR 1, R 2>
-    if (wn <= 128) return grouped ? 2 * 4 : 2 * 2;  // <1, 2, 4> or <1, 2, 2>
-    if (wn <= 256) return 2 * 4;     // <2, 2, 4>
-    if (wn <= 384) return 2 * 4;     // <3, 2, 4>
-    if (wn <= 512) return 1 * 4;     // <2, 4, 4>
-    return 0;
+// Launch shape of s1w_kernel: WPL words per lane, WR waves per row group, R rows per group, G
+// groups per block (G * WR * 64 threads, R * G rows). The lanes of a group cover 64 * WR * WPL
+// >= wn words of a row.
+struct S1wShape {
+    int wpl, wr, r, g;
+};
+
+// The instantiated shapes (wpl, wr, r, g).
+#ifndef NQ_S1W_SHAPES
+#define NQ_S1W_SHAPES(X) X(1, 1, 2, 4) X(1, 2, 4, 2) X(1, 2, 2, 2) X(2, 2, 4, 2) X(3, 2, 4, 2) X(2, 4, 4, 1)
+#endif
+
+inline S1wShape s1w_shape(int wn, bool grouped) {
+    if (wn <= 64) return {1, 1, 2, 4};
+    if (wn <= 128) return grouped ? S1wShape{1, 2, 4, 2} : S1wShape{1, 2, 2, 2};
+    if (wn <= 256) return {2, 2, 4, 2};
+    if (wn <= 384) return {3, 2, 4, 2};
+    return {2, 4, 4, 1};
 }
 
 template <typename T, int NB, bool kNorm, bool kOne>
-void launch_s1w_cfg(const S1Table& tab, int blocks, const uint16_t* x, int batch, int n, int wn, float eps,
-                    hipStream_t st) {
+void launch_s1w_cfg(const S1wShape& sh, const S1Table& tab, int blocks, const uint16_t* x, int batch, int n, int wn,
+                    float eps, hipStream_t st) {
     const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(ceil_div(batch, NB)));
-    if (wn <= 64) s1w_kernel<T, NB, 1, 1, 2, kNorm, kOne><<<grid, 256, 0, st>>>(tab, x, batch, n, wn, eps);
-    else if (wn <= 128 && !kOne) s1w_kernel<T, NB, 1, 2, 4, kNorm, kOne><<<grid, 256, 0, st>>>(tab, x, batch, n, wn, eps);
-    else if (wn <= 128) s1w_kernel<T, NB, 1, 2, 2, kNorm, kOne><<<grid, 256, 0, st>>>(tab, x, batch, n, wn, eps);
-    else if (wn <= 256) s1w_kernel<T, NB, 2, 2, 4, kNorm, kOne><<<grid, 256, 0, st>>>(tab, x, batch, n, wn, eps);
-    else if (wn <= 384) s1w_kernel<T, NB, 3, 2, 4, kNorm, kOne><<<grid, 256, 0, st>>>(tab, x, batch, n, wn, eps);
-    else s1w_kernel<T, NB, 2, 4, 4, kNorm, kOne><<<grid, 256, 0, st>>>(tab, x, batch, n, wn, eps);
+#define NQ_S1W_CASE(WPL, WR, R, G)                                                                        \
+    if (sh.wpl == WPL && sh.wr == WR && sh.r == R && sh.g == G) {                                         \
+        s1w_kernel<T, NB, WPL, WR, R, G, kNorm, kOne><<<grid, G * WR * 64, 0, st>>>(tab, x, batch, n, wn, eps); \
+        return;                                                                                           \
+    }
+    NQ_S1W_SHAPES(NQ_S1W_CASE)
+#undef NQ_S1W_CASE
 }
 
 template <typename T, int NB>
-void launch_s1w_nb(const S1Table& tab, int blocks, const uint16_t* x, int batch, int n, int wn, bool norm, float eps,
-                   hipStream_t st) {
+void launch_s1w_nb(const S1wShape& sh, const S1Table& tab, int blocks, const uint16_t* x, int batch, int n, int wn,
+                   bool norm, float eps, hipStream_t st) {
     if (tab.count == 1) {
-        if (norm) launch_s1w_cfg<T, NB, true, true>(tab, blocks, x, batch, n, wn, eps, st);
-        else launch_s1w_cfg<T, NB, false, true>(tab, blocks, x, batch, n, wn, eps, st);
+        if (norm) launch_s1w_cfg<T, NB, true, true>(sh, tab, blocks, x, batch, n, wn, eps, st);
+        else launch_s1w_cfg<T, NB, false, true>(sh, tab, blocks, x, batch, n, wn, eps, st);
     } else {
-        if (norm) launch_s1w_cfg<T, NB, true, false>(tab, blocks, x, batch, n, wn, eps, st);
-        else launch_s1w_cfg<T, NB, false, false>(tab, blocks, x, batch, n, wn, eps, st);
+        if (norm) launch_s1w_cfg<T, NB, true, false>(sh, tab, blocks, x, batch, n, wn, eps, st);
+        else launch_s1w_cfg<T, NB, false, false>(sh, tab, blocks, x, batch, n, wn, eps, st);
     }
 }
 
@@ -949,14 +961,15 @@ void launch_s1w_nb(const S1Table& tab, int blocks, const uint16_t* x, int batch,
 template <typename T>
 void launch_s1w_table(S1Table& tab, const uint16_t* x, int batch, int n, int wn, bool norm, float eps,
                       hipStream_t st) {
-    const int rpb = s1w_rows_per_block(wn, tab.count > 1);
+    const S1wShape sh = s1w_shape(wn, tab.count > 1);
+    const int rpb = sh.r * sh.g;
     int blocks = 0;
     for (int k = 0; k < tab.count; ++k) {
         tab.item[k].block_begin = blocks;
         blocks += static_cast<int>(ceil_div(tab.item[k].kpad, rpb));
     }
-    if (batch <= 1) launch_s1w_nb<T, 1>(tab, blocks, x, batch, n, wn, norm, eps, st);
-    else launch_s1w_nb<T, 2>(tab, blocks, x, batch, n, wn, norm, eps, st);
+    if (batch <= 1) launch_s1w_nb<T, 1>(sh, tab, blocks, x, batch, n, wn, norm, eps, st);
+    else launch_s1w_nb<T, 2>(sh, tab, blocks, x, batch, n, wn, norm, eps, st);
 }
 
 // Dwords s1m_kernel stages in LDS: 16 rows of sign words, and the s_in pairs when they fit too

@@ -159,14 +159,61 @@ def rotary_attention(shape: LlamaShape, layer: int, q, k, v, cos, sin, positions
     return torch.matmul(p, v_c).view(B, H, T, D).transpose(1, 2).reshape(B, T, H * D)
 
 
+def rotary_step_tables(cos, sin, positions, cache: StaticKVCache, dtype):
+    """What every layer of a one-token step at ``positions`` (one position, on the device) shares:
+    the rotary embedding as a [D, D] matrix R (x @ R == x * cos + rotate_half(x) * sin, with cos and
+    sin [1, D] of that position) and the causal mask as an additive [1, L, 1] (0 for visible cache
+    rows, -inf past the position)."""
+    D = cos.shape[-1]
+    h = D // 2
+    c, s_ = cos.float().view(-1), sin.float().view(-1)
+    R = torch.diag_embed(c)
+    idx = torch.arange(h, device=cos.device)
+    R[idx + h, idx] = -s_[:h]  # out[j < h] takes -x[j + h] * sin[j]
+    R[idx, idx + h] = s_[h:]   # out[j >= h] takes x[j - h] * sin[j]
+    visible = cache.key_index.view(1, -1, 1) <= positions.view(1, 1, 1)
+    madd = torch.zeros(visible.shape, device=cos.device, dtype=dtype).masked_fill_(~visible, float("-inf"))
+    return R.to(dtype), madd
+
+
+def rotary_attention_step(shape: LlamaShape, layer: int, qk, v, tables, positions, cache: StaticKVCache):
+    """``rotary_attention`` for one token per sequence in seven torch launches: RoPE of q and k as one
+    matrix product, the two cache writes, the scores of each kv head's query group with the scale and
+    the causal mask folded into one batched product, the softmax, the value product and the copy out.
+
+    qk [B, (H + KV) * D] (q heads then k heads, contiguous), v [B, KV * D]; ``tables`` from
+    ``rotary_step_tables``; returns [B, 1, H * D].
+    """
+    H, KV, D = shape.heads, shape.kv_heads, shape.head_dim
+    B, G = qk.shape[0], H // KV
+    R, madd = tables
+    k_c, v_c = cache.k[layer], cache.v[layer]
+    L = k_c.shape[2]
+    rot = torch.mm(qk.reshape(-1, D), R).view(B, H + KV, D)
+    k_c.index_copy_(2, positions, rot[:, H:].unsqueeze(2).to(k_c.dtype))
+    v_c.index_copy_(2, positions, v.reshape(B, KV, 1, D).to(v_c.dtype))
+    # K [B*KV, L, D] @ Q^T [B*KV, D, G]: the right operand is a contiguous copy (free for one query per kv head)
+    q_t = rot[:, :H].reshape(B * KV, G, D).transpose(1, 2).contiguous()
+    scores = torch.baddbmm(madd, k_c.view(B * KV, L, D), q_t.to(k_c.dtype), alpha=D ** -0.5)  # [B*KV, L, G]
+    p = torch.softmax(scores, dim=1)
+    out_t = torch.bmm(v_c.view(B * KV, L, D).transpose(1, 2), p)  # [B*KV, D, G]
+    return out_t.view(B, KV, D, G).transpose(2, 3).reshape(B, 1, H * D)
+
+
 class LlamaAttention(nn.Module):
     def __init__(self, shape: LlamaShape, layer: int):
         super().__init__()
         self.shape, self.layer = shape, layer
 
-    def forward(self, x, cos, sin, positions, cache: StaticKVCache):
-        out = rotary_attention(self.shape, self.layer, self.q_proj(x), self.k_proj(x), self.v_proj(x), cos, sin,
-                               positions, cache)
+    def forward(self, x, cos, sin, positions, cache: StaticKVCache, step_tables=None):
+        if step_tables is not None:  # one token per sequence
+            B = x.shape[0]
+            qk = torch.cat((self.q_proj(x), self.k_proj(x)), dim=-1).view(B, -1)
+            out = rotary_attention_step(self.shape, self.layer, qk, self.v_proj(x).view(B, -1), step_tables,
+                                        positions, cache)
+        else:
+            out = rotary_attention(self.shape, self.layer, self.q_proj(x), self.k_proj(x), self.v_proj(x), cos, sin,
+                                   positions, cache)
         return self.o_proj(out.to(x.dtype))
 
 
@@ -183,8 +230,8 @@ class LlamaDecoderLayer(nn.Module):
         self.input_layernorm = RMSNorm(shape.hidden, shape.rms_eps, device, dtype)
         self.post_attention_layernorm = RMSNorm(shape.hidden, shape.rms_eps, device, dtype)
 
-    def forward(self, x, cos, sin, positions, cache):
-        x = x + self.self_attn(self.input_layernorm(x), cos, sin, positions, cache)
+    def forward(self, x, cos, sin, positions, cache, step_tables=None):
+        x = x + self.self_attn(self.input_layernorm(x), cos, sin, positions, cache, step_tables)
         return x + self.mlp(self.post_attention_layernorm(x))
 
 
@@ -228,8 +275,9 @@ class NanoQuantLlama(nn.Module):
     def forward(self, ids, positions, cache: StaticKVCache):
         x = self.model.embed_tokens(ids)
         cos, sin = self.rope(positions, x.dtype)
+        tables = rotary_step_tables(cos, sin, positions, cache, x.dtype) if ids.shape[1] == 1 else None
         for layer in self.model.layers:
-            x = layer(x, cos, sin, positions, cache)
+            x = layer(x, cos, sin, positions, cache, tables)
         x = self.model.norm(x)
         return self.lm_head(x).float()
 
@@ -478,8 +526,9 @@ class FusedDecoder(GraphDecoder):
         tok = self.ids.index_select(1, self.pos).view(-1)
         torch.index_select(self.model.model.embed_tokens.weight, 0, tok, out=self.x)
         if self.attention == "torch":
-            cos = self.rope_cos.index_select(0, self.pos)
-            sin = self.rope_sin.index_select(0, self.pos)
+            tables = rotary_step_tables(self.rope_cos.index_select(0, self.pos),
+                                        self.rope_sin.index_select(0, self.pos), self.pos, self.cache,
+                                        self.model.dtype)
         x, h, qkv, attn, act = (t.data_ptr() for t in (self.x, self.h, self.qkv, self.attn, self.act))
         esz = self.qkv.element_size()
         for li, plan in enumerate(self.plans):
@@ -493,9 +542,8 @@ class FusedDecoder(GraphDecoder):
                     self.rope_sin.data_ptr(), self.pos.data_ptr(), attn, B, H, KV, D, self.max_len,
                     D ** -0.5, self.attn_ws.data_ptr(), self.attn_ws.numel(), st), "attention")
             else:
-                q3 = self.qkv.view(B, 1, self.qkv_width)
-                out = rotary_attention(s, li, q3[..., :H * D], q3[..., H * D:(H + KV) * D],
-                                       q3[..., (H + KV) * D:], cos, sin, self.pos, self.cache)
+                out = rotary_attention_step(s, li, self.qkv[:, :(H + KV) * D], self.qkv[:, (H + KV) * D:], tables,
+                                            self.pos, self.cache)
                 self.attn.copy_(out.view(B, H * D))
             items, n = plan["o"]
             self._check(lib.nq_gemv_group_stage1(dt, n, items, attn, B, H * D, -1.0, ws, wsb, st), "o 1")
