@@ -253,6 +253,15 @@ int nq_attention_decode(int dtype, const void* q, const void* k, const void* v, 
                         int64_t head_dim, int64_t max_len, float scaling, void* workspace, size_t workspace_bytes,
                         nq_stream_t stream);
 
+/* ---------------------------------------------------------------- measurement aid */
+
+/* Enqueue a one-thread kernel that writes the GPU's constant-rate wall clock to *dst (device
+ * memory) when it runs: stream-ordered timestamps that can sit inside a HIP graph, around steps
+ * of the graph itself. No counterpart in the reference (a benchmarking aid). */
+int nq_timestamp(uint64_t* dst, nq_stream_t stream);
+/* Ticks per second of that clock on the current device (0 on error). */
+int64_t nq_wall_clock_hz(void);
+
 #ifdef __cplusplus
 }
 #endif

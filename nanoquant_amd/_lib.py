@@ -78,6 +78,8 @@ SIGNATURES = {
     "nq_gemm_nanoquant_workspace_bytes": (_size, [_i64, _i64, _i64, _i64]),
     "nq_gemm_nanoquant": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _size,
                                  _vp]),
+    "nq_timestamp": (_int, [_vp, _vp]),
+    "nq_wall_clock_hz": (_i64, []),
 }
 
 

@@ -116,6 +116,21 @@ __device__ inline uint32_t bit_select(uint32_t mask, uint32_t a, uint32_t b) {
     return r;
 }
 
+// Buffer resource over `bytes` bytes at `base` (raw, stride 0): a load at or past `bytes` returns
+// zero, and offsets are 32-bit (no 64-bit address arithmetic per lane). The last word is the
+// gfx9 data-format field for untyped 32-bit access.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ inline rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
+}
+__device__ inline u32x4 load_b128(rsrc_t rs, uint32_t offset) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(offset), 0, 0));
+}
+// Streaming load (read once: non-temporal)
+__device__ inline uint32_t load_b32_stream(rsrc_t rs, uint32_t offset) {
+    return __builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<int>(offset), 0, 2);
+}
+
 template <typename T>
 __device__ inline uint16_t saturate_to(float v, float sat) {
     v = fminf(fmaxf(v, -sat), sat);  // as the reference's clamp: a NaN input becomes -sat

@@ -550,7 +550,8 @@ void launch_dm_split(const void* A, const uint32_t* W, const void* s_in, const v
 // grid decides the rest:
 //   >= 512 tiles (two per CU): one block per tile;
 //   128-511 tiles: K split over two wave groups inside each block (B = 2048, K = 4096,
-//     N = 1792: 46 -> 38 us);
+//     N = 1792: 46 -> 38 us). Compiled for four waves per SIMD this stage alone ran 33.6 against
+//     37.6 us in isolation, but the two-stage op ran 124.8 against 121 us, so it stays at two;
 //   fewer (B = 256 and the rank-wide stages): K split over up to 512 / tiles ranges of at least
 //     8 steps across the grid, fp32 sums into the caller's workspace, then a finishing launch;
 //     without that workspace, as above. (Against 512 / 4 and 256 / 8 over the B = 256 shapes of

@@ -270,6 +270,12 @@ __device__ inline Item pick_item(const Table& tab) {
 // Requires n % 8 == 0 (an 8-column piece is wholly inside or outside a row) and 16-byte
 // aligned x and s_in.
 //
+// Every operand comes through a buffer resource sized to its array (x per batch row), so a
+// lane's loads past the row or past the rank return zero: a zero s_in pair makes the lane's
+// products zero, so nothing is clamped or masked. The signs of a word's pair p are the word
+// shifted left by p under the sign mask; xor-ing them onto the s_in pair (one v_bitop3) gives
+// +-s_in exactly whatever the sign of s_in, and v_dot2 adds the two exact products in fp32.
+//
 // kNorm folds an RMSNorm of x into the stage: every group also sums x^2 over the whole row
 // (the lanes hold all of x anyway) and h is multiplied by rsqrt(sum / n + eps); the norm's
 // weight is expected inside s_in.
@@ -291,72 +297,56 @@ __global__ __launch_bounds__(G * WR * 64) void s1w_kernel(const S1Table tab, con
     const int b0 = blockIdx.y * NB;
     NQ_STAMP(0);
 
-    // every global load first
-    int qc[WPL];
+    const uint32_t row_bytes = static_cast<uint32_t>(n) * 2u;
+    const rsrc_t s_rs = make_rsrc(it.s_in, row_bytes);
+    const rsrc_t v_rs = make_rsrc(it.v_bits, static_cast<uint32_t>(r) * static_cast<uint32_t>(wn) * 4u);
+    rsrc_t x_rs[NB];
 #pragma unroll
-    for (int w = 0; w < WPL; ++w) qc[w] = min(p + 64 * WR * w, wn - 1);
-    uint32_t vb[R][WPL];
+    for (int b = 0; b < NB; ++b)
+        x_rs[b] = make_rsrc(x + static_cast<size_t>(min(b0 + b, batch - 1)) * static_cast<size_t>(n),
+                            b0 + b < batch ? row_bytes : 0u);
     // the mid scales, raw until the end; without s_mid the (unused) loads read s_in
     const uint16_t* msrc = it.s_mid != nullptr ? it.s_mid : it.s_in;
     const int mlim = (it.s_mid != nullptr ? r : n) - 1;
     uint16_t mid[R];
 #pragma unroll
     for (int k = 0; k < R; ++k) mid[k] = msrc[min(j0 + k, mlim)];
+    // s_in and x first (from L2), then V's words (from HBM), each in 16- and 4-byte pieces
     uint32_t sp[WPL][16];
     uint32_t xp[WPL][NB][16];
 #pragma unroll
     for (int w = 0; w < WPL; ++w)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-            const int k0 = min(32 * qc[w] + 8 * v, n - 8);
-            const u32x4 s = *reinterpret_cast<const u32x4*>(it.s_in + k0);
-            sp[w][4 * v + 0] = s.x;
-            sp[w][4 * v + 1] = s.y;
-            sp[w][4 * v + 2] = s.z;
-            sp[w][4 * v + 3] = s.w;
+            const uint32_t off = (32u * static_cast<uint32_t>(p + 64 * WR * w) + 8u * v) * 2u;
+            const u32x4 sv = load_b128(s_rs, off);
+            sp[w][4 * v + 0] = sv.x;
+            sp[w][4 * v + 1] = sv.y;
+            sp[w][4 * v + 2] = sv.z;
+            sp[w][4 * v + 3] = sv.w;
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
-                const u32x4 xv = *reinterpret_cast<const u32x4*>(
-                    x + static_cast<uint32_t>(min(b0 + b, batch - 1)) * static_cast<uint32_t>(n) + k0);
+                const u32x4 xv = load_b128(x_rs[b], off);
                 xp[w][b][4 * v + 0] = xv.x;
                 xp[w][b][4 * v + 1] = xv.y;
                 xp[w][b][4 * v + 2] = xv.z;
                 xp[w][b][4 * v + 3] = xv.w;
             }
         }
-    // V's words after x and s_in: loads return in issue order, so the sign fix-up below waits only
-    // for x and s_in (from L2) and runs while V's words come from HBM
     __builtin_amdgcn_sched_barrier(0);
+    uint32_t vb[R][WPL];
 #pragma unroll
-    for (int k = 0; k < R; ++k) {
-        const uint32_t* row = it.v_bits + static_cast<uint32_t>(min(j0 + k, r - 1)) * static_cast<uint32_t>(wn);
+    for (int k = 0; k < R; ++k)
 #pragma unroll
-        for (int w = 0; w < WPL; ++w) vb[k][w] = row[qc[w]];
-    }
+        for (int w = 0; w < WPL; ++w)
+            vb[k][w] = load_b32_stream(
+                v_rs, (static_cast<uint32_t>(j0 + k) * static_cast<uint32_t>(wn) + static_cast<uint32_t>(p + 64 * WR * w)) * 4u);
     __builtin_amdgcn_sched_barrier(0);
-
-    // zero what lies past the row or the batch; move s_in's sign onto x
-    const uint32_t mask = kSignPair;
-#pragma unroll
-    for (int w = 0; w < WPL; ++w)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int q = p + 64 * WR * w;
-            const bool ok = q < wn && 32 * q + 8 * v < n;
-#pragma unroll
-            for (int d = 0; d < 4; ++d) {
-                const int pp = 4 * v + d;
-                const uint32_t s = ok ? sp[w][pp] : 0u;
-                const uint32_t sg = s & mask;
-                sp[w][pp] = s ^ sg;
-#pragma unroll
-                for (int b = 0; b < NB; ++b) xp[w][b][pp] = (ok && b0 + b < batch) ? (xp[w][b][pp] ^ sg) : 0u;
-            }
-        }
 
     NQ_STAMP(1);
     // Even and odd pairs accumulate separately and rows are innermost, so consecutive dot2
     // instructions do not wait on each other.
+    const uint32_t mask = kSignPair;
     float acc[2][R][NB];
 #pragma unroll
     for (int e = 0; e < 2; ++e)
@@ -370,12 +360,12 @@ __global__ __launch_bounds__(G * WR * 64) void s1w_kernel(const S1Table tab, con
         for (int pp = 0; pp < 16; ++pp)
 #pragma unroll
             for (int k = 0; k < R; ++k) {
-                const uint32_t a = bit_select(mask, vb[k][w] << pp, sp[w][pp]);
+                const uint32_t a = ((vb[k][w] << pp) & mask) ^ sp[w][pp];
 #pragma unroll
                 for (int b = 0; b < NB; ++b) acc[pp & 1][k][b] = T::dot2(a, xp[w][b][pp], acc[pp & 1][k][b]);
             }
     NQ_STAMP(2);
-    // sum of squares of x (a sign flip does not change a square; zeroed slots add nothing)
+    // sum of squares of x (lanes past the row hold zeros)
     float ss[2][NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) ss[0][b] = ss[1][b] = 0.0f;
@@ -421,7 +411,7 @@ __global__ __launch_bounds__(G * WR * 64) void s1w_kernel(const S1Table tab, con
                 if (kNorm) {
                     float v = 0.0f;
 #pragma unroll
-                    for (int s = 0; s < WR; ++s) v += part[((grp * kPartRows + R) * NB + b) * WR + s];
+                    for (int s2 = 0; s2 < WR; ++s2) v += part[((grp * kPartRows + R) * NB + b) * WR + s2];
                     rs[b] = rsqrtf(v / static_cast<float>(n) + eps);
                 }
             }
@@ -433,7 +423,7 @@ __global__ __launch_bounds__(G * WR * 64) void s1w_kernel(const S1Table tab, con
                 for (int b = 0; b < NB; ++b) {
                     float v = 0.0f;
 #pragma unroll
-                    for (int s = 0; s < WR; ++s) v += part[((grp * kPartRows + k) * NB + b) * WR + s];
+                    for (int s2 = 0; s2 < WR; ++s2) v += part[((grp * kPartRows + k) * NB + b) * WR + s2];
                     v *= rs[b];
                     if (j < it.kpad && b0 + b < batch)
                         store_h(it.z_hi, it.z_lo, it.zpitch, b0 + b, j, j < r ? v * mf : 0.0f);
@@ -901,15 +891,13 @@ void launch_stage2_generic(const GemvArgs& a) {
                                                              a.plan.wr, a.plan.zpitch);
 }
 
-// Rows of V per block of the stage-1 configuration used for wn words per row (0: none).
-// Shapes measured on MI355X (graph-replayed, cold weights): n = 4096 is fastest with two waves
-// per row and one word per lane, two rows per group (3.3 us against 3.6-4.3 for the other
-// splits). Wider rows gain from more rows per block, since every block reads all of x and s_in
-// once: n = 8192, r = 3520 takes 5.8 us with four rows per group (6.9 with two, 6.2 with eight);
-// n = 11008 takes 5.3 us with three words per lane over two waves (384 words for 344) and four
-// rows per group (6.2 with two words over four waves, 6.5 and 7.7 with six and eight rows).
-// A table of several items (the decode step's q/k/v and gate/up groups) at n = 4096 takes four
-// rows per group: 612.0 against 608.8 tokens/s end to end, repeatable.
+// Launch shapes of the VALU stage 1, measured on MI355X (graph-replayed, 64-128 rotating weight
+// copies, batch 1): n = 4096 (r = 1632) 3.11 us with two words per lane, one wave and two rows per
+// group, four groups (3.23-3.74 for the other splits); n = 8192 4.48 us at r = 2240 and 5.14 at
+// r = 3520 with one word per lane over four waves, four rows; n = 11008 4.65 us with one word per
+// lane over six waves (384 words for 344), four rows per group, two groups (4.70 with three words
+// over two waves). Every block reads all of x and s_in once per group, so wide rows take more
+// rows per group; one word per lane keeps the per-wave chain of dot products short.
 // Launch shape of s1w_kernel: WPL words per lane, WR waves per row group, R rows per group, G
 // groups per block (G * WR * 64 threads, R * G rows). The lanes of a group cover 64 * WR * WPL
 // >= wn words of a row.
@@ -919,14 +907,15 @@ struct S1wShape {
 
 // The instantiated shapes (wpl, wr, r, g).
 #ifndef NQ_S1W_SHAPES
-#define NQ_S1W_SHAPES(X) X(1, 1, 2, 4) X(1, 2, 4, 2) X(1, 2, 2, 2) X(2, 2, 4, 2) X(3, 2, 4, 2) X(2, 4, 4, 1)
+#define NQ_S1W_SHAPES(X) X(1, 1, 2, 4) X(2, 1, 2, 4) X(1, 4, 4, 1) X(1, 6, 4, 2) X(2, 4, 4, 1)
 #endif
 
 inline S1wShape s1w_shape(int wn, bool grouped) {
+    (void)grouped;
     if (wn <= 64) return {1, 1, 2, 4};
-    if (wn <= 128) return grouped ? S1wShape{1, 2, 4, 2} : S1wShape{1, 2, 2, 2};
-    if (wn <= 256) return {2, 2, 4, 2};
-    if (wn <= 384) return {3, 2, 4, 2};
+    if (wn <= 128) return {2, 1, 2, 4};
+    if (wn <= 256) return {1, 4, 4, 1};
+    if (wn <= 384) return {1, 6, 4, 2};
     return {2, 4, 4, 1};
 }
 

@@ -45,3 +45,28 @@ const char* nq_last_error_message(void) { return nq::g_last_error; }
 int nq_version(void) { return 100; }
 
 }  // extern "C"
+
+// ----------------------------------------------------------------------------- measurement aid
+
+namespace nq {
+namespace {
+__global__ void wall_clock_kernel(uint64_t* dst) { *dst = wall_clock64(); }
+}  // namespace
+}  // namespace nq
+
+extern "C" {
+
+int nq_timestamp(uint64_t* dst, nq_stream_t stream) {
+    if (!dst) return nq::fail(NQ_ERR_INVALID_ARGUMENT, "nq_timestamp: null pointer");
+    nq::wall_clock_kernel<<<1, 1, 0, nq::as_stream(stream)>>>(dst);
+    return nq::check_launch("nq_timestamp");
+}
+
+int64_t nq_wall_clock_hz(void) {
+    int dev = 0, khz = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess) return 0;
+    return static_cast<int64_t>(khz) * 1000;
+}
+
+}  // extern "C"
