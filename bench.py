@@ -285,7 +285,8 @@ def bench_gemm(name, args, dev):
             "tflops": round(tflops, 2), "flops_per_call": flops,
             "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_F16_PEAK_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
-                         "traffic": measured_traffic(f"gemm_{name}", (m, n, r, B))[0]}}, c, y
+                         "traffic": measured_traffic(f"gemm_{name}", (m, n, r, B))[0],
+                         "traffic_unit": "HBM bytes per call (both launches)"}}, c, y
 
 
 def bench_pack(dev):
@@ -404,7 +405,7 @@ def measured_traffic(kernel_key, workload):
     k = rec.get("kernels", {}).get(kernel_key)
     if not k or tuple(k.get("workload", ())) != tuple(workload):
         return None, None
-    return int(k["fetch_bytes"] + k["write_bytes"]), rec.get("source")
+    return int(k["fetch_bytes"] + k["write_bytes"]), rec.get("sources", rec.get("source"))
 
 
 def calibration_copy(dev, mib):
@@ -616,6 +617,7 @@ def main():
     ap.add_argument("--gemm-steps", type=int, default=256, help="timed GEMM calls")
     ap.add_argument("--gemm-warmup", type=int, default=64, help="untimed GEMM calls before timing")
     ap.add_argument("--skip-gemm", action="store_true")
+    ap.add_argument("--gemm-shapes", default="gate,down", help="GEMM shapes to measure (gate, down)")
     ap.add_argument("--skip-pack", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=8.0, help="bounded CPU sample per dtype of the dense path")
@@ -630,7 +632,7 @@ def main():
     ap.add_argument("--decode-only", action="store_true",
                     help="run only the end-to-end decode and print its result alone (for kernel traces)")
     ap.add_argument("--gemv-only", action="store_true",
-                    help="run only the headline GEMV and the per-shape GEMV figures (for kernel traces)")
+                    help="run only the headline GEMV shape, with its per-launch figures (for kernel traces)")
     ap.add_argument("--e2e-batch", type=int, default=1)
     ap.add_argument("--e2e-prompt", type=int, default=128)
     ap.add_argument("--e2e-new", type=int, default=256)
@@ -675,6 +677,11 @@ def main():
     achieved = pb / (ms * 1e-3) / 1e9
     log(f"[bench] gemv {HEADLINE}: {ms * 1e3:.3f} us/step over {args.steps} steps, {achieved:.1f} GB/s packed")
     shapes = {HEADLINE: bench_gemv_shape(pool, dev)}
+    if args.gemv_only:  # profiling aid: the headline shape alone, so kernel names do not mix shapes
+        if args.calib_copy_mib > 0:
+            calibration_copy(dev, args.calib_copy_mib)
+        print(json.dumps({"gemv_headline_us": round(ms * 1e3, 4), "gemv": shapes}), flush=True)
+        return 0
     other = "gate" if HEADLINE == "down" else "down"
     pool_other = GemvPool(other, args.copies, args.batch, dev, seed=2023)
     shapes[other] = bench_gemv_shape(pool_other, dev)
@@ -687,9 +694,6 @@ def main():
         log(f"[bench] gemv {k} steady: {v['us']} us ({v['frac_hbm']} of HBM peak), stage 1 "
             f"{v['stage1']['us_per_launch']} us, stage 2 {v['stage2']['us_per_launch']} us")
     del pool_other
-    if args.gemv_only:
-        print(json.dumps({"gemv_headline_us": round(ms * 1e3, 4), "gemv": shapes}), flush=True)
-        return 0
 
     if args.calib_copy_mib > 0:
         calibration_copy(dev, args.calib_copy_mib)
@@ -697,7 +701,7 @@ def main():
     gemm = None
     if not args.skip_gemm:
         gemm = {}
-        for name in ("gate", "down"):
+        for name in args.gemm_shapes.split(","):
             log(f"[bench] gemm {name} B={args.gemm_batch}")
             res, c, y = bench_gemm(name, args, dev)
             gemm[name] = res

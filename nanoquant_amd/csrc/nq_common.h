@@ -126,9 +126,12 @@ __device__ inline rsrc_t make_rsrc(const void* base, uint32_t bytes) {
 __device__ inline u32x4 load_b128(rsrc_t rs, uint32_t offset) {
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(offset), 0, 0));
 }
-// Streaming load (read once: non-temporal)
+// Streaming loads (read once: non-temporal)
 __device__ inline uint32_t load_b32_stream(rsrc_t rs, uint32_t offset) {
     return __builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<int>(offset), 0, 2);
+}
+__device__ inline u32x4 load_b128_stream(rsrc_t rs, uint32_t offset) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(offset), 0, 2));
 }
 
 template <typename T>

@@ -334,13 +334,17 @@ __global__ __launch_bounds__(G * WR * 64) void s1w_kernel(const S1Table tab, con
             }
         }
     __builtin_amdgcn_sched_barrier(0);
+    // a lane past the row's last word loads nothing (an offset past the resource touches no memory)
+    const uint32_t v_end = static_cast<uint32_t>(r) * static_cast<uint32_t>(wn) * 4u;
     uint32_t vb[R][WPL];
 #pragma unroll
     for (int k = 0; k < R; ++k)
 #pragma unroll
-        for (int w = 0; w < WPL; ++w)
-            vb[k][w] = load_b32_stream(
-                v_rs, (static_cast<uint32_t>(j0 + k) * static_cast<uint32_t>(wn) + static_cast<uint32_t>(p + 64 * WR * w)) * 4u);
+        for (int w = 0; w < WPL; ++w) {
+            const int q = p + 64 * WR * w;
+            const uint32_t off = (static_cast<uint32_t>(j0 + k) * static_cast<uint32_t>(wn) + static_cast<uint32_t>(q)) * 4u;
+            vb[k][w] = load_b32_stream(v_rs, q < wn ? off : v_end);
+        }
     __builtin_amdgcn_sched_barrier(0);
 
     NQ_STAMP(1);
@@ -665,13 +669,17 @@ __global__ __launch_bounds__(256) void s2t_kernel(const S2Table tab, int batch) 
         for (int i = 0; i < 4; ++i)
             res[i] = its[0].resid[rb * static_cast<uint32_t>(its[0].ystride) + min(ie + 4 * g + i, m - 1)];
     }
+    // pieces past the block's run are not needed: their offset lies past the resource, so they load
+    // nothing (zeros)
 #pragma unroll
     for (int pi = 0; pi < P; ++pi) {
         const S2Item& it = its[pi];
+        const rsrc_t u_rs = make_rsrc(it.u_bits, vec_end * 4u);
 #pragma unroll
-        for (int k = 0; k < kUPieces; ++k)
-            pv[pi][k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
-                it.u_bits + min(base + 4u * static_cast<uint32_t>(t + k * kThr), vec_end - 4u)));
+        for (int k = 0; k < kUPieces; ++k) {
+            const int e4 = 4 * (t + k * kThr);
+            pv[pi][k] = load_b128_stream(u_rs, e4 < nwords ? (base + static_cast<uint32_t>(e4)) * 4u : vec_end * 4u);
+        }
         tail_word[pi] = it.u_bits[min(vec_end + static_cast<uint32_t>(t), total - 1u)];  // words past vec_end
     }
     __builtin_amdgcn_sched_barrier(0);
