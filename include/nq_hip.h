@@ -102,7 +102,11 @@ int nq_permute_marlin_scales(const uint16_t* scale_in, uint16_t* scale_in_out, i
 
 /* ---------------------------------------------------------------- decode GEMV */
 
-/* Bytes of workspace nq_gemv needs (the intermediate as bf16 hi/lo pairs plus a header). */
+/* Bytes of workspace nq_gemv needs: a header, the intermediate as bf16 hi/lo pairs and, for
+ * batches whose stage 1 runs the batched k-split kernel (from 64 rows, or from 16 on inputs of
+ * 8192 or more columns, up to 128 rows, n % 32 == 0), its per-range fp32 sums. A workspace that
+ * holds the header and intermediate but not those sums is accepted and runs the stage-1 kernels
+ * that keep none (results agree to rounding, not bit for bit). */
 size_t nq_gemv_workspace_bytes(int64_t batch, int64_t n, int64_t r, int64_t m);
 
 /* y[b, :] = sat(s_out * (U * ((V * (s_in * x[b, :])) * s_mid)))  for b < batch.
@@ -136,9 +140,11 @@ int nq_gemv_stage2(int dtype, const uint32_t* u_bits, const void* s_out, void* y
 
 /* nq_gemv with no workspace argument and no allocation of any kind: the intermediate lives in
  * a static device array of NQ_GEMV_NOALLOC_SCRATCH_BYTES that each GPU holds until the process
- * ends. Same arguments (minus the workspace), kernels and results as nq_gemv, bit for bit.
- * Returns NQ_ERR_WORKSPACE, launching nothing, when nq_gemv_workspace_bytes(batch, n, r, m)
- * exceeds that size (batch > 630 at r = 1632, batch > 227 at r = 4608). Every call on one GPU
+ * ends. Same arguments (minus the workspace), kernels and results as nq_gemv, bit for bit,
+ * whenever nq_gemv_workspace_bytes(batch, n, r, m) fits in the array; larger batched calls run
+ * the stage-1 kernel that keeps no per-range sums (results agree with nq_gemv's to rounding).
+ * Returns NQ_ERR_WORKSPACE, launching nothing, when the header and intermediate alone exceed
+ * that size (batch > 630 at r = 1632, batch > 227 at r = 4608). Every call on one GPU
  * shares that GPU's array: calls that overlap on one GPU (concurrent streams or threads) race,
  * so order them on one stream. The first call on a device looks up the array's address there.
  * No counterpart in the reference: for callers that cannot allocate device memory (code under

@@ -29,6 +29,14 @@ COMMON_FLAGS = [
 ]
 
 
+# Per-source additions. The GEMV source keeps MFMA accumulators in VGPRs (the VGPR form of the
+# instruction): with the AGPR form the register allocator moved the batched kernels'
+# accumulators between AGPRs and VGPRs on every loop trip (more such moves than MFMAs).
+FILE_FLAGS = {
+    "nq_gemv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
+
 def hipcc() -> str:
     path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not os.path.exists(path):
@@ -42,7 +50,7 @@ def sources():
 
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD_DIR, os.path.basename(src) + ".o")
-    cmd = [hipcc(), *COMMON_FLAGS, "-x", "hip", "-c", src, "-o", obj]
+    cmd = [hipcc(), *COMMON_FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-x", "hip", "-c", src, "-o", obj]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{proc.stdout}\n{proc.stderr}")

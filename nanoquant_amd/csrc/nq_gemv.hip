@@ -33,6 +33,7 @@
 #include <algorithm>
 #include <cstdint>
 #include <mutex>
+#include <type_traits>
 
 #include "nq_common.h"
 
@@ -822,6 +823,242 @@ __global__ __launch_bounds__(256) void s2t_kernel(const S2Table tab, int batch) 
     NQ_STAMP(3);
 }
 
+// --------------------------------------------------------------------------- stage 1, batched (k split)
+//
+// For many batch rows on wide rows of V: h[b][j] = s_mid[j] * sum_k sign(V[j][k]) s_in[k] x[b][k]
+// as v_mfma_f32_16x16x32_{f16,bf16} tiles with A = 16 rows of V x 32 k of +-s_in (the word shifted
+// left by 4g + d carries pair 4g + d's signs; one xor puts them on the s_in pair, as in s1m_kernel)
+// and B = 32 k x 16 batch rows of x. sb_kernel gives one block 16 * NW * RTW rows of V and a range
+// of kw words of k for up to 16 * CT batch rows: it copies that slice of x, of s_in and the rows'
+// words into LDS by DMA in one go, then wave w runs its RTW row tiles against all CT batch tiles,
+// decoding each A fragment once for the CT MFMAs that use it. s1m_kernel, by contrast, decodes V
+// again for every 16 batch rows and streams all of x through every block of 16 rows.
+//
+// With one k range the block applies the epilogue; with several, each block stores its raw fp32
+// sums to plane grid.y of `part` ([ks][batch][kpad]) and sb_finish1 adds the planes in order (a
+// fixed order: the result does not depend on which block finished first).
+//
+// x slice layout: column c (batch row bb + c; the last column holds s_in) is kw * 4 chunks of 16
+// bytes; chunk p of column c holds x's chunk p ^ (c % 8) (kw is even, so the swizzle stays inside
+// the column), which spreads the 16 columns one MFMA fragment read touches over the LDS banks. A
+// wave's DMA fills 64 consecutive chunks; lanes past the slice fetch a valid chunk again into the
+// rounding slack. Words: row i of the block at i * (kw + 1).
+//
+// Measured (MI355X, graph-replayed, rotating weights; stage 1 alone, us): n = 11008, r = 1632:
+// batch 16 / 64 / 128: 12.9 / 18.7 / 27.7 against 14.3 / 26.6 / 51.3 for s1m_kernel; n = 4096:
+// batch 64 / 128: 11.5 / 15.6 against 11.4 / 20.6 (and slower than s1m below 64 rows). A block
+// fetches its slice at 35-45 GB/s (phase stamps), so the plan keeps slices small; the same design
+// for stage 2 (slices of h, partial sums of y) lost to s2t_kernel at every batch and is not used.
+struct SbArgs {
+    const uint32_t* words;  // V's words [M][wpr]
+    const uint16_t* s_in;   // [wpr * 32]
+    const uint16_t* x;      // [batch][ldx]
+    const uint16_t* s_mid;  // or nullptr
+    uint16_t* z_hi;
+    uint16_t* z_lo;
+    float* part;            // [ks][batch][kpad] with several k ranges
+    int M, wpr, ldx, batch, kw;
+    int kpad, zpitch;       // rows >= M give zeros, rows < kpad are stored, columns [kpad, zpitch) zeroed
+    uint32_t kw4_magic;     // ceil(2^32 / (4 kw)): l / (4 kw) == umulhi(l, kw4_magic) for the l used here
+    uint32_t ws_magic;      // ceil(2^32 / (kw + 1))
+};
+
+// ceil(2^32 / d): n / d == __umulhi(n, magic) for n * d < 2^32.
+inline uint32_t div_magic(uint32_t d) { return static_cast<uint32_t>(((1ULL << 32) + d - 1) / d); }
+
+__device__ inline void dma16(const void* src, void* lds) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                     (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+
+__device__ inline void dma4(const void* src, void* lds) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                     (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
+}
+
+// Dwords of LDS an sb_kernel block takes (x slice, then words), each part rounded to whole DMAs.
+__host__ __device__ inline int sb_xs_dwords(int xcols, int kw) { return (xcols * kw * 4 + 63) / 64 * 64 * 4; }
+__host__ __device__ inline int sb_w_dwords(int rows, int kw) { return (rows * (kw + 1) + 63) / 64 * 64; }
+
+template <typename T, int NW, int RTW, int CT>
+__global__ __launch_bounds__(NW * 64) void sb_kernel(const SbArgs a) {
+    constexpr int BR = 16 * NW * RTW;  // rows of V per block
+    constexpr int NCOL = 16 * CT;      // batch rows per block
+    constexpr int XCOLS = NCOL + 1;    // + s_in
+    extern __shared__ __attribute__((aligned(16))) uint32_t smem[];
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int c = lane & 15;
+    const int g = lane >> 4;
+    const int i0 = static_cast<int>(blockIdx.x) * BR;
+    const int q0 = static_cast<int>(blockIdx.y) * a.kw;
+    const int qn = min(a.kw, a.wpr - q0);
+    const int bb = static_cast<int>(blockIdx.z) * NCOL;  // first batch row of the block
+    const int kw4 = a.kw * 4;
+    uint32_t* xs = smem;
+    uint32_t* wl = smem + sb_xs_dwords(XCOLS, a.kw);
+    const int wstride = a.kw + 1;
+    NQ_STAMP(0);
+
+    // 1. DMA: the x slice and s_in, then the rows' words (divisions by a multiply: the issue loop
+    //    is VALU work before the first MFMA)
+    const uint32_t xchunks = static_cast<uint32_t>(XCOLS * kw4);
+    const uint32_t kend = static_cast<uint32_t>(a.wpr) * 32u;  // elements of k
+    for (uint32_t l0 = static_cast<uint32_t>(wave) * 64u; l0 < xchunks; l0 += NW * 64) {
+        const uint32_t l = min(l0 + static_cast<uint32_t>(lane), xchunks - 1u);
+        const uint32_t col = __umulhi(l, a.kw4_magic);
+        const uint32_t p = l - col * static_cast<uint32_t>(kw4);
+        uint32_t k = static_cast<uint32_t>(q0) * 32u + 8u * (p ^ (col & 7u));
+        if (k >= kend) k = 0;  // past the last word: never read
+        const uint16_t* src;
+        if (col == NCOL) {
+            src = a.s_in + k;
+        } else {
+            const uint32_t b = min(static_cast<uint32_t>(bb) + col, static_cast<uint32_t>(a.batch - 1));
+            src = a.x + b * static_cast<uint32_t>(a.ldx) + k;
+        }
+        dma16(src, xs + l0 * 4);
+    }
+    const uint32_t wtotal = static_cast<uint32_t>(BR * wstride);
+    const uint32_t qlast = static_cast<uint32_t>(qn - 1);
+    const uint32_t rlast = static_cast<uint32_t>(a.M - 1 - i0);  // >= 0: the grid covers rows below M only
+    const uint32_t* wbase = a.words + static_cast<uint32_t>(i0) * static_cast<uint32_t>(a.wpr) + static_cast<uint32_t>(q0);
+    for (uint32_t l0 = static_cast<uint32_t>(wave) * 64u; l0 < wtotal; l0 += NW * 64) {
+        const uint32_t l = min(l0 + static_cast<uint32_t>(lane), wtotal - 1u);
+        const uint32_t row = __umulhi(l, a.ws_magic);
+        const uint32_t q = min(l - row * static_cast<uint32_t>(wstride), qlast);  // the pad slot repeats a word
+        dma4(wbase + min(row, rlast) * static_cast<uint32_t>(a.wpr) + q, wl + l0);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's DMAs have landed (vmcnt, expcnt and lgkmcnt all zero)
+    __syncthreads();
+    NQ_STAMP(1);
+
+    // 2. MFMAs over the range: A fragment of row tile rt from word (row 16 rt' + c, q) shifted by 4g
+    const uint32_t mask = kSignPair;
+    f32x4 acc[RTW * CT];
+#pragma unroll
+    for (int i = 0; i < RTW * CT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const uint32_t* wrow = wl + (16 * wave * RTW + c) * wstride;
+    const uint32_t* xcol = xs + c * kw4 * 4;
+    const uint32_t* scol = xs + NCOL * kw4 * 4;
+    const int sw = c & 7;
+    const int sh = 4 * g;
+    // the LDS operands of word q + 1 are read before word q's MFMAs (two operand sets, the loop
+    // unrolled by two so that each set keeps its registers)
+    struct Ops {
+        u32x4 bf[CT];
+        u32x4 s;
+        uint32_t w[RTW];
+    };
+    auto fetch = [&](int q, Ops& o) {
+        const int ch = (4 * q + g) ^ sw;
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) o.bf[ct] = *reinterpret_cast<const u32x4*>(xcol + (16 * ct * kw4 + ch) * 4);
+        o.s = *reinterpret_cast<const u32x4*>(scol + (4 * q + g) * 4);
+#pragma unroll
+        for (int rt = 0; rt < RTW; ++rt) o.w[rt] = wrow[16 * rt * wstride + q];
+    };
+    auto run = [&](const Ops& o) {
+#pragma unroll
+        for (int rt = 0; rt < RTW; ++rt) {
+            const uint32_t w = o.w[rt] << sh;
+            const u32x4 av = u32x4{o.s.x ^ (w & mask), o.s.y ^ ((w << 1) & mask), o.s.z ^ ((w << 2) & mask),
+                                   o.s.w ^ ((w << 3) & mask)};
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) acc[rt * CT + ct] = mfma16x16x32<T>(av, o.bf[ct], acc[rt * CT + ct]);
+        }
+    };
+    Ops o0, o1;
+    fetch(0, o0);
+    int q = 0;
+    for (; q + 1 < qn; q += 2) {
+        fetch(q + 1, o1);
+        run(o0);
+        if (q + 2 < qn) fetch(q + 2, o0);
+        run(o1);
+    }
+    if (q < qn) run(o0);
+
+    // 3. lane (c, g) holds rows 4g .. 4g+3 of each row tile for batch row 16 ct + c. The block's
+    //    [batch row][row] tile goes through LDS (rows padded by 4 floats against bank conflicts), so
+    //    that every global store below is a run of consecutive rows of one batch row.
+    constexpr int OS = BR + 4;
+    float* ot = reinterpret_cast<float*>(smem);
+    NQ_STAMP(2);
+    __syncthreads();  // every wave is done with the slice
+#pragma unroll
+    for (int rt = 0; rt < RTW; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+            *reinterpret_cast<f32x4*>(ot + (16 * ct + c) * OS + 16 * (wave * RTW + rt) + 4 * g) = acc[rt * CT + ct];
+    __syncthreads();
+    // 4. stores: 4 consecutive rows per thread, consecutive threads along a batch row
+    const bool split = gridDim.y > 1;
+    const int nb = min(NCOL, a.batch - bb);
+    constexpr int Q = BR / 4;
+    for (int e = t; e < nb * Q; e += NW * 64) {
+        const int bl = e / Q;
+        const int rl = 4 * (e - bl * Q);
+        const int row = i0 + rl;
+        if (row >= a.kpad) continue;
+        const int b = bb + bl;
+        const f32x4 v = *reinterpret_cast<const f32x4*>(ot + bl * OS + rl);
+        if (split) {
+            *reinterpret_cast<f32x4*>(a.part + (static_cast<size_t>(blockIdx.y) * a.batch + b) * a.kpad + row) = v;
+        } else {
+            const float vv[4] = {v.x, v.y, v.z, v.w};
+            uint16_t hi[4], lo[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int j = row + i;
+                const float mf = (a.s_mid != nullptr && j < a.M) ? T::to_float(a.s_mid[j]) : 1.0f;
+                const float h = j < a.M ? vv[i] * mf : 0.0f;
+                hi[i] = bf16_bits(h);
+                lo[i] = bf16_bits(h - bf16_value(hi[i]));
+            }
+            const size_t at = static_cast<size_t>(b) * a.zpitch + row;
+            *reinterpret_cast<uint2*>(a.z_hi + at) = uint2{hi[0] | (uint32_t(hi[1]) << 16), hi[2] | (uint32_t(hi[3]) << 16)};
+            *reinterpret_cast<uint2*>(a.z_lo + at) = uint2{lo[0] | (uint32_t(lo[1]) << 16), lo[2] | (uint32_t(lo[3]) << 16)};
+        }
+    }
+    if (!split && blockIdx.x == 0 && blockIdx.y == 0) zero_h_pad(a.z_hi, a.z_lo, a.zpitch, a.kpad, bb, NCOL, a.batch);
+    NQ_STAMP(3);
+}
+
+// The k ranges added in order: h[b][j] = s_mid[j] * sum (0 for j >= r), stored as (hi, lo) for
+// j < kpad, zeros in [kpad, zpitch). One thread per 4 columns of one batch row.
+template <typename T>
+__global__ __launch_bounds__(256) void sb_finish1(const SbArgs a, int ks) {
+    const int per_row = a.zpitch / 4;
+    const int e = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+    if (e >= a.batch * per_row) return;
+    const int b = e / per_row;
+    const int j0 = 4 * (e - b * per_row);
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    if (j0 < a.kpad) {
+        for (int k = 0; k < ks; ++k) {
+            const f32x4 pv = *reinterpret_cast<const f32x4*>(a.part + (static_cast<size_t>(k) * a.batch + b) * a.kpad + j0);
+            v[0] += pv.x;
+            v[1] += pv.y;
+            v[2] += pv.z;
+            v[3] += pv.w;
+        }
+    }
+    uint16_t hi[4], lo[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int j = j0 + i;
+        const float mf = (a.s_mid != nullptr && j < a.M) ? T::to_float(a.s_mid[j]) : 1.0f;
+        const float h = j < a.M ? v[i] * mf : 0.0f;
+        hi[i] = bf16_bits(h);
+        lo[i] = bf16_bits(h - bf16_value(hi[i]));
+    }
+    const size_t at = static_cast<size_t>(b) * a.zpitch + j0;
+    *reinterpret_cast<uint2*>(a.z_hi + at) = uint2{hi[0] | (uint32_t(hi[1]) << 16), hi[2] | (uint32_t(hi[3]) << 16)};
+    *reinterpret_cast<uint2*>(a.z_lo + at) = uint2{lo[0] | (uint32_t(lo[1]) << 16), lo[2] | (uint32_t(lo[3]) << 16)};
+}
+
 // --------------------------------------------------------------------------- plan and dispatch
 
 constexpr int kS2Waves = 4;
@@ -873,8 +1110,69 @@ struct GemvArgs {
     Plan plan;
     uint16_t* z_hi;
     uint16_t* z_lo;
+    float* part;        // room for the batched passes' per-range sums
+    size_t part_bytes;  // (the workspace beyond the intermediate)
     hipStream_t stream;
 };
+
+// Launch plan of the batched stage 1 (sb_kernel): RTW row tiles per wave (4 waves), CT batch tiles
+// of 16, kw words per k range, ks ranges (grid.y), passes over the batch (grid.z).
+struct SbPlan {
+    int rtw, ct, kw, ks, passes;
+    size_t part_bytes, lds_bytes;
+};
+
+// When the batched stage 1 replaces s1m_kernel (measured crossovers, see sb_kernel): from 64 batch
+// rows, or from 16 on rows of at least 256 words; at most 128 rows (8 batch tiles), and an LDS
+// slice of at most 160 KB per block.
+constexpr int kSbMinBatch = 64;
+constexpr int kSbMinBatchWide = 16;
+constexpr int kSbWideWords = 256;
+constexpr int kSbMaxBatch = 128;
+constexpr int kSbLdsBytes = 160 * 1024;
+constexpr int kSbMaxBlocks = 256;
+
+// Searches row tiles per wave (1, 2, 4: 64, 128, 256 rows per block) and k ranges for the launch
+// with the least estimated time per block, among those whose grid is one block per CU at most (a
+// second round of blocks doubles the time) and whose LDS fits. Estimate, in CU cycles: the MFMAs
+// and their operand decode per wave, the DMA of the block's slice at ~32 bytes a cycle, and, with
+// several k ranges, the finishing launch (~4000) plus the per-range sums written and read.
+inline bool sb_plan(int64_t batch, int64_t rows, int64_t wpr, int64_t kpad, SbPlan& p) {
+    if (batch > kSbMaxBatch || rows <= 0 || wpr <= 0) return false;
+    if (batch < kSbMinBatch && (batch < kSbMinBatchWide || wpr < kSbWideWords)) return false;
+    const int ct = static_cast<int>(std::min<int64_t>(8, ceil_div(batch, 16)));
+    const int passes = static_cast<int>(ceil_div(batch, 16LL * ct));
+    const int xcols = 16 * ct + 1;
+    double best = -1.0;
+    for (int rtw : {1, 2, 4}) {
+        const int br = 64 * rtw;
+        const int64_t row_blocks = ceil_div(rows, br);
+        for (int64_t want = 1; want <= wpr; ++want) {
+            const int64_t kw = std::max<int64_t>(2, (ceil_div(wpr, want) + 1) & ~int64_t{1});
+            const int64_t ks = ceil_div(wpr, kw);
+            if (row_blocks * ks * passes > kSbMaxBlocks) break;
+            const size_t lds = std::max<size_t>(
+                static_cast<size_t>(sb_xs_dwords(xcols, static_cast<int>(kw)) + sb_w_dwords(br, static_cast<int>(kw))) * 4,
+                static_cast<size_t>(16 * ct) * (br + 4) * 4);
+            if (lds > static_cast<size_t>(kSbLdsBytes)) continue;
+            const double mfma = rtw * ct * kw * 16.0 * 1.25;
+            const double dma = (xcols * 64.0 + br * 4.0) * kw / 32.0;
+            const double fin = ks > 1 ? 4000.0 + 2.0 * ks * batch * kpad * 4.0 / (256.0 * 16.0) : 0.0;
+            const double cost = mfma + dma + fin;
+            if (best < 0 || cost < best) {
+                best = cost;
+                p.rtw = rtw;
+                p.ct = ct;
+                p.kw = static_cast<int>(kw);
+                p.ks = static_cast<int>(ks);
+                p.passes = passes;
+                p.part_bytes = ks > 1 ? static_cast<size_t>(ks) * batch * kpad * 4 : 0;
+                p.lds_bytes = lds;
+            }
+        }
+    }
+    return best >= 0;
+}
 
 template <typename T, int NB>
 void launch_stage1_generic(const GemvArgs& a) {
@@ -1056,19 +1354,88 @@ inline S1Item s1_item_of(const GemvArgs& a) {
     return it;
 }
 
+// ---- batched stage 1
+
+template <typename T, int RTW, int CT>
+int launch_sb_cfg(const SbArgs& s, const SbPlan& p, hipStream_t st) {
+    constexpr int NW = 4;
+    // blocks may take more than 64 KB of LDS (once per kernel: the limit is a property of the function)
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&sb_kernel<T, NW, RTW, CT>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, kSbLdsBytes);
+    if (attr != hipSuccess) return fail(NQ_ERR_HIP, "nq_gemv batched stage 1: LDS limit: %s", hipGetErrorString(attr));
+    const dim3 grid(static_cast<unsigned>(ceil_div(s.M, 16 * NW * RTW)), static_cast<unsigned>(p.ks),
+                    static_cast<unsigned>(p.passes));
+    sb_kernel<T, NW, RTW, CT><<<grid, NW * 64, p.lds_bytes, st>>>(s);
+    return NQ_OK;
+}
+
+template <typename T, int RTW>
+int launch_sb_rtw(const SbArgs& s, const SbPlan& p, hipStream_t st) {
+    switch (p.ct) {
+        case 1: return launch_sb_cfg<T, RTW, 1>(s, p, st);
+        case 2: return launch_sb_cfg<T, RTW, 2>(s, p, st);
+        case 3: return launch_sb_cfg<T, RTW, 3>(s, p, st);
+        case 4: return launch_sb_cfg<T, RTW, 4>(s, p, st);
+        case 5: return launch_sb_cfg<T, RTW, 5>(s, p, st);
+        case 6: return launch_sb_cfg<T, RTW, 6>(s, p, st);
+        case 7: return launch_sb_cfg<T, RTW, 7>(s, p, st);
+        default: return launch_sb_cfg<T, RTW, 8>(s, p, st);
+    }
+}
+
+// Batched stage 1: rows of whole words (n % 32 == 0), 16-byte aligned x and s_in, and the per-range
+// sums fit in the workspace.
+inline bool sb1_plan(const GemvArgs& a, SbPlan& p) {
+    return a.n % 32 == 0 && a.r > 0 && aligned(a.x, 16) && aligned(a.s_in, 16) &&
+           sb_plan(a.batch, a.r, a.wn, a.plan.kpad, p) && p.part_bytes <= a.part_bytes;
+}
+
 template <typename T>
-void launch_stage1(const GemvArgs& a) {
+int launch_stage1_sb(const GemvArgs& a, const SbPlan& p) {
+    SbArgs s{};
+    s.words = a.v_bits;
+    s.s_in = a.s_in;
+    s.x = a.x;
+    s.s_mid = a.s_mid;
+    s.z_hi = a.z_hi;
+    s.z_lo = a.z_lo;
+    s.part = a.part;
+    s.M = a.r;
+    s.wpr = a.wn;
+    s.ldx = a.n;
+    s.batch = a.batch;
+    s.kw = p.kw;
+    s.kpad = a.plan.kpad;
+    s.zpitch = a.plan.zpitch;
+    s.kw4_magic = div_magic(4u * static_cast<uint32_t>(p.kw));
+    s.ws_magic = div_magic(static_cast<uint32_t>(p.kw) + 1u);
+    const int e = p.rtw == 4 ? launch_sb_rtw<T, 4>(s, p, a.stream)
+                             : (p.rtw == 2 ? launch_sb_rtw<T, 2>(s, p, a.stream) : launch_sb_rtw<T, 1>(s, p, a.stream));
+    if (e) return e;
+    if (p.ks > 1) {
+        if (int c = check_launch("nq_gemv stage 1 (batched)")) return c;
+        const int64_t threads = static_cast<int64_t>(s.batch) * s.zpitch / 4;
+        sb_finish1<T><<<dim3(static_cast<unsigned>(ceil_div(threads, 256))), 256, 0, a.stream>>>(s, p.ks);
+    }
+    return NQ_OK;
+}
+
+template <typename T>
+int launch_stage1(const GemvArgs& a) {
+    SbPlan sp;
+    if (sb1_plan(a, sp)) return launch_stage1_sb<T>(a, sp);
     if (s1w_applies(a.x, a.s_in, a.n, a.wn, a.r)) {
         S1Table tab;
         tab.count = 1;
         tab.item[0] = s1_item_of(a);
         launch_stage1_table<T>(tab, a.x, a.batch, a.n, a.wn, false, 0.0f, a.stream);
-        return;
+        return NQ_OK;
     }
     if (a.batch <= 1) launch_stage1_generic<T, 1>(a);
     else if (a.batch <= 2) launch_stage1_generic<T, 2>(a);
     else if (a.batch <= 4) launch_stage1_generic<T, 4>(a);
     else launch_stage1_generic<T, kMaxNB>(a);
+    return NQ_OK;
 }
 
 // Only the batch splits that fit in LDS are instantiated (the host never picks the others).
@@ -1173,7 +1540,7 @@ inline bool s2t_applies(const void* z_hi, const void* z_lo, const uint32_t* u_bi
 }
 
 template <typename T>
-void launch_stage2(const GemvArgs& a) {
+int launch_stage2(const GemvArgs& a) {
     if (s2t_applies(a.z_hi, a.z_lo, a.u_bits, a.m, a.plan)) {
         S2Table tab;
         tab.count = 1;
@@ -1189,20 +1556,35 @@ void launch_stage2(const GemvArgs& a) {
         it.zpitch = a.plan.zpitch;
         it.ystride = a.m;
         it.block_begin = 0;
-        if (launch_s2t_qw<T, kEpiStoreOne>(tab, a.plan.s2_qw, a.batch, a.stream)) return;
+        if (launch_s2t_qw<T, kEpiStoreOne>(tab, a.plan.s2_qw, a.batch, a.stream)) return NQ_OK;
     }
     if (a.batch <= 1) launch_stage2_generic<T, 1>(a);
     else if (a.batch <= 2) launch_stage2_generic<T, 2>(a);
     else if (a.batch <= 4) launch_stage2_generic<T, 4>(a);
     else launch_stage2_generic<T, kMaxNB>(a);
+    return NQ_OK;
 }
 
 template <typename T>
 int run_gemv(const GemvArgs& a) {
-    launch_stage1<T>(a);
+    if (int s = launch_stage1<T>(a)) return s;
     if (int s = check_launch("nq_gemv stage 1")) return s;
-    launch_stage2<T>(a);
+    if (int s = launch_stage2<T>(a)) return s;
     return check_launch("nq_gemv stage 2");
+}
+
+// The header and the intermediate (what every path needs).
+inline size_t gemv_base_bytes(int64_t batch, int64_t r) { return kHeaderBytes + 2 * z_bytes(batch, plan_of(r)); }
+
+// The per-range sums of the batched stage 1 at these sizes. A smaller workspace runs the kernels
+// that keep none.
+inline size_t gemv_part_bytes(int64_t batch, int64_t n, int64_t r, int64_t m) {
+    (void)m;
+    const Plan pl = plan_of(r);
+    size_t bytes = 0;
+    SbPlan p;
+    if (n % 32 == 0 && r > 0 && sb_plan(batch, r, ceil_div(n, 32), pl.kpad, p)) bytes = p.part_bytes;
+    return (bytes + 255) / 256 * 256;
 }
 
 }  // namespace
@@ -1213,10 +1595,8 @@ using namespace nq;
 extern "C" {
 
 size_t nq_gemv_workspace_bytes(int64_t batch, int64_t n, int64_t r, int64_t m) {
-    (void)n;
-    (void)m;
-    if (batch < 0 || r < 0) return 0;
-    return kHeaderBytes + 2 * z_bytes(batch, plan_of(r));
+    if (batch < 0 || r < 0 || n < 0 || m < 0) return 0;
+    return gemv_base_bytes(batch, r) + gemv_part_bytes(batch, n, r, m);
 }
 
 }  // extern "C"
@@ -1246,9 +1626,10 @@ int setup_gemv(const char* name, int stages, int dtype, const void* x, const voi
     if ((s1 && (!aligned(x, 2) || !aligned(s_in, 2) || !aligned(v_bits, 4) || (s_mid && !aligned(s_mid, 2)))) ||
         (s2 && (!aligned(s_out, 2) || !aligned(y, 2) || !aligned(u_bits, 4))))
         return fail(NQ_ERR_ALIGNMENT, "%s: misaligned operand", name);
-    const size_t need = nq_gemv_workspace_bytes(batch, n, r, m);
+    const size_t need = gemv_base_bytes(batch, r);
     if (workspace_bytes < need)
-        return fail(NQ_ERR_WORKSPACE, "%s: workspace has %zu bytes, needs %zu", name, workspace_bytes, need);
+        return fail(NQ_ERR_WORKSPACE, "%s: workspace has %zu bytes, needs %zu", name, workspace_bytes,
+                    nq_gemv_workspace_bytes(batch, n, r, m));
     a.x = static_cast<const uint16_t*>(x);
     a.s_in = static_cast<const uint16_t*>(s_in);
     a.v_bits = v_bits;
@@ -1265,19 +1646,21 @@ int setup_gemv(const char* name, int stages, int dtype, const void* x, const voi
     char* base = static_cast<char*>(workspace) + kHeaderBytes;
     a.z_hi = reinterpret_cast<uint16_t*>(base);
     a.z_lo = reinterpret_cast<uint16_t*>(base + z_bytes(batch, a.plan));
+    a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + need);
+    a.part_bytes = workspace_bytes - need;
     a.stream = as_stream(stream);
     return NQ_OK;
 }
 
 template <typename T>
 int run_stage1(const GemvArgs& a) {
-    launch_stage1<T>(a);
+    if (int s = launch_stage1<T>(a)) return s;
     return check_launch("nq_gemv stage 1");
 }
 
 template <typename T>
 int run_stage2(const GemvArgs& a) {
-    launch_stage2<T>(a);
+    if (int s = launch_stage2<T>(a)) return s;
     return check_launch("nq_gemv stage 2");
 }
 
@@ -1365,7 +1748,7 @@ int nq_gemv_noalloc(int dtype, const void* x, const void* s_in, const uint32_t* 
                     int64_t m, nq_stream_t stream) {
     const char* name = "nq_gemv_noalloc";
     if (batch < 0 || n < 0 || r < 0 || m < 0) return fail(NQ_ERR_INVALID_ARGUMENT, "%s: negative size", name);
-    const size_t need = nq_gemv_workspace_bytes(batch, n, r, m);
+    const size_t need = gemv_base_bytes(batch, r);
     if (need > static_cast<size_t>(NQ_GEMV_NOALLOC_SCRATCH_BYTES))
         return fail(NQ_ERR_WORKSPACE, "%s: batch %lld at rank %lld needs %zu bytes of scratch, the static buffer "
                     "holds %zu", name, (long long)batch, (long long)r, need,

@@ -157,6 +157,22 @@ GEMV_CASES = [
     ("tall_ragged_b1", 20520, 256, 96, 1, False),
     # 688 row tiles x two passes of 8 batch rows, with s_mid
     ("tall_b16_mid", 11008, 512, 64, 16, True),
+    # batches between the kernels' crossovers: the MFMA stage 1 on 4 .. 33 rows of narrow inputs,
+    # n = 1000 (not whole words), ragged ranks and rows
+    ("b4_tails", 300, 256, 70, 4, True),
+    ("b7_ragged", 1000, 512, 200, 7, True),
+    ("b33", 4100, 1024, 300, 33, False),
+    ("b32_n1000", 500, 1000, 96, 32, False),
+    # the batched stage 1 (k split over blocks, then a finishing launch that adds the ranges in
+    # order): from 64 rows, or from 16 on rows of 256 words or more; a ragged rank and batch, one
+    # k range or several, 5 and 7 batch tiles
+    ("sb_b100", 2048, 2048, 512, 100, True),
+    ("sb_b64_r200", 1000, 2048, 200, 64, True),
+    ("sb_b70_wide", 600, 8192, 500, 70, True),
+    ("sb_b20_wide_ragged", 700, 9216, 333, 20, False),
+    ("llama7b_gate_055_b64", 11008, 4096, 1632, 64, False),
+    ("llama7b_down_055_b64", 4096, 11008, 1632, 64, True),
+    ("llama7b_gate_055_b128", 11008, 4096, 1632, 128, False),
 ]
 
 
@@ -199,7 +215,8 @@ def test_gemv_parity(nq, case, dtype):
     assert err <= TOL[("gemv", dtype)], err
 
 
-@pytest.mark.parametrize("shape", [(4096, 4096, 1024, 1), (130, 200, 70, 5), (11008, 4096, 1632, 3)])
+@pytest.mark.parametrize("shape", [(4096, 4096, 1024, 1), (130, 200, 70, 5), (11008, 4096, 1632, 3),
+                                   (11008, 4096, 1632, 32), (4096, 11008, 1632, 64)])
 def test_gemv_stage_entry_points_match_nq_gemv(nq, shape):
     """nq_gemv_stage1 then nq_gemv_stage2 give nq_gemv's output bit for bit."""
     from nanoquant_amd import _lib

@@ -94,3 +94,22 @@ def test_noalloc_refuses_more_than_its_scratch(lib):
     status = lib.nq_gemv_noalloc(_lib.NQ_F16, None, None, None, None, None, None, None, batch, n, r, m, None)
     assert status == _lib.NQ_ERR_WORKSPACE
     assert b"static buffer" in lib.nq_last_error_message()
+
+
+def test_noalloc_batched_call_beyond_the_per_range_sums(lib):
+    """At 64 rows on the 4096 x 11008 shape, nq_gemv's batched stage 1 keeps per-range sums that do
+    not fit in the static array (nq_gemv_workspace_bytes exceeds it); the call still runs, with the
+    stage-1 kernel that keeps none, and agrees with nq_gemv and with float64 to the parity bar."""
+    from nanoquant_amd import _lib
+    m, n, r, batch = 4096, 11008, 1632, 64
+    announce("gemv noalloc past the per-range sums", (m, n, r, batch))
+    assert lib.nq_gemv_workspace_bytes(batch, n, r, m) > SCRATCH_BYTES
+    d = _case(44, m, n, r, batch, True, torch.float16)
+    want = _gemv_with_workspace(lib, d, _lib.NQ_F16)
+    got = _gemv_noalloc(lib, d, _lib.NQ_F16)
+    torch.cuda.synchronize()
+    c = d["raw"]
+    y64 = O.nanoquant_forward_f64(c["x"], c["s_in"], c["V"], c["s_mid"], c["U"], c["s_out"])
+    scale = np.abs(y64).max()
+    assert np.abs(got.double().cpu().numpy() - y64).max() / scale <= 1e-3
+    assert (got.double() - want.double()).abs().max().item() / scale <= 1e-3
