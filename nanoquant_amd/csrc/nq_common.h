@@ -134,6 +134,17 @@ __device__ inline u32x4 load_b128_stream(rsrc_t rs, uint32_t offset) {
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(offset), 0, 2));
 }
 
+// DMA of 16 / 4 bytes a lane from global memory into LDS (global_load_lds): a wave's lanes land in
+// consecutive slots from `lds` (which must be the same for every lane of the wave).
+__device__ inline void dma16(const void* src, void* lds) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                     (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+__device__ inline void dma4(const void* src, void* lds) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                     (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
+}
+
 template <typename T>
 __device__ inline uint16_t saturate_to(float v, float sat) {
     v = fminf(fmaxf(v, -sat), sat);  // as the reference's clamp: a NaN input becomes -sat

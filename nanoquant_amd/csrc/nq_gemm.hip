@@ -211,16 +211,6 @@ __device__ inline void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-__device__ inline void dma_to_lds16(const void* src, void* lds) {
-    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
-                                     (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
-}
-
-__device__ inline void dma_to_lds4(const void* src, void* lds) {
-    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
-                                     (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
-}
-
 template <typename T, bool kSin, bool kSout, int BP, int BQ, int WP, int WQ, int WPE, int KS, bool kSplit,
           int BKK = 64>
 __global__ __launch_bounds__((BP / WP) * (BQ / WQ) * 64 * KS) __attribute__((amdgpu_waves_per_eu(WPE)))
@@ -312,11 +302,11 @@ void gemm_dm_kernel(
     auto issue = [&](int iter, uint16_t* xs, uint32_t* ws, uint32_t* ss) {
         const uint32_t k0 = static_cast<uint32_t>((k_first + iter) * BKK);
 #pragma unroll
-        for (int j = 0; j < XPT; ++j) dma_to_lds16(A + (xoff[j] + k0), xs + (j * NTG + gw * 64) * 8);
+        for (int j = 0; j < XPT; ++j) dma16(A + (xoff[j] + k0), xs + (j * NTG + gw * 64) * 8);
         const uint32_t wrow = static_cast<uint32_t>((k_first + iter) * KT) * half_n;
 #pragma unroll
-        for (int j = 0; j < WPT; ++j) dma_to_lds4(W + (wrow + wsrc[j]), ws + j * NTG + gw * 64);
-        if (kSin) dma_to_lds4(s_in + (k0 + 2 * sidx), ss + wave * 64);
+        for (int j = 0; j < WPT; ++j) dma4(W + (wrow + wsrc[j]), ws + j * NTG + gw * 64);
+        if (kSin) dma4(s_in + (k0 + 2 * sidx), ss + wave * 64);
     };
 
     f32x16 acc[TP][TQ];

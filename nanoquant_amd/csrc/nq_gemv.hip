@@ -280,9 +280,15 @@ __device__ inline Item pick_item(const Table& tab) {
 // kNorm folds an RMSNorm of x into the stage: every group also sums x^2 over the whole row
 // (the lanes hold all of x anyway) and h is multiplied by rsqrt(sum / n + eps); the norm's
 // weight is expected inside s_in.
-template <typename T, int NB, int WPL, int WR, int R, int G, bool kNorm, bool kOne>
+//
+// kLdsX (one batch row, n % 32 == 0): s_in and x reach LDS by DMA once per block and every lane
+// reads its pairs from there, instead of each row group fetching all of both through the vector
+// cache. Chunk v (16 bytes) of word q of each array sits at slot 4q + (v ^ ((q / 4) % 4)), so the
+// 16 lanes of a quarter-wave, reading chunk v of 16 consecutive words, hit 16 distinct slots mod 16.
+template <typename T, int NB, int WPL, int WR, int R, int G, bool kNorm, bool kOne, bool kLdsX = false>
 __global__ __launch_bounds__(G * WR * 64) void s1w_kernel(const S1Table tab, const uint16_t* __restrict__ x, int batch,
                                                           int n, int wn, float eps) {
+    static_assert(!kLdsX || NB == 1, "the LDS copy of x holds one batch row");
     constexpr int kGroups = G;
     constexpr int kRows = kGroups * R;
     constexpr int kPartRows = R + (kNorm ? 1 : 0);
@@ -312,41 +318,83 @@ __global__ __launch_bounds__(G * WR * 64) void s1w_kernel(const S1Table tab, con
     uint16_t mid[R];
 #pragma unroll
     for (int k = 0; k < R; ++k) mid[k] = msrc[min(j0 + k, mlim)];
-    // s_in and x first (from L2), then V's words (from HBM), each in 16- and 4-byte pieces
     uint32_t sp[WPL][16];
     uint32_t xp[WPL][NB][16];
-#pragma unroll
-    for (int w = 0; w < WPL; ++w)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const uint32_t off = (32u * static_cast<uint32_t>(p + 64 * WR * w) + 8u * v) * 2u;
-            const u32x4 sv = load_b128(s_rs, off);
-            sp[w][4 * v + 0] = sv.x;
-            sp[w][4 * v + 1] = sv.y;
-            sp[w][4 * v + 2] = sv.z;
-            sp[w][4 * v + 3] = sv.w;
-#pragma unroll
-            for (int b = 0; b < NB; ++b) {
-                const u32x4 xv = load_b128(x_rs[b], off);
-                xp[w][b][4 * v + 0] = xv.x;
-                xp[w][b][4 * v + 1] = xv.y;
-                xp[w][b][4 * v + 2] = xv.z;
-                xp[w][b][4 * v + 3] = xv.w;
-            }
-        }
-    __builtin_amdgcn_sched_barrier(0);
     // a lane past the row's last word loads nothing (an offset past the resource touches no memory)
     const uint32_t v_end = static_cast<uint32_t>(r) * static_cast<uint32_t>(wn) * 4u;
     uint32_t vb[R][WPL];
+    auto load_v = [&]() {
 #pragma unroll
-    for (int k = 0; k < R; ++k)
+        for (int k = 0; k < R; ++k)
+#pragma unroll
+            for (int w = 0; w < WPL; ++w) {
+                const int q = p + 64 * WR * w;
+                const uint32_t off =
+                    (static_cast<uint32_t>(j0 + k) * static_cast<uint32_t>(wn) + static_cast<uint32_t>(q)) * 4u;
+                vb[k][w] = load_b32_stream(v_rs, q < wn ? off : v_end);
+            }
+    };
+    if constexpr (kLdsX) {
+        // V's words first (from HBM), then the DMA of s_in and x (from L2): chunk slot l of array
+        // a = l / (4 wn) holds chunk v = (l % 4) ^ ((q / 4) % 4) of word q = (l % (4 wn)) / 4
+        extern __shared__ __attribute__((aligned(16))) uint32_t sx[];
+        load_v();
+        const int per = 4 * wn;  // chunks per array
+        for (int l0 = __builtin_amdgcn_readfirstlane(t >> 6) * 64; l0 < 2 * per; l0 += G * WR * 64) {
+            const int l = min(l0 + lane, 2 * per - 1);
+            const int arr = l >= per ? 1 : 0;
+            const int lq = l - arr * per;
+            const int q = lq >> 2;
+            const int v = (lq & 3) ^ ((q >> 2) & 3);
+            dma16((arr ? x : it.s_in) + 32 * q + 8 * v, sx + 4 * l0);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
 #pragma unroll
         for (int w = 0; w < WPL; ++w) {
             const int q = p + 64 * WR * w;
-            const uint32_t off = (static_cast<uint32_t>(j0 + k) * static_cast<uint32_t>(wn) + static_cast<uint32_t>(q)) * 4u;
-            vb[k][w] = load_b32_stream(v_rs, q < wn ? off : v_end);
+            const int qc = min(q, wn - 1);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int slot = 4 * qc + (v ^ ((qc >> 2) & 3));
+                const u32x4 sv = *reinterpret_cast<const u32x4*>(sx + 4 * slot);
+                const u32x4 xv = *reinterpret_cast<const u32x4*>(sx + 4 * (per + slot));
+                const bool ok = q < wn;  // a lane past the row multiplies zeros
+                sp[w][4 * v + 0] = ok ? sv.x : 0u;
+                sp[w][4 * v + 1] = ok ? sv.y : 0u;
+                sp[w][4 * v + 2] = ok ? sv.z : 0u;
+                sp[w][4 * v + 3] = ok ? sv.w : 0u;
+                xp[w][0][4 * v + 0] = xv.x;
+                xp[w][0][4 * v + 1] = xv.y;
+                xp[w][0][4 * v + 2] = xv.z;
+                xp[w][0][4 * v + 3] = xv.w;
+            }
         }
-    __builtin_amdgcn_sched_barrier(0);
+    } else {
+        // s_in and x first (from L2), then V's words (from HBM), each in 16- and 4-byte pieces
+#pragma unroll
+        for (int w = 0; w < WPL; ++w)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const uint32_t off = (32u * static_cast<uint32_t>(p + 64 * WR * w) + 8u * v) * 2u;
+                const u32x4 sv = load_b128(s_rs, off);
+                sp[w][4 * v + 0] = sv.x;
+                sp[w][4 * v + 1] = sv.y;
+                sp[w][4 * v + 2] = sv.z;
+                sp[w][4 * v + 3] = sv.w;
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+                    const u32x4 xv = load_b128(x_rs[b], off);
+                    xp[w][b][4 * v + 0] = xv.x;
+                    xp[w][b][4 * v + 1] = xv.y;
+                    xp[w][b][4 * v + 2] = xv.z;
+                    xp[w][b][4 * v + 3] = xv.w;
+                }
+            }
+        __builtin_amdgcn_sched_barrier(0);
+        load_v();
+        __builtin_amdgcn_sched_barrier(0);
+    }
 
     NQ_STAMP(1);
     // Even and odd pairs accumulate separately and rows are innermost, so consecutive dot2
@@ -866,16 +914,6 @@ struct SbArgs {
 // ceil(2^32 / d): n / d == __umulhi(n, magic) for n * d < 2^32.
 inline uint32_t div_magic(uint32_t d) { return static_cast<uint32_t>(((1ULL << 32) + d - 1) / d); }
 
-__device__ inline void dma16(const void* src, void* lds) {
-    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
-                                     (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
-}
-
-__device__ inline void dma4(const void* src, void* lds) {
-    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
-                                     (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
-}
-
 // Dwords of LDS an sb_kernel block takes (x slice, then words), each part rounded to whole DMAs.
 __host__ __device__ inline int sb_xs_dwords(int xcols, int kw) { return (xcols * kw * 4 + 63) / 64 * 64 * 4; }
 __host__ __device__ inline int sb_w_dwords(int rows, int kw) { return (rows * (kw + 1) + 63) / 64 * 64; }
@@ -1198,37 +1236,56 @@ void launch_stage2_generic(const GemvArgs& a) {
 }
 
 // Launch shapes of the VALU stage 1, measured on MI355X (graph-replayed, 64-128 rotating weight
-// copies, batch 1): n = 4096 (r = 1632) 3.11 us with two words per lane, one wave and two rows per
-// group, four groups (3.23-3.74 for the other splits); n = 8192 4.48 us at r = 2240 and 5.14 at
-// r = 3520 with one word per lane over four waves, four rows; n = 11008 4.65 us with one word per
-// lane over six waves (384 words for 344), four rows per group, two groups (4.70 with three words
-// over two waves). Every block reads all of x and s_in once per group, so wide rows take more
-// rows per group; one word per lane keeps the per-wave chain of dot products short.
+// copies, batch 1, stage 1 alone): n = 4096 (r = 1632) 2.96 us with x and s_in in LDS, two words
+// per lane, one wave and two rows per group, four groups (3.13 with the same shape reading x from
+// the vector cache, 3.05-3.74 for the other splits); n = 8192 4.49 us at r = 2240 with one word per
+// lane over four waves, four rows (4.58-4.74 with x in LDS); n = 11008 4.54 us with x in LDS, six
+// words per lane over one wave per row (no cross-wave sum), two rows per group, four groups (4.64
+// for the best shape without LDS: one word per lane over six waves, four rows, two groups).
 // Launch shape of s1w_kernel: WPL words per lane, WR waves per row group, R rows per group, G
-// groups per block (G * WR * 64 threads, R * G rows). The lanes of a group cover 64 * WR * WPL
-// >= wn words of a row.
+// groups per block (G * WR * 64 threads, R * G rows), x and s_in from LDS or not. The lanes of a
+// group cover 64 * WR * WPL >= wn words of a row.
 struct S1wShape {
     int wpl, wr, r, g;
+    bool lds;
 };
 
-// The instantiated shapes (wpl, wr, r, g).
+// The instantiated shapes (wpl, wr, r, g), and those also instantiated with x in LDS.
 #ifndef NQ_S1W_SHAPES
 #define NQ_S1W_SHAPES(X) X(1, 1, 2, 4) X(2, 1, 2, 4) X(1, 4, 4, 1) X(1, 6, 4, 2) X(2, 4, 4, 1)
 #endif
+#ifndef NQ_S1W_LDS_SHAPES
+#define NQ_S1W_LDS_SHAPES(X) X(2, 1, 2, 4) X(6, 1, 2, 4)
+#endif
 
-inline S1wShape s1w_shape(int wn, bool grouped) {
-    (void)grouped;
-    if (wn <= 64) return {1, 1, 2, 4};
-    if (wn <= 128) return {2, 1, 2, 4};
-    if (wn <= 256) return {1, 4, 4, 1};
-    if (wn <= 384) return {1, 6, 4, 2};
-    return {2, 4, 4, 1};
+// lds_ok: one item, one batch row, n % 32 == 0 (the LDS copy of x and s_in, 32 * wn bytes, fits).
+inline S1wShape s1w_shape(int wn, bool lds_ok) {
+    if (wn <= 64) return {1, 1, 2, 4, false};
+    if (wn <= 128) return {2, 1, 2, 4, lds_ok};
+    if (wn <= 256) return {1, 4, 4, 1, false};
+    if (wn <= 384) return lds_ok ? S1wShape{6, 1, 2, 4, true} : S1wShape{1, 6, 4, 2, false};
+    return {2, 4, 4, 1, false};
 }
+
+// Bytes of dynamic LDS of the kLdsX stage 1: s_in and x, 16 * wn bytes each, in whole DMAs.
+inline size_t s1w_lds_bytes(int wn) { return static_cast<size_t>((8 * wn + 63) / 64 * 64) * 16; }
 
 template <typename T, int NB, bool kNorm, bool kOne>
 void launch_s1w_cfg(const S1wShape& sh, const S1Table& tab, int blocks, const uint16_t* x, int batch, int n, int wn,
                     float eps, hipStream_t st) {
     const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(ceil_div(batch, NB)));
+    if constexpr (NB == 1) {
+        if (sh.lds) {
+            const size_t lds = s1w_lds_bytes(wn);
+#define NQ_S1W_LDS_CASE(WPL, WR, R, G)                                                                      \
+    if (sh.wpl == WPL && sh.wr == WR && sh.r == R && sh.g == G) {                                           \
+        s1w_kernel<T, NB, WPL, WR, R, G, kNorm, kOne, true><<<grid, G * WR * 64, lds, st>>>(tab, x, batch, n, wn, eps); \
+        return;                                                                                             \
+    }
+            NQ_S1W_LDS_SHAPES(NQ_S1W_LDS_CASE)
+#undef NQ_S1W_LDS_CASE
+        }
+    }
 #define NQ_S1W_CASE(WPL, WR, R, G)                                                                        \
     if (sh.wpl == WPL && sh.wr == WR && sh.r == R && sh.g == G) {                                         \
         s1w_kernel<T, NB, WPL, WR, R, G, kNorm, kOne><<<grid, G * WR * 64, 0, st>>>(tab, x, batch, n, wn, eps); \
@@ -1256,7 +1313,9 @@ void launch_s1w_nb(const S1wShape& sh, const S1Table& tab, int blocks, const uin
 template <typename T>
 void launch_s1w_table(S1Table& tab, const uint16_t* x, int batch, int n, int wn, bool norm, float eps,
                       hipStream_t st) {
-    const S1wShape sh = s1w_shape(wn, tab.count > 1);
+    // x in LDS for one item at batch 1 (measured for single GEMVs; the grouped launches keep the
+    // shapes they were measured with)
+    const S1wShape sh = s1w_shape(wn, tab.count == 1 && batch == 1 && n % 32 == 0 && !norm);
     const int rpb = sh.r * sh.g;
     int blocks = 0;
     for (int k = 0; k < tab.count; ++k) {
