@@ -217,7 +217,7 @@ __global__ __launch_bounds__((BP / WP) * (BQ / WQ) * 64 * KS) __attribute__((amd
 void gemm_dm_kernel(
     const uint16_t* __restrict__ A, const uint32_t* __restrict__ W, const uint16_t* __restrict__ s_in,
     const uint16_t* __restrict__ s_out, uint16_t* __restrict__ C, int M, int K, int N, int q_tiles, int p_tiles,
-    float* __restrict__ part, int split_steps) {
+    float* __restrict__ part, int split_steps, const uint16_t* __restrict__ k_scale) {
     static_assert(BKK == 64 || BKK == 128, "64 or 128 k per step");
     constexpr int CPR = BKK / 8;       // 16-byte chunks per A-tile row
     constexpr int NWP = BP / WP;
@@ -264,8 +264,21 @@ void gemm_dm_kernel(
     const uint32_t half_n = static_cast<uint32_t>(N) >> 1;
     // steps of this block's k group or k range (the host makes K / 64 divide by KS and leaves no
     // k range empty), and the first of them
-    const int k_iters = kSplit ? min(split_steps, K / BKK - split * split_steps) : K / BKK / KS;
+    int k_iters = kSplit ? min(split_steps, K / BKK - split * split_steps) : K / BKK / KS;
     const int k_first = kSplit ? split * split_steps : grp * k_iters;
+    // k_scale (one block over all of K, K <= 32 * NT): A's columns whose k_scale entry is zero are
+    // exact zeros (the previous stage multiplied them by it; the padded rank of the NanoQuant
+    // factorisation), so the 64-k steps after the last nonzero entry add nothing and are not run.
+    // Its entries are read here and examined once the first steps' DMAs are on their way.
+    constexpr int kScaleLoads = 4;
+    const bool k_trim = KS == 1 && !kSplit && k_scale != nullptr && K <= 8 * kScaleLoads * NT;
+    u32x4 kv[kScaleLoads];
+    if (k_trim) {
+        const rsrc_t ks_rs = make_rsrc(k_scale, static_cast<uint32_t>(K) * 2u);
+#pragma unroll
+        for (int i = 0; i < kScaleLoads; ++i) kv[i] = load_b128(ks_rs, static_cast<uint32_t>(t + i * NT) * 16u);
+    }
+    __shared__ int klast[NT / 64];
 
     // lane constants: the first of the four words of its feature per 64-feature group, the shift
     // per 32-feature tile, its A-tile rows and the swizzled chunk of its 8 k per k tile
@@ -371,8 +384,27 @@ void gemm_dm_kernel(
     uint32_t* w2 = ws2[grp];
     issue(0, x0, w0, ss0);
     issue(min(1, k_iters - 1), x1, w1, ss1);
+    if (k_trim) {
+        int last = -1;  // the last nonzero entry this thread holds (zeros past K)
+#pragma unroll
+        for (int i = 0; i < kScaleLoads; ++i) {
+            const uint32_t d[4] = {kv[i].x, kv[i].y, kv[i].z, kv[i].w};
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (((d[j >> 1] >> (16 * (j & 1))) & 0x7fffu) != 0) last = 8 * (t + i * NT) + j;
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) last = max(last, __shfl_xor(last, off, 64));
+        if (lane == 0) klast[wave] = last;
+    }
     wait_vmcnt<kIssued>();
     __syncthreads();
+    if (k_trim) {
+        int last = -1;
+#pragma unroll
+        for (int w = 0; w < NT / 64; ++w) last = max(last, klast[w]);
+        k_iters = max(1, min(k_iters, (last + BKK) / BKK));  // steps up to the one holding `last`
+    }
     int it = 0;
     for (; it + 3 <= k_iters; it += 3) {
         step(x0, w0, ss0, x2, w2, ss2, it);
@@ -450,7 +482,8 @@ void gemm_dm_kernel(
 
 template <typename T, int BP, int BQ, int WP, int WQ, int WPE, int KS>
 void launch_dm(const void* A, const uint32_t* W, const void* s_in, const void* s_out, void* C, int64_t M, int64_t K,
-               int64_t N, hipStream_t stream) {
+               int64_t N, hipStream_t stream, const void* k_scale = nullptr) {
+    const auto* ksc = static_cast<const uint16_t*>(k_scale);
     const int q_tiles = static_cast<int>(ceil_div(M, BQ));
     const int p_tiles = static_cast<int>(ceil_div(N, BP));
     const dim3 grid(static_cast<unsigned>(q_tiles * p_tiles));
@@ -462,16 +495,16 @@ void launch_dm(const void* A, const uint32_t* W, const void* s_in, const void* s
     const int m = static_cast<int>(M), k = static_cast<int>(K), n = static_cast<int>(N);
     if (s_in && s_out)
         gemm_dm_kernel<T, true, true, BP, BQ, WP, WQ, WPE, KS, false>
-            <<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles, p_tiles, nullptr, 0);
+            <<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles, p_tiles, nullptr, 0, ksc);
     else if (s_in)
         gemm_dm_kernel<T, true, false, BP, BQ, WP, WQ, WPE, KS, false>
-            <<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles, p_tiles, nullptr, 0);
+            <<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles, p_tiles, nullptr, 0, ksc);
     else if (s_out)
         gemm_dm_kernel<T, false, true, BP, BQ, WP, WQ, WPE, KS, false>
-            <<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles, p_tiles, nullptr, 0);
+            <<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles, p_tiles, nullptr, 0, ksc);
     else
         gemm_dm_kernel<T, false, false, BP, BQ, WP, WQ, WPE, KS, false>
-            <<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles, p_tiles, nullptr, 0);
+            <<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles, p_tiles, nullptr, 0, ksc);
 }
 
 // C[q, o] = sat(s_out[o] * sum_s part[s][q][o]) (the planes added in order); one thread per four
@@ -520,10 +553,10 @@ void launch_dm_split(const void* A, const uint32_t* W, const void* s_in, const v
     const int m = static_cast<int>(M), k = static_cast<int>(K), n = static_cast<int>(N);
     if (s_in)
         gemm_dm_kernel<T, true, false, BP, BQ, WP, WQ, WPE, 1, true>
-            <<<grid, NT, 0, stream>>>(a, W, si, nullptr, c, m, k, n, q_tiles, p_tiles, part, split_steps);
+            <<<grid, NT, 0, stream>>>(a, W, si, nullptr, c, m, k, n, q_tiles, p_tiles, part, split_steps, nullptr);
     else
         gemm_dm_kernel<T, false, false, BP, BQ, WP, WQ, WPE, 1, true>
-            <<<grid, NT, 0, stream>>>(a, W, nullptr, nullptr, c, m, k, n, q_tiles, p_tiles, part, split_steps);
+            <<<grid, NT, 0, stream>>>(a, W, nullptr, nullptr, c, m, k, n, q_tiles, p_tiles, part, split_steps, nullptr);
     const int64_t quads = M * (N / 4);
     const dim3 fgrid(static_cast<unsigned>(ceil_div(quads, 256)));
     if (s_out)
@@ -576,9 +609,11 @@ GemmPlan plan_gemm(int64_t M, int64_t K, int64_t N) {
     return p;
 }
 
+// k_scale: the scale the previous stage gave A's columns (nullptr if none); see gemm_dm_kernel.
 template <typename T>
 int launch_gemm(const char* name, const void* A, const uint32_t* W, const void* s_in, const void* s_out, void* C,
-                int64_t M, int64_t K, int64_t N, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+                int64_t M, int64_t K, int64_t N, void* workspace, size_t workspace_bytes, hipStream_t stream,
+                const void* k_scale = nullptr) {
     GemmPlan p = plan_gemm(M, K, N);
     if (p.mode != kModeOnebit && !aligned(C, 8)) p.mode = kModeOnebit;
     if (p.mode == kModeSplit && (!workspace || workspace_bytes < p.workspace_bytes || !aligned(workspace, 16)))
@@ -587,7 +622,7 @@ int launch_gemm(const char* name, const void* A, const uint32_t* W, const void* 
         case kModeOnebit:
             return launch_onebit<T>(A, W, s_in, s_out, C, M, K, N, stream);
         case kModeTile:
-            launch_dm<T, 256, 64, 64, 64, 2, 1>(A, W, s_in, s_out, C, M, K, N, stream);
+            launch_dm<T, 256, 64, 64, 64, 2, 1>(A, W, s_in, s_out, C, M, K, N, stream, k_scale);
             break;
         case kModeGroups:
             launch_dm<T, 256, 64, 64, 64, 2, 2>(A, W, s_in, s_out, C, M, K, N, stream);
@@ -659,10 +694,11 @@ int nq_gemm_nanoquant(int dtype, const void* A, const uint32_t* v_bits, const ui
                            : launch_gemm<BF16>(n1, A, v_bits, s_g, s_l, imm, M, n, r_pad, workspace, workspace_bytes, st);
         if (s1) return s1;
     }
-    // stage 2 reuses the workspace: the finishing launch of stage 1 has read it by then (same stream)
+    // stage 2 reuses the workspace: the finishing launch of stage 1 has read it by then (same stream).
+    // It stops at the last rank column with a nonzero s_l (the rank padding gives exact zeros).
     return dtype == NQ_F16
-               ? launch_gemm<F16>(n2, imm, u_bits, nullptr, s_h, C, M, r_pad, m, workspace, workspace_bytes, st)
-               : launch_gemm<BF16>(n2, imm, u_bits, nullptr, s_h, C, M, r_pad, m, workspace, workspace_bytes, st);
+               ? launch_gemm<F16>(n2, imm, u_bits, nullptr, s_h, C, M, r_pad, m, workspace, workspace_bytes, st, s_l)
+               : launch_gemm<BF16>(n2, imm, u_bits, nullptr, s_h, C, M, r_pad, m, workspace, workspace_bytes, st, s_l);
 }
 
 }  // extern "C"
