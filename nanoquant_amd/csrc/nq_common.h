@@ -145,6 +145,33 @@ __device__ inline void dma4(const void* src, void* lds) {
                                      (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
 }
 
+// Waits until at most N of this wave's vector-memory operations (loads, DMAs) are outstanding;
+// they complete in issue order.
+template <int N>
+__device__ inline void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt has 6 bits");
+    // gfx9 s_waitcnt: vmcnt in bits 3:0 and 15:14; expcnt (6:4) and lgkmcnt (11:8) not waited on
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier for DMA pipelines. __syncthreads() carries workgroup-scope fences, and the
+// release fence makes the compiler wait for every outstanding vector-memory operation (vmcnt 0),
+// LDS DMAs issued for later steps included, which empties a multi-buffered pipeline at every
+// step. Here each wave first waits (wait_vmcnt) for its DMAs that the next step reads; this
+// function then waits for the wave's own LDS reads (lgkmcnt 0) and meets the other waves at
+// s_barrier. The LDS wait matters: the compiler places the wait for a read's data next to its
+// first use, which may come after the barrier, and a wave past the barrier may start a DMA into
+// the buffer that a slower wave's reads (still queued behind bank conflicts) have yet to see.
+// The empty asm statements with a memory clobber keep the compiler from moving any memory access
+// across the barrier.
+__device__ inline void barrier_keep_dma() {
+    asm volatile("" ::: "memory");
+    // gfx9 s_waitcnt: lgkmcnt (11:8) zero; vmcnt (3:0, 15:14) and expcnt (6:4) at their maximum
+    __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 template <typename T>
 __device__ inline uint16_t saturate_to(float v, float sat) {
     v = fminf(fmaxf(v, -sat), sat);  // as the reference's clamp: a NaN input becomes -sat

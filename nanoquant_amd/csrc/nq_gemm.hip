@@ -198,19 +198,13 @@ int launch_onebit(const void* A, const uint32_t* W, const void* s_in, const void
 // is fetched in the order the operands read it (every wave keeps its own copy, so every wave
 // issues the same number of DMAs per step). The three buffers are distinct LDS arrays, so the
 // compiler's wait counts for a buffer's reads cover only that buffer's DMAs; before the barrier
-// that ends a step each wave waits for its own DMAs of the next step.
+// that ends a step each wave waits for its own DMAs of the next step, and only for those: the
+// barrier carries no memory fence, so the DMAs of the step after stay in flight across it.
 // With KS = 2 the block holds two groups of waves with buffers of their own, each over half of
 // the k steps (for outputs too few to give every SIMD two waves); group 1 hands its accumulators
 // to group 0 through LDS at the end. With kSplit the grid repeats the tiles once per k range of
 // split_steps steps, and each block stores its raw fp32 sums to its plane of `part`
 // [splits][M][N]; gemm_split_finish_kernel adds the planes in order and applies the epilogue.
-template <int N>
-__device__ inline void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt has 6 bits");
-    // gfx9 s_waitcnt: vmcnt in bits 3:0 and 15:14; expcnt (6:4) and lgkmcnt (11:8) not waited on
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
 template <typename T, bool kSin, bool kSout, int BP, int BQ, int WP, int WQ, int WPE, int KS, bool kSplit,
           int BKK = 64>
 __global__ __launch_bounds__((BP / WP) * (BQ / WQ) * 64 * KS) __attribute__((amdgpu_waves_per_eu(WPE)))
@@ -365,6 +359,7 @@ void gemm_dm_kernel(
     auto step = [&](const uint16_t* xc, const uint32_t* wc, const uint32_t* sc, uint16_t* xf, uint32_t* wf,
                     uint32_t* sf, int it) {
         issue(min(it + 2, k_iters - 1), xf, wf, sf);
+        __builtin_amdgcn_sched_barrier(0);  // the DMAs go out first, not after the step's MFMAs
         Frag f[2];
         read_kt(f[0], xc, wc, sc, 0);
 #pragma unroll
@@ -373,7 +368,7 @@ void gemm_dm_kernel(
             compute_kt(f[kt & 1]);
         }
         wait_vmcnt<kIssued>();
-        __syncthreads();
+        barrier_keep_dma();
     };
 
     uint16_t* x0 = xs0[grp];
