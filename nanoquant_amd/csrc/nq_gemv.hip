@@ -871,6 +871,193 @@ __global__ __launch_bounds__(256) void s2t_kernel(const S2Table tab, int batch) 
     NQ_STAMP(3);
 }
 
+// --------------------------------------------------------------------------- stage 2, batched
+//
+// For many batch rows: s2t_kernel makes one pass over U per 8 batch rows, decoding U and staging
+// the intermediate again on each. s2b_kernel decodes each A fragment (16 rows of U x 32 k, as in
+// s2t_kernel) once for all of its block's batch rows. Block = 4 waves in a WR x (4 / WR) grid: wave
+// (wr, wc) runs row tiles wr + WR * j (j < RTW) of the block's RT = WR * RTW tiles of 16 rows
+// against column tiles wc * CTW + j2 (j2 < CTW), each 8 batch rows x (hi, lo) as in s2t_kernel.
+//
+// The block's words of U reach LDS by DMA first, row-major as in memory. The intermediate streams
+// through three LDS buffers in chunks of KC words of k (32 KC columns of every batch row, hi and
+// lo), each fetched by DMA two chunks ahead, so no register holds a chunk in flight. LDS row
+// R = 2 b + (0 hi, 1 lo) of a chunk holds 4 KC pieces of 16 bytes, piece p at slot p ^ (R % 8): the
+// eight lanes of a fragment read that share a bank group read eight different rows.
+//
+// Every chunk runs all of its KC steps: past the rank, the intermediate's columns [kpad, zpitch)
+// are zero (stage 1 writes them), and the host only picks KC that keep 32 KC * chunks <= zpitch,
+// so the words read past a row (the next row's, or the tile's padding) multiply zeros.
+struct S2bArgs {
+    const uint32_t* u_bits;
+    const uint16_t* s_out;
+    uint16_t* y;
+    const uint16_t* z_hi;
+    const uint16_t* z_lo;
+    int m, wr, zpitch, batch, chunks;
+    int u_slots;      // LDS dwords of the U tile (its rows' words and the padding, whole DMAs)
+    int store8;       // y takes 8-byte stores of four rows (m % 4 == 0, y 8-byte aligned)
+};
+
+template <int RT, int WR, int CTW, int KC>
+struct S2bShape {
+    static constexpr int kRTW = RT / WR;
+    static constexpr int kWC = 4 / WR;
+    static constexpr int kRows = 16 * RT;            // rows of U per block
+    static constexpr int kBatch = 8 * kWC * CTW;      // batch rows per block
+    static constexpr int kPieces = 4 * KC;            // 16-byte pieces per LDS row of a chunk
+    static constexpr int kSlots = 2 * kBatch * kPieces;  // 16-byte slots per chunk buffer
+    static_assert(RT % WR == 0 && (WR == 1 || WR == 2 || WR == 4), "row tiles split evenly over WR");
+    static_assert(KC == 2 || KC == 4, "two or four words of k per chunk");
+    static_assert(kSlots % 256 == 0, "whole DMAs per thread");
+};
+
+template <typename T, int RT, int WR, int CTW, int KC>
+__global__ __launch_bounds__(256) void s2b_kernel(const S2bArgs a) {
+    using S = S2bShape<RT, WR, CTW, KC>;
+    constexpr int RTW = S::kRTW;
+    constexpr int NP = S::kPieces;
+    constexpr int kDma = S::kSlots / 256;  // 16-byte DMAs per thread per chunk
+    // distinct LDS arrays: the compiler's wait before a buffer's reads then counts only the DMAs
+    // into that buffer, not the ones in flight into the others
+    __shared__ __attribute__((aligned(16))) uint32_t hb0[4 * S::kSlots], hb1[4 * S::kSlots], hb2[4 * S::kSlots];
+    extern __shared__ __attribute__((aligned(16))) uint32_t ut[];  // the U tile (a.u_slots dwords)
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int c = lane & 15;
+    const int g = lane >> 4;
+    const int wrow = wave % WR;
+    const int wcol = wave / WR;
+    const int i0 = static_cast<int>(blockIdx.x) * S::kRows;
+    const int bb = static_cast<int>(blockIdx.y) * S::kBatch;
+    NQ_STAMP(0);
+
+    // 1. DMA: the rows' words (clamped to the last word of U: slots past the rows are never used
+    //    for a stored output), then the first two chunks of the intermediate
+    const uint32_t wtotal = static_cast<uint32_t>(a.m) * static_cast<uint32_t>(a.wr);
+    const uint32_t wbase = static_cast<uint32_t>(i0) * static_cast<uint32_t>(a.wr);
+    for (int l0 = wave * 64; l0 < a.u_slots; l0 += 256)
+        dma4(a.u_bits + min(wbase + static_cast<uint32_t>(l0 + lane), wtotal - 1u), ut + l0);
+    // this thread's DMA sources: LDS row R = l / NP of slot l, batch row clamped below batch
+    const uint16_t* hsrc[kDma];
+#pragma unroll
+    for (int j = 0; j < kDma; ++j) {
+        const int l = j * 256 + t;
+        const int R = l / NP;
+        const int p = (l % NP) ^ (R & 7);
+        const uint32_t b = static_cast<uint32_t>(min(bb + (R >> 1), a.batch - 1));
+        hsrc[j] = ((R & 1) ? a.z_lo : a.z_hi) + b * static_cast<uint32_t>(a.zpitch) + 8 * p;
+    }
+    auto issue = [&](int ci, uint32_t* buf) {
+        const uint32_t k0 = static_cast<uint32_t>(ci) * 32u * KC;
+#pragma unroll
+        for (int j = 0; j < kDma; ++j) dma16(hsrc[j] + k0, buf + (j * 256 + wave * 64) * 4);
+    };
+    issue(0, hb0);
+    issue(min(1, a.chunks - 1), hb1);
+    // the output scales of this lane's rows (needed only by the epilogue)
+    uint16_t so[RTW][4];
+#pragma unroll
+    for (int j = 0; j < RTW; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) so[j][i] = a.s_out[min(i0 + 16 * (wrow + WR * j) + 4 * g + i, a.m - 1)];
+    wait_vmcnt<kDma>();  // the words and chunk 0 (chunk 1's DMAs may still be in flight)
+    barrier_keep_dma();
+    NQ_STAMP(1);
+
+    // 2. MFMAs, chunk by chunk
+    const uint32_t mask = kSignPair, one = kBf16OnePair;
+    const int sh = 4 * g;
+    f32x4 acc[RTW][CTW];
+#pragma unroll
+    for (int j = 0; j < RTW; ++j)
+#pragma unroll
+        for (int j2 = 0; j2 < CTW; ++j2) acc[j][j2] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const uint32_t* urow[RTW];
+#pragma unroll
+    for (int j = 0; j < RTW; ++j) urow[j] = ut + (16 * (wrow + WR * j) + c) * a.wr;
+    const int hrow = (16 * wcol * CTW + c) * NP;  // LDS row of column tile wcol * CTW, this lane's column
+    const int swz = c & 7;                         // = R % 8 for every column tile of the lane
+    struct Ops {
+        u32x4 bf[CTW];
+        uint32_t w[RTW];
+    };
+    auto fetch = [&](const uint32_t* buf, int q, int s, Ops& o) {
+        const int slot = hrow + ((4 * s + g) ^ swz);
+#pragma unroll
+        for (int j2 = 0; j2 < CTW; ++j2) o.bf[j2] = *reinterpret_cast<const u32x4*>(buf + (slot + 16 * j2 * NP) * 4);
+#pragma unroll
+        for (int j = 0; j < RTW; ++j) o.w[j] = urow[j][q];
+    };
+    auto run = [&](const Ops& o) {
+#pragma unroll
+        for (int j = 0; j < RTW; ++j) {
+            const uint32_t w = o.w[j] << sh;
+            const u32x4 av = u32x4{and_or(w, mask, one), and_or(w << 1, mask, one), and_or(w << 2, mask, one),
+                                   and_or(w << 3, mask, one)};
+#pragma unroll
+            for (int j2 = 0; j2 < CTW; ++j2) acc[j][j2] = mfma16x16x32<BF16>(av, o.bf[j2], acc[j][j2]);
+        }
+    };
+    // one chunk: DMA chunk ci + 2 into the buffer chunk ci - 1 used (the last chunk again at the
+    // end: every step issues the same DMAs, so the wait below always means chunk ci + 1), the
+    // chunk's steps with the next step's operands read first, then chunk ci + 1's DMAs, barrier
+    auto chunk = [&](const uint32_t* cur, uint32_t* free_buf, int ci) {
+        issue(min(ci + 2, a.chunks - 1), free_buf);
+        Ops o[2];
+        fetch(cur, ci * KC, 0, o[0]);
+#pragma unroll
+        for (int s = 0; s < KC; ++s) {
+            if (s + 1 < KC) fetch(cur, ci * KC + s + 1, s + 1, o[(s + 1) & 1]);
+            run(o[s & 1]);
+        }
+        wait_vmcnt<kDma>();
+        barrier_keep_dma();
+    };
+    int ci = 0;
+    for (; ci + 3 <= a.chunks; ci += 3) {
+        chunk(hb0, hb2, ci);
+        chunk(hb1, hb0, ci + 1);
+        chunk(hb2, hb1, ci + 2);
+    }
+    if (ci < a.chunks) {
+        chunk(hb0, hb2, ci);
+        if (ci + 1 < a.chunks) chunk(hb1, hb0, ci + 1);
+    }
+    wait_vmcnt<0>();  // the re-fetches land before the block's LDS is released
+    NQ_STAMP(2);
+
+    // 3. lane (c, g) of tile (j, j2) holds rows 4g .. 4g+3 of column c: batch row 8 (wcol CTW + j2)
+    //    + c / 2, hi (c even) or lo; the even lane adds its neighbour's lo, scales and stores
+#pragma unroll
+    for (int j = 0; j < RTW; ++j) {
+        const int row = i0 + 16 * (wrow + WR * j) + 4 * g;
+#pragma unroll
+        for (int j2 = 0; j2 < CTW; ++j2) {
+            const int b = bb + 8 * (wcol * CTW + j2) + (c >> 1);
+            const float vv[4] = {acc[j][j2].x, acc[j][j2].y, acc[j][j2].z, acc[j][j2].w};
+            uint16_t out[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float lo = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(vv[i]), 0xB1, 0xF, 0xF, false));
+                out[i] = saturate_to<T>((vv[i] + lo) * T::to_float(so[j][i]), T::SAT);
+            }
+            if ((c & 1) == 0 && b < a.batch) {
+                uint16_t* yp = a.y + static_cast<size_t>(b) * a.m + row;
+                if (a.store8 && row + 3 < a.m) {
+                    *reinterpret_cast<uint2*>(yp) = uint2{out[0] | (uint32_t(out[1]) << 16), out[2] | (uint32_t(out[3]) << 16)};
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (row + i < a.m) yp[i] = out[i];
+                }
+            }
+        }
+    }
+    NQ_STAMP(3);
+}
+
 // --------------------------------------------------------------------------- stage 1, batched (k split)
 //
 // For many batch rows on wide rows of V: h[b][j] = s_mid[j] * sum_k sign(V[j][k]) s_in[k] x[b][k]
@@ -1593,13 +1780,69 @@ bool launch_s2t_qw(S2Table& tab, int qw, int batch, hipStream_t st) {
     }
 }
 
+// One s2b_kernel shape over the op's arguments: grid (row blocks, batch passes); the U tile is
+// the dynamic LDS. Needs s2t_applies (s2_qw > 0 keeps zpitch >= 32 KC * chunks).
+template <typename T, int RT, int WR, int CTW, int KC>
+int launch_s2b_cfg(const GemvArgs& a) {
+    using S = S2bShape<RT, WR, CTW, KC>;
+    constexpr int kStatic = 3 * 16 * S::kSlots;
+    S2bArgs s;
+    s.u_bits = a.u_bits;
+    s.s_out = a.s_out;
+    s.y = a.y;
+    s.z_hi = a.z_hi;
+    s.z_lo = a.z_lo;
+    s.m = a.m;
+    s.wr = a.plan.wr;
+    s.zpitch = a.plan.zpitch;
+    s.batch = a.batch;
+    s.chunks = static_cast<int>(ceil_div(a.plan.wr, KC));
+    s.u_slots = static_cast<int>(ceil_div(static_cast<int64_t>(S::kRows) * a.plan.wr + KC, 64) * 64);
+    s.store8 = a.m % 4 == 0 && aligned(a.y, 8);
+    const size_t dyn = static_cast<size_t>(s.u_slots) * 4;
+    if (32LL * KC * s.chunks > a.plan.zpitch || kStatic + dyn > static_cast<size_t>(kSbLdsBytes))
+        return fail(NQ_ERR_UNSUPPORTED, "nq_gemv batched stage 2: shape does not fit");
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&s2b_kernel<T, RT, WR, CTW, KC>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, kSbLdsBytes - kStatic);
+    if (attr != hipSuccess) return fail(NQ_ERR_HIP, "nq_gemv batched stage 2: LDS limit: %s", hipGetErrorString(attr));
+    const dim3 grid(static_cast<unsigned>(ceil_div(a.m, S::kRows)), static_cast<unsigned>(ceil_div(a.batch, S::kBatch)));
+    s2b_kernel<T, RT, WR, CTW, KC><<<grid, 256, dyn, a.stream>>>(s);
+    return NQ_OK;
+}
+
 inline bool s2t_applies(const void* z_hi, const void* z_lo, const uint32_t* u_bits, int m, const Plan& plan) {
     return aligned(z_hi, 16) && aligned(z_lo, 16) && aligned(u_bits, 16) && static_cast<int64_t>(m) * plan.wr >= 4 &&
            plan.s2_qw > 0;
 }
 
+// When the batched stage 2 replaces s2t_kernel, and its shape (measured on the Llama-2-7B gate
+// and down shapes at r = 1632, batch 16 - 128; us, s2t against s2b): from 16 batch rows when
+// m * batch >= 160 K (gate, 11008 rows: 7.7 / 6.4 at 16 rows, 12.3 / 6.8 at 32, 20.8 / 8.9 at 64,
+// 38.7 / 13.1 at 128; down, 4096 rows: 4.0 / 5.3 at 16 and 5.0 / 5.5 at 32 stay with s2t, 9.1 / 6.05
+// at 64, 16.0 / 7.1 at 128). Every shape gives each wave one row tile against one to four column
+// tiles. Over 512 or more row tiles: 64-row blocks (WR = 4) of 16 batch rows up to 64 rows, 32
+// beyond, two-word chunks. Below: 32-row blocks (WR = 2) of 16 batch rows and four-word chunks up
+// to 64 rows, 32 batch rows and two-word chunks beyond. Smaller chunks leave room in LDS for more
+// resident blocks, which is what these latency-bound blocks gain from.
+constexpr int64_t kS2bMinWork = 160 * 1024;
+constexpr int kS2bMinBatch = 16;
+
+template <typename T>
+int launch_stage2_batched(const GemvArgs& a) {
+    const int64_t tiles = ceil_div(a.m, 16);
+    if (tiles >= 512) {
+        if (a.batch <= 64) return launch_s2b_cfg<T, 4, 4, 2, 2>(a);
+        return launch_s2b_cfg<T, 4, 4, 4, 2>(a);
+    }
+    if (a.batch <= 64) return launch_s2b_cfg<T, 2, 2, 1, 4>(a);
+    return launch_s2b_cfg<T, 2, 2, 2, 2>(a);
+}
+
 template <typename T>
 int launch_stage2(const GemvArgs& a) {
+    if (s2t_applies(a.z_hi, a.z_lo, a.u_bits, a.m, a.plan) && a.batch >= kS2bMinBatch &&
+        static_cast<int64_t>(a.m) * a.batch >= kS2bMinWork)
+        return launch_stage2_batched<T>(a);
     if (s2t_applies(a.z_hi, a.z_lo, a.u_bits, a.m, a.plan)) {
         S2Table tab;
         tab.count = 1;

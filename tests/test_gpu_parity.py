@@ -173,6 +173,13 @@ GEMV_CASES = [
     ("llama7b_gate_055_b64", 11008, 4096, 1632, 64, False),
     ("llama7b_down_055_b64", 4096, 11008, 1632, 64, True),
     ("llama7b_gate_055_b128", 11008, 4096, 1632, 128, False),
+    # the batched stage 2 (U decoded once per 32 k for all of a block's batch rows, the intermediate
+    # streamed through LDS): each of its four launch shapes with ragged rows, batch rows and ranks;
+    # m = 4102 takes 2-byte stores, r = 2048 rows of 64 words
+    ("s2b_ragged_b37", 5000, 512, 333, 37, True),
+    ("s2b_ragged_b90", 9000, 256, 1000, 90, False),
+    ("s2b_m4102_b128", 4102, 256, 2048, 128, False),
+    ("s2b_tall_b16", 10400, 256, 96, 16, True),
 ]
 
 
