@@ -566,8 +566,12 @@ def run_sweep(args, dev):
 def run_batch_sweep(args, dev):
     """One JSON line per (shape, batch, kind): the GEMV and the GEMM at batch 1, 2, 4, 8, 16, 32, 64, 128, 256 on
     the Llama-2-7B gate and down shapes at 0.55 bpw, both over the same rotating copies (more than 512 MB of packed
-    weights in all, so both stream from HBM). This is where one kernel should hand over to the other."""
+    weights in all, so both stream from HBM). This is where one kernel should hand over to the other. Kinds
+    gemv_stage1 and gemv_stage2 time the GEMV's two launches alone (the C ABI's stage entry points, same copies)."""
+    from nanoquant_amd import _lib
     from nanoquant_amd.decode import rank_for_bpw
+
+    lib = _lib.load()
 
     op_gemv = torch.ops.binary_kernels.nanoquant_dyn_forward
     op_gemm = torch.ops.binary_kernels.marlin_nanoquant_forward
@@ -591,11 +595,29 @@ def run_batch_sweep(args, dev):
         for B in batches:
             x = torch.randn(B, n, device=dev, generator=gen).half()
             reps = max(1, 512 // copies)
-            for kind in ("gemv", "gemm"):
+            ws_b = torch.zeros(lib.nq_gemv_workspace_bytes(B, n, r, m), dtype=torch.uint8, device=dev)
+            y_b = torch.empty(B, m, dtype=torch.float16, device=dev)
+
+            def stage(which):
+                def fn():
+                    st = torch.cuda.current_stream().cuda_stream
+                    for i in range(copies):
+                        if which == 1:
+                            s = lib.nq_gemv_stage1(_lib.NQ_F16, x.data_ptr(), s_in.data_ptr(), Vs[i].data_ptr(), None,
+                                                   B, n, r, m, ws_b.data_ptr(), ws_b.numel(), st)
+                        else:
+                            s = lib.nq_gemv_stage2(_lib.NQ_F16, Us[i].data_ptr(), s_out.data_ptr(), y_b.data_ptr(), B,
+                                                   n, r, m, ws_b.data_ptr(), ws_b.numel(), st)
+                        _lib.check(s, f"stage {which}")
+                return fn
+
+            for kind in ("gemv", "gemm", "gemv_stage1", "gemv_stage2"):
                 if kind == "gemv":
                     fn = lambda: [op_gemv(x, s_in, Vs[i], None, Us[i], s_out, **kw) for i in range(copies)]  # noqa
-                else:
+                elif kind == "gemm":
                     fn = lambda: [op_gemm(x, Wv[i], Wu[i], s_in, s_l, s_out, ws) for i in range(copies)]  # noqa
+                else:
+                    fn = stage(1 if kind == "gemv_stage1" else 2)
                 ms, graph, _ = steady_ms(fn, copies, stream, reps, 1)
                 del graph
                 print(json.dumps({"kind": kind, "linear": name, "m": m, "n": n, "r": r, "batch": B,

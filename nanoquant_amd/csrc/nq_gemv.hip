@@ -499,7 +499,7 @@ __global__ __launch_bounds__(G * WR * 64) void s1w_kernel(const S1Table tab, con
 // of the rows and add their tiles in LDS. Each wave issues the loads of CH words before their
 // MFMAs. kNorm sums x^2 of each batch row on the way (the B fragments of the block's lanes cover
 // every k of a batch row once) and scales h by rsqrt(mean(x^2) + eps).
-template <typename T, int NW, bool kNorm, bool kOne, bool kSinLds, int kLoads>
+template <typename T, int NW, bool kNorm, bool kOne, bool kSinLds, int kLoads, int RT = 1>
 __global__ __launch_bounds__(NW * 64) void s1m_kernel(const S1Table tab, const uint16_t* __restrict__ x, int batch,
                                                       int n, int wn, float eps) {
     constexpr int CH = 8;
@@ -507,8 +507,10 @@ __global__ __launch_bounds__(NW * 64) void s1m_kernel(const S1Table tab, const u
     // dwords per thread staged: the host picks the smallest of 4, 8, 12, 16 that covers the block's
     // words (a fixed 16 issued up to three quarters of redundant, clamped loads at n = 4096)
     constexpr int kMaxLoads = kLoads;
-    // [16][wn] sign words, then (kSinLds) s_in as [n / 2] pairs; wider rows read s_in from global
-    // (after the MFMAs the same memory holds the waves' partial tiles)
+    // [16 RT][wn] sign words, then (kSinLds) s_in as [n / 2] pairs; wider rows read s_in from global
+    // (after the MFMAs the same memory holds the waves' partial tiles). With RT row tiles a block
+    // runs 16 RT rows of V against the same 16 batch rows, so each fragment of x it fetches feeds
+    // RT MFMAs.
     extern __shared__ uint32_t lds[];
     const int t = threadIdx.x;
     const int lane = t & 63;
@@ -517,17 +519,17 @@ __global__ __launch_bounds__(NW * 64) void s1m_kernel(const S1Table tab, const u
     const int g = lane >> 4;
     const S1Item it = kOne ? tab.item[0] : pick_item<S1Item>(tab);
     const int r = it.r;
-    const int j0 = (static_cast<int>(blockIdx.x) - it.block_begin) * 16;
+    const int j0 = (static_cast<int>(blockIdx.x) - it.block_begin) * 16 * RT;
     const int b0 = blockIdx.y * 16;
     const uint16_t* xrow = x + static_cast<uint32_t>(min(b0 + c, batch - 1)) * static_cast<uint32_t>(n);
     const bool b_ok = b0 + c < batch;
     const uint32_t mask = kSignPair;
     uint32_t* vt = lds;
-    uint32_t* si = lds + 16 * wn;
+    uint32_t* si = lds + 16 * RT * wn;
 
     // 1. stage the block's rows of V (consecutive in memory) and s_in, dword by dword, coalesced;
     //    rows past r repeat the last row (their h is never stored)
-    const int vwords = 16 * wn;
+    const int vwords = 16 * RT * wn;
     const int total = vwords + (kSinLds ? n / 2 : 0);
     const uint32_t vbase = static_cast<uint32_t>(min(j0, r - 1)) * static_cast<uint32_t>(wn);
     const uint32_t vlast = static_cast<uint32_t>(r) * static_cast<uint32_t>(wn) - 1;
@@ -546,7 +548,9 @@ __global__ __launch_bounds__(NW * 64) void s1m_kernel(const S1Table tab, const u
     __syncthreads();
 
     // 2. MFMAs: wave w takes words w, w + NW, ...; x comes from global CH words at a time
-    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    f32x4 acc[RT][2];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) acc[rt][0] = acc[rt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
     float ss[2] = {0.0f, 0.0f};
     for (int q0 = wave; q0 < wn; q0 += NW * CH) {
         u32x4 xv[CH], sg[CH];
@@ -566,10 +570,13 @@ __global__ __launch_bounds__(NW * 64) void s1m_kernel(const S1Table tab, const u
             const u32x4 sp = kSinLds ? *reinterpret_cast<const u32x4*>(&si[min(16 * qc + 4 * g, n / 2 - 4)]) : sg[u];
             const u32x4 s = ok ? sp : u32x4{0u, 0u, 0u, 0u};
             const u32x4 xb = (ok && b_ok) ? xv[u] : u32x4{0u, 0u, 0u, 0u};
-            const uint32_t ws = vt[c * wn + qc] << (4 * g);
-            const u32x4 a = u32x4{s.x ^ (ws & mask), s.y ^ ((ws << 1) & mask), s.z ^ ((ws << 2) & mask),
-                                  s.w ^ ((ws << 3) & mask)};
-            acc[u & 1] = mfma16x16x32<T>(a, xb, acc[u & 1]);
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                const uint32_t ws = vt[(16 * rt + c) * wn + qc] << (4 * g);
+                const u32x4 a = u32x4{s.x ^ (ws & mask), s.y ^ ((ws << 1) & mask), s.z ^ ((ws << 2) & mask),
+                                      s.w ^ ((ws << 3) & mask)};
+                acc[rt][u & 1] = mfma16x16x32<T>(a, xb, acc[rt][u & 1]);
+            }
             if (kNorm) {
                 ss[u & 1] = T::dot2(xb.x, xb.x, ss[u & 1]);
                 ss[u & 1] = T::dot2(xb.y, xb.y, ss[u & 1]);
@@ -579,19 +586,22 @@ __global__ __launch_bounds__(NW * 64) void s1m_kernel(const S1Table tab, const u
         }
     }
     __syncthreads();  // every wave is done with the staged words
-    f32x4* red = reinterpret_cast<f32x4*>(lds);               // [NW][64]
-    float* ssr = reinterpret_cast<float*>(lds) + 4 * NW * 64;  // [NW][64]
-    red[wave * 64 + lane] =
-        f32x4{acc[0].x + acc[1].x, acc[0].y + acc[1].y, acc[0].z + acc[1].z, acc[0].w + acc[1].w};
+    f32x4* red = reinterpret_cast<f32x4*>(lds);                    // [RT][NW][64]
+    float* ssr = reinterpret_cast<float*>(lds) + 4 * RT * NW * 64;  // [NW][64]
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+        red[(rt * NW + wave) * 64 + lane] = f32x4{acc[rt][0].x + acc[rt][1].x, acc[rt][0].y + acc[rt][1].y,
+                                                  acc[rt][0].z + acc[rt][1].z, acc[rt][0].w + acc[rt][1].w};
     if (kNorm) ssr[wave * 64 + lane] = ss[0] + ss[1];
     __syncthreads();
 
-    // 3. sum the waves' tiles, scale, store
-    if (wave == 0) {
-        f32x4 sum = red[lane];
+    // 3. wave rt sums the waves' tiles of row tile rt, scales, stores
+    if (wave < RT) {
+        const int rt = wave;
+        f32x4 sum = red[rt * NW * 64 + lane];
 #pragma unroll
         for (int w = 1; w < NW; ++w) {
-            const f32x4 pr = red[w * 64 + lane];
+            const f32x4 pr = red[(rt * NW + w) * 64 + lane];
             sum = f32x4{sum.x + pr.x, sum.y + pr.y, sum.z + pr.z, sum.w + pr.w};
         }
         float rs = 1.0f;
@@ -606,7 +616,7 @@ __global__ __launch_bounds__(NW * 64) void s1m_kernel(const S1Table tab, const u
         const float v[4] = {sum.x, sum.y, sum.z, sum.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int j = j0 + 4 * g + i;
+            const int j = j0 + 16 * rt + 4 * g + i;
             if (b_ok && j < it.kpad) {
                 const float mf = (it.s_mid != nullptr && j < r) ? T::to_float(it.s_mid[j]) : 1.0f;
                 store_h(it.z_hi, it.z_lo, it.zpitch, b0 + c, j, j < r ? v[i] * rs * mf : 0.0f);
@@ -1080,8 +1090,9 @@ __global__ __launch_bounds__(256) void s2b_kernel(const S2bArgs a) {
 // rounding slack. Words: row i of the block at i * (kw + 1).
 //
 // Measured (MI355X, graph-replayed, rotating weights; stage 1 alone, us): n = 11008, r = 1632:
-// batch 16 / 64 / 128: 12.9 / 18.7 / 27.7 against 14.3 / 26.6 / 51.3 for s1m_kernel; n = 4096:
-// batch 64 / 128: 11.5 / 15.6 against 11.4 / 20.6 (and slower than s1m below 64 rows). A block
+// batch 16 / 64 / 128: 12.9 / 18.7 / 27.7 against 14.3 / 26.6 / 51.3 for s1m_kernel with one row
+// tile per block (19.0 at 64 rows with two); n = 4096: batch 64 / 128: 11.5 / 15.6 against 8.9 / 13.4
+// for s1m_kernel with two and four row tiles, so it runs on wide rows only. A block
 // fetches its slice at 35-45 GB/s (phase stamps), so the plan keeps slices small; the same design
 // for stage 2 (slices of h, partial sums of y) lost to s2t_kernel at every batch and is not used.
 struct SbArgs {
@@ -1347,10 +1358,10 @@ struct SbPlan {
     size_t part_bytes, lds_bytes;
 };
 
-// When the batched stage 1 replaces s1m_kernel (measured crossovers, see sb_kernel): from 64 batch
-// rows, or from 16 on rows of at least 256 words; at most 128 rows (8 batch tiles), and an LDS
-// slice of at most 160 KB per block.
-constexpr int kSbMinBatch = 64;
+// When the batched stage 1 replaces s1m_kernel (measured crossovers, see sb_kernel): from 16 batch
+// rows on rows of at least 256 words; at most 128 rows (8 batch tiles), and an LDS slice of at
+// most 160 KB per block. On narrower rows s1m_kernel with two or four row tiles per block is the
+// faster one (n = 4096, r = 1632, 64 / 128 rows: 8.9 / 13.4 us against 11.5 / 15.6).
 constexpr int kSbMinBatchWide = 16;
 constexpr int kSbWideWords = 256;
 constexpr int kSbMaxBatch = 128;
@@ -1364,7 +1375,7 @@ constexpr int kSbMaxBlocks = 256;
 // several k ranges, the finishing launch (~4000) plus the per-range sums written and read.
 inline bool sb_plan(int64_t batch, int64_t rows, int64_t wpr, int64_t kpad, SbPlan& p) {
     if (batch > kSbMaxBatch || rows <= 0 || wpr <= 0) return false;
-    if (batch < kSbMinBatch && (batch < kSbMinBatchWide || wpr < kSbWideWords)) return false;
+    if (batch < kSbMinBatchWide || wpr < kSbWideWords) return false;
     const int ct = static_cast<int>(std::min<int64_t>(8, ceil_div(batch, 16)));
     const int passes = static_cast<int>(ceil_div(batch, 16LL * ct));
     const int xcols = 16 * ct + 1;
@@ -1516,26 +1527,36 @@ void launch_s1w_table(S1Table& tab, const uint16_t* x, int batch, int n, int wn,
 // Dwords s1m_kernel stages in LDS: 16 rows of sign words, and the s_in pairs when they fit too
 // (64 KB, 16 dwords per thread of a 1024-thread block).
 constexpr int kS1mMaxStaged = 16 * 16 * 64;
-inline bool s1m_sin_lds(int n, int wn) { return 16 * wn + n / 2 <= kS1mMaxStaged; }
-inline size_t s1m_lds_bytes(int n, int wn) {
-    const size_t staged = static_cast<size_t>(16 * wn + (s1m_sin_lds(n, wn) ? n / 2 : 0)) * 4;
-    const size_t reduce = static_cast<size_t>(16) * 64 * (16 + 4);  // the waves' tiles and x^2 sums
+inline bool s1m_sin_lds(int n, int wn, int rt = 1) { return 16 * rt * wn + n / 2 <= kS1mMaxStaged; }
+inline size_t s1m_lds_bytes(int n, int wn, int rt = 1) {
+    const size_t staged = static_cast<size_t>(16 * rt * wn + (s1m_sin_lds(n, wn, rt) ? n / 2 : 0)) * 4;
+    const size_t reduce = static_cast<size_t>(16) * 64 * (16 * rt + 4);  // the waves' tiles and x^2 sums
     return std::max(staged, reduce);
 }
 // Whether the MFMA stage 1 takes rows of n columns at all (up to n = 32768).
-inline bool s1m_fits(int n, int wn) {
+inline bool s1m_fits(int n, int wn, int rt = 1) {
     (void)n;
-    return 16 * wn <= kS1mMaxStaged;
+    return 16 * rt * wn <= kS1mMaxStaged;
 }
 
-template <typename T, int NW, int LD>
+// Blocks of s1m_kernel<..., RT> may take more than 64 KB of LDS (the limit is set once per kernel).
+template <typename Kernel>
+int s1m_allow_lds(Kernel* k) {
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(k),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, kSbLdsBytes);
+    return attr == hipSuccess ? NQ_OK : fail(NQ_ERR_HIP, "nq_gemv stage 1: LDS limit: %s", hipGetErrorString(attr));
+}
+
+template <typename T, int NW, int LD, int RT>
 void launch_s1m_loads(const S1Table& tab, dim3 grid, const uint16_t* x, int batch, int n, int wn, bool norm, float eps,
                       hipStream_t st) {
-    const size_t lds = s1m_lds_bytes(n, wn);
-    const bool sl = s1m_sin_lds(n, wn);
+    const size_t lds = s1m_lds_bytes(n, wn, RT);
+    const bool sl = s1m_sin_lds(n, wn, RT);
 #define NQ_S1M(NORM, ONE)                                                                                  \
-    (sl ? (s1m_kernel<T, NW, NORM, ONE, true, LD><<<grid, NW * 64, lds, st>>>(tab, x, batch, n, wn, eps)) \
-        : (s1m_kernel<T, NW, NORM, ONE, false, LD><<<grid, NW * 64, lds, st>>>(tab, x, batch, n, wn, eps)))
+    (sl ? (s1m_allow_lds(&s1m_kernel<T, NW, NORM, ONE, true, LD, RT>),                                     \
+           s1m_kernel<T, NW, NORM, ONE, true, LD, RT><<<grid, NW * 64, lds, st>>>(tab, x, batch, n, wn, eps)) \
+        : (s1m_allow_lds(&s1m_kernel<T, NW, NORM, ONE, false, LD, RT>),                                    \
+           s1m_kernel<T, NW, NORM, ONE, false, LD, RT><<<grid, NW * 64, lds, st>>>(tab, x, batch, n, wn, eps)))
     if (tab.count == 1) {
         if (norm) NQ_S1M(true, true);
         else NQ_S1M(false, true);
@@ -1545,31 +1566,49 @@ void launch_s1m_loads(const S1Table& tab, dim3 grid, const uint16_t* x, int batc
     }
 #undef NQ_S1M
 }
-template <typename T, int NW>
+template <typename T, int NW, int RT>
 void launch_s1m_nw(const S1Table& tab, dim3 grid, const uint16_t* x, int batch, int n, int wn, bool norm, float eps,
                    hipStream_t st) {
-    const bool sl = s1m_sin_lds(n, wn);
-    const int staged = 16 * wn + (sl ? n / 2 : 0);
+    const bool sl = s1m_sin_lds(n, wn, RT);
+    const int staged = 16 * RT * wn + (sl ? n / 2 : 0);
     const int per_thread = static_cast<int>(ceil_div(staged, NW * 64));
-    if (per_thread <= 4) launch_s1m_loads<T, NW, 4>(tab, grid, x, batch, n, wn, norm, eps, st);
-    else if (per_thread <= 8) launch_s1m_loads<T, NW, 8>(tab, grid, x, batch, n, wn, norm, eps, st);
-    else if (per_thread <= 12) launch_s1m_loads<T, NW, 12>(tab, grid, x, batch, n, wn, norm, eps, st);
-    else launch_s1m_loads<T, NW, 16>(tab, grid, x, batch, n, wn, norm, eps, st);
+    if (per_thread <= 4) launch_s1m_loads<T, NW, 4, RT>(tab, grid, x, batch, n, wn, norm, eps, st);
+    else if (per_thread <= 8) launch_s1m_loads<T, NW, 8, RT>(tab, grid, x, batch, n, wn, norm, eps, st);
+    else if (per_thread <= 12) launch_s1m_loads<T, NW, 12, RT>(tab, grid, x, batch, n, wn, norm, eps, st);
+    else launch_s1m_loads<T, NW, 16, RT>(tab, grid, x, batch, n, wn, norm, eps, st);
 }
 
-// The MFMA stage 1 over every item of `tab` (16 rows per block, 16 batch rows per grid row).
+// Row tiles per block of s1m_kernel: the fewest of 1, 2 and 4 whose grid is one round of blocks
+// (one per CU; a second round costs as much as the first), else 4, the fewest rounds. Measured (us,
+// 1 / 2 / 4 row tiles, n = 4096, r = 1632): 16 batch rows 7.2 / 8.7 / 13.2, 64 rows 12.2 / 8.9 / 13.3,
+// 128 rows 21.1 / 16.3 / 13.4.
+inline int s1m_row_tiles(const S1Table& tab, int batch, int n, int wn) {
+    const int64_t passes = ceil_div(batch, 16);
+    for (int rt : {1, 2, 4}) {
+        if (!s1m_fits(n, wn, rt)) break;
+        int64_t blocks = 0;
+        for (int k = 0; k < tab.count; ++k) blocks += ceil_div(tab.item[k].kpad, 16 * rt);
+        if (blocks * passes <= 256 || rt == 4) return rt;
+    }
+    return s1m_fits(n, wn, 2) ? 2 : 1;
+}
+
+// The MFMA stage 1 over every item of `tab` (16 rt rows per block, 16 batch rows per grid row).
 template <typename T>
 void launch_s1m_table(S1Table& tab, const uint16_t* x, int batch, int n, int wn, bool norm, float eps,
-                      hipStream_t st) {
+                      hipStream_t st, int rt = 0) {
+    if (rt == 0) rt = s1m_row_tiles(tab, batch, n, wn);
     int blocks = 0;
     for (int k = 0; k < tab.count; ++k) {
         tab.item[k].block_begin = blocks;
-        blocks += static_cast<int>(ceil_div(tab.item[k].kpad, 16));
+        blocks += static_cast<int>(ceil_div(tab.item[k].kpad, 16 * rt));
     }
     // 16 waves per block: a 4096-wide row is one round of loads per wave (latency, not bytes, is
     // what a decode-size stage pays for)
     const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(ceil_div(batch, 16)));
-    launch_s1m_nw<T, 16>(tab, grid, x, batch, n, wn, norm, eps, st);
+    if (rt == 4) launch_s1m_nw<T, 16, 4>(tab, grid, x, batch, n, wn, norm, eps, st);
+    else if (rt == 2) launch_s1m_nw<T, 16, 2>(tab, grid, x, batch, n, wn, norm, eps, st);
+    else launch_s1m_nw<T, 16, 1>(tab, grid, x, batch, n, wn, norm, eps, st);
 }
 
 // Stage 1 of a table: the VALU kernel for one or two batch rows of up to 16384 columns, the MFMA

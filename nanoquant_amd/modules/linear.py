@@ -34,9 +34,9 @@ from ..kernel.utils import (binary_packer, binary_unpacker, get_kernel_function,
                             pack_binary_marlin_fused_from_packed, repack_binary_gemv)
 
 # Rows up to which kernel_type "auto" runs the GEMV; more rows run the GEMM. Measured on the
-# Llama-2-7B gate and down shapes at 0.55 bpw (bench.py --batch-sweep): at 64 rows the GEMV takes
-# 34.4 and 37.5 us against the GEMM's 35.3 and 38.5 us, at 128 rows 63 and 69 us against 41 and 45 us.
-AUTO_GEMV_MAX_ROWS = 64
+# Llama-2-7B gate and down shapes at 0.55 bpw (bench.py --batch-sweep): at 128 rows the GEMV takes
+# 29.4 and 36.5 us against the GEMM's 36.3 and 40.7 us, at 256 rows 61 and 100 us against 36 and 44 us.
+AUTO_GEMV_MAX_ROWS = 128
 
 # The GEMV tuning ints the reference fixes when it prepares the layer (linear.py:210-219). The
 # HIP kernels validate them and choose their own launch shapes.

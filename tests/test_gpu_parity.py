@@ -180,6 +180,10 @@ GEMV_CASES = [
     ("s2b_ragged_b90", 9000, 256, 1000, 90, False),
     ("s2b_m4102_b128", 4102, 256, 2048, 128, False),
     ("s2b_tall_b16", 10400, 256, 96, 16, True),
+    # the MFMA stage 1 with two and four row tiles per block (chosen to keep its grid to one round
+    # of blocks): ragged ranks and batch rows
+    ("s1m_rt2_ragged", 300, 512, 700, 120, True),
+    ("s1m_rt4_ragged", 700, 1024, 1050, 128, True),
 ]
 
 
@@ -614,7 +618,7 @@ def test_auto_kernel_routes_by_rows(nq):
     nq.load_packed_for_kernels(packed_auto, state, "auto", torch.float16)
     rng = np.random.default_rng(4)
     f = lambda t: t.detach().double().cpu().numpy().reshape(-1)  # noqa: E731
-    for rows, kernel in ((1, "gemv"), (AUTO_GEMV_MAX_ROWS, "gemv"), (AUTO_GEMV_MAX_ROWS + 1, "gemm"), (100, "gemm")):
+    for rows, kernel in ((1, "gemv"), (AUTO_GEMV_MAX_ROWS, "gemv"), (AUTO_GEMV_MAX_ROWS + 1, "gemm"), (300, "gemm")):
         x = torch.from_numpy(rng.normal(size=(rows, 256)).astype(np.float16)).cuda()
         want = layers[kernel](x)
         for got in (layers["auto"](x), packed_auto(x)):
@@ -623,5 +627,5 @@ def test_auto_kernel_routes_by_rows(nq):
                                       f(base.scale_post))
         err = np.abs(want.double().cpu().numpy() - y64).max() / np.abs(y64).max()
         assert err <= 1e-3, (rows, err)
-    x3 = torch.from_numpy(rng.normal(size=(2, 40, 256)).astype(np.float16)).cuda()  # 80 rows: the GEMM
+    x3 = torch.from_numpy(rng.normal(size=(2, 80, 256)).astype(np.float16)).cuda()  # 160 rows: the GEMM
     assert torch.equal(layers["auto"](x3), layers["gemm"](x3))
