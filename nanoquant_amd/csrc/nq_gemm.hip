@@ -516,9 +516,18 @@ __global__ __launch_bounds__(256) void gemm_split_finish_kernel(const float* __r
     const size_t plane = static_cast<size_t>(M) * static_cast<size_t>(N);
     const float* src = part + static_cast<size_t>(q) * N + o;
     f32x4 sum = *reinterpret_cast<const f32x4*>(src);
-    for (int s = 1; s < splits; ++s) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(src + s * plane);
-        sum = f32x4{sum[0] + v[0], sum[1] + v[1], sum[2] + v[2], sum[3] + v[3]};
+    // the planes' loads go out kBatch at a time before their adds (a dependent load per plane waited
+    // out a memory round trip each); the adds keep the order s = 1, 2, ...
+    constexpr int kBatch = 16;
+    for (int s0 = 1; s0 < splits; s0 += kBatch) {
+        f32x4 pv[kBatch];
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i)
+            pv[i] = s0 + i < splits ? *reinterpret_cast<const f32x4*>(src + static_cast<size_t>(s0 + i) * plane)
+                                    : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i)
+            if (s0 + i < splits) sum = f32x4{sum[0] + pv[i][0], sum[1] + pv[i][1], sum[2] + pv[i][2], sum[3] + pv[i][3]};
     }
     uint16_t h[4];
 #pragma unroll

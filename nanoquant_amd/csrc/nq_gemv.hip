@@ -1273,12 +1273,25 @@ __global__ __launch_bounds__(256) void sb_finish1(const SbArgs a, int ks) {
     const int j0 = 4 * (e - b * per_row);
     float v[4] = {0.f, 0.f, 0.f, 0.f};
     if (j0 < a.kpad) {
-        for (int k = 0; k < ks; ++k) {
-            const f32x4 pv = *reinterpret_cast<const f32x4*>(a.part + (static_cast<size_t>(k) * a.batch + b) * a.kpad + j0);
-            v[0] += pv.x;
-            v[1] += pv.y;
-            v[2] += pv.z;
-            v[3] += pv.w;
+        // the planes' loads go out kBatch at a time before their adds (one dependent load per plane
+        // made this launch wait out a memory round trip per plane); the adds keep the order k = 0, 1, ...
+        constexpr int kBatch = 16;
+        const f32x4* src = reinterpret_cast<const f32x4*>(a.part + static_cast<size_t>(b) * a.kpad + j0);
+        const size_t plane = static_cast<size_t>(a.batch) * a.kpad / 4;  // f32x4 per plane
+        for (int k0 = 0; k0 < ks; k0 += kBatch) {
+            f32x4 pv[kBatch];
+#pragma unroll
+            for (int i = 0; i < kBatch; ++i)
+                pv[i] = k0 + i < ks ? src[static_cast<size_t>(k0 + i) * plane] : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < kBatch; ++i) {
+                if (k0 + i < ks) {
+                    v[0] += pv[i].x;
+                    v[1] += pv[i].y;
+                    v[2] += pv[i].z;
+                    v[3] += pv[i].w;
+                }
+            }
         }
     }
     uint16_t hi[4], lo[4];
