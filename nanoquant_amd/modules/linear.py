@@ -35,7 +35,7 @@ from ..kernel.utils import (binary_packer, binary_unpacker, get_kernel_function,
 
 # Rows up to which kernel_type "auto" runs the GEMV; more rows run the GEMM. Measured on the
 # Llama-2-7B gate and down shapes at 0.55 bpw (bench.py --batch-sweep): at 128 rows the GEMV takes
-# 27.3 and 36.6 us against the GEMM's 36.4 and 40.7 us, at 256 rows 49 and 79 us against 36 and 44 us.
+# 27.4 and 32.1 us against the GEMM's 36.8 and 39.0 us, at 256 rows 48 and 79 us against 36 and 43 us.
 AUTO_GEMV_MAX_ROWS = 128
 
 # The GEMV tuning ints the reference fixes when it prepares the layer (linear.py:210-219). The
