@@ -1386,9 +1386,15 @@ constexpr int kSbMaxBlocks = 256;
 // second round of blocks doubles the time) and whose LDS fits. Estimate, in CU cycles: the MFMAs
 // and their operand decode per wave, the DMA of the block's slice at ~32 bytes a cycle, and, with
 // several k ranges, the finishing launch (~4000) plus the per-range sums written and read.
+inline bool sb_plan_any(int64_t batch, int64_t rows, int64_t wpr, int64_t kpad, SbPlan& p);
 inline bool sb_plan(int64_t batch, int64_t rows, int64_t wpr, int64_t kpad, SbPlan& p) {
     if (batch > kSbMaxBatch || rows <= 0 || wpr <= 0) return false;
     if (batch < kSbMinBatchWide || wpr < kSbWideWords) return false;
+    return sb_plan_any(batch, rows, wpr, kpad, p);
+}
+// The search itself, for any batch up to kSbMaxBatch.
+inline bool sb_plan_any(int64_t batch, int64_t rows, int64_t wpr, int64_t kpad, SbPlan& p) {
+    if (batch > kSbMaxBatch || rows <= 0 || wpr <= 0) return false;
     const int ct = static_cast<int>(std::min<int64_t>(8, ceil_div(batch, 16)));
     const int passes = static_cast<int>(ceil_div(batch, 16LL * ct));
     const int xcols = 16 * ct + 1;
@@ -1736,6 +1742,15 @@ int launch_stage1(const GemvArgs& a) {
     return NQ_OK;
 }
 
+// Batch rows per pass of s2t_kernel over one item (qw words per wave, twice that for a gated pair):
+// up to 8, as many as fit the LDS's 128 * QW-column intermediate.
+inline int s2t_rows_per_pass(int batch, int qw) {
+    const int want = std::min(batch, 8);
+    int nb = want <= 1 ? 1 : (want <= 2 ? 2 : (want <= 4 ? 4 : 8));
+    while (nb > 1 && nb * qw > 128) nb >>= 1;
+    return nb;
+}
+
 // Only the batch splits that fit in LDS are instantiated (the host never picks the others).
 template <typename T, int QW, int NB, int EPI, int RT>
 void launch_s2t_nb(const S2Table& tab, dim3 grid, int batch, hipStream_t st) {
@@ -1782,9 +1797,7 @@ void launch_s2t_rt(const S2Table& tab, dim3 grid, int batch, int rt, hipStream_t
 template <typename T, int QW, int EPI>
 void launch_s2t_table(S2Table& tab, int batch, hipStream_t st) {
     constexpr int P = EPI == kEpiGated ? 2 : 1;
-    const int want = std::min(batch, 8);
-    int nb = want <= 1 ? 1 : (want <= 2 ? 2 : (want <= 4 ? 4 : 8));
-    while (nb > 1 && P * nb * QW > 128) nb >>= 1;
+    const int nb = s2t_rows_per_pass(batch, P * QW);
     // row tiles per block (the gated pair stays at one: it runs two items already)
     int64_t tiles = 0;
     for (int k = 0; k < (EPI == kEpiGated ? 1 : tab.count); ++k) tiles += ceil_div(tab.item[k].m, 16);
@@ -1878,6 +1891,17 @@ inline bool s2t_applies(const void* z_hi, const void* z_lo, const uint32_t* u_bi
 // resident blocks, which is what these latency-bound blocks gain from.
 constexpr int64_t kS2bMinWork = 160 * 1024;
 constexpr int kS2bMinBatch = 16;
+// ... and below 16 rows when U is large (at least 2M words) and s2t_kernel would need two passes or
+// more: its LDS holds fewer batch rows per pass at large ranks (two at r = 4224), and every pass
+// decodes U again (Llama-3-70B gate, m = 28672: r = 4224 at 4 / 8 rows 26.9 / 50.0 -> 14.3 / 14.3 us;
+// r = 3520 at 8 rows 20.6 -> 12.1).
+constexpr int64_t kS2bMinWordsFewRows = int64_t{1} << 21;
+
+inline bool s2b_chosen(const GemvArgs& a) {
+    if (a.batch >= kS2bMinBatch && static_cast<int64_t>(a.m) * a.batch >= kS2bMinWork) return true;
+    return static_cast<int64_t>(a.m) * a.plan.wr >= kS2bMinWordsFewRows &&
+           ceil_div(a.batch, s2t_rows_per_pass(a.batch, a.plan.s2_qw)) >= 2;
+}
 
 template <typename T>
 int launch_stage2_batched(const GemvArgs& a) {
@@ -1892,9 +1916,7 @@ int launch_stage2_batched(const GemvArgs& a) {
 
 template <typename T>
 int launch_stage2(const GemvArgs& a) {
-    if (s2t_applies(a.z_hi, a.z_lo, a.u_bits, a.m, a.plan) && a.batch >= kS2bMinBatch &&
-        static_cast<int64_t>(a.m) * a.batch >= kS2bMinWork)
-        return launch_stage2_batched<T>(a);
+    if (s2t_applies(a.z_hi, a.z_lo, a.u_bits, a.m, a.plan) && s2b_chosen(a)) return launch_stage2_batched<T>(a);
     if (s2t_applies(a.z_hi, a.z_lo, a.u_bits, a.m, a.plan)) {
         S2Table tab;
         tab.count = 1;

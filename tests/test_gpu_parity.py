@@ -184,6 +184,9 @@ GEMV_CASES = [
     # of blocks): ragged ranks and batch rows
     ("s1m_rt2_ragged", 300, 512, 700, 120, True),
     ("s1m_rt4_ragged", 700, 1024, 1050, 128, True),
+    # the batched stage 2 below 16 rows: a large U (2M words or more) whose rank leaves s2t_kernel two
+    # batch rows per pass
+    ("s2b_few_rows_big_u", 16400, 256, 4224, 3, False),
 ]
 
 
