@@ -52,6 +52,21 @@ constexpr size_t kHeaderBytes = 256;  // reserved at the start of the workspace
 constexpr uint32_t kSignPair = 0x80008000u;
 constexpr uint32_t kBf16OnePair = 0x3F803F80u;
 
+// ceil(2^32 / d): n / d == __umulhi(n, magic) for n * d < 2^32.
+__host__ __device__ inline uint32_t div_magic(uint32_t d) {
+    return static_cast<uint32_t>(((1ULL << 32) + d - 1) / d);
+}
+
+// LDS row stride (words) of s1m_kernel's tile of V rows wn words wide. A multiple of 64 puts the
+// 16 rows one MFMA fragment reads in one bank; from 256 words such rows get the odd stride wn + 1
+// (Llama-3-70B, 4 batch rows: q/o 12.7 -> 12.2 us, k/v 11.05 -> 10.55, mixed-rank gate 30.3 ->
+// 26.9). On 128-word rows the padded staging measured 6% slower at 16 batch rows, and rows whose
+// stride does not share banks gain nothing from it; both keep wn. (Four row tiles of padded wide
+// rows do not fit the staging buffer.)
+__host__ __device__ inline int s1m_row_stride(int wn, int rt = 1) {
+    return rt <= 2 && wn % 64 == 0 && wn >= 256 ? (wn | 1) : wn;
+}
+
 // Bit of element e (0..31) of a half2 word.
 __device__ inline int half2_bit(int e) { return 15 - (e >> 1) + 16 * (e & 1); }
 
@@ -499,7 +514,7 @@ __global__ __launch_bounds__(G * WR * 64) void s1w_kernel(const S1Table tab, con
 // of the rows and add their tiles in LDS. Each wave issues the loads of CH words before their
 // MFMAs. kNorm sums x^2 of each batch row on the way (the B fragments of the block's lanes cover
 // every k of a batch row once) and scales h by rsqrt(mean(x^2) + eps).
-template <typename T, int NW, bool kNorm, bool kOne, bool kSinLds, int kLoads, int RT = 1>
+template <typename T, int NW, bool kNorm, bool kOne, bool kSinLds, int kLoads, int RT = 1, bool kPad = false>
 __global__ __launch_bounds__(NW * 64) void s1m_kernel(const S1Table tab, const uint16_t* __restrict__ x, int batch,
                                                       int n, int wn, float eps) {
     constexpr int CH = 8;
@@ -524,8 +539,11 @@ __global__ __launch_bounds__(NW * 64) void s1m_kernel(const S1Table tab, const u
     const uint16_t* xrow = x + static_cast<uint32_t>(min(b0 + c, batch - 1)) * static_cast<uint32_t>(n);
     const bool b_ok = b0 + c < batch;
     const uint32_t mask = kSignPair;
+    // rows of V sit vs words apart in LDS; kPad (rows of 256 words or more, see s1m_row_stride) makes
+    // the stride odd, since with wn = 256, 896 ... the 16 rows one MFMA fragment reads share a bank
+    const int vs = kPad ? (wn | 1) : wn;
     uint32_t* vt = lds;
-    uint32_t* si = lds + 16 * RT * wn;
+    uint32_t* si = lds + 16 * RT * vs;
 
     // 1. stage the block's rows of V (consecutive in memory) and s_in, dword by dword, coalesced;
     //    rows past r repeat the last row (their h is never stored)
@@ -542,9 +560,23 @@ __global__ __launch_bounds__(NW * 64) void s1m_kernel(const S1Table tab, const u
                                            : s_in32[e - vwords];
     }
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (kPad) {
+        // word e of the rows goes to row e / wn of the padded tile (a multiply-high: e * wn < 2^32)
+        const uint32_t wmagic = div_magic(static_cast<uint32_t>(wn));
 #pragma unroll
-    for (int i = 0; i < kMaxLoads; ++i)
-        if (t + i * NT < total) lds[t + i * NT] = vals[i];
+        for (int i = 0; i < kMaxLoads; ++i) {
+            const int e = t + i * NT;
+            if (e < total) {
+                const int at = e < vwords ? e + (vs - wn) * static_cast<int>(__umulhi(static_cast<uint32_t>(e), wmagic))
+                                          : e - vwords + 16 * RT * vs;
+                lds[at] = vals[i];
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < kMaxLoads; ++i)
+            if (t + i * NT < total) lds[t + i * NT] = vals[i];
+    }
     __syncthreads();
 
     // 2. MFMAs: wave w takes words w, w + NW, ...; x comes from global CH words at a time
@@ -572,7 +604,7 @@ __global__ __launch_bounds__(NW * 64) void s1m_kernel(const S1Table tab, const u
             const u32x4 xb = (ok && b_ok) ? xv[u] : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt) {
-                const uint32_t ws = vt[(16 * rt + c) * wn + qc] << (4 * g);
+                const uint32_t ws = vt[(16 * rt + c) * vs + qc] << (4 * g);
                 const u32x4 a = u32x4{s.x ^ (ws & mask), s.y ^ ((ws << 1) & mask), s.z ^ ((ws << 2) & mask),
                                       s.w ^ ((ws << 3) & mask)};
                 acc[rt][u & 1] = mfma16x16x32<T>(a, xb, acc[rt][u & 1]);
@@ -1109,8 +1141,6 @@ struct SbArgs {
     uint32_t ws_magic;      // ceil(2^32 / (kw + 1))
 };
 
-// ceil(2^32 / d): n / d == __umulhi(n, magic) for n * d < 2^32.
-inline uint32_t div_magic(uint32_t d) { return static_cast<uint32_t>(((1ULL << 32) + d - 1) / d); }
 
 // Dwords of LDS an sb_kernel block takes (x slice, then words), each part rounded to whole DMAs.
 __host__ __device__ inline int sb_xs_dwords(int xcols, int kw) { return (xcols * kw * 4 + 63) / 64 * 64 * 4; }
@@ -1546,16 +1576,16 @@ void launch_s1w_table(S1Table& tab, const uint16_t* x, int batch, int n, int wn,
 // Dwords s1m_kernel stages in LDS: 16 rows of sign words, and the s_in pairs when they fit too
 // (64 KB, 16 dwords per thread of a 1024-thread block).
 constexpr int kS1mMaxStaged = 16 * 16 * 64;
-inline bool s1m_sin_lds(int n, int wn, int rt = 1) { return 16 * rt * wn + n / 2 <= kS1mMaxStaged; }
+inline bool s1m_sin_lds(int n, int wn, int rt = 1) { return 16 * rt * s1m_row_stride(wn, rt) + n / 2 <= kS1mMaxStaged; }
 inline size_t s1m_lds_bytes(int n, int wn, int rt = 1) {
-    const size_t staged = static_cast<size_t>(16 * rt * wn + (s1m_sin_lds(n, wn, rt) ? n / 2 : 0)) * 4;
+    const size_t staged = static_cast<size_t>(16 * rt * s1m_row_stride(wn, rt) + (s1m_sin_lds(n, wn, rt) ? n / 2 : 0)) * 4;
     const size_t reduce = static_cast<size_t>(16) * 64 * (16 * rt + 4);  // the waves' tiles and x^2 sums
     return std::max(staged, reduce);
 }
 // Whether the MFMA stage 1 takes rows of n columns at all (up to n = 32768).
 inline bool s1m_fits(int n, int wn, int rt = 1) {
     (void)n;
-    return 16 * rt * wn <= kS1mMaxStaged;
+    return 16 * rt * s1m_row_stride(wn, rt) <= kS1mMaxStaged;
 }
 
 // Blocks of s1m_kernel<..., RT> may take more than 64 KB of LDS (the limit is set once per kernel).
@@ -1571,11 +1601,14 @@ void launch_s1m_loads(const S1Table& tab, dim3 grid, const uint16_t* x, int batc
                       hipStream_t st) {
     const size_t lds = s1m_lds_bytes(n, wn, RT);
     const bool sl = s1m_sin_lds(n, wn, RT);
-#define NQ_S1M(NORM, ONE)                                                                                  \
-    (sl ? (s1m_allow_lds(&s1m_kernel<T, NW, NORM, ONE, true, LD, RT>),                                     \
-           s1m_kernel<T, NW, NORM, ONE, true, LD, RT><<<grid, NW * 64, lds, st>>>(tab, x, batch, n, wn, eps)) \
-        : (s1m_allow_lds(&s1m_kernel<T, NW, NORM, ONE, false, LD, RT>),                                    \
-           s1m_kernel<T, NW, NORM, ONE, false, LD, RT><<<grid, NW * 64, lds, st>>>(tab, x, batch, n, wn, eps)))
+    const bool pad = s1m_row_stride(wn, RT) != wn;  // only ever with RT <= 2
+#define NQ_S1M_P(NORM, ONE, SL, PAD)                                                                     \
+    (s1m_allow_lds(&s1m_kernel<T, NW, NORM, ONE, SL, LD, RT, PAD>),                                      \
+     s1m_kernel<T, NW, NORM, ONE, SL, LD, RT, PAD><<<grid, NW * 64, lds, st>>>(tab, x, batch, n, wn, eps))
+    // (four row tiles run with s_in in LDS only, see s1m_row_tiles: that variant alone is built)
+#define NQ_S1M(NORM, ONE)                                                                                 \
+    (sl ? (pad && RT <= 2 ? NQ_S1M_P(NORM, ONE, true, RT <= 2) : NQ_S1M_P(NORM, ONE, true, false))     \
+        : (pad && RT <= 2 ? NQ_S1M_P(NORM, ONE, RT == 4, RT <= 2) : NQ_S1M_P(NORM, ONE, RT == 4, false)))
     if (tab.count == 1) {
         if (norm) NQ_S1M(true, true);
         else NQ_S1M(false, true);
@@ -1584,6 +1617,7 @@ void launch_s1m_loads(const S1Table& tab, dim3 grid, const uint16_t* x, int batc
         else NQ_S1M(false, false);
     }
 #undef NQ_S1M
+#undef NQ_S1M_P
 }
 template <typename T, int NW, int RT>
 void launch_s1m_nw(const S1Table& tab, dim3 grid, const uint16_t* x, int batch, int n, int wn, bool norm, float eps,
@@ -1604,7 +1638,8 @@ void launch_s1m_nw(const S1Table& tab, dim3 grid, const uint16_t* x, int batch, 
 inline int s1m_row_tiles(const S1Table& tab, int batch, int n, int wn) {
     const int64_t passes = ceil_div(batch, 16);
     for (int rt : {1, 2, 4}) {
-        if (!s1m_fits(n, wn, rt)) break;
+        // (four row tiles only with s_in in LDS: with s_in from global that variant runs out of registers)
+        if (!s1m_fits(n, wn, rt) || (rt == 4 && !s1m_sin_lds(n, wn, rt))) break;
         int64_t blocks = 0;
         for (int k = 0; k < tab.count; ++k) blocks += ceil_div(tab.item[k].kpad, 16 * rt);
         if (blocks * passes <= 256 || rt == 4) return rt;
@@ -1617,6 +1652,7 @@ template <typename T>
 void launch_s1m_table(S1Table& tab, const uint16_t* x, int batch, int n, int wn, bool norm, float eps,
                       hipStream_t st, int rt = 0) {
     if (rt == 0) rt = s1m_row_tiles(tab, batch, n, wn);
+    if (rt == 4 && !s1m_sin_lds(n, wn, 4)) rt = 2;  // the only four-row-tile variant keeps s_in in LDS
     int blocks = 0;
     for (int k = 0; k < tab.count; ++k) {
         tab.item[k].block_begin = blocks;

@@ -187,6 +187,10 @@ GEMV_CASES = [
     # the batched stage 2 below 16 rows: a large U (2M words or more) whose rank leaves s2t_kernel two
     # batch rows per pass
     ("s2b_few_rows_big_u", 16400, 256, 4224, 3, False),
+    # the MFMA stage 1 on rows of 256+ words, whose tile of V is padded to an odd stride in LDS:
+    # an even word count (padded) and an odd one (already odd)
+    ("s1m_wide_even_b5", 300, 8192, 160, 5, True),
+    ("s1m_wide_odd_b5", 300, 8224, 160, 5, True),
 ]
 
 
