@@ -449,6 +449,42 @@ void gemm_dm_kernel(
             }
         return;
     }
+    if constexpr (WP == 64 && NWP * NWQ == 4 && BQ * BKK >= 4096) {
+        // epilogue through LDS. An 8-byte store of four features per lane touches the lines of 32
+        // output rows; instead each wave scales and saturates its tile 32 rows at a time into 4 KB
+        // of the first two step buffers (128-byte rows, 16-byte chunk ch of row r at ch ^ (r % 8):
+        // the reads below are conflict-free) and stores whole 128-byte row pieces, 16 bytes a lane.
+        if constexpr (KS == 1) __syncthreads();  // every wave is done with its last step's buffers
+        uint32_t* tb = reinterpret_cast<uint32_t*>(gw < 2 ? &xs0[0][0] : &xs1[0][0]) + (gw & 1) * 1024;
+#pragma unroll
+        for (int tq = 0; tq < TQ; ++tq) {
+#pragma unroll
+            for (int tp = 0; tp < TP; ++tp)
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4) {
+                    const int ol = wp * WP + 32 * tp + 8 * g4 + 4 * kg;  // feature offset in the block
+                    uint16_t h[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float sc = kSout ? T::to_float(sos[ol + e]) : 1.0f;
+                        h[e] = saturate_to<T>(acc[tp][tq][4 * g4 + e] * sc, T::SAT_GEMM);
+                    }
+                    uint2 v;
+                    v.x = static_cast<uint32_t>(h[0]) | (static_cast<uint32_t>(h[1]) << 16);
+                    v.y = static_cast<uint32_t>(h[2]) | (static_cast<uint32_t>(h[3]) << 16);
+                    *reinterpret_cast<uint2*>(tb + 32 * c + 4 * ((4 * tp + g4) ^ (c & 7)) + 2 * kg) = v;
+                }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int rr = (lane >> 3) + 8 * j;  // row of the 32-row piece; 8 lanes a row
+                const u32x4 d = *reinterpret_cast<const u32x4*>(tb + 32 * rr + 4 * ((lane & 7) ^ (rr & 7)));
+                const int q = q0 + wq * WQ + 32 * tq + rr;
+                const int o = p0 + wp * WP + 8 * (lane & 7);
+                if (q < M && o < N) *reinterpret_cast<u32x4*>(C + static_cast<size_t>(q) * N + o) = d;
+            }
+        }
+        return;
+    }
     // epilogue: scale, saturate, four consecutive features per 8-byte store
 #pragma unroll
     for (int tp = 0; tp < TP; ++tp)
@@ -569,7 +605,7 @@ void launch_dm_split(const void* A, const uint32_t* W, const void* s_in, const v
         gemm_split_finish_kernel<T, false><<<fgrid, 256, 0, stream>>>(part, so, c, m, n, splits);
 }
 
-// How one GEMM is launched. The 32x32x16 kernel needs whole 64-k steps, 8-byte output stores
+// How one GEMM is launched. The 32x32x16 kernel needs whole 64-k steps, 16-byte output stores
 // and 32-bit element offsets into A and the words; anything else runs on the 16x16x32 kernel.
 // Block tile 256 features x 64 rows, four waves of 64 x 64: at B = 2048 on the Llama-2-7B shapes
 // this beat 128 x 128, 256 x 128 (waves of 64 x 128 or 128 x 64) and 256 x 128 with one 128 x 128
@@ -619,7 +655,7 @@ int launch_gemm(const char* name, const void* A, const uint32_t* W, const void* 
                 int64_t M, int64_t K, int64_t N, void* workspace, size_t workspace_bytes, hipStream_t stream,
                 const void* k_scale = nullptr) {
     GemmPlan p = plan_gemm(M, K, N);
-    if (p.mode != kModeOnebit && !aligned(C, 8)) p.mode = kModeOnebit;
+    if (p.mode != kModeOnebit && !aligned(C, 16)) p.mode = kModeOnebit;
     if (p.mode == kModeSplit && (!workspace || workspace_bytes < p.workspace_bytes || !aligned(workspace, 16)))
         p.mode = (K / 64) % 2 == 0 ? kModeGroups : kModeTile;
     switch (p.mode) {
