@@ -17,6 +17,9 @@ Pins (``tests/test_oracle.py``):
   by the reference's own packer (``tests/golden/make_marlin_vectors.py``).
 * ``nanoquant_forward_f64``: closed forms (all-+1 signs, one-hot inputs) and a
   brute-force triple loop on tiny shapes.
+* ``marlin_nanoquant_f64``: equal to ``nanoquant_forward_f64`` with the identity rounding;
+  a closed form whose intermediate is not representable in fp16 or bf16 (it must come out
+  rounded to the nearest value of the type); the clamp of the fp16 intermediate.
 """
 from __future__ import annotations
 
@@ -26,7 +29,7 @@ __all__ = [
     "HALF2_BIT", "LSB_BIT", "bit_position", "pack_binary_gemv", "unpack_binary_gemv",
     "gemv_kernel_sign", "marlin_bit_map", "marlin_perm_in", "marlin_perm_out",
     "pack_binary_marlin", "unpack_binary_marlin", "pack_binary_marlin_fused",
-    "MARLIN_MIN_MAX_PAR", "nanoquant_forward_f64", "compute_forward_torch",
+    "MARLIN_MIN_MAX_PAR", "nanoquant_forward_f64", "marlin_nanoquant_f64", "compute_forward_torch",
     "gemv_output_shape", "check_gemv_tuning", "GEMV_TUNING_CHOICES",
     "marlin_onebit_output_shape", "round_rank", "random_case", "pack_signs_torch", "unpack_signs_torch",
 ]
@@ -239,6 +242,26 @@ def nanoquant_forward_f64(x, s_in, V, s_mid, U, s_out):
     h = (x * np.asarray(s_in, dtype=np.float64)) @ np.asarray(V, dtype=np.float64).T
     if s_mid is not None:
         h = h * np.asarray(s_mid, dtype=np.float64)
+    y = h @ np.asarray(U, dtype=np.float64).T
+    return y * np.asarray(s_out, dtype=np.float64)
+
+
+def marlin_nanoquant_f64(x, s_in, V, s_mid, U, s_out, round_imm, sat_imm=None):
+    """The prefill GEMM's algorithm in float64 with its intermediate rounding point.
+
+    ``marlin_nanoquant_cuda`` (gemm.cpp:112-122) is two ``marlin_onebit`` products whose
+    intermediate ``imm`` is a tensor of the activation dtype: h = (s_in * x) @ V^T * s_mid is
+    clamped to +-``sat_imm`` (gemm_kernel.cu:124-126, fp16 only) and rounded by ``round_imm``
+    (a float64 -> float64 function that rounds to that dtype), then y = s_out * (h @ U^T).
+    With ``round_imm`` the identity and no clamp this is ``nanoquant_forward_f64``.
+    """
+    x = np.asarray(x, dtype=np.float64)
+    h = (x * np.asarray(s_in, dtype=np.float64)) @ np.asarray(V, dtype=np.float64).T
+    if s_mid is not None:
+        h = h * np.asarray(s_mid, dtype=np.float64)
+    if sat_imm is not None:
+        h = np.clip(h, -sat_imm, sat_imm)
+    h = round_imm(h)
     y = h @ np.asarray(U, dtype=np.float64).T
     return y * np.asarray(s_out, dtype=np.float64)
 

@@ -2,11 +2,12 @@
 
 Bars (written here, checked per case):
 * packing, unpacking, reordering: bit-exact;
-* GEMV / GEMM outputs: max|y - y*| / max|y*| against the float64 oracle computed from
-  the same fp16/bf16 inputs, <= 1e-3 for fp16 (the stated bar) and <= 4e-3 (GEMV) /
-  1e-2 (GEMM, whose intermediate is rounded to bf16 for the MFMA) for bf16, whose
-  output rounding alone is 2^-9 relative. Outputs the oracle puts beyond the fp16
-  saturation bound are excluded from the ratio and must equal the bound.
+* GEMV / GEMM outputs: max|y - y*| / max|y*| <= 1e-3 against the float64 oracle computed
+  from the same fp16/bf16 inputs. For bf16 outputs, whose own rounding is up to 2^-9
+  relative, each element's error is counted beyond half a bf16 unit in the last place of
+  y*; the bf16 GEMM is compared with the oracle of its algorithm, whose intermediate is a
+  bf16 tensor (gemm.cpp:112-122). Outputs the oracle puts beyond the fp16 saturation
+  bound are excluded from the ratio and must equal the bound.
 """
 import os
 import sys
@@ -20,8 +21,9 @@ import oracle as O
 pytestmark = pytest.mark.gpu
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "marlin_vectors.npz")
-TOL = {("gemv", torch.float16): 1e-3, ("gemv", torch.bfloat16): 4e-3,
-       ("gemm", torch.float16): 1e-3, ("gemm", torch.bfloat16): 1e-2}
+TOL = {("gemv", torch.float16): 1e-3, ("gemv", torch.bfloat16): 1e-3,
+       ("gemm", torch.float16): 1e-3, ("gemm", torch.bfloat16): 1e-3}
+SIGNIFICANT_BITS = {torch.float16: 11, torch.bfloat16: 8}
 SAT = {("gemv", torch.float16): 64504.0, ("gemm", torch.float16): 65504.0}
 NP_DTYPE = {torch.float16: np.float16}
 
@@ -57,7 +59,20 @@ def rel_err(y, y64, kind, dtype):
         stored = float(np.float16(sat))
         assert np.all(np.abs(y[~mask]) == stored), "saturated outputs must sit at the bound"
     denom = np.abs(y64[mask]).max()
-    return float(np.abs(y[mask] - y64[mask]).max() / denom), int((~mask).sum())
+    diff = np.abs(y[mask] - y64[mask])
+    if dtype == torch.bfloat16:
+        diff = np.maximum(diff - half_ulp(y64[mask], dtype), 0.0)
+    return float(diff.max() / denom), int((~mask).sum())
+
+
+def half_ulp(v, dtype):
+    """Half a unit in the last place of |v| in `dtype`: the output's own rounding error bound."""
+    _, e = np.frexp(np.abs(v))  # |v| = f * 2^e, f in [0.5, 1)
+    return np.ldexp(1.0, e - 1 - SIGNIFICANT_BITS[dtype])
+
+
+def round_bf16(h):
+    return torch.from_numpy(np.asarray(h, dtype=np.float32)).to(torch.bfloat16).double().numpy()
 
 
 # --------------------------------------------------------------------------- packing
@@ -399,7 +414,10 @@ def test_gemm_parity(nq, case, dtype):
     y = torch.ops.binary_kernels.marlin_nanoquant_forward(x, V_bits, U_bits, s1, s2, s3, ws)
     torch.cuda.synchronize()
     o = oracle_inputs(dict(c, s_mid=s_mid), dtype)
-    y64 = O.nanoquant_forward_f64(o["x"], o["s_in"], c["V"], o["s_mid"], c["U"], o["s_out"])
+    if dtype == torch.bfloat16:
+        y64 = O.marlin_nanoquant_f64(o["x"], o["s_in"], c["V"], o["s_mid"], c["U"], o["s_out"], round_imm=round_bf16)
+    else:
+        y64 = O.nanoquant_forward_f64(o["x"], o["s_in"], c["V"], o["s_mid"], c["U"], o["s_out"])
     assert tuple(y.shape) == (B, m) and y.dtype == dtype
     err, nsat = rel_err(y, y64, "gemm", dtype)
     print(f"[gemm] {name} {dtype} rel_err={err:.3e} saturated={nsat}", flush=True)

@@ -180,6 +180,36 @@ def test_forward_brute_force():
             assert abs(acc * float(c["s_out"][i]) - y[b, i]) <= 1e-12 * max(1.0, abs(y[b, i]))
 
 
+def test_marlin_f64_identity_rounding_is_the_forward():
+    c = O.random_case(7, 40, 64, 24, 3, with_mid=True)
+    args = (c["x"], c["s_in"], c["V"], c["s_mid"], c["U"], c["s_out"])
+    np.testing.assert_array_equal(O.marlin_nanoquant_f64(*args, round_imm=lambda h: h), O.nanoquant_forward_f64(*args))
+
+
+@pytest.mark.parametrize("kind", ["f16", "bf16"])
+def test_marlin_f64_rounds_the_intermediate(kind):
+    # one input column, all +1 signs: h_j = s_in[0] * x[0] = 1 + 2^-12 for every j, which neither
+    # type holds; the nearest value of both is 1.0, so y = s_out * r exactly
+    import torch
+    rnd = (lambda h: h.astype(np.float16).astype(np.float64)) if kind == "f16" else \
+        (lambda h: torch.from_numpy(h.astype(np.float32)).to(torch.bfloat16).double().numpy())
+    n, r, m = 1, 6, 5
+    x = np.array([[1.0 + 2.0 ** -12]])
+    y = O.marlin_nanoquant_f64(x, np.ones(n), np.ones((r, n)), None, np.ones((m, r)), np.full(m, 0.5), round_imm=rnd)
+    np.testing.assert_array_equal(y, np.full((1, m), 0.5 * r))
+    # and 1 + 2^-6 survives both roundings (8 significant bits suffice)
+    y = O.marlin_nanoquant_f64(np.array([[1.0 + 2.0 ** -6]]), np.ones(n), np.ones((r, n)), None, np.ones((m, r)),
+                               np.ones(m), round_imm=rnd)
+    np.testing.assert_array_equal(y, np.full((1, m), r * (1.0 + 2.0 ** -6)))
+
+
+def test_marlin_f64_clamps_the_fp16_intermediate():
+    # h = 70000 is past the fp16 bound; the first product saturates it to 65504 before stage 2
+    y = O.marlin_nanoquant_f64(np.array([[70000.0]]), np.ones(1), np.ones((2, 1)), None, np.ones((3, 2)), np.ones(3),
+                               round_imm=lambda h: h, sat_imm=65504.0)
+    np.testing.assert_array_equal(y, np.full((1, 3), 2 * 65504.0))
+
+
 def test_torch_dense_path_matches_f64():
     import torch
     c = O.random_case(6, 48, 64, 32, 2)
