@@ -609,42 +609,53 @@ void launch_dm_split(const void* A, const uint32_t* W, const void* s_in, const v
 // and 32-bit element offsets into A and the words; anything else runs on the 16x16x32 kernel.
 // Block tile 256 features x 64 rows, four waves of 64 x 64: at B = 2048 on the Llama-2-7B shapes
 // this beat 128 x 128, 256 x 128 (waves of 64 x 128 or 128 x 64) and 256 x 128 with one 128 x 128
-// wave per SIMD, whose 1376 wave tiles leave a third of the second round of the chip idle. The
-// grid decides the rest:
+// wave per SIMD. The grid decides the rest (tiles of 256 x 64 counted):
 //   >= 512 tiles (two per CU): one block per tile;
-//   128-511 tiles: K split over two wave groups inside each block (B = 2048, K = 4096,
-//     N = 1792: 46 -> 38 us). Compiled for four waves per SIMD this stage alone ran 33.6 against
-//     37.6 us in isolation, but the two-stage op ran 124.8 against 121 us, so it stays at two;
-//   fewer (B = 256 and the rank-wide stages): K split over up to 512 / tiles ranges of at least
-//     8 steps across the grid, fp32 sums into the caller's workspace, then a finishing launch;
-//     without that workspace, as above. (Against 512 / 4 and 256 / 8 over the B = 256 shapes of
-//     Llama-2-7B and Llama-3-70B, 512 / 8 was best or within 3% everywhere; 7B down at 0.55 bpw:
-//     97 us unsplit, 48 us split.)
-constexpr int64_t kSplitTarget = 512;  // blocks a split grid aims at (two per CU)
+//   160-511 tiles: K split over two wave groups inside each block (B = 2048, K = 4096,
+//     N = 1792: 46 -> 38 us);
+//   fewer, with at most 32 even 64-k steps and 128+ tiles of 32 rows: 32-row tiles, K over two
+//     wave groups (B = 256, K = 1280 -> 1120, N = 4096: 16.6 us split across the grid -> 9.1 us;
+//     B = 2048, K = 512, N = 1024: 8.8 -> 6.8 us);
+//   128-159 tiles otherwise: as 160-511;
+//   fewer: K split across the grid into about one block per CU, each range at least 8 steps, fp32
+//     sums into the caller's workspace, then a finishing launch; 64-row tiles from 64 tiles up,
+//     32-row tiles below (B = 256, K = 4096, N = 1792: 8 ranges of 28 tiles 19.6 us -> 4 ranges of
+//     56 tiles 15.8 us; B = 2048, K = 8192, N = 512: 8 ranges 34.6 -> 4 ranges 30.2 us). Without
+//     that workspace, as the grid's K groups above.
+constexpr int64_t kSplitTarget = 256;  // blocks a split grid aims at (one per CU)
 constexpr int64_t kSplitMinSteps = 8;  // 64-k steps of the shortest range
-enum GemmMode { kModeOnebit, kModeTile, kModeGroups, kModeSplit };
+enum GemmMode { kModeOnebit, kModeTile, kModeGroups, kModeGroups32, kModeSplit, kModeSplit32 };
 struct GemmPlan {
     GemmMode mode = kModeOnebit;
     int splits = 1;
     int split_steps = 0;
-    size_t workspace_bytes = 0;  // needed by kModeSplit
+    size_t workspace_bytes = 0;  // needed by kModeSplit / kModeSplit32
 };
 
 GemmPlan plan_gemm(int64_t M, int64_t K, int64_t N) {
     GemmPlan p;
     if (K % 64 || K <= 0 || M * K >= ((int64_t)1 << 31) || (K / 16) * (N / 2) >= ((int64_t)1 << 31)) return p;
     const int64_t tiles = ceil_div(M, 64) * ceil_div(N, 256);
+    const int64_t tiles32 = ceil_div(M, 32) * ceil_div(N, 256);
     const int64_t steps = K / 64;
+    const bool even = steps % 2 == 0;
     p.mode = kModeTile;
     if (tiles >= 2 * 256) return p;
-    if (steps % 2 == 0) p.mode = kModeGroups;
+    if (even) p.mode = kModeGroups;
+    if (tiles >= 160) return p;
+    if (even && steps <= 32 && tiles32 >= 128) {
+        p.mode = kModeGroups32;
+        return p;
+    }
     if (tiles >= 128) return p;
-    const int64_t want = std::min<int64_t>(ceil_div(kSplitTarget, tiles), steps / kSplitMinSteps);
+    const bool rows32 = tiles < 64;
+    const int64_t grid_tiles = rows32 ? tiles32 : tiles;
+    const int64_t want = std::min<int64_t>(kSplitTarget / grid_tiles, steps / kSplitMinSteps);
     if (want < 2) return p;
     p.split_steps = static_cast<int>(ceil_div(steps, want));
     p.splits = static_cast<int>(ceil_div(steps, p.split_steps));  // every range non-empty
     if (p.splits < 2) return p;
-    p.mode = kModeSplit;
+    p.mode = rows32 ? kModeSplit32 : kModeSplit;
     p.workspace_bytes = static_cast<size_t>(p.splits) * static_cast<size_t>(M) * static_cast<size_t>(N) * 4;
     return p;
 }
@@ -656,7 +667,8 @@ int launch_gemm(const char* name, const void* A, const uint32_t* W, const void* 
                 const void* k_scale = nullptr) {
     GemmPlan p = plan_gemm(M, K, N);
     if (p.mode != kModeOnebit && !aligned(C, 16)) p.mode = kModeOnebit;
-    if (p.mode == kModeSplit && (!workspace || workspace_bytes < p.workspace_bytes || !aligned(workspace, 16)))
+    if ((p.mode == kModeSplit || p.mode == kModeSplit32) &&
+        (!workspace || workspace_bytes < p.workspace_bytes || !aligned(workspace, 16)))
         p.mode = (K / 64) % 2 == 0 ? kModeGroups : kModeTile;
     switch (p.mode) {
         case kModeOnebit:
@@ -667,8 +679,15 @@ int launch_gemm(const char* name, const void* A, const uint32_t* W, const void* 
         case kModeGroups:
             launch_dm<T, 256, 64, 64, 64, 2, 2>(A, W, s_in, s_out, C, M, K, N, stream);
             break;
+        case kModeGroups32:
+            launch_dm<T, 256, 32, 64, 32, 2, 2>(A, W, s_in, s_out, C, M, K, N, stream);
+            break;
         case kModeSplit:
             launch_dm_split<T, 256, 64, 64, 64, 2>(A, W, s_in, s_out, C, M, K, N, static_cast<float*>(workspace),
+                                                   p.splits, p.split_steps, stream);
+            break;
+        case kModeSplit32:
+            launch_dm_split<T, 256, 32, 64, 32, 2>(A, W, s_in, s_out, C, M, K, N, static_cast<float*>(workspace),
                                                    p.splits, p.split_steps, stream);
             break;
     }

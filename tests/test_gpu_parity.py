@@ -393,6 +393,9 @@ GEMM_CASES = [
     ("llama7b_gate_055_b2048", 2048, 4096, 1632, 11008, False),
     # stage 2 on 1024 blocks of 64 rows x 256 features, the last row block ragged: 1000 = 15 * 64 + 40
     ("wide_ragged_rows", 1000, 256, 128, 16384, True),
+    # small grids on 32-row tiles, the last one ragged (200 = 6 * 32 + 8): stage 1 splits K across the
+    # grid (7 tiles, 8 ranges), stage 2 (4 steps, 224 tiles) splits it over two wave groups
+    ("small_grid_ragged", 200, 4096, 256, 8192, True),
 ]
 
 
@@ -447,7 +450,8 @@ def test_gemm_onebit_scale_variants(nq, scales, K):
     assert err <= 1e-3, err
 
 
-@pytest.mark.parametrize("B,K,N", [(256, 4096, 1280), (100, 11008, 512)], ids=["b256_k4096", "b100_k11008"])
+@pytest.mark.parametrize("B,K,N", [(256, 4096, 1280), (100, 11008, 512), (1100, 4096, 1024)],
+                         ids=["b256_k4096_rows32", "b100_k11008_rows32", "b1100_k4096_rows64"])
 def test_gemm_split_k(nq, B, K, N):
     """Small grids split K across blocks (fp32 planes in the workspace the op allocates, added
     by a finishing launch); the same call through the C ABI without a workspace runs unsplit.
