@@ -617,13 +617,16 @@ void launch_dm_split(const void* A, const uint32_t* W, const void* s_in, const v
 //     wave groups (B = 256, K = 1280 -> 1120, N = 4096: 16.6 us split across the grid -> 9.1 us;
 //     B = 2048, K = 512, N = 1024: 8.8 -> 6.8 us);
 //   128-159 tiles otherwise: as 160-511;
-//   fewer: K split across the grid into about one block per CU, each range at least 8 steps, fp32
-//     sums into the caller's workspace, then a finishing launch; 64-row tiles from 64 tiles up,
-//     32-row tiles below (B = 256, K = 4096, N = 1792: 8 ranges of 28 tiles 19.6 us -> 4 ranges of
-//     56 tiles 15.8 us; B = 2048, K = 8192, N = 512: 8 ranges 34.6 -> 4 ranges 30.2 us). Without
-//     that workspace, as the grid's K groups above.
-constexpr int64_t kSplitTarget = 256;  // blocks a split grid aims at (one per CU)
-constexpr int64_t kSplitMinSteps = 8;  // 64-k steps of the shortest range
+//   fewer: K split across the grid, each range at least 8 steps, fp32 sums into the caller's
+//     workspace, then a finishing launch. Up to 128 steps: about one block per CU, on 32-row tiles
+//     below 64 tiles of 64 rows (B = 256, K = 4096, N = 1792: 8 ranges of 28 tiles 19.6 us -> 4
+//     ranges of 56 tiles 15.8 us; B = 2048, K = 8192, N = 512: 8 ranges 34.6 -> 4 ranges 30.2 us).
+//     Longer K: about two blocks per CU on 64-row tiles (B = 256, K = 28672, N = 3584: 9 ranges of
+//     56 tiles 66.8 us, against 93.2 us for 2 ranges of 112 32-row tiles). Without that workspace,
+//     as the grid's K groups above.
+constexpr int64_t kSplitTarget = 256;    // blocks a split grid aims at (one per CU; two for long K)
+constexpr int64_t kSplitMinSteps = 8;    // 64-k steps of the shortest range
+constexpr int64_t kSplitLongSteps = 128; // beyond this many steps K counts as long
 enum GemmMode { kModeOnebit, kModeTile, kModeGroups, kModeGroups32, kModeSplit, kModeSplit32 };
 struct GemmPlan {
     GemmMode mode = kModeOnebit;
@@ -648,9 +651,10 @@ GemmPlan plan_gemm(int64_t M, int64_t K, int64_t N) {
         return p;
     }
     if (tiles >= 128) return p;
-    const bool rows32 = tiles < 64;
+    const bool long_k = steps > kSplitLongSteps;
+    const bool rows32 = !long_k && tiles < 64;
     const int64_t grid_tiles = rows32 ? tiles32 : tiles;
-    const int64_t want = std::min<int64_t>(kSplitTarget / grid_tiles, steps / kSplitMinSteps);
+    const int64_t want = std::min<int64_t>((long_k ? 2 : 1) * kSplitTarget / grid_tiles, steps / kSplitMinSteps);
     if (want < 2) return p;
     p.split_steps = static_cast<int>(ceil_div(steps, want));
     p.splits = static_cast<int>(ceil_div(steps, p.split_steps));  // every range non-empty

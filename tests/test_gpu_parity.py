@@ -451,7 +451,7 @@ def test_gemm_onebit_scale_variants(nq, scales, K):
 
 
 @pytest.mark.parametrize("B,K,N", [(256, 4096, 1280), (100, 11008, 512), (1100, 4096, 1024)],
-                         ids=["b256_k4096_rows32", "b100_k11008_rows32", "b1100_k4096_rows64"])
+                         ids=["b256_k4096_rows32", "b100_k11008_long_k", "b1100_k4096_rows64"])
 def test_gemm_split_k(nq, B, K, N):
     """Small grids split K across blocks (fp32 planes in the workspace the op allocates, added
     by a finishing launch); the same call through the C ABI without a workspace runs unsplit.
