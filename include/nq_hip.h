@@ -200,7 +200,8 @@ int nq_gemv_group_stage2(int dtype, int64_t count, const nq_gemv_item* items, in
  *   A  dtype [M, K] row-major       w_bits uint32 Marlin words [K/16, N/2]
  *   s_in, s_out: permuted as pack_binary_marlin returns them, or NULL (= ones)
  *   C  dtype [M, N]
- * K % 16 == 0, N % 64 == 0. fp32 accumulation; fp16 outputs saturate at +-65504.
+ * K % 16 == 0, N % 64 == 0. fp32 accumulation; fp16 outputs saturate at +-65504. A must be
+ * 16-byte aligned, w_bits 8-byte; a C that is not 16-byte aligned runs the slower 16x16 kernel.
  * workspace: device memory (16-byte aligned) of nq_gemm_onebit_workspace_bytes(M, K, N) bytes
  * lets a small grid split K across blocks (fp32 partial sums, added in a fixed order by a second
  * launch); NULL or a smaller one runs unsplit. Calls that share a workspace must be ordered (one
