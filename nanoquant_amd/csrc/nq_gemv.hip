@@ -1666,12 +1666,17 @@ void launch_s1m_table(S1Table& tab, const uint16_t* x, int batch, int n, int wn,
     else launch_s1m_nw<T, 16, 1>(tab, grid, x, batch, n, wn, norm, eps, st);
 }
 
-// Stage 1 of a table: the VALU kernel for one or two batch rows of up to 16384 columns, the MFMA
-// kernel from three rows on and for wider rows.
+// Stage 1 of a table: the VALU kernel for one or two batch rows of up to 16384 columns (and for
+// three or four rows of up to 4096 columns when V holds fewer than 256 K words, two rows a pass:
+// 4096 x 1632 at 3 / 4 rows 5.7 / 5.8 -> 5.0 / 5.5 us; on wider rows, or from r = 2048, where the
+// second pass re-reads more of V, the MFMA kernel stays ahead), the MFMA kernel otherwise.
 template <typename T>
 void launch_stage1_table(S1Table& tab, const uint16_t* x, int batch, int n, int wn, bool norm, float eps,
                          hipStream_t st) {
-    if ((batch >= 3 || wn > 512) && s1m_fits(n, wn)) launch_s1m_table<T>(tab, x, batch, n, wn, norm, eps, st);
+    int64_t v_words = 0;
+    for (int k = 0; k < tab.count; ++k) v_words = std::max<int64_t>(v_words, static_cast<int64_t>(tab.item[k].r) * wn);
+    const bool valu_rows = batch <= 2 || (batch <= 4 && wn <= 128 && v_words < 256 * 1024);
+    if ((!valu_rows || wn > 512) && s1m_fits(n, wn)) launch_s1m_table<T>(tab, x, batch, n, wn, norm, eps, st);
     else launch_s1w_table<T>(tab, x, batch, n, wn, norm, eps, st);
 }
 
