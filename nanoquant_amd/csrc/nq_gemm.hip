@@ -610,9 +610,10 @@ void launch_dm_split(const void* A, const uint32_t* W, const void* s_in, const v
 // Block tile 256 features x 64 rows, four waves of 64 x 64: at B = 2048 on the Llama-2-7B shapes
 // this beat 128 x 128, 256 x 128 (waves of 64 x 128 or 128 x 64) and 256 x 128 with one 128 x 128
 // wave per SIMD. The grid decides the rest (tiles of 256 x 64 counted):
-//   >= 512 tiles (two per CU): one block per tile;
-//   160-511 tiles: K split over two wave groups inside each block (B = 2048, K = 4096,
-//     N = 1792: 46 -> 38 us);
+//   more than 256 tiles: one block per tile (B = 2048, K = 8192, N = 2304, 288 tiles: 119.0 us
+//     with K over two wave groups -> 105.2 us; K = 4096, N = 3072, 384 tiles: 64.3 -> 59.8 us);
+//   160-256 tiles: K split over two wave groups inside each block (B = 2048, K = 4096,
+//     N = 1792, 224 tiles: 46 -> 38 us against one block per tile; 256 tiles: 42.7 -> 40.3 us);
 //   fewer, with at most 32 even 64-k steps and 128+ tiles of 32 rows: 32-row tiles, K over two
 //     wave groups (B = 256, K = 1280 -> 1120, N = 4096: 16.6 us split across the grid -> 9.1 us;
 //     B = 2048, K = 512, N = 1024: 8.8 -> 6.8 us);
@@ -643,7 +644,7 @@ GemmPlan plan_gemm(int64_t M, int64_t K, int64_t N) {
     const int64_t steps = K / 64;
     const bool even = steps % 2 == 0;
     p.mode = kModeTile;
-    if (tiles >= 2 * 256) return p;
+    if (tiles > 256) return p;
     if (even) p.mode = kModeGroups;
     if (tiles >= 160) return p;
     if (even && steps <= 32 && tiles32 >= 128) {
