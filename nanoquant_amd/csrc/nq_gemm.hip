@@ -607,9 +607,12 @@ void launch_dm_split(const void* A, const uint32_t* W, const void* s_in, const v
 
 // How one GEMM is launched. The 32x32x16 kernel needs whole 64-k steps, 16-byte output stores
 // and 32-bit element offsets into A and the words; anything else runs on the 16x16x32 kernel.
-// Block tile 256 features x 64 rows, four waves of 64 x 64: at B = 2048 on the Llama-2-7B shapes
-// this beat 128 x 128, 256 x 128 (waves of 64 x 128 or 128 x 64) and 256 x 128 with one 128 x 128
-// wave per SIMD. The grid decides the rest (tiles of 256 x 64 counted):
+// Block tile 256 features x 64 rows, four waves of 64 x 64, or 256 x 128 with waves of 64 x 128
+// (each sign fragment decoded once for four MFMAs instead of two; two waves per SIMD). The grid
+// decides (tiles of 256 x 64 counted):
+//   1024 tiles or more: one block per 256 x 128 tile (B = 2048, K = 1792, N = 11008: 85.5 -> 77 us;
+//     K = 3584, N = 28672: 360 -> 338 us; 5-9% on every such stage 2 measured; at 512 tiles the
+//     64-row tile stays ahead, 31.2 against 32.2 us on N = 4096);
 //   more than 256 tiles: one block per tile (B = 2048, K = 8192, N = 2304, 288 tiles: 119.0 us
 //     with K over two wave groups -> 105.2 us; K = 4096, N = 3072, 384 tiles: 64.3 -> 59.8 us);
 //   160-256 tiles: K split over two wave groups inside each block (B = 2048, K = 4096,
@@ -628,7 +631,7 @@ void launch_dm_split(const void* A, const uint32_t* W, const void* s_in, const v
 constexpr int64_t kSplitTarget = 256;    // blocks a split grid aims at (one per CU; two for long K)
 constexpr int64_t kSplitMinSteps = 8;    // 64-k steps of the shortest range
 constexpr int64_t kSplitLongSteps = 128; // beyond this many steps K counts as long
-enum GemmMode { kModeOnebit, kModeTile, kModeGroups, kModeGroups32, kModeSplit, kModeSplit32 };
+enum GemmMode { kModeOnebit, kModeTile, kModeTile128, kModeGroups, kModeGroups32, kModeSplit, kModeSplit32 };
 struct GemmPlan {
     GemmMode mode = kModeOnebit;
     int splits = 1;
@@ -643,7 +646,7 @@ GemmPlan plan_gemm(int64_t M, int64_t K, int64_t N) {
     const int64_t tiles32 = ceil_div(M, 32) * ceil_div(N, 256);
     const int64_t steps = K / 64;
     const bool even = steps % 2 == 0;
-    p.mode = kModeTile;
+    p.mode = tiles >= 1024 ? kModeTile128 : kModeTile;
     if (tiles > 256) return p;
     if (even) p.mode = kModeGroups;
     if (tiles >= 160) return p;
@@ -680,6 +683,9 @@ int launch_gemm(const char* name, const void* A, const uint32_t* W, const void* 
             return launch_onebit<T>(A, W, s_in, s_out, C, M, K, N, stream);
         case kModeTile:
             launch_dm<T, 256, 64, 64, 64, 2, 1>(A, W, s_in, s_out, C, M, K, N, stream, k_scale);
+            break;
+        case kModeTile128:
+            launch_dm<T, 256, 128, 64, 128, 2, 1>(A, W, s_in, s_out, C, M, K, N, stream, k_scale);
             break;
         case kModeGroups:
             launch_dm<T, 256, 64, 64, 64, 2, 2>(A, W, s_in, s_out, C, M, K, N, stream);
