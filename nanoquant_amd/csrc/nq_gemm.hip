@@ -194,7 +194,7 @@ int launch_onebit(const void* A, const uint32_t* W, const void* s_in, const void
 // a lane for the A tile, 4 for sign words and s_in) straight into one of three LDS buffers,
 // two steps ahead, so no register holds a tile in flight. A wave's DMA writes 64 consecutive
 // LDS slots, so the A tile is unpadded (128-byte rows) and bank conflicts are avoided by where
-// each lane fetches from: LDS chunk p of row r holds the row's 16-byte chunk p ^ (r % 8). s_in
+// each lane fetches from: LDS chunk p of row r holds the row's 16-byte chunk p ^ ((r / 2) % 8). s_in
 // is fetched in the order the operands read it (every wave keeps its own copy, so every wave
 // issues the same number of DMAs per step). The three buffers are distinct LDS arrays, so the
 // compiler's wait counts for a buffer's reads cover only that buffer's DMAs; before the barrier
@@ -214,6 +214,12 @@ void gemm_dm_kernel(
     float* __restrict__ part, int split_steps, const uint16_t* __restrict__ k_scale) {
     static_assert(BKK == 64 || BKK == 128, "64 or 128 k per step");
     constexpr int CPR = BKK / 8;       // 16-byte chunks per A-tile row
+    // LDS chunk p of A-tile row r holds the row's chunk p ^ xswz(r). 64 banks of 4 bytes serve a
+    // 16-byte read 16 lanes at a time, and the 16 lanes of such a phase read one chunk of 16
+    // consecutive rows, so those must fall in 16 different 16-byte bank groups: with 128-byte
+    // rows, r % 2 picks the half of the banks and (r / 2) % 8 the group within it (r % 8 alone
+    // put rows r and r + 8 on the same banks); 256-byte rows span the banks, so r % 16.
+    auto xswz = [](int r) { return BKK == 64 ? (r >> 1) & 7 : r & 15; };
     constexpr int NWP = BP / WP;
     constexpr int NWQ = BQ / WQ;
     constexpr int NTG = NWP * NWQ * 64;  // threads of one k group
@@ -291,7 +297,7 @@ void gemm_dm_kernel(
     for (int j = 0; j < XPT; ++j) {
         const int ci = j * NTG + tg;
         const int r = ci / CPR;
-        xoff[j] = static_cast<uint32_t>(min(q0 + r, M - 1)) * static_cast<uint32_t>(K) + 8 * ((ci % CPR) ^ (r & 7));
+        xoff[j] = static_cast<uint32_t>(min(q0 + r, M - 1)) * static_cast<uint32_t>(K) + 8 * ((ci % CPR) ^ xswz(r));
     }
     uint32_t wsrc[WPT];
 #pragma unroll
@@ -333,7 +339,7 @@ void gemm_dm_kernel(
         u32x4 x[TQ];
     };
     auto read_kt = [&](Frag& f, const uint16_t* xs, const uint32_t* ws, const uint32_t* ss, int kt) {
-        const int pos = (2 * kt + kg) ^ (c & 7);
+        const int pos = (2 * kt + kg) ^ xswz(c);  // the wave's rows start at multiples of 32
 #pragma unroll
         for (int g = 0; g < TG; ++g) f.w[g] = *reinterpret_cast<const u32x4*>(ws + kt * WROW + wl[g]);
         f.s = kSin ? *reinterpret_cast<const u32x4*>(ss + wave * 64 + 8 * kt + 4 * kg) : u32x4{one, one, one, one};
@@ -452,8 +458,9 @@ void gemm_dm_kernel(
     if constexpr (WP == 64 && NWP * NWQ == 4 && BQ * BKK >= 4096) {
         // epilogue through LDS. An 8-byte store of four features per lane touches the lines of 32
         // output rows; instead each wave scales and saturates its tile 32 rows at a time into 4 KB
-        // of the first two step buffers (128-byte rows, 16-byte chunk ch of row r at ch ^ (r % 8):
-        // the reads below are conflict-free) and stores whole 128-byte row pieces, 16 bytes a lane.
+        // of the first two step buffers (128-byte rows, 16-byte chunk ch of row r at ch ^ ((r / 2) % 8):
+        // the 16-byte reads below are conflict-free, and 32 lanes' 8-byte writes meet two to a bank
+        // group, where r % 8 put four) and stores whole 128-byte row pieces, 16 bytes a lane.
         if constexpr (KS == 1) __syncthreads();  // every wave is done with its last step's buffers
         uint32_t* tb = reinterpret_cast<uint32_t*>(gw < 2 ? &xs0[0][0] : &xs1[0][0]) + (gw & 1) * 1024;
 #pragma unroll
@@ -472,12 +479,12 @@ void gemm_dm_kernel(
                     uint2 v;
                     v.x = static_cast<uint32_t>(h[0]) | (static_cast<uint32_t>(h[1]) << 16);
                     v.y = static_cast<uint32_t>(h[2]) | (static_cast<uint32_t>(h[3]) << 16);
-                    *reinterpret_cast<uint2*>(tb + 32 * c + 4 * ((4 * tp + g4) ^ (c & 7)) + 2 * kg) = v;
+                    *reinterpret_cast<uint2*>(tb + 32 * c + 4 * ((4 * tp + g4) ^ ((c >> 1) & 7)) + 2 * kg) = v;
                 }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int rr = (lane >> 3) + 8 * j;  // row of the 32-row piece; 8 lanes a row
-                const u32x4 d = *reinterpret_cast<const u32x4*>(tb + 32 * rr + 4 * ((lane & 7) ^ (rr & 7)));
+                const u32x4 d = *reinterpret_cast<const u32x4*>(tb + 32 * rr + 4 * ((lane & 7) ^ ((rr >> 1) & 7)));
                 const int q = q0 + wq * WQ + 32 * tq + rr;
                 const int o = p0 + wp * WP + 8 * (lane & 7);
                 if (q < M && o < N) *reinterpret_cast<u32x4*>(C + static_cast<size_t>(q) * N + o) = d;
