@@ -243,15 +243,20 @@ def test_gemm_split_workspace_sizes():
     assert lib.nq_gemm_onebit_workspace_bytes(2048, 4096, 1792) == 0
     assert lib.nq_gemm_onebit_workspace_bytes(256, 4096 + 16, 1280) == 0
     assert lib.nq_gemm_onebit_workspace_bytes(0, 4096, 1280) == 0
-    # B=256, K=4096, N=1280: 20 tiles of 64 x 256, 64 steps -> 8 ranges of 8 steps
-    assert lib.nq_gemm_onebit_workspace_bytes(256, 4096, 1280) == 8 * 256 * 1280 * 4
-    # B=256, K=11008 (172 steps), N=1792: 28 tiles -> ceil(512 / 28) = 19 ranges of ceil(172 / 19) = 10 steps,
-    # so 18 ranges cover the steps
+    # B=256, K=4096 (64 steps, not long), N=1280: 20 tiles of 64 x 256, so the split runs 40 tiles of
+    # 32 x 256 -> 256 // 40 = 6 ranges of ceil(64 / 6) = 11 steps, and 6 ranges cover the steps
+    assert lib.nq_gemm_onebit_workspace_bytes(256, 4096, 1280) == 6 * 256 * 1280 * 4
+    # B=256, K=1792 (28 even steps), N=4096: 64 tiles, 128 of 32 rows -> K over two wave groups, no split
+    assert lib.nq_gemm_onebit_workspace_bytes(256, 1792, 4096) == 0
+    # B=256, K=11008 (172 steps: long), N=1792: 28 tiles of 64 rows -> 2 * 256 // 28 = 18 ranges of
+    # ceil(172 / 18) = 10 steps, and 18 ranges cover the steps
     assert lib.nq_gemm_onebit_workspace_bytes(256, 11008, 1792) == 18 * 256 * 1792 * 4
     # two stages share the workspace: the larger need
     s1 = lib.nq_gemm_onebit_workspace_bytes(256, 11008, 1792)
-    s2 = lib.nq_gemm_onebit_workspace_bytes(256, 1792, 4096)
-    assert lib.nq_gemm_nanoquant_workspace_bytes(256, 11008, 1792, 4096) == max(s1, s2) > 0
+    s2 = lib.nq_gemm_onebit_workspace_bytes(256, 4096, 1792)  # 28 tiles, 56 of 32 rows: 4 ranges of 16
+    assert s2 == 4 * 256 * 1792 * 4
+    assert lib.nq_gemm_nanoquant_workspace_bytes(256, 11008, 1792, 4096) == max(s1, 0) > 0
+    assert lib.nq_gemm_nanoquant_workspace_bytes(256, 4096, 1792, 11008) == max(s2, 0) > 0
 
 
 def test_repack_marlin_argument_errors_need_no_gpu():
