@@ -548,6 +548,7 @@ def run_sweep(args, dev):
         r_pad = -(-r // 256) * 256
         wv, wu = words(n // 16, r_pad // 2), words(r_pad // 16, m // 2)
         s_g, s_l, s_h = scales(n), scales(r_pad), scales(m)
+        s_l[r:] = 0  # as pack_binary_marlin_fused pads the rank (r is a multiple of 32, so the zeros stay last)
         ws = torch.zeros(m // 128 * 32, dtype=torch.int32, device=dev)
         for B in (256, 2048):
             x = torch.randn(B, n, device=dev, generator=gen).half()
@@ -591,6 +592,7 @@ def run_batch_sweep(args, dev):
         Wv = [words(n // 16, r_pad // 2) for _ in range(copies)]
         Wu = [words(r_pad // 16, m // 2) for _ in range(copies)]
         s_in, s_out, s_l = scales(n), scales(m), scales(r_pad)
+        s_l[r:] = 0  # the packer's zero scale_l over the padded rank
         ws = torch.zeros(m // 128 * 32, dtype=torch.int32, device=dev)
         for B in batches:
             x = torch.randn(B, n, device=dev, generator=gen).half()
