@@ -391,7 +391,8 @@ GEMM_CASES = [
     ("llama7b_gate_055_b256", 256, 4096, 1632, 11008, False),
     ("llama7b_down_055_b256", 256, 11008, 1632, 4096, False),
     ("llama7b_gate_055_b2048", 2048, 4096, 1632, 11008, False),
-    # stage 2 on 1024 blocks of 64 rows x 256 features, the last row block ragged: 1000 = 15 * 64 + 40
+    # stage 2 counts 1024 tiles of 64 rows x 256 features, so it runs 512 blocks of 128 rows x 256
+    # features (waves of 64 x 128), the last row block ragged: 1000 = 7 * 128 + 104
     ("wide_ragged_rows", 1000, 256, 128, 16384, True),
     # small grids on 32-row tiles, the last one ragged (200 = 6 * 32 + 8): stage 1 splits K across the
     # grid (7 tiles, 8 ranges), stage 2 (4 steps, 224 tiles) splits it over two wave groups

@@ -3,7 +3,8 @@
 The fixed cases of ``test_gpu_parity.py`` pick shapes at each kernel's switch points; these
 draw sizes at random (fixed seeds, so a failure names a reproducible case) over ranges that
 cross every launch rule: GEMV rows, columns that are and are not multiples of 8 or 32, ranks
-of any size, 1-160 batch rows, with and without s_mid; GEMM batch rows 1-600, K and the rank
+of any size, 1-160 batch rows, with and without s_mid; GEMM batch rows 1-600 (every sixth case
+1025-1600 rows on 16384-19200 outputs, which runs stage 2 on 128-row blocks), K and the rank
 multiples of 32 (the fused packer rounds the rank to 32 before padding it to 256, and so fails
 on others, as the reference's does: kernel/utils.py:255-271), outputs a multiple of 64 (the
 Marlin layout). Bar: max|y - y*| / max|y*| <= 1e-3 in fp16, as the reference's own check
@@ -53,6 +54,9 @@ def gemv_shape(seed):
 
 def gemm_shape(seed):
     rng = np.random.default_rng(2000 + seed)
+    if seed % 6 == 5:  # past 1024 tiles of 64 x 256: stage 2 on 128-row blocks, the last one ragged
+        B = int(rng.integers(1025, 1601))
+        return B, 32 * int(rng.integers(2, 13)), 32 * int(rng.integers(1, 5)), 64 * int(rng.integers(256, 301)), True
     B = int(rng.choice([int(rng.integers(1, 64)), int(rng.integers(64, 257)), int(rng.integers(257, 601))]))
     n = 32 * int(rng.integers(1, 100))
     m = 64 * int(rng.integers(1, 60))
