@@ -1415,12 +1415,19 @@ struct SbPlan {
     size_t part_bytes, lds_bytes;
 };
 
-// When the batched stage 1 replaces s1m_kernel (measured crossovers, see sb_kernel): from 16 batch
-// rows on rows of at least 256 words; at most 128 rows (8 batch tiles), and an LDS slice of at
-// most 160 KB per block. On narrower rows s1m_kernel with two or four row tiles per block is the
-// faster one (n = 4096, r = 1632, 64 / 128 rows: 8.9 / 13.4 us against 11.5 / 15.6).
-constexpr int kSbMinBatchWide = 16;
+// When the batched stage 1 replaces s1m_kernel (measured crossovers, see sb_kernel): on rows of at
+// least 256 words, from a batch that falls with the row width (sb_min_batch); at most 128 rows (8
+// batch tiles), and an LDS slice of at most 160 KB per block. On narrower rows s1m_kernel with two
+// or four row tiles per block is the faster one (n = 4096, r = 1632, 64 / 128 rows: 8.9 / 13.4 us
+// against 11.5 / 15.6).
 constexpr int kSbWideWords = 256;
+// The smallest batch that runs it, by words per row (same-box A/B of the GEMV op against the MFMA
+// stage 1, us): 512 words or more (Llama-3-70B down_proj, n = 28672, r = 3520 and 2912): from 3
+// rows (27.1 -> 22.5 at 3, 34.4 -> 24.7 at 8, 41.8 -> 28.0 at 12); 320-511 words (n = 11008): from
+// 8 (r = 1632: 15.0 -> 13.7 at 8, 17.2 -> 14.2 at 12, 5-6% slower at 3-6; r = 2976: 16.0 / 16.0
+// at 8, 19.4 -> 17.4 at 12); 256-319 words (n = 8192): from 16 (Llama-3-70B q/o at 12 rows
+// 17.6 -> 16.8, gate 25.0 / 25.2, both slower at 3-4). The batch-1 and batch-2 kernels stay.
+inline int64_t sb_min_batch(int64_t wpr) { return wpr >= 512 ? 3 : wpr >= 320 ? 8 : 16; }
 constexpr int kSbMaxBatch = 128;
 constexpr int kSbLdsBytes = 160 * 1024;
 constexpr int kSbMaxBlocks = 256;
@@ -1433,7 +1440,7 @@ constexpr int kSbMaxBlocks = 256;
 inline bool sb_plan_any(int64_t batch, int64_t rows, int64_t wpr, int64_t kpad, SbPlan& p);
 inline bool sb_plan(int64_t batch, int64_t rows, int64_t wpr, int64_t kpad, SbPlan& p) {
     if (batch > kSbMaxBatch || rows <= 0 || wpr <= 0) return false;
-    if (batch < kSbMinBatchWide || wpr < kSbWideWords) return false;
+    if (wpr < kSbWideWords || batch < sb_min_batch(wpr)) return false;
     return sb_plan_any(batch, rows, wpr, kpad, p);
 }
 // The search itself, for any batch up to kSbMaxBatch.
