@@ -104,8 +104,8 @@ int nq_permute_marlin_scales(const uint16_t* scale_in, uint16_t* scale_in_out, i
 
 /* Bytes of workspace nq_gemv needs: a header, the intermediate as bf16 hi/lo pairs and, for
  * batches whose stage 1 runs the batched k-split kernel (inputs of 8192 or more columns, n % 32 == 0,
- * up to 128 rows: from 16 rows, from 8 on 10240 or more columns, from 3 on 16384 or more), its
- * per-range fp32 sums. A workspace that holds the header and intermediate but not those sums is
+ * up to 128 rows: from 16 rows, from 8 on 10240 or more columns, from 3 on 16384, from 1 on more),
+ * its per-range fp32 sums. A workspace that holds the header and intermediate but not those sums is
  * accepted and runs the stage-1 kernels that keep none (results agree to rounding, not bit for
  * bit). */
 size_t nq_gemv_workspace_bytes(int64_t batch, int64_t n, int64_t r, int64_t m);

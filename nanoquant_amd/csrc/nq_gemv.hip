@@ -1421,13 +1421,16 @@ struct SbPlan {
 // or four row tiles per block is the faster one (n = 4096, r = 1632, 64 / 128 rows: 8.9 / 13.4 us
 // against 11.5 / 15.6).
 constexpr int kSbWideWords = 256;
-// The smallest batch that runs it, by words per row (same-box A/B of the GEMV op against the MFMA
-// stage 1, us): 512 words or more (Llama-3-70B down_proj, n = 28672, r = 3520 and 2912): from 3
-// rows (27.1 -> 22.5 at 3, 34.4 -> 24.7 at 8, 41.8 -> 28.0 at 12); 320-511 words (n = 11008): from
-// 8 (r = 1632: 15.0 -> 13.7 at 8, 17.2 -> 14.2 at 12, 5-6% slower at 3-6; r = 2976: 16.0 / 16.0
-// at 8, 19.4 -> 17.4 at 12); 256-319 words (n = 8192): from 16 (Llama-3-70B q/o at 12 rows
-// 17.6 -> 16.8, gate 25.0 / 25.2, both slower at 3-4). The batch-1 and batch-2 kernels stay.
-inline int64_t sb_min_batch(int64_t wpr) { return wpr >= 512 ? 3 : wpr >= 320 ? 8 : 16; }
+// The smallest batch that runs it, by words per row (same-box A/B of the GEMV op against the
+// kernels it replaces, us). Over 512 words the VALU stage 1 does not apply and the MFMA one runs
+// from one row: from 1 (Llama-3-70B down_proj, n = 28672, r = 3520: 25.7 / 25.9 / 27.3 / 34.4 /
+// 41.9 -> 22.2 / 22.3 / 22.6 / 24.8 / 28.1 at 1 / 2 / 3 / 8 / 12 rows; r = 2912 24.0 -> 20.3 at
+// 1; n = 20480, r = 2048: 18.7 -> 15.1 at 1). 512 words (n = 16384, r = 1632): from 3 (17.0 ->
+// 14.2; the VALU kernel at 1 / 2 rows 8.8 / 10.7 against 13.5 / 13.9). 320-511 words (n = 11008):
+// from 8 (r = 1632: 15.0 -> 13.7 at 8, 17.2 -> 14.2 at 12, 5-6% slower at 3-6; r = 2976: 16.0 /
+// 16.0 at 8, 19.4 -> 17.4 at 12). 256-319 words (n = 8192): from 16 (Llama-3-70B q/o at 12 rows
+// 17.6 -> 16.8, gate 25.0 / 25.2, both slower at 3-4).
+inline int64_t sb_min_batch(int64_t wpr) { return wpr > 512 ? 1 : wpr == 512 ? 3 : wpr >= 320 ? 8 : 16; }
 constexpr int kSbMaxBatch = 128;
 constexpr int kSbLdsBytes = 160 * 1024;
 constexpr int kSbMaxBlocks = 256;
