@@ -1422,15 +1422,20 @@ struct SbPlan {
 // against 11.5 / 15.6).
 constexpr int kSbWideWords = 256;
 // The smallest batch that runs it, by words per row (same-box A/B of the GEMV op against the
-// kernels it replaces, us). Over 512 words the VALU stage 1 does not apply and the MFMA one runs
-// from one row: from 1 (Llama-3-70B down_proj, n = 28672, r = 3520: 25.7 / 25.9 / 27.3 / 34.4 /
-// 41.9 -> 22.2 / 22.3 / 22.6 / 24.8 / 28.1 at 1 / 2 / 3 / 8 / 12 rows; r = 2912 24.0 -> 20.3 at
-// 1; n = 20480, r = 2048: 18.7 -> 15.1 at 1). 512 words (n = 16384, r = 1632): from 3 (17.0 ->
-// 14.2; the VALU kernel at 1 / 2 rows 8.8 / 10.7 against 13.5 / 13.9). 320-511 words (n = 11008):
+// kernels it replaces, us). Over 1024 words: from 1 (no VALU shape covers the row). 513-1024
+// words: from 2, where it replaced the MFMA stage 1 (Llama-3-70B down_proj, n = 28672, r = 3520:
+// 25.9 / 27.3 / 34.4 / 41.9 -> 22.3 / 22.6 / 24.8 / 28.1 at 2 / 3 / 8 / 12 rows; r = 2912 25.0
+// -> 20.8 at 2); one row runs the VALU kernel with four words per lane over four waves (r = 3520:
+// 25.7 with the MFMA kernel, 21.9 with this one, 17.5; r = 2912 24.0 / 20.0 / 14.8; n = 20480,
+// r = 2048: 18.7 / 14.7 / 11.0), which at two rows holds twice the operands and is slower (30.7).
+// 512 words (n = 16384, r = 1632): from 3 (17.0 -> 14.2; the VALU kernel at 1 / 2 rows 8.8 / 10.7
+// against 13.5 / 13.9). 320-511 words (n = 11008):
 // from 8 (r = 1632: 15.0 -> 13.7 at 8, 17.2 -> 14.2 at 12, 5-6% slower at 3-6; r = 2976: 16.0 /
 // 16.0 at 8, 19.4 -> 17.4 at 12). 256-319 words (n = 8192): from 16 (Llama-3-70B q/o at 12 rows
 // 17.6 -> 16.8, gate 25.0 / 25.2, both slower at 3-4).
-inline int64_t sb_min_batch(int64_t wpr) { return wpr > 512 ? 1 : wpr == 512 ? 3 : wpr >= 320 ? 8 : 16; }
+inline int64_t sb_min_batch(int64_t wpr) {
+    return wpr > 1024 ? 1 : wpr > 512 ? 2 : wpr == 512 ? 3 : wpr >= 320 ? 8 : 16;
+}
 constexpr int kSbMaxBatch = 128;
 constexpr int kSbLdsBytes = 160 * 1024;
 constexpr int kSbMaxBlocks = 256;
@@ -1523,7 +1528,7 @@ struct S1wShape {
 
 // The instantiated shapes (wpl, wr, r, g), and those also instantiated with x in LDS.
 #ifndef NQ_S1W_SHAPES
-#define NQ_S1W_SHAPES(X) X(1, 1, 2, 4) X(2, 1, 2, 4) X(1, 4, 4, 1) X(1, 6, 4, 2) X(2, 4, 4, 1)
+#define NQ_S1W_SHAPES(X) X(1, 1, 2, 4) X(2, 1, 2, 4) X(1, 4, 4, 1) X(1, 6, 4, 2) X(2, 4, 4, 1) X(4, 4, 4, 1)
 #endif
 #ifndef NQ_S1W_LDS_SHAPES
 #define NQ_S1W_LDS_SHAPES(X) X(2, 1, 2, 4) X(6, 1, 2, 4)
@@ -1535,7 +1540,8 @@ inline S1wShape s1w_shape(int wn, bool lds_ok) {
     if (wn <= 128) return {2, 1, 2, 4, lds_ok};
     if (wn <= 256) return {1, 4, 4, 1, false};
     if (wn <= 384) return lds_ok ? S1wShape{6, 1, 2, 4, true} : S1wShape{1, 6, 4, 2, false};
-    return {2, 4, 4, 1, false};
+    if (wn <= 512) return {2, 4, 4, 1, false};
+    return {4, 4, 4, 1, false};  // up to 1024 words, one batch row
 }
 
 // Bytes of dynamic LDS of the kLdsX stage 1: s_in and x, 16 * wn bytes each, in whole DMAs.
@@ -1579,7 +1585,7 @@ void launch_s1w_nb(const S1wShape& sh, const S1Table& tab, int blocks, const uin
 }
 
 // One launch over every item of `tab` (block ranges filled in here). The caller checked that
-// the fast stage 1 applies: n >= 8, n % 8 == 0, wn <= 512, x and each s_in 16-byte aligned,
+// the fast stage 1 applies: n >= 8, n % 8 == 0, wn <= 1024, x and each s_in 16-byte aligned,
 // every r > 0.
 template <typename T>
 void launch_s1w_table(S1Table& tab, const uint16_t* x, int batch, int n, int wn, bool norm, float eps,
@@ -1700,13 +1706,17 @@ void launch_stage1_table(S1Table& tab, const uint16_t* x, int batch, int n, int 
     int64_t v_words = 0;
     for (int k = 0; k < tab.count; ++k) v_words = std::max<int64_t>(v_words, static_cast<int64_t>(tab.item[k].r) * wn);
     const bool valu_rows = batch <= 2 || (batch <= 4 && wn <= 128 && v_words < 256 * 1024);
-    if ((!valu_rows || wn > 512) && s1m_fits(n, wn)) launch_s1m_table<T>(tab, x, batch, n, wn, norm, eps, st);
-    else launch_s1w_table<T>(tab, x, batch, n, wn, norm, eps, st);
+    // past 512 words the VALU shape covers one batch row (four words per lane)
+    if ((!valu_rows || wn > 1024 || (wn > 512 && batch > 1)) && s1m_fits(n, wn))
+        launch_s1m_table<T>(tab, x, batch, n, wn, norm, eps, st);
+    else
+        launch_s1w_table<T>(tab, x, batch, n, wn, norm, eps, st);
 }
 
-// The fast stage 1 (s1w up to 16384 columns, s1m up to 32768, by launch_stage1_table) applies.
+// The fast stage 1 (s1w up to 16384 columns, 32768 at one batch row; s1m up to 32768; chosen by
+// launch_stage1_table) applies.
 inline bool s1w_applies(const uint16_t* x, const uint16_t* s_in, int n, int wn, int r) {
-    return n >= 8 && n % 8 == 0 && r > 0 && aligned(x, 16) && aligned(s_in, 16) && (wn <= 512 || s1m_fits(n, wn));
+    return n >= 8 && n % 8 == 0 && r > 0 && aligned(x, 16) && aligned(s_in, 16) && (wn <= 1024 || s1m_fits(n, wn));
 }
 
 inline S1Item s1_item_of(const GemvArgs& a) {

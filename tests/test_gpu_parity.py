@@ -180,9 +180,10 @@ GEMV_CASES = [
     ("b32_n1000", 500, 1000, 96, 32, False),
     # the batched stage 1 (k split over blocks, then a finishing launch that adds the ranges in
     # order) runs on rows of 256 words or more: from 16 batch rows, from 8 on rows of 320 words or
-    # more, from 3 on rows of 512, from 1 on longer rows; a ragged rank and batch, one k range or
-    # several, 1, 2, 5 and 7 batch tiles. Narrower rows (64 words) at 64 and 100 rows, and each
-    # threshold's batch just below it, run the MFMA or VALU stage 1.
+    # more, from 3 on rows of 512, from 2 on rows of 513-1024 (whose one-row case runs the VALU
+    # kernel with four words per lane over four waves), from 1 on longer rows; a ragged rank and
+    # batch, one k range or several, 1, 2, 5 and 7 batch tiles. Narrower rows (64 words) at 64
+    # and 100 rows, and each threshold's batch just below it, run the MFMA or VALU stage 1.
     ("sb_b100", 2048, 2048, 512, 100, True),
     ("sb_b64_r200", 1000, 2048, 200, 64, True),
     ("sb_b70_wide", 600, 8192, 500, 70, True),
@@ -192,7 +193,9 @@ GEMV_CASES = [
     ("sb_b8_n11008", 1000, 11008, 200, 8, True),
     ("s1m_b7_n11008", 600, 11008, 150, 7, False),
     ("s1m_b12_n8192", 500, 8192, 256, 12, True),
-    ("sb_b1_n20000", 300, 20000, 333, 1, True),
+    ("s1w_b1_n20000", 300, 20000, 333, 1, True),
+    ("s1w_b1_n32768", 700, 32768, 500, 1, False),
+    ("sb_b1_n40000", 200, 40000, 96, 1, True),
     ("sb_b2_n28672", 1000, 28672, 160, 2, False),
     ("s1w_b2_n16384", 400, 16384, 200, 2, False),
     ("llama7b_gate_055_b64", 11008, 4096, 1632, 64, False),
