@@ -1431,10 +1431,16 @@ constexpr int kSbWideWords = 256;
 // 512 words (n = 16384, r = 1632): from 3 (17.0 -> 14.2; the VALU kernel at 1 / 2 rows 8.8 / 10.7
 // against 13.5 / 13.9). 320-511 words (n = 11008):
 // from 8 (r = 1632: 15.0 -> 13.7 at 8, 17.2 -> 14.2 at 12, 5-6% slower at 3-6; r = 2976: 16.0 /
-// 16.0 at 8, 19.4 -> 17.4 at 12). 256-319 words (n = 8192): from 16 (Llama-3-70B q/o at 12 rows
-// 17.6 -> 16.8, gate 25.0 / 25.2, both slower at 3-4).
-inline int64_t sb_min_batch(int64_t wpr) {
-    return wpr > 1024 ? 1 : wpr > 512 ? 2 : wpr == 512 ? 3 : wpr >= 320 ? 8 : 16;
+// 16.0 at 8, 19.4 -> 17.4 at 12). 256-319 words (n = 8192): from 8 when V is under 256 K words
+// (Llama-3-70B k/v, r = 512: 11.8 / 13.2 -> 11.1 / 11.2 at 8 / 12 rows; slower at 3-4, where the
+// VALU kernel runs), else from 16 (q/o at 8 / 12 rows 14.5 / 17.6 against 14.5 / 16.8, gate 23.4
+// / 25.0 against 24.5 / 25.1, both slower at 3-4).
+inline int64_t sb_min_batch(int64_t wpr, int64_t rows) {
+    if (wpr > 1024) return 1;
+    if (wpr > 512) return 2;
+    if (wpr == 512) return 3;
+    if (wpr >= 320) return 8;
+    return rows * wpr < 256 * 1024 ? 8 : 16;
 }
 constexpr int kSbMaxBatch = 128;
 constexpr int kSbLdsBytes = 160 * 1024;
@@ -1448,7 +1454,7 @@ constexpr int kSbMaxBlocks = 256;
 inline bool sb_plan_any(int64_t batch, int64_t rows, int64_t wpr, int64_t kpad, SbPlan& p);
 inline bool sb_plan(int64_t batch, int64_t rows, int64_t wpr, int64_t kpad, SbPlan& p) {
     if (batch > kSbMaxBatch || rows <= 0 || wpr <= 0) return false;
-    if (wpr < kSbWideWords || batch < sb_min_batch(wpr)) return false;
+    if (wpr < kSbWideWords || batch < sb_min_batch(wpr, rows)) return false;
     return sb_plan_any(batch, rows, wpr, kpad, p);
 }
 // The search itself, for any batch up to kSbMaxBatch.
@@ -1698,16 +1704,18 @@ void launch_s1m_table(S1Table& tab, const uint16_t* x, int batch, int n, int wn,
     else launch_s1m_nw<T, 16, 1>(tab, grid, x, batch, n, wn, norm, eps, st);
 }
 
-// Stage 1 of a table: the VALU kernel for one or two batch rows of up to 16384 columns (and for
-// three or four rows of up to 4096 columns when V holds fewer than 256 K words, two rows a pass:
-// 4096 x 1632 at 3 / 4 rows 5.7 / 5.8 -> 5.0 / 5.5 us; on wider rows, or from r = 2048, where the
-// second pass re-reads more of V, the MFMA kernel stays ahead), the MFMA kernel otherwise.
+// Stage 1 of a table: the VALU kernel for one or two batch rows of up to 16384 columns (32768 at
+// one row), and for three or four rows of up to 8192 columns when V holds fewer than 256 K words,
+// two rows a pass (4096 x 1632 at 3 / 4 rows 5.7 / 5.8 -> 5.0 / 5.5 us; the Llama-3-70B k/v GEMV,
+// 8192 x 512, 11.2 / 11.3 -> 7.5 / 7.6 us for the op); with more of V, where the second pass
+// re-reads more of it (r from 2048 at 4096 columns, Llama-3-70B q/o and gate at 8192), the MFMA
+// kernel stays ahead, and it runs otherwise.
 template <typename T>
 void launch_stage1_table(S1Table& tab, const uint16_t* x, int batch, int n, int wn, bool norm, float eps,
                          hipStream_t st) {
     int64_t v_words = 0;
     for (int k = 0; k < tab.count; ++k) v_words = std::max<int64_t>(v_words, static_cast<int64_t>(tab.item[k].r) * wn);
-    const bool valu_rows = batch <= 2 || (batch <= 4 && wn <= 128 && v_words < 256 * 1024);
+    const bool valu_rows = batch <= 2 || (batch <= 4 && wn <= 256 && v_words < 256 * 1024);
     // past 512 words the VALU shape covers one batch row (four words per lane)
     if ((!valu_rows || wn > 1024 || (wn > 512 && batch > 1)) && s1m_fits(n, wn))
         launch_s1m_table<T>(tab, x, batch, n, wn, norm, eps, st);

@@ -192,7 +192,10 @@ GEMV_CASES = [
     ("sb_b5_n20000_ragged", 300, 20000, 333, 5, False),
     ("sb_b8_n11008", 1000, 11008, 200, 8, True),
     ("s1m_b7_n11008", 600, 11008, 150, 7, False),
-    ("s1m_b12_n8192", 500, 8192, 256, 12, True),
+    ("s1m_b12_n8192", 500, 8192, 2048, 12, True),
+    ("sb_b8_n8192_small_v", 1024, 8192, 448, 8, False),
+    ("s1w_b4_n8192_small_v", 1024, 8192, 512, 4, True),
+    ("s1m_b4_n8192", 600, 8192, 1100, 4, False),
     ("s1w_b1_n20000", 300, 20000, 333, 1, True),
     ("s1w_b1_n32768", 700, 32768, 500, 1, False),
     ("sb_b1_n40000", 200, 40000, 96, 1, True),
