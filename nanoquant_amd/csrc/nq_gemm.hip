@@ -624,9 +624,11 @@ void launch_dm_split(const void* A, const uint32_t* W, const void* s_in, const v
 //     with K over two wave groups -> 105.2 us; K = 4096, N = 3072, 384 tiles: 64.3 -> 59.8 us);
 //   160-256 tiles: K split over two wave groups inside each block (B = 2048, K = 4096,
 //     N = 1792, 224 tiles: 46 -> 38 us against one block per tile; 256 tiles: 42.7 -> 40.3 us);
-//   fewer, with at most 32 even 64-k steps and 128+ tiles of 32 rows: 32-row tiles, K over two
+//   fewer, with at most 64 even 64-k steps and 128+ tiles of 32 rows: 32-row tiles, K over two
 //     wave groups (B = 256, K = 1280 -> 1120, N = 4096: 16.6 us split across the grid -> 9.1 us;
-//     B = 2048, K = 512, N = 1024: 8.8 -> 6.8 us);
+//     B = 2048, K = 512, N = 1024: 8.8 -> 6.8 us; up to 32 steps at first, then measured on the
+//     op at B = 256 with 36-56 steps: Llama-3-70B q/o 45.4 -> 41.0 us, down 93.4 -> 86.4,
+//     Llama-2-7B down at 1.0 bpw 53.9 -> 49.7);
 //   128-159 tiles otherwise: as 160-511;
 //   fewer: K split across the grid, each range at least 8 steps, fp32 sums into the caller's
 //     workspace, then a finishing launch. Up to 128 steps: about one block per CU, on 32-row tiles
@@ -657,7 +659,7 @@ GemmPlan plan_gemm(int64_t M, int64_t K, int64_t N) {
     if (tiles > 256) return p;
     if (even) p.mode = kModeGroups;
     if (tiles >= 160) return p;
-    if (even && steps <= 32 && tiles32 >= 128) {
+    if (even && steps <= 64 && tiles32 >= 128) {
         p.mode = kModeGroups32;
         return p;
     }

@@ -413,6 +413,9 @@ GEMM_CASES = [
     # small grids on 32-row tiles, the last one ragged (200 = 6 * 32 + 8): stage 1 splits K across the
     # grid (7 tiles, 8 ranges), stage 2 (4 steps, 224 tiles) splits it over two wave groups
     ("small_grid_ragged", 200, 4096, 256, 8192, True),
+    # 32-row tiles with K over two wave groups at 56 steps (stage 2 of a rank-3520 factorisation,
+    # 144 tiles of 32 rows, the last ragged: 260 = 8 * 32 + 4)
+    ("groups32_56_steps", 260, 512, 3520, 4096, False),
 ]
 
 
@@ -467,8 +470,9 @@ def test_gemm_onebit_scale_variants(nq, scales, K):
     assert err <= 1e-3, err
 
 
-@pytest.mark.parametrize("B,K,N", [(256, 4096, 1280), (100, 11008, 512), (1100, 4096, 1024)],
-                         ids=["b256_k4096_rows32", "b100_k11008_long_k", "b1100_k4096_rows64"])
+# 72 tiles of 64 rows with an odd 65 steps (so no split over wave groups) split on 64-row tiles
+@pytest.mark.parametrize("B,K,N", [(256, 4096, 1280), (100, 11008, 512), (1100, 4160, 1024)],
+                         ids=["b256_k4096_rows32", "b100_k11008_long_k", "b1100_k4160_rows64"])
 def test_gemm_split_k(nq, B, K, N):
     """Small grids split K across blocks (fp32 planes in the workspace the op allocates, added
     by a finishing launch); the same call through the C ABI without a workspace runs unsplit.
