@@ -1971,7 +1971,7 @@ inline bool s2t_applies(const void* z_hi, const void* z_lo, const uint32_t* u_bi
 // 38.7 / 13.1 at 128; down, 4096 rows: 4.0 / 5.3 at 16 and 5.0 / 5.5 at 32 stay with s2t, 9.1 / 6.05
 // at 64, 16.0 / 7.1 at 128). Every shape gives each wave one row tile against one to four column
 // tiles. Over 512 or more row tiles: 64-row blocks (WR = 4) of 16 batch rows up to 64 rows, 32
-// beyond, two-word chunks. Below: 32-row blocks (WR = 2) of 16 batch rows and four-word chunks up
+// beyond, two-word chunks (640-1023 tiles at 16 rows or fewer: as below 512). Below: 32-row blocks (WR = 2) of 16 batch rows and four-word chunks up
 // to 64 rows, 32 batch rows and two-word chunks beyond. Smaller chunks leave room in LDS for more
 // resident blocks, which is what these latency-bound blocks gain from.
 constexpr int64_t kS2bMinWork = 160 * 1024;
@@ -1992,6 +1992,10 @@ template <typename T>
 int launch_stage2_batched(const GemvArgs& a) {
     const int64_t tiles = ceil_div(a.m, 16);
     if (tiles >= 512) {
+        // 640-1023 row tiles (the 11008-row gate/up factors) at 16 rows or fewer: 32-row blocks with
+        // four-word chunks (same-box, r = 1632 / 2976: 14.52 / 18.67 -> 13.93 / 17.42 us per GEMV; at
+        // 1792 tiles, Llama-3-70B gate/up, they lose 12-25%, at 512 they tie, at 24 rows they lose)
+        if (tiles >= 640 && tiles < 1024 && a.batch <= 16) return launch_s2b_cfg<T, 2, 2, 1, 4>(a);
         if (a.batch <= 64) return launch_s2b_cfg<T, 4, 4, 2, 2>(a);
         return launch_s2b_cfg<T, 4, 4, 4, 2>(a);
     }
