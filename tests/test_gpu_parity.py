@@ -195,7 +195,8 @@ GEMV_CASES = [
     ("s1m_b12_n8192", 500, 8192, 2048, 12, True),
     ("sb_b8_n8192_small_v", 1024, 8192, 448, 8, False),
     ("s1w_b4_n8192_small_v", 1024, 8192, 512, 4, True),
-    ("s1m_b4_n8192", 600, 8192, 1100, 4, False),
+    ("s1m_b4_n8192", 600, 8192, 2600, 4, False),
+    ("s1w_b3_n8192_r2400", 500, 8192, 2400, 3, True),
     ("s1w_b1_n20000", 300, 20000, 333, 1, True),
     ("s1w_b1_n32768", 700, 32768, 500, 1, False),
     ("sb_b1_n40000", 200, 40000, 96, 1, True),
