@@ -1705,20 +1705,22 @@ void launch_s1m_table(S1Table& tab, const uint16_t* x, int batch, int n, int wn,
 }
 
 // Stage 1 of a table: the VALU kernel for one or two batch rows of up to 16384 columns (32768 at
-// one row), and for three or four rows of up to 8192 columns when V holds fewer than 256 K words or
-// the rank is at most 2496, two rows a pass (4096 x 1632 at 3 / 4 rows 5.7 / 5.8 -> 5.0 / 5.5 us;
-// the Llama-3-70B k/v GEMV, 8192 x 512, 11.2 / 11.3 -> 7.5 / 7.6 us for the op; same-box A/B of
-// the op at 3 / 4 rows: 8192 columns at r = 1792 / 2048 / 2240 / 2400 / 2496 8.4-10.5% / 6.6-9.6%
-// / 2.3-5% / 1.8-4.2% / 1.1-4.4% faster, 4096 columns at r = 2048 3.5-7.4% faster); past that
-// the second pass re-reads too much of V (4096 columns at r = 2560 / 2976: 4.6-10.4% / 3.8-8.5%
-// slower; 8192 at 3520: 6-10% slower) and the MFMA kernel runs, as it does otherwise.
+// one row), for three or four rows of up to 8192 columns when V holds fewer than 256 K words, two
+// rows a pass (4096 x 1632 at 3 / 4 rows 5.7 / 5.8 -> 5.0 / 5.5 us; the Llama-3-70B k/v GEMV, 8192
+// x 512, 11.2 / 11.3 -> 7.5 / 7.6 us for the op), and for three rows when the rank is at most 2496
+// (same-box A/B of the op: 8192 columns at r = 1792 / 2048 / 2240 / 2400 / 2496 10.5 / 9.6 / 2.8-5
+// / 3.1-4.9 / 4.4% faster, 4096 columns at r = 2048 4.6-7.4%; at four rows the gain holds with
+// s_mid, 1-2.8%, and turns into a 0.2-0.7% loss without it, so four rows keep the MFMA kernel);
+// past that the second pass re-reads too much of V (4096 columns at r = 2560 / 2976: 4.6 / 3.8%
+// slower at three rows; 8192 at 3520: 6%) and the MFMA kernel runs, as it does otherwise.
 template <typename T>
 void launch_stage1_table(S1Table& tab, const uint16_t* x, int batch, int n, int wn, bool norm, float eps,
                          hipStream_t st) {
     int r_max = 0;
     for (int k = 0; k < tab.count; ++k) r_max = std::max(r_max, tab.item[k].r);
     const int64_t v_words = static_cast<int64_t>(r_max) * wn;
-    const bool valu_rows = batch <= 2 || (batch <= 4 && wn <= 256 && (v_words < 256 * 1024 || r_max <= 2496));
+    const bool valu_rows = batch <= 2 || (batch <= 4 && wn <= 256 && v_words < 256 * 1024) ||
+                           (batch == 3 && wn <= 256 && r_max <= 2496);
     // past 512 words the VALU shape covers one batch row (four words per lane)
     if ((!valu_rows || wn > 1024 || (wn > 512 && batch > 1)) && s1m_fits(n, wn))
         launch_s1m_table<T>(tab, x, batch, n, wn, norm, eps, st);
