@@ -103,11 +103,14 @@ def rel(y, y64):
     return float(np.abs(y - y64).max() / np.abs(y64).max())
 
 
-@pytest.mark.parametrize("batch", [1, 2, 5, 18])  # VALU stage 1 for 1-2 rows, MFMA stage 1 from 3
-def test_group_norm_and_residual(lib, batch):
+# n = 512: VALU stage 1 for 1-2 rows, MFMA stage 1 from 3; n = 20000 (625-word rows): the VALU
+# shape with four words per lane over four waves at one row, the MFMA stage 1 from 2
+@pytest.mark.parametrize("n", [512, 20000])
+@pytest.mark.parametrize("batch", [1, 2, 5, 18])
+def test_group_norm_and_residual(lib, batch, n):
     from nanoquant_amd import _lib
-    announce("group norm + residual", batch)
-    n, m, r, eps = 512, 320, 160, 1e-5
+    announce("group norm + residual", batch, n)
+    m, r, eps = 320, 160, 1e-5
     c = make_linear(21, m, n, r, with_mid=True)
     rng = np.random.default_rng(5)
     x = (rng.normal(size=(batch, n)) * 3.0).astype(np.float16)
