@@ -4,10 +4,11 @@ A step is one decode GEMV (``torch.ops.binary_kernels.nanoquant_dyn_forward``: b
 of the Llama-2-7B down_proj shape at 0.55 bpw (m=4096, n=11008, r=1632; the 4096x11008
 0.55-bpw GEMV), batch 1, fp16, on a weight copy that differs from the previous step's: step i
 uses copy i mod ``--copies`` of a pool (128 copies, 394 MB) larger than the 256 MB Infinity
-Cache, so every step streams its weights from HBM. ``--warmup`` untimed steps, then exactly
-``--steps`` timed steps, each set recorded as one HIP graph and replayed; the timed replay is
-bracketed by device synchronisation and timed with HIP events on the replay stream (a spin
-kernel ahead of it keeps the GPU busy while the host enqueues, so no launch gap is timed).
+Cache, so every step streams its weights from HBM. One HIP graph holds ``--warmup`` untimed
+steps, a GPU wall-clock stamp (``nq_timestamp``), exactly ``--steps`` timed steps and a second
+stamp. The graph is replayed once untimed (its first dispatches), then once more behind a spin
+kernel, between device synchronisations; the time per step is the difference of the second
+replay's stamps divided by ``--steps``.
 
 The JSON line carries:
 * ``value``: packed bytes per GEMV / time per GEMV, GB/s (``ms_per_step`` the time);
@@ -17,6 +18,9 @@ The JSON line carries:
   bytes per GEMV from ``rocprofv3 --pmc`` runs on these kernels (``profiles/pmc_traffic.json``)
   when that file describes this workload, else null;
 * ``gemv``: the down and gate shapes at batch 1, each timed over 2048 steps at steady state;
+* ``floor``: what every decode-sized launch pays before any arithmetic, in the same 128-copy
+  graph rotation: an empty launch, a bare cold read of 1, 2 and 3 MB, and the GEMV's own two
+  reads (V's words, then U's) as two dependent launches with nothing else in them;
 * ``gemm``: the prefill GEMM (``marlin_nanoquant_forward``) at B=2048 on the gate and down
   shapes, TFLOP/s = 2*B*r*(n+m) / time against 2.5 PFLOP/s dense fp16;
 * ``pack``: sign packing, unpacking, reordering and Marlin packing of the down factors, GB/s of
@@ -30,7 +34,7 @@ The JSON line carries:
 * ``parity``: relative error of the GEMVs and GEMMs against the float64 oracle on the same
   inputs (the CPU leg; null with ``--skip-cpu``).
 
-``--sweep`` prints one line per config shape (GEMV at batch 1/4/16, GEMM at 256/2048);
+``--floor`` prints the ``floor`` section alone; ``--sweep`` prints one line per config shape (GEMV at batch 1/4/16, GEMM at 256/2048);
 ``--batch-sweep`` the GEMV and the GEMM at batch 1..256 on the 7B gate and down shapes.
 Multi-GPU runs are not part of this build: ``--gpus`` above 1 exits with a message.
 """
@@ -222,13 +226,16 @@ def bench_gemv_headline(args, dev):
         outs = timed_steps()
         stamp(1)
     torch.cuda.synchronize()
-    with torch.cuda.stream(stream):
-        torch.cuda._sleep(SPIN_CYCLES)
-        graph.replay()
-    torch.cuda.synchronize()
+    # the first replay (untimed) takes the graph's first dispatches; the second one is stamped
+    for _ in range(2):
+        with torch.cuda.stream(stream):
+            torch.cuda._sleep(SPIN_CYCLES)
+            graph.replay()
+        torch.cuda.synchronize()
     t0, t1 = stamps.tolist()
     ms = (t1 - t0) / lib.nq_wall_clock_hz() * 1e3 / args.steps
-    how = "GPU wall-clock stamps inside the graph, after the warm-up steps and after the timed steps"
+    how = ("GPU wall-clock stamps inside the graph, after the warm-up steps and after the timed steps, on the "
+           "graph's second replay")
     del graph
     graph_ok = bool(torch.equal(outs[0], y_first))
     del outs
@@ -259,6 +266,74 @@ def bench_gemv_shape(pool, dev, steps=2048):
             "total_bytes_gbs": round(gemv_total_bytes(m, n, r, pool.batch) / (ms * 1e-3) / 1e9, 2),
             "stage1": dict(kernel="s1w_kernel (V's sign words)", **kern(stage1_bytes(n, r), ms1)),
             "stage2": dict(kernel="s2t_kernel (U's sign words)", **kern(stage2_bytes(m, r), ms2))}
+
+
+FLOOR_READS_MB = (1, 2, 3)
+
+
+def bench_floor(dev, copies=128, replays=8):
+    """The fixed costs of a decode-sized launch, each as a graph of ``copies`` steps replayed at
+    steady state (``steady_ms``), reads rotating over ``copies`` distinct buffers (more bytes than
+    the 256 MB Infinity Cache holds, so every read comes from HBM):
+
+    * an empty launch of 1 x 64 and of 256 x 256 threads, and two dependent empty launches of the
+      GEMV's grids (204 and 256 blocks of 256 threads) per step;
+    * a bare cold read of 1, 2 and 3 MB over 256 blocks (one per CU), 16 bytes a lane, every load
+      issued first; the 2 MB read with one word stored per block; the same 2 MB read from one
+      buffer every step (L2 / Infinity Cache warm);
+    * the headline GEMV's reads alone: V's 2,245,632 bytes over 204 blocks, then U's 835,584 over
+      256 blocks, as two dependent launches (without and with a word stored per block), and all
+      3,081,216 bytes in one launch.
+    """
+    from nanoquant_amd import _lib
+    lib = _lib.load()
+    stream = torch.cuda.Stream(device=dev)
+    m, n, r = SHAPES[HEADLINE]
+    v_bytes, u_bytes = stage1_bytes(n, r), stage2_bytes(m, r)
+    per_copy = max(FLOOR_READS_MB[-1] << 20, v_bytes + u_bytes)
+    bufs = [torch.zeros(per_copy, dtype=torch.uint8, device=dev) for _ in range(copies)]
+    sink = torch.zeros(1 << 12, dtype=torch.int32, device=dev)
+    torch.cuda.synchronize()
+
+    def launches(parts, rotate=True):
+        # parts: (kind, byte offset, bytes or threads, blocks) launched in order in every step; kind
+        # "read" loads only, "read+store" also stores one word per block
+        def fn():
+            st = torch.cuda.current_stream().cuda_stream
+            for i in range(copies):
+                base = bufs[i if rotate else 0].data_ptr()
+                for kind, off, size, blocks in parts:
+                    if kind == "empty":
+                        _lib.check(lib.nq_probe_empty(blocks, size, st), "probe empty")
+                    else:
+                        _lib.check(lib.nq_probe_read(base + off, size, blocks, sink.data_ptr(),
+                                                     int(kind == "read+store"), st), "probe read")
+        return fn
+
+    two = [("read", 0, v_bytes, 204), ("read", v_bytes, u_bytes, 256)]
+    cases = [("empty_1x64", [("empty", 0, 64, 1)], True),
+             ("empty_256x256", [("empty", 0, 256, 256)], True),
+             ("two_dependent_empty_204_256", [("empty", 0, 256, 204), ("empty", 0, 256, 256)], True)]
+    cases += [(f"read_{mb}MB_cold_256_blocks", [("read", 0, mb << 20, 256)], True) for mb in FLOOR_READS_MB]
+    cases += [("read_2MB_cold_256_blocks_store", [("read+store", 0, 2 << 20, 256)], True),
+              ("read_2MB_warm_256_blocks", [("read", 0, 2 << 20, 256)], False),
+              ("gemv_reads_two_launches", two, True),
+              ("gemv_reads_two_launches_store", [("read+store",) + p[1:] for p in two], True),
+              ("gemv_reads_one_launch", [("read", 0, v_bytes + u_bytes, 256)], True)]
+    out = {}
+    for name, parts, rotate in cases:
+        ms, g, _ = steady_ms(launches(parts, rotate), copies, stream, replays)
+        del g
+        read = sum(p[2] for p in parts if p[0] != "empty")
+        out[name] = {"us": round(ms * 1e3, 4), "launches": len(parts)}
+        if read:
+            out[name].update(bytes=read, gbs=round(read / (ms * 1e-3) / 1e9, 2),
+                             frac_hbm=round(read / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
+        log(f"[bench] floor {name}: {out[name]}")
+    del bufs
+    torch.cuda.empty_cache()
+    return {"method": f"graph of {copies} steps, {replays} timed replays after 2 warm ones, GPU events around them; "
+                      "reads rotate over distinct buffers unless marked warm", "cases": out}
 
 
 def bench_gemm(name, args, dev):
@@ -383,9 +458,17 @@ def cpu_baseline(args):
     med_u, reps_u = _median_time(lambda: O.unpack_signs_torch(words, tuple(V.shape), "lsb_first"),
                                  args.cpu_pack_seconds)
     nbytes = V.numel() + 4 * words.numel()
+    # the Marlin packer on the shape the GPU pack leg times: V^T padded to [r_pad, n]
+    r_pad = -(-r // 256) * 256
+    W = torch.from_numpy(np.where(np.random.default_rng(7).random((r_pad, n)) < 0.5, -1, 1).astype(np.int8))
+    med_m, reps_m = _median_time(lambda: O.pack_marlin_torch(W), args.cpu_pack_seconds)
+    mbytes = W.numel() + 4 * (n // 16) * (r_pad // 2)
     pack = {"pack_signs": {"us": round(med_p * 1e6, 1), "gbs": round(nbytes / med_p / 1e9, 3), "reps": reps_p},
             "unpack_signs": {"us": round(med_u * 1e6, 1), "gbs": round(nbytes / med_u / 1e9, 3), "reps": reps_u},
-            "sample": f"eager-torch restatement of kernel/utils.py:51-183 on V [{r}, {n}] int8, lsb_first"}
+            "pack_marlin": {"us": round(med_m * 1e6, 1), "gbs": round(mbytes / med_m / 1e9, 3), "reps": reps_m,
+                            "what": f"int8 V^T [{r_pad}, {n}] -> Marlin words (kernel/utils.py:186-205)"},
+            "sample": f"eager-torch restatements of kernel/utils.py:51-205 on V [{r}, {n}] int8 (lsb_first) and "
+                      f"V^T [{r_pad}, {n}] (Marlin), {args.cpu_pack_seconds:.0f} s bounded sample each"}
     bf = per["bfloat16"]
     return {"value": bf["packed_gbs"], "unit": "GB/s", "cores": cores, "kind": "port",
             "sample": (f"oracle compute_forward_torch (reference dense path, linear.py:282-291), bf16, B=1, m={m} "
@@ -661,6 +744,8 @@ def main():
     ap.add_argument("--e2e-prompt", type=int, default=128)
     ap.add_argument("--e2e-new", type=int, default=256)
     ap.add_argument("--e2e-steps-per-graph", type=int, default=15)
+    ap.add_argument("--floor", action="store_true",
+                    help="measure only the launch and cold-read floor of decode-sized kernels and print it")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="also run one device copy of this many MiB (PMC byte-counter calibration)")
     args = ap.parse_args()
@@ -687,6 +772,9 @@ def main():
         return 0
     if args.batch_sweep:  # the hand-over between the GEMV and the GEMM, one JSON line each
         run_batch_sweep(args, dev)
+        return 0
+    if args.floor:  # the launch and cold-read floor alone
+        print(json.dumps({"floor": bench_floor(dev)}), flush=True)
         return 0
     if args.decode_only:  # profiling aid: only the end-to-end decode, reported on its own line
         log(f"[bench] decode e2e B={args.e2e_batch} prompt={args.e2e_prompt} new={args.e2e_new}")
@@ -721,6 +809,9 @@ def main():
 
     if args.calib_copy_mib > 0:
         calibration_copy(dev, args.calib_copy_mib)
+
+    log("[bench] floor")
+    floor = bench_floor(dev)
 
     gemm = None
     if not args.skip_gemm:
@@ -780,6 +871,7 @@ def main():
                      "algorithmic_bytes": pb, "us_per_op": round(ms * 1e3, 4),
                      "kernels": {"stage1": head["stage1"], "stage2": head["stage2"]}},
         "gemv": shapes,
+        "floor": floor,
         "gemm": gemm,
         "pack": pack,
         "decode_e2e": decode,

@@ -103,11 +103,13 @@ int nq_permute_marlin_scales(const uint16_t* scale_in, uint16_t* scale_in_out, i
 /* ---------------------------------------------------------------- decode GEMV */
 
 /* Bytes of workspace nq_gemv needs: a header, the intermediate as bf16 hi/lo pairs and, for
- * batches whose stage 1 runs the batched k-split kernel (inputs of 8192 or more columns, n % 32 == 0,
- * up to 128 rows: from 16 rows, from 8 on 10240 or more columns, from 3 on 16384, from 1 on more),
- * its per-range fp32 sums. A workspace that holds the header and intermediate but not those sums is
- * accepted and runs the stage-1 kernels that keep none (results agree to rounding, not bit for
- * bit). */
+ * batches whose stage 1 runs the batched k-split kernel, its per-range fp32 sums. That kernel runs
+ * on rows of 256 or more words (n >= 8161), n % 32 == 0, up to 128 batch rows, from a batch set by
+ * the words per row w = n / 32: w > 1024 from 1 row; 513 <= w <= 1024 from 2; w = 512 from 3;
+ * 320 <= w <= 511 from 8; 256 <= w <= 319 from 8 when V holds fewer than 256 K words (r * w),
+ * else from 16. This function is the authority: size workspaces from it, not from this list. A
+ * workspace that holds the header and intermediate but not those sums is accepted and runs the
+ * stage-1 kernels that keep none (results agree to rounding, not bit for bit). */
 size_t nq_gemv_workspace_bytes(int64_t batch, int64_t n, int64_t r, int64_t m);
 
 /* y[b, :] = sat(s_out * (U * ((V * (s_in * x[b, :])) * s_mid)))  for b < batch.
@@ -269,6 +271,17 @@ int nq_attention_decode(int dtype, const void* q, const void* k, const void* v, 
 int nq_timestamp(uint64_t* dst, nq_stream_t stream);
 /* Ticks per second of that clock on the current device (0 on error). */
 int64_t nq_wall_clock_hz(void);
+
+/* Latency-floor probes (no counterpart in the reference; benchmarking aids). nq_probe_empty
+ * enqueues a kernel of `blocks` x `threads` that does nothing: the fixed cost of one launch.
+ * nq_probe_read streams `bytes` (a multiple of 16, 16-byte aligned, below 2 GiB) from `src` in
+ * `blocks` (1 .. 2^20) equal contiguous runs of at most 64 KB, 16 bytes a lane, every load of a
+ * lane issued before the first use: the cost of one cold read of that size with nothing else to
+ * do. `sink` (device, `blocks` words) receives one word per block (the xor of the first wave's
+ * data) when `store` is nonzero; otherwise it is written only when a block's xor of its data
+ * equals a fixed constant, so the launch pays for no store. */
+int nq_probe_empty(int64_t blocks, int64_t threads, nq_stream_t stream);
+int nq_probe_read(const void* src, int64_t bytes, int64_t blocks, uint32_t* sink, int store, nq_stream_t stream);
 
 #ifdef __cplusplus
 }

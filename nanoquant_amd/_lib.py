@@ -80,6 +80,8 @@ SIGNATURES = {
                                  _vp]),
     "nq_timestamp": (_int, [_vp, _vp]),
     "nq_wall_clock_hz": (_i64, []),
+    "nq_probe_empty": (_int, [_i64, _i64, _vp]),
+    "nq_probe_read": (_int, [_vp, _i64, _i64, _vp, _int, _vp]),
 }
 
 

@@ -62,9 +62,13 @@ __host__ __device__ inline uint32_t div_magic(uint32_t d) {
 // (Llama-3-70B, 4 batch rows: q/o 12.7 -> 12.2 us, k/v 11.05 -> 10.55, mixed-rank gate 30.3 ->
 // 26.9). On 128-word rows the padded staging measured 6% slower at 16 batch rows, and rows whose
 // stride does not share banks gain nothing from it; both keep wn. (Four row tiles of padded wide
-// rows do not fit the staging buffer.)
+// rows do not fit the staging buffer; rows whose padded tile would not fit keep wn, so that the
+// MFMA kernel still takes them: 1024-word rows at one row tile, 512-word rows at two.)
+// s1m_kernel stages up to kS1mMaxStaged dwords in LDS: 16 rows of sign words per row tile, and the
+// s_in pairs when they fit too (64 KB, 16 dwords per thread of a 1024-thread block).
+constexpr int kS1mMaxStaged = 16 * 16 * 64;
 __host__ __device__ inline int s1m_row_stride(int wn, int rt = 1) {
-    return rt <= 2 && wn % 64 == 0 && wn >= 256 ? (wn | 1) : wn;
+    return rt <= 2 && wn % 64 == 0 && wn >= 256 && 16 * rt * (wn | 1) <= kS1mMaxStaged ? (wn | 1) : wn;
 }
 
 // Bit of element e (0..31) of a half2 word.
@@ -295,15 +299,9 @@ __device__ inline Item pick_item(const Table& tab) {
 // kNorm folds an RMSNorm of x into the stage: every group also sums x^2 over the whole row
 // (the lanes hold all of x anyway) and h is multiplied by rsqrt(sum / n + eps); the norm's
 // weight is expected inside s_in.
-//
-// kLdsX (one batch row, n % 32 == 0): s_in and x reach LDS by DMA once per block and every lane
-// reads its pairs from there, instead of each row group fetching all of both through the vector
-// cache. Chunk v (16 bytes) of word q of each array sits at slot 4q + (v ^ ((q / 4) % 4)), so the
-// 16 lanes of a quarter-wave, reading chunk v of 16 consecutive words, hit 16 distinct slots mod 16.
-template <typename T, int NB, int WPL, int WR, int R, int G, bool kNorm, bool kOne, bool kLdsX = false>
+template <typename T, int NB, int WPL, int WR, int R, int G, bool kNorm, bool kOne>
 __global__ __launch_bounds__(G * WR * 64) void s1w_kernel(const S1Table tab, const uint16_t* __restrict__ x, int batch,
                                                           int n, int wn, float eps) {
-    static_assert(!kLdsX || NB == 1, "the LDS copy of x holds one batch row");
     constexpr int kGroups = G;
     constexpr int kRows = kGroups * R;
     constexpr int kPartRows = R + (kNorm ? 1 : 0);
@@ -349,67 +347,29 @@ __global__ __launch_bounds__(G * WR * 64) void s1w_kernel(const S1Table tab, con
                 vb[k][w] = load_b32_stream(v_rs, q < wn ? off : v_end);
             }
     };
-    if constexpr (kLdsX) {
-        // V's words first (from HBM), then the DMA of s_in and x (from L2): chunk slot l of array
-        // a = l / (4 wn) holds chunk v = (l % 4) ^ ((q / 4) % 4) of word q = (l % (4 wn)) / 4
-        extern __shared__ __attribute__((aligned(16))) uint32_t sx[];
-        load_v();
-        const int per = 4 * wn;  // chunks per array
-        for (int l0 = __builtin_amdgcn_readfirstlane(t >> 6) * 64; l0 < 2 * per; l0 += G * WR * 64) {
-            const int l = min(l0 + lane, 2 * per - 1);
-            const int arr = l >= per ? 1 : 0;
-            const int lq = l - arr * per;
-            const int q = lq >> 2;
-            const int v = (lq & 3) ^ ((q >> 2) & 3);
-            dma16((arr ? x : it.s_in) + 32 * q + 8 * v, sx + 4 * l0);
-        }
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
+    // s_in and x first (from L2), then V's words (from HBM), each in 16- and 4-byte pieces
 #pragma unroll
-        for (int w = 0; w < WPL; ++w) {
-            const int q = p + 64 * WR * w;
-            const int qc = min(q, wn - 1);
+    for (int w = 0; w < WPL; ++w)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int slot = 4 * qc + (v ^ ((qc >> 2) & 3));
-                const u32x4 sv = *reinterpret_cast<const u32x4*>(sx + 4 * slot);
-                const u32x4 xv = *reinterpret_cast<const u32x4*>(sx + 4 * (per + slot));
-                const bool ok = q < wn;  // a lane past the row multiplies zeros
-                sp[w][4 * v + 0] = ok ? sv.x : 0u;
-                sp[w][4 * v + 1] = ok ? sv.y : 0u;
-                sp[w][4 * v + 2] = ok ? sv.z : 0u;
-                sp[w][4 * v + 3] = ok ? sv.w : 0u;
-                xp[w][0][4 * v + 0] = xv.x;
-                xp[w][0][4 * v + 1] = xv.y;
-                xp[w][0][4 * v + 2] = xv.z;
-                xp[w][0][4 * v + 3] = xv.w;
+        for (int v = 0; v < 4; ++v) {
+            const uint32_t off = (32u * static_cast<uint32_t>(p + 64 * WR * w) + 8u * v) * 2u;
+            const u32x4 sv = load_b128(s_rs, off);
+            sp[w][4 * v + 0] = sv.x;
+            sp[w][4 * v + 1] = sv.y;
+            sp[w][4 * v + 2] = sv.z;
+            sp[w][4 * v + 3] = sv.w;
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const u32x4 xv = load_b128(x_rs[b], off);
+                xp[w][b][4 * v + 0] = xv.x;
+                xp[w][b][4 * v + 1] = xv.y;
+                xp[w][b][4 * v + 2] = xv.z;
+                xp[w][b][4 * v + 3] = xv.w;
             }
         }
-    } else {
-        // s_in and x first (from L2), then V's words (from HBM), each in 16- and 4-byte pieces
-#pragma unroll
-        for (int w = 0; w < WPL; ++w)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const uint32_t off = (32u * static_cast<uint32_t>(p + 64 * WR * w) + 8u * v) * 2u;
-                const u32x4 sv = load_b128(s_rs, off);
-                sp[w][4 * v + 0] = sv.x;
-                sp[w][4 * v + 1] = sv.y;
-                sp[w][4 * v + 2] = sv.z;
-                sp[w][4 * v + 3] = sv.w;
-#pragma unroll
-                for (int b = 0; b < NB; ++b) {
-                    const u32x4 xv = load_b128(x_rs[b], off);
-                    xp[w][b][4 * v + 0] = xv.x;
-                    xp[w][b][4 * v + 1] = xv.y;
-                    xp[w][b][4 * v + 2] = xv.z;
-                    xp[w][b][4 * v + 3] = xv.w;
-                }
-            }
-        __builtin_amdgcn_sched_barrier(0);
-        load_v();
-        __builtin_amdgcn_sched_barrier(0);
-    }
+    __builtin_amdgcn_sched_barrier(0);
+    load_v();
+    __builtin_amdgcn_sched_barrier(0);
 
     NQ_STAMP(1);
     // Even and odd pairs accumulate separately and rows are innermost, so consecutive dot2
@@ -500,6 +460,158 @@ __global__ __launch_bounds__(G * WR * 64) void s1w_kernel(const S1Table tab, con
         }
     }
     if (static_cast<int>(blockIdx.x) == it.block_begin) zero_h_pad(it.z_hi, it.z_lo, it.zpitch, it.kpad, b0, NB, batch);
+    NQ_STAMP(3);
+}
+
+// --------------------------------------------------------------------------- stage 1, one batch row
+//
+// s1l_kernel: one batch row, n % 32 == 0, rows of up to 384 words. Block = G groups of WR waves;
+// group gi owns rows j0 .. j0+R-1 (R even), lane p = (wave % WR) * 64 + lane of a group holds words
+// q = p + 64 WR w (w < WPL) of those rows, so a row's words are split over the group's WR waves.
+//
+// Order of the memory work: V's words first (HBM, the long wait), then one DMA of the item's s_in
+// and of x into LDS (L2), then the block waits for all of it. In LDS, word q of the two arrays takes
+// nine 16-byte slots from 9 q: s_in pieces 0..3 (elements 32 q + 8 v .. +7), x pieces 0..3, one pad.
+// A quarter wave reads piece v of 16 consecutive words at a 144-byte stride, which lands in 16
+// distinct slots mod 16 (no bank conflict), and each piece is an immediate offset from the word's
+// slot. Lanes past the row read a zero word placed after the DMA region (zslot), so their products
+// are zero; their loads of V run into the next row or past the array (zeros) and need no clamp.
+//
+// The arithmetic takes two rows per shift: the rows' words as one 64-bit value shifted left by the
+// pair index put each row's pair signs on bits 15 and 31 of its half (the bits the shift carries
+// from the low word into the high one land below bit 15 - p and are masked off). One v_bitop3 per
+// row xors them onto the s_in pair and v_dot2 adds the two exact products in fp32: 2.5 VALU per
+// pair and row instead of 3. The LDS reads of word w + 1 are issued before word w's arithmetic.
+//
+// kNorm: group 0 also sums x^2 over the words it holds, and h is scaled by rsqrt(sum / n + eps).
+// Measured against the VALU kernel with x in LDS (same rotation of 128 weight copies, us per
+// launch): n = 11008, r = 1632: 4.53 -> 3.86; n = 4096, r = 1632 / 1120: 2.92 / 2.87 -> 2.67 / 2.62;
+// n = 8192, r = 2240 / 512: 4.51 / 3.12 -> 4.26 / 2.81.
+constexpr int kS1lMaxWords = 384;
+
+// LDS slot (16 bytes) of the zero word, and the dynamic LDS bytes, of s1l_kernel at wn words.
+__host__ __device__ inline int s1l_zero_slot(int wn) { return (9 * wn + 63) / 64 * 64; }
+inline size_t s1l_lds_bytes(int wn) { return static_cast<size_t>(s1l_zero_slot(wn) + 9) * 16; }
+
+template <typename T, int WPL, int R, int G, int WR, bool kNorm, bool kOne>
+__global__ __launch_bounds__(G * WR * 64) void s1l_kernel(const S1Table tab, const uint16_t* __restrict__ x, int n,
+                                                          int wn, float eps) {
+    static_assert(R % 2 == 0, "rows go in pairs");
+    extern __shared__ __attribute__((aligned(16))) uint32_t sx[];
+    __shared__ float part[(G * R + 1) * WR];
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int grp = wave / WR, h = wave % WR;
+    const S1Item it = kOne ? tab.item[0] : pick_item<S1Item>(tab);
+    const int r = it.r;
+    const int j0 = (static_cast<int>(blockIdx.x) - it.block_begin) * (G * R) + grp * R;
+    const int zslot = s1l_zero_slot(wn);
+    NQ_STAMP(0);
+
+    // V's words of this wave's rows
+    const rsrc_t v_rs = make_rsrc(it.v_bits, static_cast<uint32_t>(r) * static_cast<uint32_t>(wn) * 4u);
+    uint32_t vb[WPL][R];
+#pragma unroll
+    for (int w = 0; w < WPL; ++w)
+#pragma unroll
+        for (int k = 0; k < R; ++k)
+            vb[w][k] = load_b32_stream(v_rs, (static_cast<uint32_t>(j0 + k) * static_cast<uint32_t>(wn) +
+                                              static_cast<uint32_t>(h * 64 + lane + 64 * WR * w)) * 4u);
+    uint16_t mid[R];
+    const uint16_t* msrc = it.s_mid != nullptr ? it.s_mid : it.s_in;
+    const int mlim = (it.s_mid != nullptr ? r : n) - 1;
+#pragma unroll
+    for (int k = 0; k < R; ++k) mid[k] = msrc[min(j0 + k, mlim)];
+    // the DMA of s_in and x: slot l = 9 q + v (each wave's lanes fill 64 consecutive slots; the
+    // last round's lanes past the region repeat its last piece into slots below zslot)
+    const int slots = 9 * wn;
+    const uint32_t magic9 = div_magic(9);
+    for (int l0 = wave * 64; l0 < slots; l0 += G * WR * 64) {
+        const int l = min(l0 + lane, slots - 1);
+        const int q = static_cast<int>(__umulhi(static_cast<uint32_t>(l), magic9));
+        const int v = l - 9 * q;
+        const uint16_t* src = v < 4 ? it.s_in + 32 * q + 8 * v : (v < 8 ? x + 32 * q + 8 * (v - 4) : x + 32 * q);
+        dma16(src, sx + 4 * l0);
+    }
+    if (t < 36) sx[4 * zslot + t] = 0u;
+    wait_vmcnt<0>();
+    barrier_keep_dma();
+    NQ_STAMP(1);
+
+    const uint32_t mask = kSignPair;
+    float acc[2][R];
+#pragma unroll
+    for (int k = 0; k < R; ++k) acc[0][k] = acc[1][k] = 0.0f;
+    float ss[2] = {0.0f, 0.0f};
+    u32x4 cur[8], nxt[8];
+    auto fetch = [&](u32x4* d, int w) {
+        const int q = h * 64 + lane + 64 * WR * w;
+        const u32x4* p = reinterpret_cast<const u32x4*>(sx) + (q < wn ? 9 * q : zslot);
+#pragma unroll
+        for (int v = 0; v < 8; ++v) d[v] = p[v];
+    };
+    fetch(cur, 0);
+#pragma unroll
+    for (int w = 0; w < WPL; ++w) {
+        if (w + 1 < WPL) fetch(nxt, w + 1);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int pp = 0; pp < 16; ++pp) {
+            const uint32_t s = cur[pp >> 2][pp & 3], xv = cur[4 + (pp >> 2)][pp & 3];
+#pragma unroll
+            for (int k = 0; k < R; k += 2) {
+                const uint64_t sh = ((static_cast<uint64_t>(vb[w][k + 1]) << 32) | vb[w][k]) << pp;
+                const uint32_t a0 = (static_cast<uint32_t>(sh) & mask) ^ s;
+                const uint32_t a1 = (static_cast<uint32_t>(sh >> 32) & mask) ^ s;
+                acc[pp & 1][k] = T::dot2(a0, xv, acc[pp & 1][k]);
+                acc[pp & 1][k + 1] = T::dot2(a1, xv, acc[pp & 1][k + 1]);
+            }
+            if (kNorm && grp == 0) ss[pp & 1] = T::dot2(xv, xv, ss[pp & 1]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int v = 0; v < 8; ++v) cur[v] = nxt[v];
+    }
+    NQ_STAMP(2);
+
+    if (WR == 1 && !kNorm) {
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+            const int j = j0 + k;
+            const float v = wave_sum_dpp(acc[0][k] + acc[1][k]);
+            const float mf = it.s_mid != nullptr ? T::to_float(mid[k]) : 1.0f;
+            if (lane == 0 && j < it.kpad) store_h(it.z_hi, it.z_lo, it.zpitch, 0, j, j < r ? v * mf : 0.0f);
+        }
+    } else {
+        // the waves' row sums (and group 0's x^2 sums, row G R) through LDS
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+            const float v = wave_sum_dpp(acc[0][k] + acc[1][k]);
+            if (lane == 0) part[(grp * R + k) * WR + h] = v;
+        }
+        if (kNorm && grp == 0) {
+            const float v = wave_sum_dpp(ss[0] + ss[1]);
+            if (lane == 0) part[G * R * WR + h] = v;
+        }
+        __syncthreads();
+        if (h == 0 && lane < R) {
+            const int j = j0 + lane;
+            float v = 0.0f, sq = 0.0f;
+#pragma unroll
+            for (int s2 = 0; s2 < WR; ++s2) {
+                v += part[(grp * R + lane) * WR + s2];
+                if (kNorm) sq += part[G * R * WR + s2];
+            }
+            if (kNorm) v *= rsqrtf(sq / static_cast<float>(n) + eps);
+            uint16_t mk = mid[0];
+#pragma unroll
+            for (int k = 1; k < R; ++k) mk = lane == k ? mid[k] : mk;
+            const float mf = it.s_mid != nullptr ? T::to_float(mk) : 1.0f;
+            if (j < it.kpad) store_h(it.z_hi, it.z_lo, it.zpitch, 0, j, j < r ? v * mf : 0.0f);
+        }
+    }
+    if (static_cast<int>(blockIdx.x) == it.block_begin) zero_h_pad(it.z_hi, it.z_lo, it.zpitch, it.kpad, 0, 1, 1);
     NQ_STAMP(3);
 }
 
@@ -1517,60 +1629,37 @@ void launch_stage2_generic(const GemvArgs& a) {
                                                              a.plan.wr, a.plan.zpitch);
 }
 
-// Launch shapes of the VALU stage 1, measured on MI355X (graph-replayed, 64-128 rotating weight
-// copies, batch 1, stage 1 alone): n = 4096 (r = 1632) 2.96 us with x and s_in in LDS, two words
-// per lane, one wave and two rows per group, four groups (3.13 with the same shape reading x from
-// the vector cache, 3.05-3.74 for the other splits); n = 8192 4.49 us at r = 2240 with one word per
-// lane over four waves, four rows (4.58-4.74 with x in LDS); n = 11008 4.54 us with x in LDS, six
-// words per lane over one wave per row (no cross-wave sum), two rows per group, four groups (4.64
-// for the best shape without LDS: one word per lane over six waves, four rows, two groups).
-// Launch shape of s1w_kernel: WPL words per lane, WR waves per row group, R rows per group, G
-// groups per block (G * WR * 64 threads, R * G rows), x and s_in from LDS or not. The lanes of a
-// group cover 64 * WR * WPL >= wn words of a row.
+// Launch shapes of s1w_kernel, which runs at two batch rows, on rows of 385-1024 words, and on
+// rows that are not whole words (s1l_kernel takes one batch row otherwise), measured on MI355X
+// (graph-replayed, 64-128 rotating weight copies, stage 1 alone): n = 8192 4.49 us at r = 2240 with
+// one word per lane over four waves, four rows; n = 11008 4.64 us with one word per lane over six
+// waves, four rows, two groups. WPL words per lane, WR waves per row group, R rows per group, G
+// groups per block (G * WR * 64 threads, R * G rows). The lanes of a group cover 64 * WR * WPL >= wn
+// words of a row.
 struct S1wShape {
     int wpl, wr, r, g;
-    bool lds;
 };
 
-// The instantiated shapes (wpl, wr, r, g), and those also instantiated with x in LDS.
+// The instantiated shapes (wpl, wr, r, g).
 #ifndef NQ_S1W_SHAPES
 #define NQ_S1W_SHAPES(X) X(1, 1, 2, 4) X(2, 1, 2, 4) X(1, 4, 4, 1) X(1, 6, 4, 2) X(2, 4, 4, 1) X(4, 4, 4, 1)
 #endif
-#ifndef NQ_S1W_LDS_SHAPES
-#define NQ_S1W_LDS_SHAPES(X) X(2, 1, 2, 4) X(6, 1, 2, 4)
-#endif
 
-// lds_ok: one item, one batch row, n % 32 == 0 (the LDS copy of x and s_in, 32 * wn bytes, fits).
-inline S1wShape s1w_shape(int wn, bool lds_ok) {
-    if (wn <= 64) return {1, 1, 2, 4, false};
-    if (wn <= 128) return {2, 1, 2, 4, lds_ok};
-    if (wn <= 256) return {1, 4, 4, 1, false};
-    if (wn <= 384) return lds_ok ? S1wShape{6, 1, 2, 4, true} : S1wShape{1, 6, 4, 2, false};
-    if (wn <= 512) return {2, 4, 4, 1, false};
+inline S1wShape s1w_shape(int wn) {
+    if (wn <= 64) return {1, 1, 2, 4};
+    if (wn <= 128) return {2, 1, 2, 4};
+    if (wn <= 256) return {1, 4, 4, 1};
+    if (wn <= 384) return {1, 6, 4, 2};
+    if (wn <= 512) return {2, 4, 4, 1};
     // up to 1024 words, one batch row (x and s_in staged in LDS instead, 16 rows per block, measured
     // slower: Llama-3-70B down_proj 19.6 against 17.6 us, its mixed-rank draw 18.3 against 14.9)
-    return {4, 4, 4, 1, false};
+    return {4, 4, 4, 1};
 }
-
-// Bytes of dynamic LDS of the kLdsX stage 1: s_in and x, 16 * wn bytes each, in whole DMAs.
-inline size_t s1w_lds_bytes(int wn) { return static_cast<size_t>((8 * wn + 63) / 64 * 64) * 16; }
 
 template <typename T, int NB, bool kNorm, bool kOne>
 void launch_s1w_cfg(const S1wShape& sh, const S1Table& tab, int blocks, const uint16_t* x, int batch, int n, int wn,
                     float eps, hipStream_t st) {
     const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(ceil_div(batch, NB)));
-    if constexpr (NB == 1) {
-        if (sh.lds) {
-            const size_t lds = s1w_lds_bytes(wn);
-#define NQ_S1W_LDS_CASE(WPL, WR, R, G)                                                                      \
-    if (sh.wpl == WPL && sh.wr == WR && sh.r == R && sh.g == G) {                                           \
-        s1w_kernel<T, NB, WPL, WR, R, G, kNorm, kOne, true><<<grid, G * WR * 64, lds, st>>>(tab, x, batch, n, wn, eps); \
-        return;                                                                                             \
-    }
-            NQ_S1W_LDS_SHAPES(NQ_S1W_LDS_CASE)
-#undef NQ_S1W_LDS_CASE
-        }
-    }
 #define NQ_S1W_CASE(WPL, WR, R, G)                                                                        \
     if (sh.wpl == WPL && sh.wr == WR && sh.r == R && sh.g == G) {                                         \
         s1w_kernel<T, NB, WPL, WR, R, G, kNorm, kOne><<<grid, G * WR * 64, 0, st>>>(tab, x, batch, n, wn, eps); \
@@ -1592,15 +1681,61 @@ void launch_s1w_nb(const S1wShape& sh, const S1Table& tab, int blocks, const uin
     }
 }
 
+// Launch shapes of s1l_kernel (words per lane, rows per wave, groups, waves per group), the
+// fastest of a sweep of 14 on the GEMV shapes of each width (n = 4096 / 8192 / 11008).
+struct S1lShape {
+    int wpl, r, g, wr;
+};
+inline S1lShape s1l_shape(int wn) {
+    if (wn <= 64) return {1, 2, 4, 1};
+    if (wn <= 128) return {2, 2, 4, 1};
+    if (wn <= 256) return {1, 2, 2, 4};
+    return {2, 2, 4, 3};  // up to kS1lMaxWords
+}
+
+template <typename T, bool kNorm, bool kOne>
+void launch_s1l_cfg(const S1lShape& sh, const S1Table& tab, int blocks, const uint16_t* x, int n, int wn, float eps,
+                    hipStream_t st) {
+    const size_t lds = s1l_lds_bytes(wn);
+#define NQ_S1L_CASE(WPL, R, G, WR)                                                                           \
+    if (sh.wpl == WPL && sh.r == R && sh.g == G && sh.wr == WR) {                                            \
+        s1l_kernel<T, WPL, R, G, WR, kNorm, kOne><<<blocks, G * WR * 64, lds, st>>>(tab, x, n, wn, eps);     \
+        return;                                                                                              \
+    }
+    NQ_S1L_CASE(1, 2, 4, 1)
+    NQ_S1L_CASE(2, 2, 4, 1)
+    NQ_S1L_CASE(1, 2, 2, 4)
+    NQ_S1L_CASE(2, 2, 4, 3)
+#undef NQ_S1L_CASE
+}
+
+// Whether s1l_kernel takes the stage: one batch row, rows of whole words (n % 32 == 0; x and s_in
+// are 16-byte aligned), up to kS1lMaxWords words.
+inline bool s1l_applies(int batch, int n, int wn) { return batch == 1 && n % 32 == 0 && wn <= kS1lMaxWords; }
+
 // One launch over every item of `tab` (block ranges filled in here). The caller checked that
 // the fast stage 1 applies: n >= 8, n % 8 == 0, wn <= 1024, x and each s_in 16-byte aligned,
 // every r > 0.
 template <typename T>
 void launch_s1w_table(S1Table& tab, const uint16_t* x, int batch, int n, int wn, bool norm, float eps,
                       hipStream_t st) {
-    // x in LDS for one item at batch 1 (measured for single GEMVs; the grouped launches keep the
-    // shapes they were measured with)
-    const S1wShape sh = s1w_shape(wn, tab.count == 1 && batch == 1 && n % 32 == 0 && !norm);
+    if (s1l_applies(batch, n, wn)) {
+        const S1lShape sh = s1l_shape(wn);
+        int blocks = 0;
+        for (int k = 0; k < tab.count; ++k) {
+            tab.item[k].block_begin = blocks;
+            blocks += static_cast<int>(ceil_div(tab.item[k].kpad, sh.r * sh.g));
+        }
+        if (tab.count == 1) {
+            if (norm) launch_s1l_cfg<T, true, true>(sh, tab, blocks, x, n, wn, eps, st);
+            else launch_s1l_cfg<T, false, true>(sh, tab, blocks, x, n, wn, eps, st);
+        } else {
+            if (norm) launch_s1l_cfg<T, true, false>(sh, tab, blocks, x, n, wn, eps, st);
+            else launch_s1l_cfg<T, false, false>(sh, tab, blocks, x, n, wn, eps, st);
+        }
+        return;
+    }
+    const S1wShape sh = s1w_shape(wn);
     const int rpb = sh.r * sh.g;
     int blocks = 0;
     for (int k = 0; k < tab.count; ++k) {
@@ -1611,9 +1746,6 @@ void launch_s1w_table(S1Table& tab, const uint16_t* x, int batch, int n, int wn,
     else launch_s1w_nb<T, 2>(sh, tab, blocks, x, batch, n, wn, norm, eps, st);
 }
 
-// Dwords s1m_kernel stages in LDS: 16 rows of sign words, and the s_in pairs when they fit too
-// (64 KB, 16 dwords per thread of a 1024-thread block).
-constexpr int kS1mMaxStaged = 16 * 16 * 64;
 inline bool s1m_sin_lds(int n, int wn, int rt = 1) { return 16 * rt * s1m_row_stride(wn, rt) + n / 2 <= kS1mMaxStaged; }
 inline size_t s1m_lds_bytes(int n, int wn, int rt = 1) {
     const size_t staged = static_cast<size_t>(16 * rt * s1m_row_stride(wn, rt) + (s1m_sin_lds(n, wn, rt) ? n / 2 : 0)) * 4;
@@ -1626,11 +1758,21 @@ inline bool s1m_fits(int n, int wn, int rt = 1) {
     return 16 * rt * s1m_row_stride(wn, rt) <= kS1mMaxStaged;
 }
 
+// Raises a kernel's dynamic LDS limit. Each caller runs it once per kernel, on the kernel's first
+// launch, which may come inside a caller's stream capture (a graph or torch.compile's CUDA graphs):
+// the thread's capture mode is relaxed around the call, which is no stream operation.
+inline hipError_t allow_lds_bytes(const void* kernel, int bytes) {
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    const hipError_t ex = hipThreadExchangeStreamCaptureMode(&mode);
+    const hipError_t e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (ex == hipSuccess) (void)hipThreadExchangeStreamCaptureMode(&mode);
+    return e;
+}
+
 // Blocks of s1m_kernel<..., RT> may take more than 64 KB of LDS (the limit is set once per kernel).
 template <typename Kernel>
 int s1m_allow_lds(Kernel* k) {
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(k),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, kSbLdsBytes);
+    static const hipError_t attr = allow_lds_bytes(reinterpret_cast<const void*>(k), kSbLdsBytes);
     return attr == hipSuccess ? NQ_OK : fail(NQ_ERR_HIP, "nq_gemv stage 1: LDS limit: %s", hipGetErrorString(attr));
 }
 
@@ -1754,8 +1896,8 @@ template <typename T, int RTW, int CT>
 int launch_sb_cfg(const SbArgs& s, const SbPlan& p, hipStream_t st) {
     constexpr int NW = 4;
     // blocks may take more than 64 KB of LDS (once per kernel: the limit is a property of the function)
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&sb_kernel<T, NW, RTW, CT>),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, kSbLdsBytes);
+    static const hipError_t attr = allow_lds_bytes(reinterpret_cast<const void*>(&sb_kernel<T, NW, RTW, CT>),
+                                                   kSbLdsBytes);
     if (attr != hipSuccess) return fail(NQ_ERR_HIP, "nq_gemv batched stage 1: LDS limit: %s", hipGetErrorString(attr));
     const dim3 grid(static_cast<unsigned>(ceil_div(s.M, 16 * NW * RTW)), static_cast<unsigned>(p.ks),
                     static_cast<unsigned>(p.passes));
@@ -1957,8 +2099,8 @@ int launch_s2b_cfg(const GemvArgs& a) {
     const size_t dyn = static_cast<size_t>(s.u_slots) * 4;
     if (32LL * KC * s.chunks > a.plan.zpitch || kStatic + dyn > static_cast<size_t>(kSbLdsBytes))
         return fail(NQ_ERR_UNSUPPORTED, "nq_gemv batched stage 2: shape does not fit");
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&s2b_kernel<T, RT, WR, CTW, KC>),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, kSbLdsBytes - kStatic);
+    static const hipError_t attr = allow_lds_bytes(reinterpret_cast<const void*>(&s2b_kernel<T, RT, WR, CTW, KC>),
+                                                   kSbLdsBytes - kStatic);
     if (attr != hipSuccess) return fail(NQ_ERR_HIP, "nq_gemv batched stage 2: LDS limit: %s", hipGetErrorString(attr));
     const dim3 grid(static_cast<unsigned>(ceil_div(a.m, S::kRows)), static_cast<unsigned>(ceil_div(a.batch, S::kBatch)));
     s2b_kernel<T, RT, WR, CTW, KC><<<grid, 256, dyn, a.stream>>>(s);
@@ -2197,8 +2339,13 @@ int scratch_of_current_device(const char* name, void** out) {
                     kMaxScratchDevices);
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (g_scratch_ptr[dev] == nullptr) {
+        // the first call on a device may come inside a caller's stream capture: the lookup is no
+        // stream operation, and the thread's capture mode is relaxed around it
         void* p = nullptr;
+        hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+        const hipError_t ex = hipThreadExchangeStreamCaptureMode(&mode);
         e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (ex == hipSuccess) (void)hipThreadExchangeStreamCaptureMode(&mode);
         if (e != hipSuccess || p == nullptr)
             return fail(NQ_ERR_HIP, "%s: hipGetSymbolAddress(scratch) on device %d: %s", name, dev,
                         hipGetErrorString(e));

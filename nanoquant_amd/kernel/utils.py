@@ -1,9 +1,11 @@
 """Packers and op lookup with the signatures of the reference's ``kernel/utils.py``.
 
 Each function keeps the reference's name, arguments, return values, layouts and
-errors (``src/nanoquant/kernel/utils.py:33-284,503-507``); the bit work runs in the
-gfx950 HIP library. Tensors that live on the CPU are packed on the current GPU and
-the result is returned on the caller's device; without a GPU these functions raise.
+errors (``src/nanoquant/kernel/utils.py:33-284,503-507``). Like the reference's
+device-agnostic torch packers, each packs a tensor where it lives: CUDA tensors with
+the gfx950 HIP library, CPU tensors on the host (``_host.py``, the same words bit for
+bit), so a packed state dict can be written and read on a machine without a GPU. A
+CUDA tensor never takes the host path, and a CPU tensor never the GPU one.
 """
 from __future__ import annotations
 
@@ -12,6 +14,7 @@ from typing import Tuple
 import torch
 
 from .. import _lib
+from . import _host
 
 MARLIN_MIN_MAX_PAR = 32
 
@@ -45,12 +48,15 @@ def _method_code(method: str) -> int:
         raise ValueError(f"Unsupported method: '{method}'. Supported methods are 'lsb_first', 'half2'.") from None
 
 
-def _on_gpu(t: torch.Tensor) -> torch.Tensor:
-    if t.is_cuda:
-        return t.contiguous()
-    if not torch.cuda.is_available():
-        raise RuntimeError("nanoquant_amd packs signs with HIP kernels and needs a GPU; no GPU is available")
-    return t.to(device=torch.device("cuda", torch.cuda.current_device())).contiguous()
+def _on_host(*tensors: torch.Tensor) -> bool:
+    """True for CPU tensors (packed on the host); CUDA tensors go to the HIP kernels; anything
+    else, or a mix, is refused."""
+    kinds = {t.device.type for t in tensors if t is not None}
+    if kinds == {"cpu"}:
+        return True
+    if kinds == {"cuda"}:
+        return False
+    raise RuntimeError(f"nanoquant_amd packs CPU or CUDA tensors, all on one device; got {sorted(kinds)}")
 
 
 def pack_binary_gemv(tensor: torch.Tensor, method: str = "lsb_first") -> torch.Tensor:
@@ -65,7 +71,9 @@ def pack_binary_gemv(tensor: torch.Tensor, method: str = "lsb_first") -> torch.T
     n_rows, n_cols = tensor.shape
     code = _method_code(method)
     words = (n_cols + 31) // 32
-    src = _on_gpu(tensor)
+    if _on_host(tensor):
+        return _host.pack_signs(tensor, code)
+    src = tensor.contiguous()
     out = torch.empty((n_rows, words), dtype=torch.int32, device=src.device)
     if out.numel():
         lib = _lib.load()
@@ -73,7 +81,7 @@ def pack_binary_gemv(tensor: torch.Tensor, method: str = "lsb_first") -> torch.T
             status = lib.nq_pack_signs(src.data_ptr(), out.data_ptr(), n_rows, n_cols, code,
                                        _lib.stream_of(src.device))
         _lib.check(status, "pack_binary_gemv")
-    return out if tensor.is_cuda else out.to(tensor.device)
+    return out
 
 
 def unpack_binary_gemv(packed_tensor: torch.Tensor, original_shape: Tuple[int, int],
@@ -91,7 +99,9 @@ def unpack_binary_gemv(packed_tensor: torch.Tensor, original_shape: Tuple[int, i
     code = _method_code(method)
     if packed_tensor.dtype not in (torch.int32, torch.uint32):
         raise TypeError(f"packed words must be int32, got {packed_tensor.dtype}")
-    src = _on_gpu(packed_tensor)
+    if _on_host(packed_tensor):
+        return _host.unpack_signs(packed_tensor, n_rows, n_cols, code)
+    src = packed_tensor.contiguous()
     out = torch.empty((n_rows, n_cols), dtype=torch.int8, device=src.device)
     if out.numel():
         lib = _lib.load()
@@ -99,7 +109,7 @@ def unpack_binary_gemv(packed_tensor: torch.Tensor, original_shape: Tuple[int, i
             status = lib.nq_unpack_signs(src.data_ptr(), out.data_ptr(), n_rows, n_cols, code,
                                          _lib.stream_of(src.device))
         _lib.check(status, "unpack_binary_gemv")
-    return out if packed_tensor.is_cuda else out.to(packed_tensor.device)
+    return out
 
 
 def repack_binary_gemv(packed_tensor: torch.Tensor, original_shape: Tuple[int, int], src_method: str = "lsb_first",
@@ -119,7 +129,9 @@ def repack_binary_gemv(packed_tensor: torch.Tensor, original_shape: Tuple[int, i
     if packed_tensor.dtype not in (torch.int32, torch.uint32):
         raise TypeError(f"packed words must be int32, got {packed_tensor.dtype}")
     s_code, d_code = _method_code(src_method), _method_code(dst_method)
-    src = _on_gpu(packed_tensor)
+    if _on_host(packed_tensor):
+        return _host.repack_signs(packed_tensor, n_rows, n_cols, s_code, d_code)
+    src = packed_tensor.contiguous()
     out = torch.empty(src.shape, dtype=torch.int32, device=src.device)
     if out.numel():
         lib = _lib.load()
@@ -127,12 +139,12 @@ def repack_binary_gemv(packed_tensor: torch.Tensor, original_shape: Tuple[int, i
             status = lib.nq_repack_signs(src.data_ptr(), out.data_ptr(), n_rows, n_cols, s_code, d_code,
                                          _lib.stream_of(src.device))
         _lib.check(status, "repack_binary_gemv")
-    return out if packed_tensor.is_cuda else out.to(packed_tensor.device)
+    return out
 
 
 def _permute_scales(scale_in, scale_out):
-    s_in = _on_gpu(scale_in.reshape(-1))
-    s_out = _on_gpu(scale_out.reshape(-1))
+    s_in = scale_in.reshape(-1).contiguous()
+    s_out = scale_out.reshape(-1).contiguous()
     for name, s in (("scale_in", s_in), ("scale_out", s_out)):
         if s.element_size() != 2:
             raise TypeError(f"{name} must be a 16-bit float tensor, got {s.dtype}")
@@ -140,6 +152,8 @@ def _permute_scales(scale_in, scale_out):
         raise RuntimeError(f"shape '[{s_in.numel() // 16}, 2, 4, 2]' is invalid for input of size {s_in.numel()}")
     if s_out.numel() % 32:
         raise RuntimeError(f"shape '[{s_out.numel() // 32}, 4, 4, 2]' is invalid for input of size {s_out.numel()}")
+    if _on_host(s_in, s_out):
+        return _host.permute_marlin_scales(s_in, s_out)
     p_in = torch.empty_like(s_in)
     p_out = torch.empty_like(s_out)
     lib = _lib.load()
@@ -161,17 +175,18 @@ def pack_binary_marlin(weight: torch.Tensor, scale_in: torch.Tensor,
     O, K = weight.shape
     if O % 64 or K % 16:
         raise RuntimeError(f"shape '[{O // 64}, 4, 2, 8, {K // 16}, 2, 4, 2]' is invalid for input of size {O * K}")
-    w = _on_gpu(weight if weight.dtype == torch.int8 else weight.to(torch.int8))
-    words = torch.empty((K // 16, O // 2), dtype=torch.int32, device=w.device)
-    if words.numel():
-        lib = _lib.load()
-        with torch.cuda.device(w.device):
-            status = lib.nq_pack_marlin(w.data_ptr(), words.data_ptr(), O, K, _lib.stream_of(w.device))
-        _lib.check(status, "pack_binary_marlin")
+    w = (weight if weight.dtype == torch.int8 else weight.to(torch.int8)).contiguous()
+    if _on_host(w, scale_in, scale_out):
+        words = _host.pack_marlin(w)
+    else:
+        words = torch.empty((K // 16, O // 2), dtype=torch.int32, device=w.device)
+        if words.numel():
+            lib = _lib.load()
+            with torch.cuda.device(w.device):
+                status = lib.nq_pack_marlin(w.data_ptr(), words.data_ptr(), O, K, _lib.stream_of(w.device))
+            _lib.check(status, "pack_binary_marlin")
     s_in, s_out = _permute_scales(scale_in, scale_out)
     workspace_size = s_out.numel() // 128 * MARLIN_MIN_MAX_PAR
-    if not weight.is_cuda:
-        words, s_in, s_out = words.to(weight.device), s_in.to(weight.device), s_out.to(weight.device)
     return words, s_in, s_out, workspace_size
 
 
@@ -230,7 +245,9 @@ def repack_binary_marlin(packed_tensor: torch.Tensor, original_shape: Tuple[int,
     if O_pad < O or K_pad < K or O_pad % 64 or K_pad % 16:
         raise RuntimeError(f"padded shape ({O_pad}, {K_pad}) must cover ({O}, {K}) with O % 64 == 0 and K % 16 == 0")
     code = _method_code(src_method)
-    src = _on_gpu(packed_tensor)
+    if _on_host(packed_tensor):
+        return _host.repack_marlin(packed_tensor, O, K, O_pad, K_pad, code)
+    src = packed_tensor.contiguous()
     words = torch.empty((K_pad // 16, O_pad // 2), dtype=torch.int32, device=src.device)
     if words.numel():
         lib = _lib.load()
@@ -238,7 +255,7 @@ def repack_binary_marlin(packed_tensor: torch.Tensor, original_shape: Tuple[int,
             status = lib.nq_repack_marlin(src.data_ptr(), O, K, code, words.data_ptr(), O_pad, K_pad,
                                           _lib.stream_of(src.device))
         _lib.check(status, "repack_binary_marlin")
-    return words if packed_tensor.is_cuda else words.to(packed_tensor.device)
+    return words
 
 
 def marlin_rank(rank: int) -> int:
@@ -273,12 +290,7 @@ def pack_binary_marlin_fused_from_packed(V_packed: torch.Tensor, V_shape: Tuple[
     _, scale_h_marlin = _permute_scales(scale_l, scale_h)
     workspace_size = max(scale_l_marlin.numel(), scale_h_marlin.numel()) // 128 * MARLIN_MIN_MAX_PAR
     workspace = torch.zeros(workspace_size, device=V_bits.device, dtype=torch.int32)
-    dev = V_packed.device
-    outs = (V_bits, U_bits, scale_g_marlin, scale_l_marlin, scale_h_marlin)
-    if dev.type != "cuda":
-        outs = tuple(t.to(dev) for t in outs)
-        workspace = workspace.to(dev)
-    return (*outs, workspace)
+    return V_bits, U_bits, scale_g_marlin, scale_l_marlin, scale_h_marlin, workspace
 
 
 # Aliases of the reference (kernel/utils.py:503-506)

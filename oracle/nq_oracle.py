@@ -13,8 +13,8 @@ Pins (``tests/test_oracle.py``):
   ``checkpoint_audit.py:33-35``, and an independent decode of the ``half2`` words
   by the sign extraction the reference GEMV kernel itself performs
   (``gemv_kernel.cu:93-96,114`` with ``cuda_utils.cuh:94-101``).
-* ``pack_binary_marlin`` / ``pack_binary_marlin_fused``: golden vectors written
-  by the reference's own packer (``tests/golden/make_marlin_vectors.py``).
+* ``pack_binary_marlin`` / ``pack_binary_marlin_fused`` / ``pack_marlin_torch``: golden
+  vectors written by the reference's own packer (``tests/golden/make_marlin_vectors.py``).
 * ``nanoquant_forward_f64``: closed forms (all-+1 signs, one-hot inputs) and a
   brute-force triple loop on tiny shapes.
 * ``marlin_nanoquant_f64``: equal to ``nanoquant_forward_f64`` with the identity rounding;
@@ -32,6 +32,7 @@ __all__ = [
     "MARLIN_MIN_MAX_PAR", "nanoquant_forward_f64", "marlin_nanoquant_f64", "compute_forward_torch",
     "gemv_output_shape", "check_gemv_tuning", "GEMV_TUNING_CHOICES",
     "marlin_onebit_output_shape", "round_rank", "random_case", "pack_signs_torch", "unpack_signs_torch",
+    "pack_marlin_torch",
 ]
 
 MARLIN_MIN_MAX_PAR = 32  # kernel/utils.py:21, gemm.cpp:33
@@ -298,6 +299,24 @@ def pack_signs_torch(signs, method: str = "lsb_first"):
     weights = torch.from_numpy((np.uint64(1) << bit_position(method).astype(np.uint64)).astype(np.uint32)
                                .view(np.int32).copy())
     return (bits * weights).sum(dim=2, dtype=torch.int32).contiguous()
+
+
+def pack_marlin_torch(weight):
+    """The Marlin packer of kernel/utils.py:186-205 as eager torch ops on the CPU (the timed CPU
+    baseline of Marlin packing). The [O, K] weight is viewed as (O/64, 4, 2, 8, K/16, 2, 4, 2) =
+    (tile_out, o16, o8, o1, tile_red, r8, r2, r1) and permuted to (tile_red, tile_out, o1, r2, o16,
+    r1, o8, r8), so that each run of 32 values is one word's elements (:192-196); element
+    (o16, r1, o8, r8) takes bit 15 - (2 o8 + r8) + 16 r1 - 4 o16 (:198-202); bits (1 - v) // 2
+    weighted by 2^bit are summed in int32 (:204) into words [K/16, O/2] (:205). Checked against the
+    reference-written vectors in tests/test_oracle.py."""
+    import torch
+
+    O_, K_ = weight.shape
+    v = weight.reshape(O_ // 64, 4, 2, 8, K_ // 16, 2, 4, 2).permute(4, 0, 3, 6, 1, 7, 2, 5).reshape(-1, 32).int()
+    o16, r1, o8, r8 = np.meshgrid(np.arange(4), np.arange(2), np.arange(2), np.arange(2), indexing="ij")
+    bit = (15 - (2 * o8 + r8) + 16 * r1 - 4 * o16).reshape(-1).astype(np.uint64)
+    weights = torch.from_numpy((np.uint64(1) << bit).astype(np.uint32).view(np.int32).copy())
+    return (((1 - v) // 2) * weights).sum(dim=1, dtype=torch.int32).reshape(K_ // 16, O_ // 2).contiguous()
 
 
 def unpack_signs_torch(packed, shape, method: str = "lsb_first"):

@@ -2,8 +2,9 @@
 
 * Llama-2-7B linears at 0.55 and 1.0 bpw: GEMV at batch 1, 4, 16 and GEMM at batch 256 and
   2048 on q/k/v/o (4096 x 4096), gate/up (11008 x 4096) and down (4096 x 11008);
-* Llama-3-70B linears at 0.55 bpw, uniform and mixture-of-rank: GEMM at batch 2048 on q/o, k/v,
-  gate/up and down (the GEMV cells are in test_gpu_parity.py);
+* Llama-3-70B linears at 0.55 bpw, uniform and mixture-of-rank: GEMV at batch 1, 4 and 16 and
+  GEMM at batch 2048 on q/o, k/v, gate/up and down, and mixture-of-rank draws of down and k/v at
+  GEMV batch 16;
 * the end-to-end decode model at its stated size (32 layers, hidden 4096, FFN 11008, vocab
   32000, all linears at 0.55 bpw): graph replay against eager stepping, the fused step against
   the unfused one, and one layer's seven linears against the oracle.
@@ -111,6 +112,11 @@ L3 = [("qo", 8192, 8192), ("kv", 1024, 8192), ("gate_up", 28672, 8192), ("down",
 # GEMV cells not covered in test_gpu_parity.py: the 1.0-bpw ranks at every batch, 0.55 bpw at 4 and 16
 GEMV_CELLS = [(f"l2_{name}_{bpw}_b{B}", m, n, rank_at(bpw, m, n), B)
               for bpw in (1.0, 0.55) for name, m, n in L2 for B in (1, 4, 16)]
+# every Llama-3-70B GEMV cell: down at 4 and 16 rows runs the k-split stage 1 and its finishing
+# launch at r = 3520 over 8192 rows of U, gate/up at 16 rows the batched stage 2 on 3.15 M words
+GEMV_CELLS += [(f"l3_{name}_0.55_b{B}", m, n, rank_at(0.55, m, n), B) for name, m, n in L3 for B in (1, 4, 16)]
+GEMV_CELLS += [("l3_down_mixed_b16", 8192, 28672, mixed_rank(rank_at(0.55, 8192, 28672), 17), 16),
+               ("l3_kv_mixed_b16", 1024, 8192, mixed_rank(rank_at(0.55, 1024, 8192), 19), 16)]
 
 GEMM_CELLS = ([(f"l2_{name}_{bpw}_b{B}", m, n, rank_at(bpw, m, n), B)
                for bpw in (1.0, 0.55) for name, m, n in L2 for B in (256, 2048)] +
@@ -141,7 +147,8 @@ def test_gemm_config_cells(nq, cell):
 # --------------------------------------------------------------------------- config 5 at full size
 
 E2E_STEPS = 16
-FUSED_FIRST_STEP_TOL = 2e-2
+# measured 2.9e-3 (torch attention) and 3.0e-3 (HIP attention) on this model
+FUSED_FIRST_STEP_TOL = 5e-3
 
 
 @pytest.fixture(scope="module")
@@ -179,7 +186,7 @@ def test_llama7b_graph_replay_equals_eager(llama7b, step):
 
 def test_llama7b_fused_first_step_logits(llama7b):
     """The fused step folds RMSNorm into the GEMV and fuses the residual and SiLU·mul epilogues,
-    which rounds differently from the unfused torch ops: first-step logits agree within 2e-2 of
+    which rounds differently from the unfused torch ops: first-step logits agree within 5e-3 of
     their largest magnitude."""
     from nanoquant_amd.decode import FusedDecoder, GraphDecoder
     model, prompt = llama7b

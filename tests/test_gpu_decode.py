@@ -160,3 +160,44 @@ def test_fused_decode_matches_dense(name, attention):
     for j, (a, b) in enumerate(zip(lg_g, lg_e[::2])):
         assert torch.equal(a, b), j
     check_against_dense(dense, ids_e, lg_e, prompt.shape[1])
+
+
+@pytest.mark.parametrize("heads,kv_heads,pos", [(32, 32, 200), (8, 2, 77), (32, 32, 0)])
+def test_attention_step_against_rotary_attention(heads, kv_heads, pos):
+    """The decode step's attention (``rotary_attention_step``: RoPE as one [D, D] product, the scale
+    and causal mask folded into ``baddbmm``, fp16 scores) against ``rotary_attention`` (elementwise
+    RoPE, fp32 scores) on the same fp16 cache and inputs, one layer at a time: outputs within 2e-3
+    of their largest magnitude and the written K/V rows within fp16 rounding of each other."""
+    from nanoquant_amd.decode import StaticKVCache, rotary_attention, rotary_attention_step, rotary_step_tables
+    shape = LlamaShape(hidden=heads * 128, layers=2, heads=heads, kv_heads=kv_heads, ffn=512, vocab=1000)
+    announce("attention step vs rotary_attention", heads, kv_heads, pos)
+    D, B, L = shape.head_dim, 1, 384
+    gen = torch.Generator(device="cuda").manual_seed(pos + heads)
+    caches = [StaticKVCache(shape, B, L, "cuda", torch.float16) for _ in range(2)]
+    for layer in range(shape.layers):
+        k0 = torch.randn(B, kv_heads, L, D, device="cuda", generator=gen).half()
+        v0 = torch.randn(B, kv_heads, L, D, device="cuda", generator=gen).half()
+        for c in caches:
+            c.k[layer].copy_(k0)
+            c.v[layer].copy_(v0)
+    positions = torch.tensor([pos], device="cuda")
+    inv = 1.0 / (10000.0 ** (torch.arange(0, D, 2, device="cuda").float() / D))
+    ang = positions.float()[:, None] * inv[None, :]
+    emb = torch.cat((ang, ang), dim=-1)
+    cos, sin = emb.cos().half(), emb.sin().half()
+    tables = rotary_step_tables(cos, sin, positions, caches[1], torch.float16)
+    for layer in range(shape.layers):
+        q = torch.randn(B, 1, heads * D, device="cuda", generator=gen).half()
+        k = torch.randn(B, 1, kv_heads * D, device="cuda", generator=gen).half()
+        v = torch.randn(B, 1, kv_heads * D, device="cuda", generator=gen).half()
+        ref = rotary_attention(shape, layer, q, k, v, cos, sin, positions, caches[0]).double()
+        qk = torch.cat((q, k), dim=-1).view(B, -1)
+        got = rotary_attention_step(shape, layer, qk, v.view(B, -1), tables, positions, caches[1]).double()
+        torch.cuda.synchronize()
+        rel = float((got - ref).abs().max() / ref.abs().max())
+        k_ref = caches[0].k[layer].double()
+        k_rel = float((caches[1].k[layer].double() - k_ref).abs().max() / k_ref.abs().max())
+        print(f"[decode] layer {layer} attention step rel {rel:.3e}, K write rel {k_rel:.3e}", flush=True)
+        assert rel <= 2e-3, (layer, rel)
+        assert torch.equal(caches[1].v[layer], caches[0].v[layer])
+        assert k_rel <= 2e-3, (layer, k_rel)  # RoPE rounded once (product) against three times (elementwise)

@@ -17,6 +17,7 @@ import pytest
 import torch
 
 import oracle as O
+from nanoquant_amd.kernel import utils as ku
 
 pytestmark = pytest.mark.gpu
 
@@ -149,6 +150,39 @@ def test_marlin_pack_large_and_unpack(nq, OK):
     np.testing.assert_array_equal(back.cpu().numpy(), w)
 
 
+@pytest.mark.parametrize("shape", [(1, 1), (33, 95), (300, 1000), (1632, 11008)])
+def test_host_and_hip_packers_write_the_same_words(nq, shape):
+    """The same signs packed as a CPU tensor (host path) and as a CUDA tensor (HIP kernels): sign
+    words in both orders, their unpacking and reordering, and the Marlin words and scales of the
+    factor padded to whole tiles, bit for bit."""
+    rows, cols = shape
+    announce("host vs HIP packers", shape)
+    rng = np.random.default_rng(rows + cols)
+    s = torch.from_numpy(np.where(rng.random(shape) < 0.5, -1, 1).astype(np.int8))
+    for method in ("lsb_first", "half2"):
+        w_host = nq.pack_binary_gemv(s, method=method)
+        w_dev = nq.pack_binary_gemv(s.cuda(), method=method)
+        assert w_host.device.type == "cpu" and w_dev.is_cuda
+        assert torch.equal(w_host, w_dev.cpu()), method
+        assert torch.equal(nq.unpack_binary_gemv(w_host, shape, method=method),
+                           nq.unpack_binary_gemv(w_dev, shape, method=method).cpu())
+        other = "half2" if method == "lsb_first" else "lsb_first"
+        assert torch.equal(ku.repack_binary_gemv(w_host, shape, method, other),
+                           ku.repack_binary_gemv(w_dev, shape, method, other).cpu())
+    O_, K_ = -(-rows // 64) * 64, -(-cols // 16) * 16
+    w = torch.ones(O_, K_, dtype=torch.int8)
+    w[:rows, :cols] = s
+    s_in = torch.from_numpy(np.abs(rng.normal(1, .2, K_)).astype(np.float16))
+    s_out = torch.from_numpy(np.abs(rng.normal(1, .2, O_)).astype(np.float16))
+    host = nq.pack_binary_marlin(w, s_in, s_out)
+    dev = nq.pack_binary_marlin(w.cuda(), s_in.cuda(), s_out.cuda())
+    for a, b in zip(host[:3], dev[:3]):
+        assert torch.equal(a, b.cpu())
+    lsb = nq.pack_binary_gemv(s, method="lsb_first")
+    assert torch.equal(ku.repack_binary_marlin(lsb, shape, (O_, K_)),
+                       ku.repack_binary_marlin(lsb.cuda(), shape, (O_, K_)).cpu())
+
+
 # --------------------------------------------------------------------------- GEMV
 
 GEMV_CASES = [
@@ -223,6 +257,19 @@ GEMV_CASES = [
     # an even word count (padded) and an odd one (already odd)
     ("s1m_wide_even_b5", 300, 8192, 160, 5, True),
     ("s1m_wide_odd_b5", 300, 8224, 160, 5, True),
+    # 1024-word rows (n = 32737 .. 32768) where the k-split stage 1 does not run (more than 128
+    # batch rows; n % 32 != 0): the MFMA kernel with the unpadded stride (the padded one would not
+    # fit its staging buffer)
+    ("s1m_b130_n32768", 200, 32768, 96, 130, False),
+    # one batch row, whole words of up to 384 per row: the stage 1 with s_in and x in LDS, rows in
+    # pairs per 64-bit shift, words split over 1-3 waves per row group; ragged ranks (rows past the
+    # rank store zeros), s_mid, a rank of 1, each launch shape's width bucket (<= 64, 128, 256, 384)
+    ("s1l_b1_n1024_mid", 300, 1024, 70, 1, True),
+    ("s1l_b1_n4096_mid_ragged", 500, 4096, 333, 1, True),
+    ("s1l_b1_n8192_mid", 600, 8192, 250, 1, True),
+    ("s1l_b1_n12288_mid", 400, 12288, 130, 1, True),
+    ("s1l_b1_n11008_r1", 64, 11008, 1, 1, True),
+    ("s1m_b3_n32760", 300, 32760, 130, 3, True),
 ]
 
 

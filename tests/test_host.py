@@ -188,10 +188,10 @@ def test_packer_errors_before_device_work():
                                     torch.ones(64), None, torch.ones(64))
 
 
-@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-GPU error")
-def test_packers_refuse_to_run_without_a_gpu():
-    with pytest.raises(RuntimeError, match="needs a GPU"):
-        ku.pack_binary_gemv(torch.ones(2, 2, dtype=torch.int8))
+def test_packers_refuse_mixed_devices():
+    meta = torch.ones(64, dtype=torch.float16, device="meta")
+    with pytest.raises(RuntimeError, match="CPU or CUDA tensors"):
+        ku.pack_binary_marlin(torch.ones(64, 64, dtype=torch.int8), meta, torch.ones(64, dtype=torch.float16))
 
 
 def make_layer(in_f, out_f, rank, seed=0, with_mid=False, bias=False, dtype=torch.float32, device="cpu"):

@@ -104,6 +104,14 @@ def test_marlin_single_matches_reference_vectors():
         assert (O.unpack_binary_marlin(words, O_, K_) == g[f"single{i}_w"]).all()
 
 
+def test_marlin_torch_eager_packer_matches_reference_vectors():
+    import torch
+    g = _golden()
+    for i in range(int(g["n_single"])):
+        words = O.pack_marlin_torch(torch.from_numpy(g[f"single{i}_w"].astype(np.int8)))
+        assert (words.numpy().view(np.uint32) == g[f"single{i}_words"].view(np.uint32)).all(), i
+
+
 def test_marlin_fused_matches_reference_vectors():
     g = _golden()
     for i in range(int(g["n_fused"])):

@@ -113,3 +113,32 @@ def test_noalloc_batched_call_beyond_the_per_range_sums(lib):
     scale = np.abs(y64).max()
     assert np.abs(got.double().cpu().numpy() - y64).max() / scale <= 1e-3
     assert (got.double() - want.double()).abs().max().item() / scale <= 1e-3
+
+
+@pytest.mark.parametrize("shape", [(4096, 11008, 1632, 1, False), (1000, 1024, 288, 5, True)])
+def test_noalloc_captured_in_a_graph(lib, shape):
+    """nq_gemv_noalloc recorded into a HIP graph (torch.cuda.graph) and replayed three times, each
+    time after new contents were written into x and with eager nq_gemv calls between the replays:
+    every replay bit-identical to nq_gemv on the same inputs."""
+    from nanoquant_amd import _lib
+    m, n, r, batch, mid = shape
+    announce("gemv noalloc under graph capture", shape)
+    d = _case(50, m, n, r, batch, mid, torch.float16)
+    y = torch.empty(batch, m, dtype=torch.float16, device="cuda")
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph, stream=stream):
+        status = lib.nq_gemv_noalloc(_lib.NQ_F16, d["x"].data_ptr(), d["s_in"].data_ptr(), d["V"].data_ptr(),
+                                     _ptr(d["s_mid"]), d["U"].data_ptr(), d["s_out"].data_ptr(), y.data_ptr(),
+                                     batch, n, r, m, torch.cuda.current_stream().cuda_stream)
+    assert status == _lib.NQ_OK, lib.nq_last_error_message()
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    for rep in range(3):
+        d["x"].copy_(torch.randn(batch, n, device="cuda", generator=gen).half())
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want = _gemv_with_workspace(lib, d, _lib.NQ_F16)
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), want.view(torch.int16)), rep
