@@ -525,6 +525,7 @@ def bench_decode(args, dev):
         "fused_torch_attention": (True, "torch", spg),
         "fused_torch_attention_spg1": (True, "torch", 1),
         "unfused": (False, "torch", spg),
+        "fused_rope_kernel_torch_attention": (True, "rope", spg),
         "fused_hip_attention": (True, "hip", spg),
     }
     runs = {}
@@ -545,6 +546,8 @@ def bench_decode(args, dev):
     first = {}
     for name, make in (("unfused", lambda: GraphDecoder(model, B, T + 2, device=dev)),
                        ("fused_torch_attention", lambda: FusedDecoder(model, B, T + 2, device=dev)),
+                       ("fused_rope_kernel_torch_attention",
+                        lambda: FusedDecoder(model, B, T + 2, device=dev, attention="rope")),
                        ("fused_hip_attention", lambda: FusedDecoder(model, B, T + 2, device=dev, attention="hip"))):
         dec = make()
         dec.prefill(prompt)

@@ -263,6 +263,21 @@ int nq_attention_decode(int dtype, const void* q, const void* k, const void* v, 
                         int64_t head_dim, int64_t max_len, float scaling, void* workspace, size_t workspace_bytes,
                         nq_stream_t stream);
 
+/* Rotary embedding and KV-cache write of one new token per sequence, with the attention products
+ * left to the caller: the first part of nq_attention_decode on its own. qkv [batch, qkv_stride]
+ * holds heads query heads, kv_heads key heads and kv_heads value heads of head_dim (even) each;
+ * the query heads are rotated into q_out [batch, q_stride] (q_out may be qkv), the key heads
+ * rotated into k_cache[b, kvh, p, :] and the value heads copied into v_cache[b, kvh, p, :]
+ * ([batch, kv_heads, max_len, head_dim] each), p = *position (device int64). rope_cos/rope_sin
+ * [max_len, head_dim]. Rounded as the unfused path: T(x cos) + T(rotate_half(x) sin), summed in
+ * T. A position outside [0, max_len) zeroes q_out and writes no cache row. No counterpart in the
+ * reference, whose decode step runs Hugging Face's rotary embedding and cache update
+ * (kernel/test_decode.py:385-402). */
+int nq_rope_kv_write(int dtype, const void* qkv, int64_t qkv_stride, void* k_cache, void* v_cache,
+                     const void* rope_cos, const void* rope_sin, const int64_t* position, void* q_out,
+                     int64_t q_stride, int64_t batch, int64_t heads, int64_t kv_heads, int64_t head_dim,
+                     int64_t max_len, nq_stream_t stream);
+
 /* ---------------------------------------------------------------- measurement aid */
 
 /* Enqueue a one-thread kernel that writes the GPU's constant-rate wall clock to *dst (device

@@ -284,6 +284,63 @@ __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(const float*
     }
 }
 
+// Rotary embedding and KV-cache write of one new token per sequence, for a decode step whose
+// attention products run elsewhere: step 1 of attn_decode_kernel on its own. One thread per
+// (sequence, head slot, dimension pair d < D/2) of the q, k and v heads of a [batch, qkv_stride]
+// row: the query heads are rotated into q_out (which may be the q part of the same row: each
+// thread reads and writes only its own pair), the key heads rotated into k_cache[b, kvh, p, :],
+// the value heads copied into v_cache[b, kvh, p, :], with p read from device memory (so a graph
+// replays it as the position advances). Rounded as the unfused path: T(x cos) and
+// T(rotate_half(x) sin), then their sum to T. A position outside [0, max_len) writes zeros to
+// q_out and nothing to the caches.
+template <typename T>
+__global__ __launch_bounds__(256) void rope_kv_kernel(const uint16_t* qkv, int qkv_stride, uint16_t* __restrict__ k_cache,
+                                                      uint16_t* __restrict__ v_cache,
+                                                      const uint16_t* __restrict__ rope_cos,
+                                                      const uint16_t* __restrict__ rope_sin,
+                                                      const int64_t* __restrict__ position, uint16_t* q_out,
+                                                      int q_stride, int batch, int heads, int kv_heads, int head_dim,
+                                                      int max_len) {
+#pragma clang fp contract(off)
+    const int half = head_dim / 2;
+    const int slots = heads + 2 * kv_heads;
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= static_cast<int64_t>(batch) * slots * half) return;
+    const int d = static_cast<int>(i % half);
+    const int64_t bh = i / half;
+    const int hs = static_cast<int>(bh % slots);
+    const int b = static_cast<int>(bh / slots);
+    const int64_t p64 = *position;
+    const uint16_t* src = qkv + static_cast<size_t>(b) * qkv_stride + static_cast<size_t>(hs) * head_dim;
+    uint16_t* qdst = q_out + static_cast<size_t>(b) * q_stride + static_cast<size_t>(hs) * head_dim;
+    if (p64 < 0 || p64 >= max_len) {
+        if (hs < heads) qdst[d] = qdst[d + half] = 0;
+        return;
+    }
+    const size_t p = static_cast<size_t>(p64);
+    const uint16_t x0 = src[d], x1 = src[d + half];
+    if (hs >= heads + kv_heads) {  // a value head
+        const size_t row = ((static_cast<size_t>(b) * kv_heads + (hs - heads - kv_heads)) * max_len + p) * head_dim;
+        v_cache[row + d] = x0;
+        v_cache[row + d + half] = x1;
+        return;
+    }
+    const float c0 = T::to_float(rope_cos[p * head_dim + d]), c1 = T::to_float(rope_cos[p * head_dim + d + half]);
+    const float s0 = T::to_float(rope_sin[p * head_dim + d]), s1 = T::to_float(rope_sin[p * head_dim + d + half]);
+    const float f0 = T::to_float(x0), f1 = T::to_float(x1);
+    // rotate_half: element d < D/2 takes -x[d + D/2], element d + D/2 takes x[d]
+    const uint16_t r0 = T::from_float(T::to_float(T::from_float(f0 * c0)) + T::to_float(T::from_float(-f1 * s0)));
+    const uint16_t r1 = T::from_float(T::to_float(T::from_float(f1 * c1)) + T::to_float(T::from_float(f0 * s1)));
+    if (hs < heads) {
+        qdst[d] = r0;
+        qdst[d + half] = r1;
+    } else {
+        const size_t row = ((static_cast<size_t>(b) * kv_heads + (hs - heads)) * max_len + p) * head_dim;
+        k_cache[row + d] = r0;
+        k_cache[row + d + half] = r1;
+    }
+}
+
 template <typename T, int G>
 void launch_attn(const void* q, const void* k, const void* v, int64_t qkv_stride, void* k_cache, void* v_cache,
                  const void* rope_cos, const void* rope_sin, const int64_t* position, void* out, int64_t batch,
@@ -367,6 +424,47 @@ int nq_attention_decode(int dtype, const void* q, const void* k, const void* v, 
                                                           rope_cos, rope_sin, position, out, batch, kv_heads, max_len,
                                                           scaling, parts, st);
     if (!ok) return fail(NQ_ERR_UNSUPPORTED, "%s: no kernel for this head grouping", name);
+    return check_launch(name);
+}
+
+int nq_rope_kv_write(int dtype, const void* qkv, int64_t qkv_stride, void* k_cache, void* v_cache,
+                     const void* rope_cos, const void* rope_sin, const int64_t* position, void* q_out,
+                     int64_t q_stride, int64_t batch, int64_t heads, int64_t kv_heads, int64_t head_dim,
+                     int64_t max_len, nq_stream_t stream) {
+    const char* name = "nq_rope_kv_write";
+    if (dtype != NQ_F16 && dtype != NQ_BF16) return fail(NQ_ERR_DTYPE, "%s: unsupported dtype %d", name, dtype);
+    if (batch < 0 || heads <= 0 || kv_heads <= 0 || max_len <= 0 || head_dim <= 0 || head_dim % 2)
+        return fail(NQ_ERR_INVALID_ARGUMENT, "%s: bad sizes (head_dim must be even)", name);
+    if (qkv_stride < (heads + 2 * kv_heads) * head_dim || q_stride < heads * head_dim)
+        return fail(NQ_ERR_SHAPE, "%s: row strides too small", name);
+    if (batch * qkv_stride > INT32_MAX / 2 || batch * q_stride > INT32_MAX / 2 || max_len > INT32_MAX / 2 ||
+        batch * kv_heads * max_len * head_dim > ((int64_t)1 << 40) || batch * (heads + 2 * kv_heads) * head_dim > INT32_MAX / 2)
+        return fail(NQ_ERR_UNSUPPORTED, "%s: sizes too large", name);
+    if (batch == 0) return NQ_OK;
+    if (!qkv || !k_cache || !v_cache || !rope_cos || !rope_sin || !position || !q_out)
+        return fail(NQ_ERR_INVALID_ARGUMENT, "%s: null pointer", name);
+    if (!aligned(qkv, 2) || !aligned(k_cache, 2) || !aligned(v_cache, 2) || !aligned(rope_cos, 2) ||
+        !aligned(rope_sin, 2) || !aligned(position, 8) || !aligned(q_out, 2))
+        return fail(NQ_ERR_ALIGNMENT, "%s: misaligned operand", name);
+    const int64_t threads = batch * (heads + 2 * kv_heads) * (head_dim / 2);
+    const dim3 grid(static_cast<unsigned>(ceil_div(threads, 256)));
+    hipStream_t st = as_stream(stream);
+    const auto* a = static_cast<const uint16_t*>(qkv);
+    auto* kc = static_cast<uint16_t*>(k_cache);
+    auto* vc = static_cast<uint16_t*>(v_cache);
+    const auto* cs = static_cast<const uint16_t*>(rope_cos);
+    const auto* sn = static_cast<const uint16_t*>(rope_sin);
+    auto* qo = static_cast<uint16_t*>(q_out);
+    if (dtype == NQ_F16)
+        rope_kv_kernel<F16><<<grid, 256, 0, st>>>(a, static_cast<int>(qkv_stride), kc, vc, cs, sn, position, qo,
+                                                  static_cast<int>(q_stride), static_cast<int>(batch),
+                                                  static_cast<int>(heads), static_cast<int>(kv_heads),
+                                                  static_cast<int>(head_dim), static_cast<int>(max_len));
+    else
+        rope_kv_kernel<BF16><<<grid, 256, 0, st>>>(a, static_cast<int>(qkv_stride), kc, vc, cs, sn, position, qo,
+                                                   static_cast<int>(q_stride), static_cast<int>(batch),
+                                                   static_cast<int>(heads), static_cast<int>(kv_heads),
+                                                   static_cast<int>(head_dim), static_cast<int>(max_len));
     return check_launch(name);
 }
 

@@ -176,13 +176,46 @@ def rotary_step_tables(cos, sin, positions, cache: StaticKVCache, dtype):
     return R.to(dtype), madd
 
 
-def rotary_attention_step(shape: LlamaShape, layer: int, qk, v, tables, positions, cache: StaticKVCache):
+def causal_mask_table(positions, cache: StaticKVCache, dtype):
+    """The causal mask of a one-token step at ``positions`` (one position, on the device) as an
+    additive [1, L, 1]: 0 for visible cache rows, -inf past the position."""
+    visible = cache.key_index.view(1, -1, 1) <= positions.view(1, 1, 1)
+    return torch.zeros(visible.shape, device=positions.device, dtype=dtype).masked_fill_(~visible, float("-inf"))
+
+
+def attention_products_step(shape: LlamaShape, layer: int, q, madd, cache: StaticKVCache, out):
+    """The attention products of a one-token step whose rotary embedding and cache write are done
+    (``nq_rope_kv_write``): the scores of each kv head's query group against the cache with the scale
+    and causal mask folded into one batched product, the softmax, and the value product written into
+    ``out`` [B, H * D] (directly when each kv head serves one query head, else through a copy).
+
+    q [B, H * D] (rotated, contiguous); ``madd`` from ``causal_mask_table``."""
+    H, KV, D = shape.heads, shape.kv_heads, shape.head_dim
+    B, G = q.shape[0], H // KV
+    k_c, v_c = cache.k[layer], cache.v[layer]
+    L = k_c.shape[2]
+    # K [B*KV, L, D] @ Q^T [B*KV, D, G]: the right operand contiguous (a view when G == 1)
+    q_t = q.view(B * KV, G, D).transpose(1, 2)
+    if G > 1:
+        q_t = q_t.contiguous()
+    scores = torch.baddbmm(madd, k_c.view(B * KV, L, D), q_t, alpha=D ** -0.5)  # [B*KV, L, G]
+    p = torch.softmax(scores, dim=1)
+    vt = v_c.view(B * KV, L, D).transpose(1, 2)
+    if G == 1:
+        torch.bmm(vt, p, out=out.view(B * KV, D, 1))
+    else:
+        out.view(B, KV, G, D).copy_(torch.bmm(vt, p).view(B, KV, D, G).transpose(2, 3))
+    return out
+
+
+def rotary_attention_step(shape: LlamaShape, layer: int, qk, v, tables, positions, cache: StaticKVCache, out=None):
     """``rotary_attention`` for one token per sequence in seven torch launches: RoPE of q and k as one
     matrix product, the two cache writes, the scores of each kv head's query group with the scale and
     the causal mask folded into one batched product, the softmax, the value product and the copy out.
 
     qk [B, (H + KV) * D] (q heads then k heads, contiguous), v [B, KV * D]; ``tables`` from
-    ``rotary_step_tables``; returns [B, 1, H * D].
+    ``rotary_step_tables``; returns [B, 1, H * D], written into ``out`` [B, H * D] when it is given
+    and each kv head serves one query head (the value product then needs no copy).
     """
     H, KV, D = shape.heads, shape.kv_heads, shape.head_dim
     B, G = qk.shape[0], H // KV
@@ -196,6 +229,9 @@ def rotary_attention_step(shape: LlamaShape, layer: int, qk, v, tables, position
     q_t = rot[:, :H].reshape(B * KV, G, D).transpose(1, 2).contiguous()
     scores = torch.baddbmm(madd, k_c.view(B * KV, L, D), q_t.to(k_c.dtype), alpha=D ** -0.5)  # [B*KV, L, G]
     p = torch.softmax(scores, dim=1)
+    if out is not None and G == 1:
+        torch.bmm(v_c.view(B * KV, L, D).transpose(1, 2), p, out=out.view(B * KV, D, 1))
+        return out.view(B, 1, H * D)
     out_t = torch.bmm(v_c.view(B * KV, L, D).transpose(1, 2), p)  # [B*KV, D, G]
     return out_t.view(B, KV, D, G).transpose(2, 3).reshape(B, 1, H * D)
 
@@ -419,7 +455,9 @@ class FusedDecoder(GraphDecoder):
     2. q, k, v stage 2 in one launch, into one [B, (heads + 2 kv_heads) * head_dim] buffer;
     3. rotary embedding, KV-cache write and attention: in torch ops (``attention="torch"``, the
        default, as the benchmark's end-to-end configuration keeps the non-linear ops in
-       PyTorch) or in one HIP launch pair (``attention="hip"``, ``nq_attention_decode``);
+       PyTorch), or the rotary embedding and cache write in one HIP launch (``nq_rope_kv_write``)
+       and the attention products in torch (``attention="rope"``), or all of it in one HIP launch
+       pair (``attention="hip"``, ``nq_attention_decode``);
     4, 5. o_proj, its stage 2 adding the residual;
     6. gate and up stage 1 in one launch, post_attention_layernorm folded in;
     7. gate and up stage 2 in one launch storing silu(gate) * up;
@@ -434,8 +472,8 @@ class FusedDecoder(GraphDecoder):
         super().__init__(model, batch, max_len, steps_per_graph, device)
         from . import _lib
 
-        if attention not in ("torch", "hip"):
-            raise ValueError(f"attention must be 'torch' or 'hip', got {attention!r}")
+        if attention not in ("torch", "rope", "hip"):
+            raise ValueError(f"attention must be 'torch', 'rope' or 'hip', got {attention!r}")
         self.attention = attention
 
         self._lib = _lib
@@ -457,6 +495,7 @@ class FusedDecoder(GraphDecoder):
         self.h = torch.zeros(batch, s.hidden, device=dev, dtype=dt)
         self.qkv = torch.zeros(batch, self.qkv_width, device=dev, dtype=dt)
         self.attn = torch.zeros(batch, H * D, device=dev, dtype=dt)
+        self.q_rot = torch.zeros(batch, H * D, device=dev, dtype=dt)
         self.act = torch.zeros(batch, s.ffn, device=dev, dtype=dt)
         cos, sin = model.rope(torch.arange(max_len, device=dev), dt)
         self.rope_cos, self.rope_sin = cos.contiguous(), sin.contiguous()
@@ -529,6 +568,8 @@ class FusedDecoder(GraphDecoder):
             tables = rotary_step_tables(self.rope_cos.index_select(0, self.pos),
                                         self.rope_sin.index_select(0, self.pos), self.pos, self.cache,
                                         self.model.dtype)
+        elif self.attention == "rope":
+            madd = causal_mask_table(self.pos, self.cache, self.model.dtype)
         x, h, qkv, attn, act = (t.data_ptr() for t in (self.x, self.h, self.qkv, self.attn, self.act))
         esz = self.qkv.element_size()
         for li, plan in enumerate(self.plans):
@@ -541,10 +582,17 @@ class FusedDecoder(GraphDecoder):
                     self.cache.k[li].data_ptr(), self.cache.v[li].data_ptr(), self.rope_cos.data_ptr(),
                     self.rope_sin.data_ptr(), self.pos.data_ptr(), attn, B, H, KV, D, self.max_len,
                     D ** -0.5, self.attn_ws.data_ptr(), self.attn_ws.numel(), st), "attention")
+            elif self.attention == "rope":
+                self._check(lib.nq_rope_kv_write(
+                    dt, qkv, self.qkv_width, self.cache.k[li].data_ptr(), self.cache.v[li].data_ptr(),
+                    self.rope_cos.data_ptr(), self.rope_sin.data_ptr(), self.pos.data_ptr(), self.q_rot.data_ptr(),
+                    H * D, B, H, KV, D, self.max_len, st), "rope")
+                attention_products_step(s, li, self.q_rot, madd, self.cache, self.attn)
             else:
                 out = rotary_attention_step(s, li, self.qkv[:, :(H + KV) * D], self.qkv[:, (H + KV) * D:], tables,
-                                            self.pos, self.cache)
-                self.attn.copy_(out.view(B, H * D))
+                                            self.pos, self.cache, out=self.attn)
+                if out.data_ptr() != self.attn.data_ptr():
+                    self.attn.copy_(out.view(B, H * D))
             items, n = plan["o"]
             self._check(lib.nq_gemv_group_stage1(dt, n, items, attn, B, H * D, -1.0, ws, wsb, st), "o 1")
             self._check(lib.nq_gemv_group_stage2(dt, n, items, B, self._lib.NQ_EPI_RESIDUAL, ws, wsb, st), "o 2")

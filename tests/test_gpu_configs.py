@@ -171,14 +171,15 @@ def _tokens(decoder_cls, model, prompt, steps, use_graph, **kw):
     return dec.ids[:, :prompt.shape[1] + steps + 1].cpu()
 
 
-@pytest.mark.parametrize("step", ["unfused", "fused_torch_attention", "fused_hip_attention"])
+@pytest.mark.parametrize("step", ["unfused", "fused_torch_attention", "fused_rope_kernel", "fused_hip_attention"])
 def test_llama7b_graph_replay_equals_eager(llama7b, step):
     from nanoquant_amd.decode import FusedDecoder, GraphDecoder
     model, prompt = llama7b
     announce("llama-2-7b decode, graph vs eager", step, E2E_STEPS)
     cls, kw = GraphDecoder, {}
     if step != "unfused":
-        cls, kw = FusedDecoder, {"attention": "torch" if step == "fused_torch_attention" else "hip"}
+        cls, kw = FusedDecoder, {"attention": {"fused_torch_attention": "torch", "fused_rope_kernel": "rope",
+                                               "fused_hip_attention": "hip"}[step]}
     graph_ids = _tokens(cls, model, prompt, E2E_STEPS, True, **kw)
     eager_ids = _tokens(cls, model, prompt, E2E_STEPS, False, **kw)
     assert torch.equal(graph_ids, eager_ids)
@@ -194,11 +195,12 @@ def test_llama7b_fused_first_step_logits(llama7b):
     first = []
     for make in (lambda: GraphDecoder(model, 1, prompt.shape[1] + 2),
                  lambda: FusedDecoder(model, 1, prompt.shape[1] + 2, attention="torch"),
-                 lambda: FusedDecoder(model, 1, prompt.shape[1] + 2, attention="hip")):
+                 lambda: FusedDecoder(model, 1, prompt.shape[1] + 2, attention="hip"),
+                 lambda: FusedDecoder(model, 1, prompt.shape[1] + 2, attention="rope")):
         dec = make()
         dec.prefill(prompt)
         first.append(dec.decode(1, use_graph=False).double().cpu())
-    for name, other in (("torch attention", first[1]), ("hip attention", first[2])):
+    for name, other in (("torch attention", first[1]), ("hip attention", first[2]), ("rope kernel", first[3])):
         rel = float((other - first[0]).abs().max() / first[0].abs().max())
         print(f"[decode] fused ({name}) vs unfused first-step logits rel {rel:.3e}", flush=True)
         assert rel <= FUSED_FIRST_STEP_TOL, (name, rel)

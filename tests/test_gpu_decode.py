@@ -139,7 +139,7 @@ def run_fused(model, prompt, new, use_graph, steps_per_graph=1, attention="torch
     return dec.ids[:, :T + new].cpu(), [lg.cpu() for lg in logits]
 
 
-@pytest.mark.parametrize("attention", ["torch", "hip"])
+@pytest.mark.parametrize("attention", ["torch", "rope", "hip"])
 @pytest.mark.parametrize("name", list(FUSED_SHAPES))
 def test_fused_decode_matches_dense(name, attention):
     shape = FUSED_SHAPES[name]
@@ -201,3 +201,50 @@ def test_attention_step_against_rotary_attention(heads, kv_heads, pos):
         assert rel <= 2e-3, (layer, rel)
         assert torch.equal(caches[1].v[layer], caches[0].v[layer])
         assert k_rel <= 2e-3, (layer, k_rel)  # RoPE rounded once (product) against three times (elementwise)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("B,heads,kv_heads,D,pos", [(1, 32, 32, 128, 130), (2, 8, 2, 128, 0), (3, 4, 1, 64, 63),
+                                                    (2, 4, 2, 128, 400)])
+def test_rope_kv_write_against_torch(dtype, B, heads, kv_heads, D, pos):
+    """nq_rope_kv_write against the elementwise torch rotary embedding (x * cos + rotate_half(x) *
+    sin, each product and the sum rounded to the dtype, as rotary_attention runs it) and the cache
+    rows torch's index_copy_ writes: bit for bit, every other cache row untouched; a position past
+    the cache (pos = 400 with 384 rows) zeroes q and writes no row."""
+    from nanoquant_amd import _lib
+    from nanoquant_amd.decode import _rotate_half
+    lib = _lib.load()
+    announce("rope kv write", dtype, (B, heads, kv_heads, D, pos))
+    L = 384
+    gen = torch.Generator(device="cuda").manual_seed(B * 1000 + heads + pos)
+    width = (heads + 2 * kv_heads) * D + 8  # a padded row
+    qkv = (torch.randn(B, width, device="cuda", generator=gen) * 2).to(dtype)
+    k_cache = torch.randn(B, kv_heads, L, D, device="cuda", generator=gen).to(dtype)
+    v_cache = torch.randn(B, kv_heads, L, D, device="cuda", generator=gen).to(dtype)
+    inv = 1.0 / (10000.0 ** (torch.arange(0, D, 2, device="cuda").float() / D))
+    ang = torch.arange(L, device="cuda").float()[:, None] * inv[None, :]
+    emb = torch.cat((ang, ang), dim=-1)
+    cos, sin = emb.cos().to(dtype).contiguous(), emb.sin().to(dtype).contiguous()
+    position = torch.tensor([pos], device="cuda", dtype=torch.int64)
+    q_out = torch.full((B, heads * D), 7.0, device="cuda", dtype=dtype)
+    k0, v0 = k_cache.clone(), v_cache.clone()
+    _lib.check(lib.nq_rope_kv_write(_lib.dtype_code(dtype), qkv.data_ptr(), width, k_cache.data_ptr(),
+                                    v_cache.data_ptr(), cos.data_ptr(), sin.data_ptr(), position.data_ptr(),
+                                    q_out.data_ptr(), heads * D, B, heads, kv_heads, D, L,
+                                    torch.cuda.current_stream().cuda_stream), "rope")
+    torch.cuda.synchronize()
+    if pos >= L:
+        assert torch.equal(q_out, torch.zeros_like(q_out))
+        assert torch.equal(k_cache, k0) and torch.equal(v_cache, v0)
+        return
+    c, s_ = cos[pos], sin[pos]
+    q = qkv[:, :heads * D].reshape(B, heads, D)
+    k = qkv[:, heads * D:(heads + kv_heads) * D].reshape(B, kv_heads, D)
+    v = qkv[:, (heads + kv_heads) * D:(heads + 2 * kv_heads) * D].reshape(B, kv_heads, D)
+    q_ref = q * c + _rotate_half(q) * s_
+    k_ref = k * c + _rotate_half(k) * s_
+    assert torch.equal(q_out.view(B, heads, D), q_ref)
+    k0[:, :, pos] = k_ref
+    v0[:, :, pos] = v
+    assert torch.equal(k_cache, k0)
+    assert torch.equal(v_cache, v0)
