@@ -197,6 +197,21 @@ int nq_gemv_group_stage1(int dtype, int64_t count, const nq_gemv_item* items, co
 int nq_gemv_group_stage2(int dtype, int64_t count, const nq_gemv_item* items, int64_t batch, int epilogue,
                          void* workspace, size_t workspace_bytes, nq_stream_t stream);
 
+/* Stage 2 of the q, k and v projections of a decode step (items[0..2], after nq_gemv_group_stage1
+ * over the same three items) with the rotary embedding and the KV-cache write folded into the
+ * store: each projection output is rounded to dtype as NQ_EPI_STORE rounds it, then q is rotated
+ * into items[0].y, k is rotated into k_cache[b, kvh, p, :] and v copied into v_cache[b, kvh, p, :]
+ * ([batch, items[1].m / head_dim, max_len, head_dim] each), p = *position (device int64, read when
+ * the kernel runs, so a graph replays it). rope_cos/rope_sin [max_len, head_dim]; the rotation is
+ * nq_rope_kv_write's, bit for bit (outputs equal nq_gemv_group_stage2 with NQ_EPI_STORE followed by
+ * nq_rope_kv_write). head_dim a multiple of 16; every m a multiple of head_dim; items[1].m ==
+ * items[2].m. y of items 1 and 2 is not written (any valid pointer). A position outside
+ * [0, max_len) zeroes q and writes no cache row. No counterpart in the reference (its decode step
+ * runs Hugging Face's rotary embedding and cache update, kernel/test_decode.py:385-402). */
+int nq_gemv_group_stage2_rope(int dtype, const nq_gemv_item* items, int64_t batch, void* k_cache, void* v_cache,
+                              const void* rope_cos, const void* rope_sin, const int64_t* position, int64_t head_dim,
+                              int64_t max_len, void* workspace, size_t workspace_bytes, nq_stream_t stream);
+
 /* ---------------------------------------------------------------- prefill GEMM */
 
 /* C[M, N] = sat((A[M, K] * W) * s_out) with W[k, o] = sign(k, o) * s_in[k]:

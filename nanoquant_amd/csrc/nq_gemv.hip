@@ -240,7 +240,7 @@ struct S1Item {
     uint16_t* z_hi;
     uint16_t* z_lo;
     int r, kpad, zpitch;
-    int block_begin;  // first blockIdx.x of the item
+    int blocks;  // blockIdx.x < blocks do the item's rows (each item has a grid plane, blockIdx.z)
 };
 
 struct S1Table {
@@ -257,29 +257,44 @@ struct S2Item {
     const uint16_t* z_lo;
     int m, wr, zpitch;
     int ystride;  // elements between batch rows of y and resid
-    int block_begin;
+    int blocks;  // blockIdx.x < blocks do the item's rows (each item has a grid plane, blockIdx.z)
+    int rope;         // kEpiRope: 1 rotate into y (queries), 2 rotate into cache (keys), 3 copy into cache (values)
+    uint16_t* cache;  // kEpiRope, kinds 2 and 3: [batch, m / head_dim, max_len, head_dim]
+};
+
+// The rotary step of kEpiRope: position p = *pos (device), cos/sin rows [max_len, head_dim].
+struct S2Rope {
+    const int64_t* pos;
+    const uint16_t* cos;
+    const uint16_t* sin;
+    int head_dim, max_len;
 };
 
 struct S2Table {
     S2Item item[kMaxItems];
     int count;
+    S2Rope rope;
 };
 
 // Stage-2 epilogues: y = sat(s_out * acc); y = resid + that (rounded as two T operations);
 // gated pair (items 0 and 1 over the same rows): y0 = silu(gate) * up, each a T value;
-// kEpiStoreOne is kEpiStore for a one-item table (no item lookup).
-enum Epilogue { kEpiStore = 0, kEpiResidual = 1, kEpiGated = 2, kEpiStoreOne = 3 };
+// kEpiStoreOne is kEpiStore for a one-item table (no item lookup); kEpiRope: the q, k, v
+// projections of a decode step with the rotary embedding at position p applied to q and k, q stored
+// to y, k and v written into their caches at row p.
+enum Epilogue { kEpiStore = 0, kEpiResidual = 1, kEpiGated = 2, kEpiStoreOne = 3, kEpiRope = 4 };
 
-// The item of this block. Every item is read with a constant index and the choice is a
-// select, so the kernel arguments come in one batch of scalar loads (an index computed from
-// loaded values would cost a second, dependent round of loads).
+// The item of this block: a table launch gives each item a grid plane of its own (blockIdx.z), so
+// the item's fields are one round of scalar loads at an offset known when the wave starts. (A
+// single plane, the item found by comparing blockIdx.x with the items' first blocks, took several
+// dependent rounds of scalar loads: ~0.5-0.8 us of each launch.) Blocks of a plane past the item's
+// own count exit at once (item_done).
 template <typename Item, typename Table>
 __device__ inline Item pick_item(const Table& tab) {
-    Item it = tab.item[0];
-#pragma unroll
-    for (int i = 1; i < kMaxItems; ++i)
-        if (i < tab.count && static_cast<int>(blockIdx.x) >= tab.item[i].block_begin) it = tab.item[i];
-    return it;
+    return tab.item[blockIdx.z];
+}
+template <typename Item>
+__device__ inline bool item_done(const Item& it) {
+    return static_cast<int>(blockIdx.x) >= it.blocks;
 }
 
 // --------------------------------------------------------------------------- stage 1, VALU rows
@@ -312,8 +327,9 @@ __global__ __launch_bounds__(G * WR * 64) void s1w_kernel(const S1Table tab, con
     const int grp = wave / WR;
     const int p = (wave % WR) * 64 + lane;
     const S1Item it = kOne ? tab.item[0] : pick_item<S1Item>(tab);
+    if (!kOne && item_done(it)) return;
     const int r = it.r;
-    const int j0 = (static_cast<int>(blockIdx.x) - it.block_begin) * kRows + grp * R;
+    const int j0 = static_cast<int>(blockIdx.x) * kRows + grp * R;
     const int b0 = blockIdx.y * NB;
     NQ_STAMP(0);
 
@@ -459,7 +475,7 @@ __global__ __launch_bounds__(G * WR * 64) void s1w_kernel(const S1Table tab, con
             }
         }
     }
-    if (static_cast<int>(blockIdx.x) == it.block_begin) zero_h_pad(it.z_hi, it.z_lo, it.zpitch, it.kpad, b0, NB, batch);
+    if (blockIdx.x == 0) zero_h_pad(it.z_hi, it.z_lo, it.zpitch, it.kpad, b0, NB, batch);
     NQ_STAMP(3);
 }
 
@@ -504,8 +520,9 @@ __global__ __launch_bounds__(G * WR * 64) void s1l_kernel(const S1Table tab, con
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int grp = wave / WR, h = wave % WR;
     const S1Item it = kOne ? tab.item[0] : pick_item<S1Item>(tab);
+    if (!kOne && item_done(it)) return;
     const int r = it.r;
-    const int j0 = (static_cast<int>(blockIdx.x) - it.block_begin) * (G * R) + grp * R;
+    const int j0 = static_cast<int>(blockIdx.x) * (G * R) + grp * R;
     const int zslot = s1l_zero_slot(wn);
     NQ_STAMP(0);
 
@@ -611,7 +628,7 @@ __global__ __launch_bounds__(G * WR * 64) void s1l_kernel(const S1Table tab, con
             if (j < it.kpad) store_h(it.z_hi, it.z_lo, it.zpitch, 0, j, j < r ? v * mf : 0.0f);
         }
     }
-    if (static_cast<int>(blockIdx.x) == it.block_begin) zero_h_pad(it.z_hi, it.z_lo, it.zpitch, it.kpad, 0, 1, 1);
+    if (blockIdx.x == 0) zero_h_pad(it.z_hi, it.z_lo, it.zpitch, it.kpad, 0, 1, 1);
     NQ_STAMP(3);
 }
 
@@ -645,8 +662,9 @@ __global__ __launch_bounds__(NW * 64) void s1m_kernel(const S1Table tab, const u
     const int c = lane & 15;
     const int g = lane >> 4;
     const S1Item it = kOne ? tab.item[0] : pick_item<S1Item>(tab);
+    if (!kOne && item_done(it)) return;
     const int r = it.r;
-    const int j0 = (static_cast<int>(blockIdx.x) - it.block_begin) * 16 * RT;
+    const int j0 = static_cast<int>(blockIdx.x) * 16 * RT;
     const int b0 = blockIdx.y * 16;
     const uint16_t* xrow = x + static_cast<uint32_t>(min(b0 + c, batch - 1)) * static_cast<uint32_t>(n);
     const bool b_ok = b0 + c < batch;
@@ -767,7 +785,7 @@ __global__ __launch_bounds__(NW * 64) void s1m_kernel(const S1Table tab, const u
             }
         }
     }
-    if (static_cast<int>(blockIdx.x) == it.block_begin) zero_h_pad(it.z_hi, it.z_lo, it.zpitch, it.kpad, b0, 16, batch);
+    if (blockIdx.x == 0) zero_h_pad(it.z_hi, it.z_lo, it.zpitch, it.kpad, b0, 16, batch);
 }
 
 // --------------------------------------------------------------------------- stage 2, MFMA
@@ -822,17 +840,38 @@ __global__ __launch_bounds__(256) void s2t_kernel(const S2Table tab, int batch) 
     S2Item its[P];
     its[0] = (EPI == kEpiGated || EPI == kEpiStoreOne) ? tab.item[0] : pick_item<S2Item>(tab);
     if (P == 2) its[P - 1] = tab.item[1];
+    if (EPI != kEpiGated && EPI != kEpiStoreOne && item_done(its[0])) return;
     const int m = its[0].m;
     const int wr = its[0].wr;  // gated items share m and wr
-    const int i0 = (static_cast<int>(blockIdx.x) - its[0].block_begin) * kRows;
+    const int i0 = static_cast<int>(blockIdx.x) * kRows;
     const int b0 = blockIdx.y * NB;
-    const int ie = i0 + 16 * min(wave, RT - 1);  // first row of the tile whose epilogue this wave may run
+    // kEpiRope: tile row r (< 16) holds feature d of a head's first half for r < 8 and its rotary
+    // partner d + head_dim / 2 for r >= 8, so the epilogue finds the partner of each value in the
+    // lane 32 away (rows 4g .. 4g+3 against 4(g ^ 2) ..): block bi of an item takes features
+    // head * head_dim + 8 j + (r % 8) + (r / 8) * head_dim / 2, head = bi / (head_dim / 16),
+    // j = bi % (head_dim / 16). Otherwise the tile's rows are rows i0 .. of U in order.
+    int f0 = i0, fhalf = 8;
+    if (EPI == kEpiRope) {
+        const int D = tab.rope.head_dim;
+        const int bi = static_cast<int>(blockIdx.x);
+        f0 = (bi / (D / 16)) * D + 8 * (bi % (D / 16));
+        fhalf = D / 2;
+    }
+    auto feat = [&](int r) { return f0 + (r & 7) + (r >> 3) * fhalf; };  // row of U of tile row r
+    const int re = 16 * min(wave, RT - 1);  // first tile row whose epilogue this wave may run
+    const int64_t p64 = EPI == kEpiRope ? *tab.rope.pos : 0;
     NQ_STAMP(0);
 
     // 1. every global load: the tiles' words as 16-byte pieces, h, the output scales
     const uint32_t total = static_cast<uint32_t>(m) * static_cast<uint32_t>(wr);
     const uint32_t vec_end = total & ~3u;  // the host guarantees total >= 4
-    const uint32_t base = static_cast<uint32_t>(i0) * static_cast<uint32_t>(wr);  // a multiple of 16
+    // tile word e is word e of U's run from row f0 for e < 8 wr, else word e - 8 wr of the run from
+    // row f0 + fhalf (one contiguous run from row i0 without kEpiRope); runs start at multiples of 8
+    // rows, so the 16-byte pieces below never straddle them
+    const uint32_t base1 = static_cast<uint32_t>(f0) * static_cast<uint32_t>(wr);
+    const uint32_t base2 = static_cast<uint32_t>(f0 + fhalf) * static_cast<uint32_t>(wr);
+    const uint32_t split = 8u * static_cast<uint32_t>(wr);
+    auto gword = [&](uint32_t e) { return e < split ? base1 + e : base2 + (e - split); };
     const int rows = min(kRows, m - i0);
     const int nwords = rows * wr;
     u32x4 pv[P][kUPieces];
@@ -863,14 +902,14 @@ __global__ __launch_bounds__(256) void s2t_kernel(const S2Table tab, int batch) 
 #pragma unroll
     for (int pi = 0; pi < P; ++pi)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) so[pi][i] = its[pi].s_out[min(ie + 4 * g + i, m - 1)];
+        for (int i = 0; i < 4; ++i) so[pi][i] = its[pi].s_out[min(feat(re + 4 * g + i), m - 1)];
     // the residual of this lane's outputs (batch row b0 + c/2, rows i0 + 4g + i)
     uint16_t res[4] = {0, 0, 0, 0};
     if (EPI == kEpiResidual) {
         const uint32_t rb = static_cast<uint32_t>(min(b0 + min(c >> 1, NB - 1), batch - 1));
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            res[i] = its[0].resid[rb * static_cast<uint32_t>(its[0].ystride) + min(ie + 4 * g + i, m - 1)];
+            res[i] = its[0].resid[rb * static_cast<uint32_t>(its[0].ystride) + min(feat(re + 4 * g + i), m - 1)];
     }
     // pieces past the block's run are not needed: their offset lies past the resource, so they load
     // nothing (zeros)
@@ -881,9 +920,22 @@ __global__ __launch_bounds__(256) void s2t_kernel(const S2Table tab, int batch) 
 #pragma unroll
         for (int k = 0; k < kUPieces; ++k) {
             const int e4 = 4 * (t + k * kThr);
-            pv[pi][k] = load_b128_stream(u_rs, e4 < nwords ? (base + static_cast<uint32_t>(e4)) * 4u : vec_end * 4u);
+            pv[pi][k] = load_b128_stream(u_rs, e4 < nwords ? gword(static_cast<uint32_t>(e4)) * 4u : vec_end * 4u);
         }
         tail_word[pi] = it.u_bits[min(vec_end + static_cast<uint32_t>(t), total - 1u)];  // words past vec_end
+    }
+    // the rotary cos/sin entries of this lane's epilogue rows (row p of the tables; p outside the
+    // tables reads row 0, and those values are never used)
+    uint16_t rcos[4] = {0, 0, 0, 0}, rsin[4] = {0, 0, 0, 0};
+    if (EPI == kEpiRope) {
+        const int D = tab.rope.head_dim;
+        const size_t prow = p64 >= 0 && p64 < tab.rope.max_len ? static_cast<size_t>(p64) * D : 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int d = feat(re + 4 * g + i) % D;
+            rcos[i] = tab.rope.cos[prow + d];
+            rsin[i] = tab.rope.sin[prow + d];
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -919,11 +971,15 @@ __global__ __launch_bounds__(256) void s2t_kernel(const S2Table tab, int batch) 
 #pragma unroll
         for (int k = 0; k < kUPieces; ++k) {
             const int e4 = 4 * (t + k * kThr);
-            if (e4 < nwords && base + e4 + 4 <= vec_end) *reinterpret_cast<u32x4*>(tile[pi] + e4) = pv[pi][k];
+            if (e4 < nwords && gword(static_cast<uint32_t>(e4)) + 4 <= vec_end)
+                *reinterpret_cast<u32x4*>(tile[pi] + e4) = pv[pi][k];
         }
         if (t < 3) {
             const uint32_t w = vec_end + t;
-            if (w < total && w >= base && w < base + nwords) tile[pi][w - base] = tail_word[pi];
+            const uint32_t n1 = min(split, static_cast<uint32_t>(nwords));
+            if (w < total && w >= base1 && w < base1 + n1) tile[pi][w - base1] = tail_word[pi];
+            else if (w < total && nwords > static_cast<int>(split) && w >= base2 && w < base2 + (nwords - split))
+                tile[pi][split + (w - base2)] = tail_word[pi];
         }
     }
     __syncthreads();
@@ -1008,7 +1064,32 @@ __global__ __launch_bounds__(256) void s2t_kernel(const S2Table tab, int batch) 
                 const float lo = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v[pi][i]), 0xB1, 0xF, 0xF, false));
                 out[pi] = (v[pi][i] + lo) * T::to_float(so[pi][i]);
             }
-            const int row = ie + 4 * g + i;
+            const int row = feat(re + 4 * g + i);
+            if (EPI == kEpiRope) {
+                // q and k rotated as the unfused path rounds it: T(x cos) + T(rotate_half(x) sin), the
+                // partner value from the lane 32 away (every lane takes part in the exchange)
+#pragma clang fp contract(off)
+                const S2Item& it = its[0];
+                const int D = tab.rope.head_dim;
+                const uint16_t val = saturate_to<T>(out[0], T::SAT);
+                const float x = T::to_float(val);
+                const float xp = __shfl_xor(x, 32, 64);
+                const int d = row % D;
+                const float xr = d < D / 2 ? -xp : xp;
+                const uint16_t rot = T::from_float(T::to_float(T::from_float(x * T::to_float(rcos[i]))) +
+                                                   T::to_float(T::from_float(xr * T::to_float(rsin[i]))));
+                const bool p_ok = p64 >= 0 && p64 < tab.rope.max_len;
+                if (b_ok && row < m) {
+                    if (it.rope == 1) {
+                        its[0].y[static_cast<size_t>(b0 + bcol) * its[0].ystride + row] = p_ok ? rot : uint16_t(0);
+                    } else if (p_ok) {
+                        const size_t at = ((static_cast<size_t>(b0 + bcol) * (m / D) + row / D) * tab.rope.max_len +
+                                           static_cast<size_t>(p64)) * D + d;
+                        it.cache[at] = it.rope == 2 ? rot : val;
+                    }
+                }
+                continue;
+            }
             if (b_ok && row < m) {
                 uint16_t val = saturate_to<T>(out[0], T::SAT);
                 if (EPI == kEpiResidual) {
@@ -1659,7 +1740,8 @@ inline S1wShape s1w_shape(int wn) {
 template <typename T, int NB, bool kNorm, bool kOne>
 void launch_s1w_cfg(const S1wShape& sh, const S1Table& tab, int blocks, const uint16_t* x, int batch, int n, int wn,
                     float eps, hipStream_t st) {
-    const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(ceil_div(batch, NB)));
+    const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(ceil_div(batch, NB)),
+                    static_cast<unsigned>(tab.count));
 #define NQ_S1W_CASE(WPL, WR, R, G)                                                                        \
     if (sh.wpl == WPL && sh.wr == WR && sh.r == R && sh.g == G) {                                         \
         s1w_kernel<T, NB, WPL, WR, R, G, kNorm, kOne><<<grid, G * WR * 64, 0, st>>>(tab, x, batch, n, wn, eps); \
@@ -1681,6 +1763,17 @@ void launch_s1w_nb(const S1wShape& sh, const S1Table& tab, int blocks, const uin
     }
 }
 
+// One grid plane per item of a stage-1 table, `rows` rows per block: each item's own block count;
+// returns the planes' width (the largest count).
+inline int item_planes(S1Table& tab, int rows) {
+    int blocks = 0;
+    for (int k = 0; k < tab.count; ++k) {
+        tab.item[k].blocks = static_cast<int>(ceil_div(tab.item[k].kpad, rows));
+        blocks = std::max(blocks, tab.item[k].blocks);
+    }
+    return blocks;
+}
+
 // Launch shapes of s1l_kernel (words per lane, rows per wave, groups, waves per group), the
 // fastest of a sweep of 14 on the GEMV shapes of each width (n = 4096 / 8192 / 11008).
 struct S1lShape {
@@ -1699,7 +1792,8 @@ void launch_s1l_cfg(const S1lShape& sh, const S1Table& tab, int blocks, const ui
     const size_t lds = s1l_lds_bytes(wn);
 #define NQ_S1L_CASE(WPL, R, G, WR)                                                                           \
     if (sh.wpl == WPL && sh.r == R && sh.g == G && sh.wr == WR) {                                            \
-        s1l_kernel<T, WPL, R, G, WR, kNorm, kOne><<<blocks, G * WR * 64, lds, st>>>(tab, x, n, wn, eps);     \
+        s1l_kernel<T, WPL, R, G, WR, kNorm, kOne>                                                           \
+            <<<dim3(blocks, 1, tab.count), G * WR * 64, lds, st>>>(tab, x, n, wn, eps);                      \
         return;                                                                                              \
     }
     NQ_S1L_CASE(1, 2, 4, 1)
@@ -1721,11 +1815,7 @@ void launch_s1w_table(S1Table& tab, const uint16_t* x, int batch, int n, int wn,
                       hipStream_t st) {
     if (s1l_applies(batch, n, wn)) {
         const S1lShape sh = s1l_shape(wn);
-        int blocks = 0;
-        for (int k = 0; k < tab.count; ++k) {
-            tab.item[k].block_begin = blocks;
-            blocks += static_cast<int>(ceil_div(tab.item[k].kpad, sh.r * sh.g));
-        }
+        const int blocks = item_planes(tab, sh.r * sh.g);
         if (tab.count == 1) {
             if (norm) launch_s1l_cfg<T, true, true>(sh, tab, blocks, x, n, wn, eps, st);
             else launch_s1l_cfg<T, false, true>(sh, tab, blocks, x, n, wn, eps, st);
@@ -1736,12 +1826,7 @@ void launch_s1w_table(S1Table& tab, const uint16_t* x, int batch, int n, int wn,
         return;
     }
     const S1wShape sh = s1w_shape(wn);
-    const int rpb = sh.r * sh.g;
-    int blocks = 0;
-    for (int k = 0; k < tab.count; ++k) {
-        tab.item[k].block_begin = blocks;
-        blocks += static_cast<int>(ceil_div(tab.item[k].kpad, rpb));
-    }
+    const int blocks = item_planes(tab, sh.r * sh.g);
     if (batch <= 1) launch_s1w_nb<T, 1>(sh, tab, blocks, x, batch, n, wn, norm, eps, st);
     else launch_s1w_nb<T, 2>(sh, tab, blocks, x, batch, n, wn, norm, eps, st);
 }
@@ -1833,14 +1918,11 @@ void launch_s1m_table(S1Table& tab, const uint16_t* x, int batch, int n, int wn,
                       hipStream_t st, int rt = 0) {
     if (rt == 0) rt = s1m_row_tiles(tab, batch, n, wn);
     if (rt == 4 && !s1m_sin_lds(n, wn, 4)) rt = 2;  // the only four-row-tile variant keeps s_in in LDS
-    int blocks = 0;
-    for (int k = 0; k < tab.count; ++k) {
-        tab.item[k].block_begin = blocks;
-        blocks += static_cast<int>(ceil_div(tab.item[k].kpad, 16 * rt));
-    }
+    const int blocks = item_planes(tab, 16 * rt);
     // 16 waves per block: a 4096-wide row is one round of loads per wave (latency, not bytes, is
     // what a decode-size stage pays for)
-    const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(ceil_div(batch, 16)));
+    const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(ceil_div(batch, 16)),
+                    static_cast<unsigned>(tab.count));
     if (rt == 4) launch_s1m_nw<T, 16, 4>(tab, grid, x, batch, n, wn, norm, eps, st);
     else if (rt == 2) launch_s1m_nw<T, 16, 2>(tab, grid, x, batch, n, wn, norm, eps, st);
     else launch_s1m_nw<T, 16, 1>(tab, grid, x, batch, n, wn, norm, eps, st);
@@ -1886,7 +1968,7 @@ inline S1Item s1_item_of(const GemvArgs& a) {
     it.r = a.r;
     it.kpad = a.plan.kpad;
     it.zpitch = a.plan.zpitch;
-    it.block_begin = 0;
+    it.blocks = 0;
     return it;
 }
 
@@ -2033,14 +2115,16 @@ void launch_s2t_table(S2Table& tab, int batch, hipStream_t st) {
     // row tiles per block (the gated pair stays at one: it runs two items already)
     int64_t tiles = 0;
     for (int k = 0; k < (EPI == kEpiGated ? 1 : tab.count); ++k) tiles += ceil_div(tab.item[k].m, 16);
-    const int rt = EPI == kEpiGated ? 1 : s2t_row_tiles(nb, QW, tiles, ceil_div(batch, nb));
+    const int rt = EPI == kEpiGated || EPI == kEpiRope ? 1 : s2t_row_tiles(nb, QW, tiles, ceil_div(batch, nb));
+    // one grid plane per item (a gated pair runs item 1 inside item 0's blocks)
+    const int items = EPI == kEpiGated ? 1 : tab.count;
     int blocks = 0;
-    const int items = EPI == kEpiGated ? 1 : tab.count;  // a gated pair runs item 1 inside item 0's blocks
-    for (int k = 0; k < items; ++k) {
-        tab.item[k].block_begin = blocks;
-        blocks += static_cast<int>(ceil_div(tab.item[k].m, 16 * rt));
+    for (int k = 0; k < tab.count; ++k) {
+        tab.item[k].blocks = static_cast<int>(ceil_div(tab.item[k].m, 16 * rt));
+        blocks = std::max(blocks, tab.item[k].blocks);
     }
-    const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(ceil_div(batch, nb)));
+    const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(ceil_div(batch, nb)),
+                    static_cast<unsigned>(items));
     if (nb == 1) launch_s2t_nb<T, QW, 1, EPI, 1>(tab, grid, batch, st);
     else if constexpr (EPI == kEpiGated) {
         if (nb == 2) launch_s2t_nb<T, QW, 2, EPI, 1>(tab, grid, batch, st);
@@ -2167,7 +2251,7 @@ int launch_stage2(const GemvArgs& a) {
         it.wr = a.plan.wr;
         it.zpitch = a.plan.zpitch;
         it.ystride = a.m;
-        it.block_begin = 0;
+        it.blocks = 0;
         if (launch_s2t_qw<T, kEpiStoreOne>(tab, a.plan.s2_qw, a.batch, a.stream)) return NQ_OK;
     }
     if (a.batch <= 1) launch_stage2_generic<T, 1>(a);
@@ -2472,7 +2556,7 @@ int nq_gemv_group_stage1(int dtype, int64_t count, const nq_gemv_item* items, co
         it.r = static_cast<int>(in.r);
         it.kpad = g.plan[k].kpad;
         it.zpitch = g.plan[k].zpitch;
-        it.block_begin = 0;
+        it.blocks = 0;
     }
     const bool norm = rms_eps >= 0.0f;
     if (dtype == NQ_F16)
@@ -2484,13 +2568,74 @@ int nq_gemv_group_stage1(int dtype, int64_t count, const nq_gemv_item* items, co
     return check_launch(name);
 }
 
+}  // extern "C"
+
+namespace nq {
+namespace {
+
+// The group stage 2 with any epilogue; `rope` (kEpiRope only) carries the rotary step and the caches.
+struct RopeArgs {
+    S2Rope rope;
+    uint16_t* k_cache;
+    uint16_t* v_cache;
+};
+
+int group_stage2(const char* name, int dtype, int64_t count, const nq_gemv_item* items, int64_t batch, int epilogue,
+                 const RopeArgs* rope, void* workspace, size_t workspace_bytes, nq_stream_t stream);
+
+}  // namespace
+}  // namespace nq
+
+extern "C" {
+
 int nq_gemv_group_stage2(int dtype, int64_t count, const nq_gemv_item* items, int64_t batch, int epilogue,
                          void* workspace, size_t workspace_bytes, nq_stream_t stream) {
-    const char* name = "nq_gemv_group_stage2";
+    return group_stage2("nq_gemv_group_stage2", dtype, count, items, batch, epilogue, nullptr, workspace,
+                        workspace_bytes, stream);
+}
+
+int nq_gemv_group_stage2_rope(int dtype, const nq_gemv_item* items, int64_t batch, void* k_cache, void* v_cache,
+                              const void* rope_cos, const void* rope_sin, const int64_t* position, int64_t head_dim,
+                              int64_t max_len, void* workspace, size_t workspace_bytes, nq_stream_t stream) {
+    const char* name = "nq_gemv_group_stage2_rope";
+    if (!items) return fail(NQ_ERR_INVALID_ARGUMENT, "%s: null items", name);
+    if (head_dim < 16 || head_dim % 16 || max_len <= 0 || max_len > INT32_MAX / 2)
+        return fail(NQ_ERR_INVALID_ARGUMENT, "%s: head_dim must be a positive multiple of 16 and max_len positive",
+                    name);
+    for (int k = 0; k < 3; ++k)
+        if (items[k].m % head_dim)
+            return fail(NQ_ERR_SHAPE, "%s: item %d: m %lld is not whole heads of %lld", name, k,
+                        (long long)items[k].m, (long long)head_dim);
+    if (items[1].m != items[2].m) return fail(NQ_ERR_SHAPE, "%s: the key and value items differ in m", name);
+    if (batch > 0 && (!k_cache || !v_cache || !rope_cos || !rope_sin || !position))
+        return fail(NQ_ERR_INVALID_ARGUMENT, "%s: null pointer", name);
+    if (!aligned(k_cache, 2) || !aligned(v_cache, 2) || !aligned(rope_cos, 2) || !aligned(rope_sin, 2) ||
+        !aligned(position, 8))
+        return fail(NQ_ERR_ALIGNMENT, "%s: misaligned operand", name);
+    if (batch * (items[1].m / head_dim) * max_len * head_dim > ((int64_t)1 << 40))
+        return fail(NQ_ERR_UNSUPPORTED, "%s: caches too large", name);
+    RopeArgs ra;
+    ra.rope.pos = position;
+    ra.rope.cos = static_cast<const uint16_t*>(rope_cos);
+    ra.rope.sin = static_cast<const uint16_t*>(rope_sin);
+    ra.rope.head_dim = static_cast<int>(head_dim);
+    ra.rope.max_len = static_cast<int>(max_len);
+    ra.k_cache = static_cast<uint16_t*>(k_cache);
+    ra.v_cache = static_cast<uint16_t*>(v_cache);
+    return group_stage2(name, dtype, 3, items, batch, -1, &ra, workspace, workspace_bytes, stream);
+}
+
+}  // extern "C"
+
+namespace nq {
+namespace {
+
+int group_stage2(const char* name, int dtype, int64_t count, const nq_gemv_item* items, int64_t batch, int epilogue,
+                 const RopeArgs* rope, void* workspace, size_t workspace_bytes, nq_stream_t stream) {
     GroupLayout g;
     if (int s = group_layout(name, count, items, batch, workspace, g)) return s;
     if (int s = check_group_common(name, dtype, batch, workspace, workspace_bytes, g)) return s;
-    if (epilogue != NQ_EPI_STORE && epilogue != NQ_EPI_RESIDUAL && epilogue != NQ_EPI_GATED)
+    if (rope == nullptr && epilogue != NQ_EPI_STORE && epilogue != NQ_EPI_RESIDUAL && epilogue != NQ_EPI_GATED)
         return fail(NQ_ERR_INVALID_ARGUMENT, "%s: unknown epilogue %d", name, epilogue);
     if (epilogue == NQ_EPI_GATED && (count != 2 || items[0].m != items[1].m || items[0].r != items[1].r))
         return fail(NQ_ERR_SHAPE, "%s: the gated epilogue takes two items (gate, up) of equal m and r", name);
@@ -2521,7 +2666,9 @@ int nq_gemv_group_stage2(int dtype, int64_t count, const nq_gemv_item* items, in
         it.wr = g.plan[k].wr;
         it.zpitch = g.plan[k].zpitch;
         it.ystride = static_cast<int>(in.y_stride);
-        it.block_begin = 0;
+        it.blocks = 0;
+        it.rope = rope == nullptr ? 0 : static_cast<int>(k) + 1;  // q, k, v
+        it.cache = rope == nullptr ? nullptr : (k == 1 ? rope->k_cache : k == 2 ? rope->v_cache : nullptr);
     }
     // one launch per class of items that share the stage-2 word split (equal ranks always do)
     const int b = static_cast<int>(batch);
@@ -2532,13 +2679,17 @@ int nq_gemv_group_stage2(int dtype, int64_t count, const nq_gemv_item* items, in
         const int qw = g.plan[k0].s2_qw;
         S2Table tab;
         tab.count = 0;
+        tab.rope = rope != nullptr ? rope->rope : S2Rope{nullptr, nullptr, nullptr, 0, 0};
         for (int64_t k = k0; k < count; ++k)
             if (!done[k] && g.plan[k].s2_qw == qw) {
                 tab.item[tab.count++] = all[k];
                 done[k] = true;
             }
         bool ok;
-        if (dtype == NQ_F16) {
+        if (rope != nullptr) {
+            ok = dtype == NQ_F16 ? launch_s2t_qw<F16, kEpiRope>(tab, qw, b, st)
+                                 : launch_s2t_qw<BF16, kEpiRope>(tab, qw, b, st);
+        } else if (dtype == NQ_F16) {
             ok = epilogue == NQ_EPI_STORE      ? launch_s2t_qw<F16, kEpiStore>(tab, qw, b, st)
                  : epilogue == NQ_EPI_RESIDUAL ? launch_s2t_qw<F16, kEpiResidual>(tab, qw, b, st)
                                                : launch_s2t_qw<F16, kEpiGated>(tab, qw, b, st);
@@ -2553,4 +2704,5 @@ int nq_gemv_group_stage2(int dtype, int64_t count, const nq_gemv_item* items, in
     return NQ_OK;
 }
 
-}  // extern "C"
+}  // namespace
+}  // namespace nq

@@ -104,8 +104,9 @@ class RMSNorm(nn.Module):
         self.eps = eps
 
     def forward(self, x):
-        xf = x.float()
-        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
+        # x * rsqrt(mean(x^2) + eps) in fp32 (torch's fused RMS norm: one launch instead of five on
+        # the GPU, the same values), cast back, then the weight
+        xf = F.rms_norm(x.float(), (x.shape[-1],), eps=self.eps)
         return self.weight * xf.to(x.dtype)
 
 
@@ -176,20 +177,14 @@ def rotary_step_tables(cos, sin, positions, cache: StaticKVCache, dtype):
     return R.to(dtype), madd
 
 
-def causal_mask_table(positions, cache: StaticKVCache, dtype):
-    """The causal mask of a one-token step at ``positions`` (one position, on the device) as an
-    additive [1, L, 1]: 0 for visible cache rows, -inf past the position."""
-    visible = cache.key_index.view(1, -1, 1) <= positions.view(1, 1, 1)
-    return torch.zeros(visible.shape, device=positions.device, dtype=dtype).masked_fill_(~visible, float("-inf"))
-
-
 def attention_products_step(shape: LlamaShape, layer: int, q, madd, cache: StaticKVCache, out):
     """The attention products of a one-token step whose rotary embedding and cache write are done
     (``nq_rope_kv_write``): the scores of each kv head's query group against the cache with the scale
     and causal mask folded into one batched product, the softmax, and the value product written into
     ``out`` [B, H * D] (directly when each kv head serves one query head, else through a copy).
 
-    q [B, H * D] (rotated, contiguous); ``madd`` from ``causal_mask_table``."""
+    q [B, H * D] (rotated, contiguous); ``madd`` [1, L, 1]: the additive causal mask of the step's
+    position (0 for visible cache rows, -inf past it)."""
     H, KV, D = shape.heads, shape.kv_heads, shape.head_dim
     B, G = q.shape[0], H // KV
     k_c, v_c = cache.k[layer], cache.v[layer]
@@ -455,9 +450,9 @@ class FusedDecoder(GraphDecoder):
     2. q, k, v stage 2 in one launch, into one [B, (heads + 2 kv_heads) * head_dim] buffer;
     3. rotary embedding, KV-cache write and attention: in torch ops (``attention="torch"``, the
        default, as the benchmark's end-to-end configuration keeps the non-linear ops in
-       PyTorch), or the rotary embedding and cache write in one HIP launch (``nq_rope_kv_write``)
-       and the attention products in torch (``attention="rope"``), or all of it in one HIP launch
-       pair (``attention="hip"``, ``nq_attention_decode``);
+       PyTorch), or the rotary embedding and cache write folded into step 2's stores
+       (``nq_gemv_group_stage2_rope``) and the attention products in torch (``attention="rope"``),
+       or all of it in one HIP launch pair (``attention="hip"``, ``nq_attention_decode``);
     4, 5. o_proj, its stage 2 adding the residual;
     6. gate and up stage 1 in one launch, post_attention_layernorm folded in;
     7. gate and up stage 2 in one launch storing silu(gate) * up;
@@ -484,6 +479,8 @@ class FusedDecoder(GraphDecoder):
             raise ValueError(f"the fused decode step needs a float16 or bfloat16 model, got {dt}")
         if attention == "hip" and s.head_dim != 128:
             raise ValueError(f"the HIP attention of the fused decode step needs head_dim 128, got {s.head_dim}")
+        if attention == "rope" and s.head_dim % 16:
+            raise ValueError(f"the rotary store of the fused decode step needs head_dim % 16 == 0, got {s.head_dim}")
         for lin in model.linears():
             if getattr(lin, "kernel_type", None) != "gemv":
                 raise ValueError("the fused decode step needs every linear prepared for the 'gemv' kernel")
@@ -496,6 +493,10 @@ class FusedDecoder(GraphDecoder):
         self.qkv = torch.zeros(batch, self.qkv_width, device=dev, dtype=dt)
         self.attn = torch.zeros(batch, H * D, device=dev, dtype=dt)
         self.q_rot = torch.zeros(batch, H * D, device=dev, dtype=dt)
+        # the additive causal mask of every position (row p: 0 for cache rows <= p, -inf after)
+        rows = torch.arange(max_len, device=dev)
+        self.masks = torch.zeros(max_len, max_len, device=dev, dtype=dt).masked_fill_(
+            rows.view(1, -1) > rows.view(-1, 1), float("-inf"))
         self.act = torch.zeros(batch, s.ffn, device=dev, dtype=dt)
         cos, sin = model.rope(torch.arange(max_len, device=dev), dt)
         self.rope_cos, self.rope_sin = cos.contiguous(), sin.contiguous()
@@ -547,6 +548,9 @@ class FusedDecoder(GraphDecoder):
         return {
             "qkv": self._items([(a.q_proj, w1, self.qkv, 0, W, None), (a.k_proj, w1, self.qkv, H * D, W, None),
                                 (a.v_proj, w1, self.qkv, (H + KV) * D, W, None)]),
+            # the same three items with q stored rotated into q_rot (k and v go to the caches)
+            "qkv_rope": self._items([(a.q_proj, w1, self.q_rot, 0, H * D, None), (a.k_proj, w1, self.qkv, 0, W, None),
+                                     (a.v_proj, w1, self.qkv, 0, W, None)])[0],
             "o": self._items([(a.o_proj, None, self.h, 0, s.hidden, self.x)]),
             "gu": self._items([(mlp.gate_proj, w2, self.act, 0, s.ffn, None),
                                (mlp.up_proj, w2, self.act, 0, s.ffn, None)]),
@@ -569,13 +573,19 @@ class FusedDecoder(GraphDecoder):
                                         self.rope_sin.index_select(0, self.pos), self.pos, self.cache,
                                         self.model.dtype)
         elif self.attention == "rope":
-            madd = causal_mask_table(self.pos, self.cache, self.model.dtype)
+            madd = self.masks.index_select(0, self.pos).view(1, -1, 1)
         x, h, qkv, attn, act = (t.data_ptr() for t in (self.x, self.h, self.qkv, self.attn, self.act))
         esz = self.qkv.element_size()
         for li, plan in enumerate(self.plans):
             items, n = plan["qkv"]
             self._check(lib.nq_gemv_group_stage1(dt, n, items, x, B, s.hidden, plan["eps1"], ws, wsb, st), "qkv 1")
-            self._check(lib.nq_gemv_group_stage2(dt, n, items, B, self._lib.NQ_EPI_STORE, ws, wsb, st), "qkv 2")
+            if self.attention == "rope":
+                items_r = plan["qkv_rope"]
+                self._check(lib.nq_gemv_group_stage2_rope(
+                    dt, items_r, B, self.cache.k[li].data_ptr(), self.cache.v[li].data_ptr(), self.rope_cos.data_ptr(),
+                    self.rope_sin.data_ptr(), self.pos.data_ptr(), D, self.max_len, ws, wsb, st), "qkv 2 rope")
+            else:
+                self._check(lib.nq_gemv_group_stage2(dt, n, items, B, self._lib.NQ_EPI_STORE, ws, wsb, st), "qkv 2")
             if self.attention == "hip":
                 self._check(lib.nq_attention_decode(
                     dt, qkv, qkv + H * D * esz, qkv + (H + KV) * D * esz, self.qkv_width,
@@ -583,10 +593,6 @@ class FusedDecoder(GraphDecoder):
                     self.rope_sin.data_ptr(), self.pos.data_ptr(), attn, B, H, KV, D, self.max_len,
                     D ** -0.5, self.attn_ws.data_ptr(), self.attn_ws.numel(), st), "attention")
             elif self.attention == "rope":
-                self._check(lib.nq_rope_kv_write(
-                    dt, qkv, self.qkv_width, self.cache.k[li].data_ptr(), self.cache.v[li].data_ptr(),
-                    self.rope_cos.data_ptr(), self.rope_sin.data_ptr(), self.pos.data_ptr(), self.q_rot.data_ptr(),
-                    H * D, B, H, KV, D, self.max_len, st), "rope")
                 attention_products_step(s, li, self.q_rot, madd, self.cache, self.attn)
             else:
                 out = rotary_attention_step(s, li, self.qkv[:, :(H + KV) * D], self.qkv[:, (H + KV) * D:], tables,

@@ -261,3 +261,66 @@ def test_attention_position_outside_cache(lib):
     assert lib.nq_attention_decode(_lib.NQ_F16, p0, p0, p0, W, kc.data_ptr(), vc.data_ptr(), cs.data_ptr(),
                                    cs.data_ptr(), d_pos.data_ptr(), out.data_ptr(), B, H, KV, D, L, 0.1,
                                    ws.data_ptr(), 16, None) == _lib.NQ_ERR_WORKSPACE
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("B,heads,kv_heads,D,r_qkv,pos", [(1, 4, 4, 128, (96, 96, 96), 37), (2, 8, 2, 128, (160, 96, 96), 0),
+                                                          (3, 4, 1, 64, (64, 64, 64), 63), (1, 2, 2, 64, (96, 96, 96), 80)])
+def test_group_stage2_rope_equals_store_then_rope_kernel(lib, dtype, B, heads, kv_heads, D, r_qkv, pos):
+    """nq_gemv_group_stage2_rope (the q/k/v stage 2 with the rotary embedding and cache write in its
+    store) against nq_gemv_group_stage2 (NQ_EPI_STORE) followed by nq_rope_kv_write on the same
+    intermediate: q, the caches' new rows and every other cache row bit for bit; ranks equal and
+    unequal (two launches); a position past the cache (80 of 64 rows) zeroes q and writes no row."""
+    from nanoquant_amd import _lib
+    announce("group stage 2 rope", dtype, (B, heads, kv_heads, D, r_qkv, pos))
+    n, L = 256, 64
+    ms = (heads * D, kv_heads * D, kv_heads * D)
+    width = sum(ms)
+    rng = np.random.default_rng(B * 100 + heads + pos)
+    x = torch.from_numpy((rng.normal(size=(B, n)) * 2.0).astype(np.float16)).cuda().to(dtype)
+    keep, its_store, its_rope = [], [], []
+    qkv = torch.zeros(B, width, dtype=dtype, device="cuda")
+    q_rot = torch.full((B, heads * D), 3.0, dtype=dtype, device="cuda")
+    off = 0
+    for i, (m, r) in enumerate(zip(ms, r_qkv)):
+        c = make_linear(70 + i, m, n, r, with_mid=(i == 2))
+        V, U = words(c["V"]), words(c["U"])
+        s_in = torch.from_numpy(c["s_in"]).cuda().to(dtype)
+        s_out = torch.from_numpy(c["s_out"]).cuda().to(dtype)
+        s_mid = None if c["s_mid"] is None else torch.from_numpy(c["s_mid"]).cuda().to(dtype)
+        keep += [V, U, s_in, s_out, s_mid]
+        its_store.append(item(_lib, V, s_in, s_mid, U, s_out, qkv, off, width, None, r, m))
+        its_rope.append(item(_lib, V, s_in, s_mid, U, s_out, q_rot if i == 0 else qkv, 0,
+                             heads * D if i == 0 else width, None, r, m))
+        off += m
+    gen = torch.Generator(device="cuda").manual_seed(pos)
+    caches = [torch.randn(B, kv_heads, L, D, device="cuda", generator=gen).to(dtype) for _ in range(2)]
+    caches_ref = [t.clone() for t in caches]
+    inv = 1.0 / (10000.0 ** (torch.arange(0, D, 2, device="cuda").float() / D))
+    emb = torch.arange(L, device="cuda").float()[:, None] * inv[None, :]
+    emb = torch.cat((emb, emb), dim=-1)
+    cos, sin = emb.cos().to(dtype).contiguous(), emb.sin().to(dtype).contiguous()
+    position = torch.tensor([pos], dtype=torch.int64, device="cuda")
+    dc = _lib.dtype_code(dtype)
+    st = torch.cuda.current_stream().cuda_stream
+    arr_s = (_lib.GemvItem * 3)(*its_store)
+    arr_r = (_lib.GemvItem * 3)(*its_rope)
+    need = lib.nq_gemv_group_workspace_bytes(3, arr_s, B)
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    # reference: stage 1, stage 2 with plain stores, then the rotary kernel
+    _lib.check(lib.nq_gemv_group_stage1(dc, 3, arr_s, x.data_ptr(), B, n, -1.0, ws.data_ptr(), need, st), "s1")
+    _lib.check(lib.nq_gemv_group_stage2(dc, 3, arr_s, B, _lib.NQ_EPI_STORE, ws.data_ptr(), need, st), "s2")
+    q_ref = torch.full_like(q_rot, 3.0)
+    _lib.check(lib.nq_rope_kv_write(dc, qkv.data_ptr(), width, caches_ref[0].data_ptr(), caches_ref[1].data_ptr(),
+                                    cos.data_ptr(), sin.data_ptr(), position.data_ptr(), q_ref.data_ptr(),
+                                    heads * D, B, heads, kv_heads, D, L, st), "rope")
+    # fused: the same intermediate, stage 2 with the rotary store
+    _lib.check(lib.nq_gemv_group_stage2_rope(dc, arr_r, B, caches[0].data_ptr(), caches[1].data_ptr(),
+                                             cos.data_ptr(), sin.data_ptr(), position.data_ptr(), D, L,
+                                             ws.data_ptr(), need, st), "s2 rope")
+    torch.cuda.synchronize()
+    assert torch.equal(q_rot.view(torch.int16), q_ref.view(torch.int16))
+    assert torch.equal(caches[0].view(torch.int16), caches_ref[0].view(torch.int16))
+    assert torch.equal(caches[1].view(torch.int16), caches_ref[1].view(torch.int16))
+    if pos >= L:
+        assert torch.equal(q_rot, torch.zeros_like(q_rot))

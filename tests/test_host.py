@@ -71,6 +71,25 @@ def test_c_abi_argument_errors_need_no_gpu():
     # (2 + 128) floats per query head per 64-position chunk
     assert lib.nq_attention_decode_workspace_bytes(1, 32, 32, 128, 384) == 32 * 6 * 130 * 4
     assert lib.nq_attention_decode_workspace_bytes(1, 32, 32, 64, 384) == 0
+    # the rotary store of the q/k/v stage 2 and the standalone rotary kernel
+    qkv_items = (_lib.GemvItem * 3)()
+    for it, m in zip(qkv_items, (4096, 4096, 4096)):
+        it.r, it.m, it.y_stride = 1120, m, 12288
+    rope2 = lambda hd, L: lib.nq_gemv_group_stage2_rope(  # noqa: E731
+        0, qkv_items, 1, None, None, None, None, None, hd, L, None, 0, None)
+    assert rope2(120, 384) == _lib.NQ_ERR_INVALID_ARGUMENT  # head_dim not a multiple of 16
+    assert rope2(128, 0) == _lib.NQ_ERR_INVALID_ARGUMENT
+    assert rope2(128, 384) == _lib.NQ_ERR_INVALID_ARGUMENT  # null caches
+    qkv_items[2].m = 2048
+    assert rope2(128, 384) == _lib.NQ_ERR_SHAPE  # k and v differ
+    qkv_items[0].m = 4000
+    assert rope2(128, 384) == _lib.NQ_ERR_SHAPE  # q is not whole heads
+    rope = lambda dt, hd, stride: lib.nq_rope_kv_write(  # noqa: E731
+        dt, None, stride, None, None, None, None, None, None, 32 * hd, 1, 32, 32, hd, 384, None)
+    assert rope(9, 128, 96 * 128) == _lib.NQ_ERR_DTYPE
+    assert rope(0, 127, 96 * 127) == _lib.NQ_ERR_INVALID_ARGUMENT  # odd head_dim
+    assert rope(0, 128, 95 * 128) == _lib.NQ_ERR_SHAPE  # row too short for q, k and v
+    assert rope(0, 128, 96 * 128) == _lib.NQ_ERR_INVALID_ARGUMENT  # null pointers
 
 
 # The schema strings of the reference extension (kernel/pybind.cpp:85-104), written out here as
