@@ -264,7 +264,8 @@ def bench_gemv_shape(pool, dev, steps=2048):
             "packed_bytes": pb, "packed_gbs": round(pb / (ms * 1e-3) / 1e9, 2),
             "frac_hbm": round(pb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "total_bytes_gbs": round(gemv_total_bytes(m, n, r, pool.batch) / (ms * 1e-3) / 1e9, 2),
-            "stage1": dict(kernel="s1w_kernel (V's sign words)", **kern(stage1_bytes(n, r), ms1)),
+            "stage1": dict(kernel="s1l_kernel (V's sign words)" if pool.batch == 1 and n % 32 == 0 and (n // 32) <= 384
+                           else "stage-1 kernel (V's sign words)", **kern(stage1_bytes(n, r), ms1)),
             "stage2": dict(kernel="s2t_kernel (U's sign words)", **kern(stage2_bytes(m, r), ms2))}
 
 
@@ -868,7 +869,7 @@ def main():
                                f"({pb * args.copies / 1e6:.0f} MB) replayed in a HIP graph",
                    "m": m, "n": n, "r": r, "batch": args.batch, "copies": args.copies, "timing": timing_how},
         "gemv_us": round(ms * 1e3, 4),
-        "roofline": {"bound": "hbm", "kernel": "the GEMV's two launches (s1w_kernel, then s2t_kernel)",
+        "roofline": {"bound": "hbm", "kernel": "the GEMV's two launches (s1l_kernel, then s2t_kernel)",
                      "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_src,
                      "algorithmic_bytes": pb, "us_per_op": round(ms * 1e3, 4),
