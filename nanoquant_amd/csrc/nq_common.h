@@ -145,6 +145,28 @@ __device__ inline void dma4(const void* src, void* lds) {
                                      (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
 }
 
+// LDS byte address of a pointer into __shared__ memory.
+__device__ inline uint32_t lds_addr(const void* p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)p));
+}
+
+// The same DMAs issued from inline assembly, which the compiler does not track: 16 / 4 bytes a lane
+// from base + voff (base wave-uniform, voff a byte offset per lane) into LDS at the wave-uniform
+// byte address lds, lane after lane. A DMA issued through the builtin counts, for the compiler's
+// wait insertion, as an LDS event whose completion order it cannot know, so wherever a later LDS
+// read's data is needed it waits for every outstanding LDS read (lgkmcnt 0): a read issued early
+// for the next k tile is drained at the current tile's first use. With the DMAs untracked, LDS reads
+// get partial waits. The caller waits for these DMAs itself (wait_vmcnt: the compiler's own vmcnt
+// waits count only the loads it knows, so they can only wait longer than needed) and orders them
+// against LDS reads with barrier_keep_dma. M0 is written without being declared: on gfx950 the
+// compiler uses it only to set up LDS DMAs, and a kernel that calls these calls no builtin DMA.
+__device__ inline void dma16_lds(const void* base, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds) : "memory");
+}
+__device__ inline void dma4_lds(const void* base, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "s"(lds) : "memory");
+}
+
 // Waits until at most N of this wave's vector-memory operations (loads, DMAs) are outstanding;
 // they complete in issue order.
 template <int N>
