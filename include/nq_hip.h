@@ -206,11 +206,16 @@ int nq_gemv_group_stage2(int dtype, int64_t count, const nq_gemv_item* items, in
  * nq_rope_kv_write's, bit for bit (outputs equal nq_gemv_group_stage2 with NQ_EPI_STORE followed by
  * nq_rope_kv_write). head_dim a multiple of 16; every m a multiple of head_dim; items[1].m ==
  * items[2].m. y of items 1 and 2 is not written (any valid pointer). A position outside
- * [0, max_len) zeroes q and writes no cache row. No counterpart in the reference (its decode step
- * runs Hugging Face's rotary embedding and cache update, kernel/test_decode.py:385-402). */
+ * [0, max_len) zeroes q and writes no cache row. scores_mask (optional, NULL for none): the
+ * attention scores buffer [batch * kv_heads, max_len, groups] (groups = items[0].m / items[1].m query
+ * heads per kv head) into which the launch writes the step's additive causal mask, 0 for cache
+ * positions <= *position and -inf after it, so that the scores product can add into it in place.
+ * No counterpart in the reference (its decode step runs Hugging Face's rotary embedding, cache update
+ * and mask, kernel/test_decode.py:385-402). */
 int nq_gemv_group_stage2_rope(int dtype, const nq_gemv_item* items, int64_t batch, void* k_cache, void* v_cache,
                               const void* rope_cos, const void* rope_sin, const int64_t* position, int64_t head_dim,
-                              int64_t max_len, void* workspace, size_t workspace_bytes, nq_stream_t stream);
+                              int64_t max_len, void* scores_mask, void* workspace, size_t workspace_bytes,
+                              nq_stream_t stream);
 
 /* ---------------------------------------------------------------- prefill GEMM */
 

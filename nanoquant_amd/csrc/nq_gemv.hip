@@ -268,6 +268,9 @@ struct S2Rope {
     const uint16_t* cos;
     const uint16_t* sin;
     int head_dim, max_len;
+    uint16_t* mask;       // optional: the step's additive causal mask [rows][max_len][groups]
+    uint32_t mask_total;  // elements of mask
+    int mask_groups;      // query heads per kv head
 };
 
 struct S2Table {
@@ -837,6 +840,20 @@ __global__ __launch_bounds__(256) void s2t_kernel(const S2Table tab, int batch) 
     const int wave = t >> 6;
     const int c = lane & 15;
     const int g = lane >> 4;
+    if (EPI == kEpiRope && tab.rope.mask != nullptr) {
+        // the additive causal mask of the step into the attention scores: element (row, p, group)
+        // is 0 for a cache position p <= the step's position and -inf after it; every thread of the
+        // grid takes every nthr-th element, before any block leaves
+        const int64_t pm = *tab.rope.pos;
+        const uint32_t nthr = gridDim.x * gridDim.y * gridDim.z * 256u;
+        const uint32_t gid = ((blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * 256u + threadIdx.x;
+        const uint16_t neg_inf = T::from_float(-__builtin_huge_valf());
+        for (uint32_t e = gid; e < tab.rope.mask_total; e += nthr) {
+            const int p = static_cast<int>((e / static_cast<uint32_t>(tab.rope.mask_groups)) %
+                                           static_cast<uint32_t>(tab.rope.max_len));
+            tab.rope.mask[e] = p <= pm ? uint16_t(0) : neg_inf;
+        }
+    }
     S2Item its[P];
     its[0] = (EPI == kEpiGated || EPI == kEpiStoreOne) ? tab.item[0] : pick_item<S2Item>(tab);
     if (P == 2) its[P - 1] = tab.item[1];
@@ -2596,7 +2613,8 @@ int nq_gemv_group_stage2(int dtype, int64_t count, const nq_gemv_item* items, in
 
 int nq_gemv_group_stage2_rope(int dtype, const nq_gemv_item* items, int64_t batch, void* k_cache, void* v_cache,
                               const void* rope_cos, const void* rope_sin, const int64_t* position, int64_t head_dim,
-                              int64_t max_len, void* workspace, size_t workspace_bytes, nq_stream_t stream) {
+                              int64_t max_len, void* scores_mask, void* workspace, size_t workspace_bytes,
+                              nq_stream_t stream) {
     const char* name = "nq_gemv_group_stage2_rope";
     if (!items) return fail(NQ_ERR_INVALID_ARGUMENT, "%s: null items", name);
     if (head_dim < 16 || head_dim % 16 || max_len <= 0 || max_len > INT32_MAX / 2)
@@ -2614,12 +2632,19 @@ int nq_gemv_group_stage2_rope(int dtype, const nq_gemv_item* items, int64_t batc
         return fail(NQ_ERR_ALIGNMENT, "%s: misaligned operand", name);
     if (batch * (items[1].m / head_dim) * max_len * head_dim > ((int64_t)1 << 40))
         return fail(NQ_ERR_UNSUPPORTED, "%s: caches too large", name);
+    if (scores_mask && (!aligned(scores_mask, 2) || items[0].m % items[1].m ||
+                        batch * (items[0].m / head_dim) * max_len >= ((int64_t)1 << 31)))
+        return fail(NQ_ERR_SHAPE, "%s: the scores mask needs whole query groups per kv head, fewer than 2^31 elements "
+                                  "and 2-byte alignment", name);
     RopeArgs ra;
     ra.rope.pos = position;
     ra.rope.cos = static_cast<const uint16_t*>(rope_cos);
     ra.rope.sin = static_cast<const uint16_t*>(rope_sin);
     ra.rope.head_dim = static_cast<int>(head_dim);
     ra.rope.max_len = static_cast<int>(max_len);
+    ra.rope.mask = static_cast<uint16_t*>(scores_mask);
+    ra.rope.mask_total = scores_mask ? static_cast<uint32_t>(batch * (items[0].m / head_dim) * max_len) : 0u;
+    ra.rope.mask_groups = scores_mask ? static_cast<int>(items[0].m / items[1].m) : 1;
     ra.k_cache = static_cast<uint16_t*>(k_cache);
     ra.v_cache = static_cast<uint16_t*>(v_cache);
     return group_stage2(name, dtype, 3, items, batch, -1, &ra, workspace, workspace_bytes, stream);

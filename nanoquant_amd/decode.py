@@ -177,14 +177,16 @@ def rotary_step_tables(cos, sin, positions, cache: StaticKVCache, dtype):
     return R.to(dtype), madd
 
 
-def attention_products_step(shape: LlamaShape, layer: int, q, madd, cache: StaticKVCache, out):
+def attention_products_step(shape: LlamaShape, layer: int, q, madd, cache: StaticKVCache, out, scores=None):
     """The attention products of a one-token step whose rotary embedding and cache write are done
     (``nq_rope_kv_write``): the scores of each kv head's query group against the cache with the scale
     and causal mask folded into one batched product, the softmax, and the value product written into
     ``out`` [B, H * D] (directly when each kv head serves one query head, else through a copy).
 
     q [B, H * D] (rotated, contiguous); ``madd`` [1, L, 1]: the additive causal mask of the step's
-    position (0 for visible cache rows, -inf past it)."""
+    position (0 for visible cache rows, -inf past it). With ``scores`` [B * KV, L, G] already holding
+    that mask (``nq_gemv_group_stage2_rope`` writes it), the product adds into it in place and the
+    mask is not copied in first (``madd`` is then unused)."""
     H, KV, D = shape.heads, shape.kv_heads, shape.head_dim
     B, G = q.shape[0], H // KV
     k_c, v_c = cache.k[layer], cache.v[layer]
@@ -193,7 +195,10 @@ def attention_products_step(shape: LlamaShape, layer: int, q, madd, cache: Stati
     q_t = q.view(B * KV, G, D).transpose(1, 2)
     if G > 1:
         q_t = q_t.contiguous()
-    scores = torch.baddbmm(madd, k_c.view(B * KV, L, D), q_t, alpha=D ** -0.5)  # [B*KV, L, G]
+    if scores is None:
+        scores = torch.baddbmm(madd, k_c.view(B * KV, L, D), q_t, alpha=D ** -0.5)  # [B*KV, L, G]
+    else:
+        scores.baddbmm_(k_c.view(B * KV, L, D), q_t, alpha=D ** -0.5)
     p = torch.softmax(scores, dim=1)
     vt = v_c.view(B * KV, L, D).transpose(1, 2)
     if G == 1:
@@ -493,10 +498,9 @@ class FusedDecoder(GraphDecoder):
         self.qkv = torch.zeros(batch, self.qkv_width, device=dev, dtype=dt)
         self.attn = torch.zeros(batch, H * D, device=dev, dtype=dt)
         self.q_rot = torch.zeros(batch, H * D, device=dev, dtype=dt)
-        # the additive causal mask of every position (row p: 0 for cache rows <= p, -inf after)
-        rows = torch.arange(max_len, device=dev)
-        self.masks = torch.zeros(max_len, max_len, device=dev, dtype=dt).masked_fill_(
-            rows.view(1, -1) > rows.view(-1, 1), float("-inf"))
+        # attention scores of the rope step [B * KV, L, G]: the q/k/v launch writes the step's causal
+        # mask into it, the scores product adds into it in place
+        self.scores = torch.zeros(batch * KV, max_len, H // KV, device=dev, dtype=dt)
         self.act = torch.zeros(batch, s.ffn, device=dev, dtype=dt)
         cos, sin = model.rope(torch.arange(max_len, device=dev), dt)
         self.rope_cos, self.rope_sin = cos.contiguous(), sin.contiguous()
@@ -572,8 +576,6 @@ class FusedDecoder(GraphDecoder):
             tables = rotary_step_tables(self.rope_cos.index_select(0, self.pos),
                                         self.rope_sin.index_select(0, self.pos), self.pos, self.cache,
                                         self.model.dtype)
-        elif self.attention == "rope":
-            madd = self.masks.index_select(0, self.pos).view(1, -1, 1)
         x, h, qkv, attn, act = (t.data_ptr() for t in (self.x, self.h, self.qkv, self.attn, self.act))
         esz = self.qkv.element_size()
         for li, plan in enumerate(self.plans):
@@ -583,7 +585,8 @@ class FusedDecoder(GraphDecoder):
                 items_r = plan["qkv_rope"]
                 self._check(lib.nq_gemv_group_stage2_rope(
                     dt, items_r, B, self.cache.k[li].data_ptr(), self.cache.v[li].data_ptr(), self.rope_cos.data_ptr(),
-                    self.rope_sin.data_ptr(), self.pos.data_ptr(), D, self.max_len, ws, wsb, st), "qkv 2 rope")
+                    self.rope_sin.data_ptr(), self.pos.data_ptr(), D, self.max_len, self.scores.data_ptr(), ws, wsb,
+                    st), "qkv 2 rope")
             else:
                 self._check(lib.nq_gemv_group_stage2(dt, n, items, B, self._lib.NQ_EPI_STORE, ws, wsb, st), "qkv 2")
             if self.attention == "hip":
@@ -593,7 +596,7 @@ class FusedDecoder(GraphDecoder):
                     self.rope_sin.data_ptr(), self.pos.data_ptr(), attn, B, H, KV, D, self.max_len,
                     D ** -0.5, self.attn_ws.data_ptr(), self.attn_ws.numel(), st), "attention")
             elif self.attention == "rope":
-                attention_products_step(s, li, self.q_rot, madd, self.cache, self.attn)
+                attention_products_step(s, li, self.q_rot, None, self.cache, self.attn, scores=self.scores)
             else:
                 out = rotary_attention_step(s, li, self.qkv[:, :(H + KV) * D], self.qkv[:, (H + KV) * D:], tables,
                                             self.pos, self.cache, out=self.attn)

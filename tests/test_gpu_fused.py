@@ -270,7 +270,9 @@ def test_group_stage2_rope_equals_store_then_rope_kernel(lib, dtype, B, heads, k
     """nq_gemv_group_stage2_rope (the q/k/v stage 2 with the rotary embedding and cache write in its
     store) against nq_gemv_group_stage2 (NQ_EPI_STORE) followed by nq_rope_kv_write on the same
     intermediate: q, the caches' new rows and every other cache row bit for bit; ranks equal and
-    unequal (two launches); a position past the cache (80 of 64 rows) zeroes q and writes no row."""
+    unequal (two launches); a position past the cache (80 of 64 rows) zeroes q and writes no row. The
+    scores buffer it is given holds the step's causal mask afterwards (0 up to the position, -inf
+    after; all visible past the cache)."""
     from nanoquant_amd import _lib
     announce("group stage 2 rope", dtype, (B, heads, kv_heads, D, r_qkv, pos))
     n, L = 256, 64
@@ -315,10 +317,15 @@ def test_group_stage2_rope_equals_store_then_rope_kernel(lib, dtype, B, heads, k
                                     cos.data_ptr(), sin.data_ptr(), position.data_ptr(), q_ref.data_ptr(),
                                     heads * D, B, heads, kv_heads, D, L, st), "rope")
     # fused: the same intermediate, stage 2 with the rotary store
+    # the scores buffer of the step's attention, which the launch fills with the causal mask
+    scores = torch.full((B * kv_heads, L, heads // kv_heads), 7.0, dtype=dtype, device="cuda")
     _lib.check(lib.nq_gemv_group_stage2_rope(dc, arr_r, B, caches[0].data_ptr(), caches[1].data_ptr(),
                                              cos.data_ptr(), sin.data_ptr(), position.data_ptr(), D, L,
-                                             ws.data_ptr(), need, st), "s2 rope")
+                                             scores.data_ptr(), ws.data_ptr(), need, st), "s2 rope")
     torch.cuda.synchronize()
+    visible = (torch.arange(L, device="cuda") <= pos).view(1, L, 1).expand_as(scores)
+    want_mask = torch.zeros_like(scores).masked_fill_(~visible, float("-inf"))
+    assert torch.equal(scores.view(torch.int16), want_mask.view(torch.int16))
     assert torch.equal(q_rot.view(torch.int16), q_ref.view(torch.int16))
     assert torch.equal(caches[0].view(torch.int16), caches_ref[0].view(torch.int16))
     assert torch.equal(caches[1].view(torch.int16), caches_ref[1].view(torch.int16))

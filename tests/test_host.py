@@ -76,7 +76,7 @@ def test_c_abi_argument_errors_need_no_gpu():
     for it, m in zip(qkv_items, (4096, 4096, 4096)):
         it.r, it.m, it.y_stride = 1120, m, 12288
     rope2 = lambda hd, L: lib.nq_gemv_group_stage2_rope(  # noqa: E731
-        0, qkv_items, 1, None, None, None, None, None, hd, L, None, 0, None)
+        0, qkv_items, 1, None, None, None, None, None, hd, L, None, None, 0, None)
     assert rope2(120, 384) == _lib.NQ_ERR_INVALID_ARGUMENT  # head_dim not a multiple of 16
     assert rope2(128, 0) == _lib.NQ_ERR_INVALID_ARGUMENT
     assert rope2(128, 384) == _lib.NQ_ERR_INVALID_ARGUMENT  # null caches
