@@ -529,33 +529,38 @@ def bench_decode(args, dev):
         "fused_rope_kernel_torch_attention": (True, "rope", spg),
         "fused_hip_attention": (True, "hip", spg),
     }
+    only = [v for v in args.decode_variants.split(",") if v] if args.decode_variants else list(variants)
+    unknown = [v for v in only if v not in variants]
+    if unknown:
+        raise SystemExit(f"bench.py: unknown decode variant(s) {unknown}; known: {list(variants)}")
     runs = {}
     for name, (fused, attention, k) in variants.items():
-        if (new - 1) % k:
+        if (new - 1) % k or name not in only:
             continue
         generate(model, prompt, 1 + k, steps_per_graph=k, fused=fused, attention=attention)  # warm-up
         torch.cuda.reset_peak_memory_stats(dev)
         ids, tps, prof = generate(model, prompt, new, steps_per_graph=k, fused=fused, attention=attention)
         runs[name] = (tps, prof, ids, torch.cuda.max_memory_allocated(dev))
         log(f"[bench] decode e2e {name}: {tps:.1f} tok/s, {prof['ms_per_token']:.3f} ms/token")
-    head = "fused_torch_attention"
+    head = "fused_torch_attention" if "fused_torch_attention" in runs else next(iter(runs))
     tps, prof, ids, peak = runs[head]
     same = all(torch.equal(r[2], ids) for k, r in runs.items() if k.startswith("fused_torch"))
     # first decode step of each step kind from the same prefix: the fused step rounds the folded
     # norm and the epilogues differently, so its logits are compared, not its greedy tokens (a
     # random-init model's logits are nearly flat, so any rounding difference flips near-ties)
     first = {}
-    for name, make in (("unfused", lambda: GraphDecoder(model, B, T + 2, device=dev)),
-                       ("fused_torch_attention", lambda: FusedDecoder(model, B, T + 2, device=dev)),
-                       ("fused_rope_kernel_torch_attention",
-                        lambda: FusedDecoder(model, B, T + 2, device=dev, attention="rope")),
-                       ("fused_hip_attention", lambda: FusedDecoder(model, B, T + 2, device=dev, attention="hip"))):
+    steps_kinds = () if args.decode_variants else (
+        ("unfused", lambda: GraphDecoder(model, B, T + 2, device=dev)),
+        ("fused_torch_attention", lambda: FusedDecoder(model, B, T + 2, device=dev)),
+        ("fused_rope_kernel_torch_attention", lambda: FusedDecoder(model, B, T + 2, device=dev, attention="rope")),
+        ("fused_hip_attention", lambda: FusedDecoder(model, B, T + 2, device=dev, attention="hip")))
+    for name, make in steps_kinds:
         dec = make()
         dec.prefill(prompt)
         first[name] = dec.decode(1, use_graph=False).double()
         del dec
     rel = {k: float((v - first["unfused"]).abs().max() / first["unfused"].abs().max())
-           for k, v in first.items() if k != "unfused"}
+           for k, v in first.items() if k != "unfused"} if first else None
     # bytes one step must read: packed sign words and scales of every linear, the fp16
     # lm_head, one embedding row, and the K/V cache up to the step's position (mean over steps)
     lin_bytes = 0
@@ -570,8 +575,17 @@ def bench_decode(args, dev):
     return {"model": "random-init Llama-2-7B architecture, 7 NanoQuant linears per layer at 0.55 bpw (GEMV kernel)",
             "batch": B, "prompt": T, "new_tokens": new, "tokens_per_s": round(tps, 2),
             "ms_per_token": round(prof["ms_per_token"], 4),
-            "step": ("fused linears (q/k/v and gate/up stage 1 each one launch with RMSNorm folded in, SiLU*mul "
+            "step": head if head != "fused_torch_attention" else
+                    ("fused linears (q/k/v and gate/up stage 1 each one launch with RMSNorm folded in, SiLU*mul "
                      "and residual epilogues) with RoPE, KV write and attention in torch ops; HIP graph"),
+            "variants": {"fused_torch_attention": "the step above (config 5 as written: non-linear ops of the "
+                                                  "attention in torch)",
+                         "fused_torch_attention_spg1": "the same, one step per graph",
+                         "unfused": "one NanoQuantLinear GEMV op per linear, everything else in torch",
+                         "fused_rope_kernel_torch_attention": "the q/k/v stage 2 also applies RoPE, writes the KV "
+                                                              "cache rows and the step's causal mask; the scores, "
+                                                              "softmax and value products in torch",
+                         "fused_hip_attention": "RoPE, KV write and attention in nq_attention_decode"},
             "steps_per_graph": spg,
             "tokens_per_s_by_variant": {k: round(v[0], 2) for k, v in runs.items()},
             "peak_memory_bytes_by_variant": {k: int(v[3]) for k, v in runs.items()},
@@ -748,6 +762,9 @@ def main():
     ap.add_argument("--e2e-prompt", type=int, default=128)
     ap.add_argument("--e2e-new", type=int, default=256)
     ap.add_argument("--e2e-steps-per-graph", type=int, default=15)
+    ap.add_argument("--decode-variants", default="",
+                    help="comma-separated decode variants to run (default: all; a subset skips the first-step "
+                         "logits comparison, for kernel traces of one variant)")
     ap.add_argument("--floor", action="store_true",
                     help="measure only the launch and cold-read floor of decode-sized kernels and print it")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
