@@ -375,10 +375,17 @@ void gemm_dm_kernel(
     auto compute_kt = [&](const Frag& f) {
 #pragma unroll
         for (int tp = 0; tp < TP; ++tp) {
+            // two words per 64-bit shift: sft <= 15, so the bits the shift carries from the low word
+            // into the high one land below bit 15 and the mask drops them (one v_lshlrev_b64 for
+            // two v_lshlrev_b32; same-box A/B: B = 2048 gate / down 1.5 / 1.9% faster, B = 256 gate 3%)
             const u32x4 w = f.w[tp / 2];
             const int sft = shb[tp];
-            const u32x4 a = u32x4{f.s.x ^ ((w.x << sft) & mask), f.s.y ^ ((w.y << sft) & mask),
-                                  f.s.z ^ ((w.z << sft) & mask), f.s.w ^ ((w.w << sft) & mask)};
+            const uint64_t w01 = ((static_cast<uint64_t>(w.y) << 32) | w.x) << sft;
+            const uint64_t w23 = ((static_cast<uint64_t>(w.w) << 32) | w.z) << sft;
+            const u32x4 a = u32x4{f.s.x ^ (static_cast<uint32_t>(w01) & mask),
+                                  f.s.y ^ (static_cast<uint32_t>(w01 >> 32) & mask),
+                                  f.s.z ^ (static_cast<uint32_t>(w23) & mask),
+                                  f.s.w ^ (static_cast<uint32_t>(w23 >> 32) & mask)};
 #pragma unroll
             for (int tq = 0; tq < TQ; ++tq) acc[tp][tq] = mfma32x32x16<T>(a, f.x[tq], acc[tp][tq]);
         }
