@@ -205,7 +205,8 @@ int launch_onebit(const void* A, const uint32_t* W, const void* s_in, const void
 // for those: the barrier carries no memory fence, so the DMAs of the step after stay in flight.
 // With KS = 2 the block holds two groups of waves with buffers of their own, each over half of
 // the k steps (for outputs too few to give every SIMD two waves); group 1 hands its accumulators
-// to group 0 through LDS at the end. With kSplit the grid repeats the tiles once per k range of
+// to group 0 through LDS at the end. With KS = 4 (long K) four groups each take a quarter of the
+// steps and hand their sums to group 0 one group at a time through the step buffers. With kSplit the grid repeats the tiles once per k range of
 // split_steps steps, and each block stores its raw fp32 sums to its plane of `part`
 // [splits][M][N]; gemm_split_finish_kernel adds the planes in order and applies the epilogue.
 template <typename T, bool kSin, bool kSout, int BP, int BQ, int WP, int WQ, int WPE, int KS, bool kSplit,
@@ -240,12 +241,18 @@ void gemm_dm_kernel(
     constexpr int kAcc = TP * TQ * 16;                   // accumulators per lane
     static_assert(XCH % NTG == 0 && WWORDS % NTG == 0, "tile pieces must divide evenly");
     static_assert(WP % 64 == 0 && BP % 64 == 0, "features come in whole 64-feature word groups");
-    static_assert(KS == 1 || KS == 2, "one or two k groups");
+    static_assert(KS == 1 || KS == 2 || KS == 4, "one, two or four k groups");
     static_assert(!kSplit || (KS == 1 && !kSout), "a k range of the grid is one wave group, scaled later");
-    __shared__ __attribute__((aligned(16))) uint16_t xs0[KS][BQ * BKK], xs1[KS][BQ * BKK], xs2[KS][BQ * BKK];
+    __shared__ __attribute__((aligned(16))) uint16_t xsall[3][KS][BQ * BKK];
+    auto& xs0 = xsall[0];
+    auto& xs1 = xsall[1];
+    auto& xs2 = xsall[2];
     __shared__ __attribute__((aligned(16))) uint32_t ws0[KS][WWORDS], ws1[KS][WWORDS], ws2[KS][WWORDS];
     __shared__ __attribute__((aligned(16))) uint32_t ss0[kSin ? NT : 4], ss1[kSin ? NT : 4], ss2[kSin ? NT : 4];
-    __shared__ float red[KS == 2 ? kAcc * NTG : 1];
+    __shared__ float red_arr[KS == 2 ? kAcc * NTG : 1];
+    // with four groups one group's sums at a time pass through the step buffers, free by then
+    static_assert(KS != 4 || 3 * KS * BQ * BKK * 2 >= kAcc * NTG * 4, "the step buffers hold one group's sums");
+    float* red = KS == 4 ? reinterpret_cast<float*>(&xsall[0][0][0]) : red_arr;
     __shared__ uint16_t sos[BP];
 
     const int t = threadIdx.x;
@@ -448,6 +455,31 @@ void gemm_dm_kernel(
     }
     wait_vmcnt<0>();  // the tail's re-fetches land before the block's LDS is reused or released
 
+    if (KS == 4) {  // groups 1, 2 and 3 join group 0's sums in that order (deterministic)
+        __syncthreads();  // every wave is done with its last step's buffers
+#pragma unroll
+        for (int src = 1; src < 4; ++src) {
+            if (grp == src) {
+#pragma unroll
+                for (int tp = 0; tp < TP; ++tp)
+#pragma unroll
+                    for (int tq = 0; tq < TQ; ++tq)
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) red[((tp * TQ + tq) * 16 + i) * NTG + tg] = acc[tp][tq][i];
+            }
+            __syncthreads();
+            if (grp == 0) {
+#pragma unroll
+                for (int tp = 0; tp < TP; ++tp)
+#pragma unroll
+                    for (int tq = 0; tq < TQ; ++tq)
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) acc[tp][tq][i] += red[((tp * TQ + tq) * 16 + i) * NTG + tg];
+            }
+            __syncthreads();
+        }
+        if (grp != 0) return;
+    }
     if (KS == 2) {  // group 1's sums join group 0's (lane-contiguous, conflict-free)
         if (grp == 1) {
 #pragma unroll
@@ -653,7 +685,8 @@ void launch_dm_split(const void* A, const uint32_t* W, const void* s_in, const v
 //   more than 256 tiles: one block per tile (B = 2048, K = 8192, N = 2304, 288 tiles: 119.0 us
 //     with K over two wave groups -> 105.2 us; K = 4096, N = 3072, 384 tiles: 64.3 -> 59.8 us);
 //   160-256 tiles: K split over two wave groups inside each block (B = 2048, K = 4096,
-//     N = 1792, 224 tiles: 46 -> 38 us against one block per tile; 256 tiles: 42.7 -> 40.3 us);
+//     N = 1792, 224 tiles: 46 -> 38 us against one block per tile; 256 tiles: 42.7 -> 40.3 us),
+//     over four from 128 steps;
 //   fewer, with at most 64 even 64-k steps and 128+ tiles of 32 rows: 32-row tiles, K over two
 //     wave groups (B = 256, K = 1280 -> 1120, N = 4096: 16.6 us split across the grid -> 9.1 us;
 //     B = 2048, K = 512, N = 1024: 8.8 -> 6.8 us; up to 32 steps at first, then measured on the
@@ -727,7 +760,13 @@ int launch_gemm(const char* name, const void* A, const uint32_t* W, const void* 
             launch_dm<T, 256, 128, 64, 128, 2, 1>(A, W, s_in, s_out, C, M, K, N, stream, k_scale);
             break;
         case kModeGroups:
-            launch_dm<T, 256, 64, 64, 64, 2, 2>(A, W, s_in, s_out, C, M, K, N, stream);
+            // long K over four wave groups (16 waves a block, four per SIMD, 128 VGPRs): B = 2048,
+            // K = 11008, N = 1792 (172 steps) 2.5% faster per op, same-box A/B; at 64 steps no change,
+            // at 28 steps (B = 256, N = 11008) 5.6% slower
+            if ((K / 64) % 4 == 0 && K / 64 >= 128)
+                launch_dm<T, 256, 64, 64, 64, 4, 4>(A, W, s_in, s_out, C, M, K, N, stream);
+            else
+                launch_dm<T, 256, 64, 64, 64, 2, 2>(A, W, s_in, s_out, C, M, K, N, stream);
             break;
         case kModeGroups32:
             launch_dm<T, 256, 32, 64, 32, 2, 2>(A, W, s_in, s_out, C, M, K, N, stream);

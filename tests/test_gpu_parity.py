@@ -464,6 +464,9 @@ GEMM_CASES = [
     # 32-row tiles with K over two wave groups at 56 steps (stage 2 of a rank-3520 factorisation,
     # 144 tiles of 32 rows, the last ragged: 260 = 8 * 32 + 4)
     ("groups32_56_steps", 260, 512, 3520, 4096, False),
+    # K over four wave groups: stage 1 of 128 steps over 160 tiles (16 row tiles, the last ragged:
+    # 1000 = 15 * 64 + 40, times 10 feature tiles), group sums added through the step buffers
+    ("groups4_long_k", 1000, 8192, 2560, 320, True),
 ]
 
 
