@@ -27,15 +27,19 @@ The JSON line carries:
   bytes read plus written against 8 TB/s;
 * ``decode_e2e``: greedy decode of a random-init Llama-2-7B-architecture model with every linear
   NanoQuant-factorised at 0.55 bpw (prompt 128, 256 new tokens, batch 1): the fused-linears step
-  with attention in torch (the headline), the unfused step, and the step with the HIP attention;
+  with attention in torch (the headline), the unfused step, the step whose q/k/v launch also
+  applies RoPE and writes the cache rows and the causal mask (attention products in torch), and
+  the step with the HIP attention;
 * ``cpu_baseline``: the reference's dense dequantize-and-matmul forward (two ``F.linear`` on
   dense +-1 factors, modules/linear.py:282-291) on the host cores at batch 1 in bf16 (the
   reference's module dtype; ``value``) and fp32, and its packers in eager torch;
 * ``parity``: relative error of the GEMVs and GEMMs against the float64 oracle on the same
   inputs (the CPU leg; null with ``--skip-cpu``).
 
-``--floor`` prints the ``floor`` section alone; ``--sweep`` prints one line per config shape (GEMV at batch 1/4/16, GEMM at 256/2048);
-``--batch-sweep`` the GEMV and the GEMM at batch 1..256 on the 7B gate and down shapes.
+``--floor`` prints the ``floor`` section alone; ``--sweep`` prints one line per config shape (GEMV
+at batch 1/4/16, GEMM at 256/2048); ``--batch-sweep`` the GEMV and the GEMM at batch 1..256 on the
+7B gate and down shapes; ``--gemv-only``, ``--decode-only`` (with ``--decode-variants``) and the
+``--skip-*`` switches narrow a run for kernel traces.
 Multi-GPU runs are not part of this build: ``--gpus`` above 1 exits with a message.
 """
 from __future__ import annotations
