@@ -38,7 +38,7 @@ The JSON line carries:
 
 ``--floor`` prints the ``floor`` section alone; ``--sweep`` prints one line per config shape (GEMV
 at batch 1/4/16, GEMM at 256/2048); ``--batch-sweep`` the GEMV and the GEMM at batch 1..256 on the
-7B gate and down shapes; ``--gemv-only``, ``--decode-only`` (with ``--decode-variants``) and the
+7B gate and down shapes (every config shape with ``--batch-sweep-shapes configs``); ``--gemv-only``, ``--decode-only`` (with ``--decode-variants``) and the
 ``--skip-*`` switches narrow a run for kernel traces.
 Multi-GPU runs are not part of this build: ``--gpus`` above 1 exits with a message.
 """
@@ -669,13 +669,23 @@ def run_sweep(args, dev):
         torch.cuda.empty_cache()
 
 
+def batch_sweep_shapes(which):
+    """(model, linear, m, n, r) of the batch sweep: the Llama-2-7B gate and down shapes at 0.55 bpw ("7b"), or
+    every distinct shape of the benchmark configs without the mixture-of-rank ones ("configs")."""
+    from nanoquant_amd.decode import rank_for_bpw
+
+    if which == "7b":
+        return [("llama2-7b@0.55", name, m, n, rank_for_bpw(m, n, 0.55))
+                for name, m, n in [("gate,up", 11008, 4096), ("down", 4096, 11008)]]
+    return [s for s in sweep_shapes() if not s[0].endswith("mixed")]
+
+
 def run_batch_sweep(args, dev):
-    """One JSON line per (shape, batch, kind): the GEMV and the GEMM at batch 1, 2, 4, 8, 16, 32, 64, 128, 256 on
-    the Llama-2-7B gate and down shapes at 0.55 bpw, both over the same rotating copies (more than 512 MB of packed
+    """One JSON line per (shape, batch, kind): the GEMV and the GEMM at the --batches sizes (1, 2, 4, ..., 256 by
+    default) on the --batch-sweep-shapes shapes, both over the same rotating copies (more than 512 MB of packed
     weights in all, so both stream from HBM). This is where one kernel should hand over to the other. Kinds
     gemv_stage1 and gemv_stage2 time the GEMV's two launches alone (the C ABI's stage entry points, same copies)."""
     from nanoquant_amd import _lib
-    from nanoquant_amd.decode import rank_for_bpw
 
     lib = _lib.load()
 
@@ -687,8 +697,7 @@ def run_batch_sweep(args, dev):
     words = _words(gen, dev)
     scales = lambda k: (torch.rand(k, device=dev, generator=gen) * 0.4 + 0.8).half()  # noqa: E731
     batches = [int(b) for b in args.batches.split(",")]
-    for name, m, n in [("gate,up", 11008, 4096), ("down", 4096, 11008)]:
-        r = rank_for_bpw(m, n, 0.55)
+    for model, name, m, n, r in batch_sweep_shapes(args.batch_sweep_shapes):
         r_pad = -(-r // 256) * 256
         pb = packed_bytes(m, n, r)
         copies = int(min(128, max(8, -(-(512 << 20) // pb))))
@@ -727,7 +736,7 @@ def run_batch_sweep(args, dev):
                     fn = stage(1 if kind == "gemv_stage1" else 2)
                 ms, graph, _ = steady_ms(fn, copies, stream, reps, 1)
                 del graph
-                print(json.dumps({"kind": kind, "linear": name, "m": m, "n": n, "r": r, "batch": B,
+                print(json.dumps({"kind": kind, "model": model, "linear": name, "m": m, "n": n, "r": r, "batch": B,
                                   "us": round(ms * 1e3, 3),
                                   "packed_gbs": round(pb / (ms * 1e-3) / 1e9, 1),
                                   "tflops": round(2.0 * B * r * (n + m) / (ms * 1e-3) / 1e12, 2)}), flush=True)
@@ -758,6 +767,8 @@ def main():
     ap.add_argument("--batch-sweep", action="store_true",
                     help="measure GEMV and GEMM at the --batches sizes on the 7B gate and down shapes instead")
     ap.add_argument("--batches", default="1,2,4,8,16,32,64,128,256")
+    ap.add_argument("--batch-sweep-shapes", choices=("7b", "configs"), default="7b",
+                    help="shapes of --batch-sweep: the 7B gate and down (0.55 bpw), or every config shape")
     ap.add_argument("--decode-only", action="store_true",
                     help="run only the end-to-end decode and print its result alone (for kernel traces)")
     ap.add_argument("--gemv-only", action="store_true",

@@ -1655,21 +1655,28 @@ inline int64_t sb_min_batch(int64_t wpr, int64_t rows) {
 constexpr int kSbMaxBatch = 128;
 constexpr int kSbLdsBytes = 160 * 1024;
 constexpr int kSbMaxBlocks = 256;
+// Rounds of blocks the search may take when no plan fits one round (see sb_plan_any).
+constexpr int kSbMaxRounds = 4;
 
 // Searches row tiles per wave (1, 2, 4: 64, 128, 256 rows per block) and k ranges for the launch
-// with the least estimated time per block, among those whose grid is one block per CU at most (a
-// second round of blocks doubles the time) and whose LDS fits. Estimate, in CU cycles: the MFMAs
-// and their operand decode per wave, the DMA of the block's slice at ~32 bytes a cycle, and, with
-// several k ranges, the finishing launch (~4000) plus the per-range sums written and read.
+// with the least estimated time, among those whose grid is one block per CU at most (a second round
+// of blocks doubles the time) and whose LDS fits. Estimate, in CU cycles: the MFMAs and their
+// operand decode per wave, the DMA of the block's slice at ~32 bytes a cycle, and, with several k
+// ranges, the finishing launch (~4000) plus the per-range sums written and read.
+//
+// Where no plan fits one round (the x slice of 16 * ct + 1 columns crowds the rows' words out of
+// LDS: Llama-3-70B down_proj, n = 28672, from 48 batch rows; n = 11008 at r = 2976 at 128 rows), the
+// search is repeated with up to kSbMaxRounds rounds of blocks, each plan's estimate multiplied by its
+// rounds. The alternative, s1m_kernel, streams all of x through every block of 16 rows of V (n =
+// 28672, r = 3520, stage 1 at 48 / 64 / 128 rows: 102.8 / 136.6 / 237.9 us with s1m_kernel).
 inline bool sb_plan_any(int64_t batch, int64_t rows, int64_t wpr, int64_t kpad, SbPlan& p);
 inline bool sb_plan(int64_t batch, int64_t rows, int64_t wpr, int64_t kpad, SbPlan& p) {
     if (batch > kSbMaxBatch || rows <= 0 || wpr <= 0) return false;
     if (wpr < kSbWideWords || batch < sb_min_batch(wpr, rows)) return false;
     return sb_plan_any(batch, rows, wpr, kpad, p);
 }
-// The search itself, for any batch up to kSbMaxBatch.
-inline bool sb_plan_any(int64_t batch, int64_t rows, int64_t wpr, int64_t kpad, SbPlan& p) {
-    if (batch > kSbMaxBatch || rows <= 0 || wpr <= 0) return false;
+// The search over grids of up to max_rounds rounds of blocks.
+inline bool sb_plan_rounds(int64_t batch, int64_t rows, int64_t wpr, int64_t kpad, int max_rounds, SbPlan& p) {
     const int ct = static_cast<int>(std::min<int64_t>(8, ceil_div(batch, 16)));
     const int passes = static_cast<int>(ceil_div(batch, 16LL * ct));
     const int xcols = 16 * ct + 1;
@@ -1680,7 +1687,8 @@ inline bool sb_plan_any(int64_t batch, int64_t rows, int64_t wpr, int64_t kpad, 
         for (int64_t want = 1; want <= wpr; ++want) {
             const int64_t kw = std::max<int64_t>(2, (ceil_div(wpr, want) + 1) & ~int64_t{1});
             const int64_t ks = ceil_div(wpr, kw);
-            if (row_blocks * ks * passes > kSbMaxBlocks) break;
+            const int64_t blocks = row_blocks * ks * passes;
+            if (blocks > int64_t{kSbMaxBlocks} * max_rounds) break;
             const size_t lds = std::max<size_t>(
                 static_cast<size_t>(sb_xs_dwords(xcols, static_cast<int>(kw)) + sb_w_dwords(br, static_cast<int>(kw))) * 4,
                 static_cast<size_t>(16 * ct) * (br + 4) * 4);
@@ -1688,7 +1696,7 @@ inline bool sb_plan_any(int64_t batch, int64_t rows, int64_t wpr, int64_t kpad, 
             const double mfma = rtw * ct * kw * 16.0 * 1.25;
             const double dma = (xcols * 64.0 + br * 4.0) * kw / 32.0;
             const double fin = ks > 1 ? 4000.0 + 2.0 * ks * batch * kpad * 4.0 / (256.0 * 16.0) : 0.0;
-            const double cost = mfma + dma + fin;
+            const double cost = (mfma + dma) * static_cast<double>(ceil_div(blocks, kSbMaxBlocks)) + fin;
             if (best < 0 || cost < best) {
                 best = cost;
                 p.rtw = rtw;
@@ -1702,6 +1710,11 @@ inline bool sb_plan_any(int64_t batch, int64_t rows, int64_t wpr, int64_t kpad, 
         }
     }
     return best >= 0;
+}
+// The search itself, for any batch up to kSbMaxBatch: one round of blocks if any plan fits it.
+inline bool sb_plan_any(int64_t batch, int64_t rows, int64_t wpr, int64_t kpad, SbPlan& p) {
+    if (batch > kSbMaxBatch || rows <= 0 || wpr <= 0) return false;
+    return sb_plan_rounds(batch, rows, wpr, kpad, 1, p) || sb_plan_rounds(batch, rows, wpr, kpad, kSbMaxRounds, p);
 }
 
 template <typename T, int NB>

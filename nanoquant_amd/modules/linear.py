@@ -19,7 +19,7 @@ The layer computes ``y = s_post * (U (s_mid * (V (s_pre * x))))`` with ``V`` [ra
 * a state dict in which ``V``/``U`` appear as ``{name}_packed`` lsb_first sign words plus
   ``{name}_shape`` (:359-394), expanded back on load (:396-433).
 
-Additions of this package: kernel type "auto" (GEMV up to ``AUTO_GEMV_MAX_ROWS`` rows, GEMM
+Additions of this package: kernel type "auto" (GEMV up to ``auto_gemv_max_rows`` rows, GEMM
 beyond), ``_prepare_kernel_from_packed`` and ``load_packed_for_kernels`` (kernel words made
 straight from checkpoint words). Quantization-time training, knowledge distillation and the
 gemlite kernel are not part of this package.
@@ -33,10 +33,26 @@ import torch.nn.functional as F
 from ..kernel.utils import (binary_packer, binary_unpacker, get_kernel_function, marlin_nanoquant_packer,
                             pack_binary_marlin_fused_from_packed, repack_binary_gemv)
 
-# Rows up to which kernel_type "auto" runs the GEMV; more rows run the GEMM. Measured on the
-# Llama-2-7B gate and down shapes at 0.55 bpw (bench.py --batch-sweep): at 128 rows the GEMV takes
-# 27.4 and 32.1 us against the GEMM's 36.8 and 39.0 us, at 256 rows 48 and 79 us against 36 and 43 us.
-AUTO_GEMV_MAX_ROWS = 128
+# Kernel type "auto" runs the GEMV while rows * rank * (in + out) stays within a work bound, and
+# at most AUTO_GEMV_MAX_ROWS rows (at least AUTO_GEMV_MIN_ROWS); the GEMM otherwise. The bound
+# depends on the layer's orientation: the GEMV's cost grows with the rows faster on a tall U (its
+# stage 2) than on a wide V (its k-split stage 1), and the GEMM runs slower on a long K. Fitted on
+# both kernels at 16-256 rows on every Llama-2-7B (1.0 and 0.55 bpw) and Llama-3-70B (0.55 bpw)
+# linear shape (bench.py --batch-sweep --batch-sweep-shapes configs): the sum of the picked times
+# over the 80 cells is 0.4% above always picking the faster op (worst cell 10.7%: Llama-3-70B q/o
+# at 64 rows), against 10.3% above (worst 73%, Llama-3-70B down_proj at 128 rows) for a fixed
+# switch at 128 rows. The GEMV won or tied at 16 rows on every shape.
+AUTO_GEMV_WORK_TALL = 2.3e9  # out_features >= in_features
+AUTO_GEMV_WORK_WIDE = 3.5e9  # in_features > out_features
+AUTO_GEMV_MIN_ROWS = 16
+AUTO_GEMV_MAX_ROWS = 256
+
+
+def auto_gemv_max_rows(in_features: int, out_features: int, rank: int) -> int:
+    """Rows up to which kernel type "auto" runs the GEMV on a layer of these sizes."""
+    work = AUTO_GEMV_WORK_WIDE if in_features > out_features else AUTO_GEMV_WORK_TALL
+    rows = int(work // max(1, rank * (in_features + out_features)))
+    return max(AUTO_GEMV_MIN_ROWS, min(AUTO_GEMV_MAX_ROWS, rows))
 
 # The GEMV tuning ints the reference fixes when it prepares the layer (linear.py:210-219). The
 # HIP kernels validate them and choose their own launch shapes.
@@ -143,7 +159,7 @@ class NanoQuantLinear(nn.Module):
 
     def _run_kernel(self, rows):
         kind = self.kernel_type
-        if kind == "gemv" or (kind == "auto" and rows.size(0) <= AUTO_GEMV_MAX_ROWS):
+        if kind == "gemv" or (kind == "auto" and rows.size(0) <= self.auto_gemv_rows):
             return self.kernel_forward(rows, self.scale_pre, self.V_int8, self.scale_mid, self.U_int8,
                                        self.scale_post, **self.kernel_kwargs)
         if kind == "gemm":
@@ -167,6 +183,7 @@ class NanoQuantLinear(nn.Module):
         self.do_kernel_inference = True
         self.kernel_type = kernel_type
         self.dtype = dtype
+        self.auto_gemv_rows = auto_gemv_max_rows(self.in_features, self.out_features, self.rank)
         for name in ("scale_pre", "scale_post", "scale_mid"):
             value = getattr(self, name, None)
             setattr(self, name, None if value is None else _frozen(value.to(dtype).squeeze(0)))
@@ -204,7 +221,7 @@ class NanoQuantLinear(nn.Module):
 
         "gemv": half2 sign words. "gemm": the Marlin layout (a missing ``scale_mid`` becomes ones,
         linear.py:221-225). "auto" (this package): both, the GEMV taking up to
-        ``AUTO_GEMV_MAX_ROWS`` rows and the GEMM more.
+        ``auto_gemv_max_rows(in, out, rank)`` rows and the GEMM more.
         """
         self._check_kernel_type(kernel_type)
         self._enter_kernel_mode(kernel_type, dtype)

@@ -270,6 +270,12 @@ GEMV_CASES = [
     ("s1l_b1_n12288_mid", 400, 12288, 130, 1, True),
     ("s1l_b1_n11008_r1", 64, 11008, 1, 1, True),
     ("s1m_b3_n32760", 300, 32760, 130, 3, True),
+    # the batched stage 1 where no plan fits one round of blocks (the x slice of 48+ batch rows
+    # leaves too little LDS for the rows' words): two rounds at 48 and 128 rows, three at 100, with
+    # ragged ranks and batch
+    ("sb_rounds_b48_n28672", 300, 28672, 3000, 48, True),
+    ("sb_rounds_b128_n11008", 500, 11008, 2976, 128, False),
+    ("sb_rounds_b100_n28672", 200, 28672, 2900, 100, True),
 ]
 
 
@@ -701,26 +707,36 @@ def test_load_packed_for_kernels_matches_dense_route(nq, kernel):
     assert torch.equal(ya, yb)
 
 
-def test_auto_kernel_routes_by_rows(nq):
-    """kernel_type "auto" runs the GEMV up to AUTO_GEMV_MAX_ROWS rows and the GEMM beyond: its
+# (in, out, rank) of the auto-routing layers: a small one, whose GEMV limit is the 256-row cap, and
+# the Llama-2-7B q/k/v/o shape at 0.55 bpw, whose limit the work bound sets (250 rows)
+AUTO_LAYERS = [(256, 320, 96), (4096, 4096, 1120)]
+
+
+@pytest.mark.parametrize("sizes", AUTO_LAYERS, ids=[f"{i}x{o}_r{r}" for i, o, r in AUTO_LAYERS])
+def test_auto_kernel_routes_by_rows(nq, sizes):
+    """kernel_type "auto" runs the GEMV up to auto_gemv_max_rows rows and the GEMM beyond: its
     outputs equal those of the layer prepared for that kernel, bit for bit, from the dense
     factors and from the packed state dict alike."""
-    announce("auto kernel")
+    announce("auto kernel", sizes)
     import copy
-    from nanoquant_amd.modules.linear import AUTO_GEMV_MAX_ROWS
+    from nanoquant_amd.modules.linear import auto_gemv_max_rows
     from tests.test_host import make_layer
-    base, c = make_layer(256, 320, 96, seed=12, with_mid=True, device="cuda")
+    n_in, n_out, rank = sizes
+    limit = auto_gemv_max_rows(n_in, n_out, rank)
+    assert limit == (256 if n_in == 256 else 250), limit
+    base, c = make_layer(n_in, n_out, rank, seed=12, with_mid=True, device="cuda")
     state = {k: v.clone() for k, v in base.state_dict().items()}
     layers = {}
     for kt in ("gemv", "gemm", "auto"):
         layers[kt] = copy.deepcopy(base)
         layers[kt]._prepare_kernel(kt, torch.float16)
-    packed_auto, _ = make_layer(256, 320, 96, seed=99, with_mid=True, device="cuda")
+    packed_auto, _ = make_layer(n_in, n_out, rank, seed=99, with_mid=True, device="cuda")
     nq.load_packed_for_kernels(packed_auto, state, "auto", torch.float16)
+    assert layers["auto"].auto_gemv_rows == limit and packed_auto.auto_gemv_rows == limit
     rng = np.random.default_rng(4)
     f = lambda t: t.detach().double().cpu().numpy().reshape(-1)  # noqa: E731
-    for rows, kernel in ((1, "gemv"), (AUTO_GEMV_MAX_ROWS, "gemv"), (AUTO_GEMV_MAX_ROWS + 1, "gemm"), (300, "gemm")):
-        x = torch.from_numpy(rng.normal(size=(rows, 256)).astype(np.float16)).cuda()
+    for rows, kernel in ((1, "gemv"), (limit, "gemv"), (limit + 1, "gemm"), (300, "gemm")):
+        x = torch.from_numpy(rng.normal(size=(rows, n_in)).astype(np.float16)).cuda()
         want = layers[kernel](x)
         for got in (layers["auto"](x), packed_auto(x)):
             assert torch.equal(got, want), (rows, kernel)
@@ -728,5 +744,5 @@ def test_auto_kernel_routes_by_rows(nq):
                                       f(base.scale_post))
         err = np.abs(want.double().cpu().numpy() - y64).max() / np.abs(y64).max()
         assert err <= 1e-3, (rows, err)
-    x3 = torch.from_numpy(rng.normal(size=(2, 80, 256)).astype(np.float16)).cuda()  # 160 rows: the GEMM
+    x3 = torch.from_numpy(rng.normal(size=(2, 130, n_in)).astype(np.float16)).cuda()  # 260 rows: the GEMM
     assert torch.equal(layers["auto"](x3), layers["gemm"](x3))
