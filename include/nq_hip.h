@@ -217,6 +217,19 @@ int nq_gemv_group_stage2_rope(int dtype, const nq_gemv_item* items, int64_t batc
                               int64_t max_len, void* scores_mask, void* workspace, size_t workspace_bytes,
                               nq_stream_t stream);
 
+/* Stage 2 of the q, k and v projections of a decode step (items[0..2], after nq_gemv_group_stage1
+ * over the same three items) with the value-cache write folded into the store, for a step whose
+ * rotary embedding and key-cache write run elsewhere: q and k are stored into items[0].y and
+ * items[1].y exactly as NQ_EPI_STORE stores them, v is rounded the same way and copied into
+ * v_cache[b, kvh, p, :] ([batch, items[2].m / head_dim, max_len, head_dim]), p = *position (device
+ * int64, read when the kernel runs, so a graph replays it); items[2].y is not written (any valid
+ * pointer). A position outside [0, max_len) writes no cache row. head_dim a multiple of 16; every m
+ * a multiple of head_dim. No counterpart in the reference (its decode step writes the cache in
+ * Hugging Face's cache update, kernel/test_decode.py:385-402); it saves the step one launch. */
+int nq_gemv_group_stage2_kv(int dtype, const nq_gemv_item* items, int64_t batch, void* v_cache,
+                            const int64_t* position, int64_t head_dim, int64_t max_len, void* workspace,
+                            size_t workspace_bytes, nq_stream_t stream);
+
 /* ---------------------------------------------------------------- prefill GEMM */
 
 /* C[M, N] = sat((A[M, K] * W) * s_out) with W[k, o] = sign(k, o) * s_in[k]:
@@ -297,6 +310,17 @@ int nq_rope_kv_write(int dtype, const void* qkv, int64_t qkv_stride, void* k_cac
                      const void* rope_cos, const void* rope_sin, const int64_t* position, void* q_out,
                      int64_t q_stride, int64_t batch, int64_t heads, int64_t kv_heads, int64_t head_dim,
                      int64_t max_len, nq_stream_t stream);
+
+/* ---------------------------------------------------------------- dense GEMV */
+
+/* y[b, j] = dtype(sum_k w[j, k] x[b, k]) for b < batch, j < m: a dense linear of a few rows, the
+ * lm_head of a decode step. w dtype [m, n] row-major, x dtype [batch, n] contiguous (both 16-byte
+ * aligned), y dtype rows of ldy >= m elements. fp32 sum, rounded once to dtype (overflow to +-inf
+ * as a torch linear does). n a multiple of 8. Each wave streams one row of w with 8 KB of loads in
+ * flight, which is what reading a large w from HBM takes. No counterpart in the reference, whose
+ * decode step runs the lm_head as torch's linear (kernel/test_decode.py:387-394). */
+int nq_dense_gemv(int dtype, const void* w, const void* x, void* y, int64_t batch, int64_t n, int64_t m, int64_t ldy,
+                  nq_stream_t stream);
 
 /* ---------------------------------------------------------------- measurement aid */
 

@@ -72,11 +72,13 @@ SIGNATURES = {
     "nq_gemv_group_stage2": (_int, [_int, _i64, _items_p, _i64, _int, _vp, _size, _vp]),
     "nq_gemv_group_stage2_rope": (_int, [_int, _items_p, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _vp,
                                          _size, _vp]),
+    "nq_gemv_group_stage2_kv": (_int, [_int, _items_p, _i64, _vp, _vp, _i64, _i64, _vp, _size, _vp]),
     "nq_attention_decode_workspace_bytes": (_size, [_i64, _i64, _i64, _i64, _i64]),
     "nq_attention_decode": (_int, [_int, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
                                    _i64, ctypes.c_float, _vp, _size, _vp]),
     "nq_rope_kv_write": (_int, [_int, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
                                  _vp]),
+    "nq_dense_gemv": (_int, [_int, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
     "nq_gemm_onebit_workspace_bytes": (_size, [_i64, _i64, _i64]),
     "nq_gemm_onebit": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _size, _vp]),
     "nq_gemm_nanoquant_workspace_bytes": (_size, [_i64, _i64, _i64, _i64]),

@@ -372,6 +372,67 @@ bool launch_attn_g(int g, const void* q, const void* k, const void* v, int64_t q
 #undef NQ_ATTN
 }
 
+// ---- dense GEMV: the lm_head of a decode step
+//
+// y[b][j] = T(sum_k W[j][k] x[b][k]) (fp32 sum, one rounding), W [m][n] row-major in T. A decode
+// step reaches its lm_head after its layers have streamed their weights through the caches, so W
+// comes from HBM, and streaming it at speed takes many bytes in flight per CU: each wave owns one
+// row of W and issues every 16-byte load of a 4096-column group of it at once (8 per lane,
+// non-temporal), x's matching chunks come from L2, and the wave's sum is reduced across lanes.
+// Loads past the row's end read zeros (buffer resource bounds), so n need only be a multiple of 8.
+// NB batch rows per block (grid.y covers the batch); blocks hold 4 rows of W.
+constexpr int kDenseCols = 4096;  // columns of W a wave has in flight: 64 lanes x 8 x 8 elements
+
+template <typename T, int NB>
+__global__ __launch_bounds__(256) void dense_gemv_kernel(const uint16_t* __restrict__ w, const uint16_t* __restrict__ x,
+                                                         uint16_t* __restrict__ y, int m, int n, int batch, int ldy) {
+    const int lane = threadIdx.x & 63;
+    const int row = static_cast<int>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (row >= m) return;  // a whole wave (the kernel has no barrier)
+    const int b0 = static_cast<int>(blockIdx.y) * NB;
+    const uint32_t row_bytes = static_cast<uint32_t>(n) * 2u;
+    const rsrc_t wr = make_rsrc(w + static_cast<size_t>(row) * static_cast<size_t>(n), row_bytes);
+    rsrc_t xr[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+        xr[b] = make_rsrc(x + static_cast<size_t>(min(b0 + b, batch - 1)) * static_cast<size_t>(n), row_bytes);
+    float acc[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[b] = 0.0f;
+    for (int c0 = 0; c0 < n; c0 += kDenseCols) {
+        u32x4 wv[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            wv[k] = load_b128_stream(wr, static_cast<uint32_t>(c0 + (k * 64 + lane) * 8) * 2u);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const u32x4 xv = load_b128(xr[b], static_cast<uint32_t>(c0 + (k * 64 + lane) * 8) * 2u);
+                acc[b] = T::dot2(wv[k].x, xv.x, acc[b]);
+                acc[b] = T::dot2(wv[k].y, xv.y, acc[b]);
+                acc[b] = T::dot2(wv[k].z, xv.z, acc[b]);
+                acc[b] = T::dot2(wv[k].w, xv.w, acc[b]);
+            }
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const float s = wave_sum(acc[b]);
+        if (lane == 0 && b0 + b < batch) y[static_cast<size_t>(b0 + b) * ldy + row] = T::from_float(s);
+    }
+}
+
+template <typename T>
+void launch_dense_gemv(const uint16_t* w, const uint16_t* x, uint16_t* y, int m, int n, int batch, int ldy,
+                       hipStream_t st) {
+    const int nb = batch >= 4 ? 4 : (batch >= 2 ? 2 : 1);
+    const dim3 grid(static_cast<unsigned>(ceil_div(m, 4)), static_cast<unsigned>(ceil_div(batch, nb)));
+    if (nb == 4) dense_gemv_kernel<T, 4><<<grid, 256, 0, st>>>(w, x, y, m, n, batch, ldy);
+    else if (nb == 2) dense_gemv_kernel<T, 2><<<grid, 256, 0, st>>>(w, x, y, m, n, batch, ldy);
+    else dense_gemv_kernel<T, 1><<<grid, 256, 0, st>>>(w, x, y, m, n, batch, ldy);
+}
+
 }  // namespace
 }  // namespace nq
 
@@ -465,6 +526,34 @@ int nq_rope_kv_write(int dtype, const void* qkv, int64_t qkv_stride, void* k_cac
                                                    static_cast<int>(q_stride), static_cast<int>(batch),
                                                    static_cast<int>(heads), static_cast<int>(kv_heads),
                                                    static_cast<int>(head_dim), static_cast<int>(max_len));
+    return check_launch(name);
+}
+
+int nq_dense_gemv(int dtype, const void* w, const void* x, void* y, int64_t batch, int64_t n, int64_t m, int64_t ldy,
+                  nq_stream_t stream) {
+    const char* name = "nq_dense_gemv";
+    if (dtype != NQ_F16 && dtype != NQ_BF16) return fail(NQ_ERR_DTYPE, "%s: unsupported dtype %d", name, dtype);
+    if (batch < 0 || n <= 0 || m <= 0 || ldy < m)
+        return fail(NQ_ERR_INVALID_ARGUMENT, "%s: bad sizes (batch %lld, n %lld, m %lld, ldy %lld)", name,
+                    (long long)batch, (long long)n, (long long)m, (long long)ldy);
+    if (n % 8) return fail(NQ_ERR_SHAPE, "%s: n must be a multiple of 8, got %lld", name, (long long)n);
+    if (n > (int64_t{1} << 28) || m > INT32_MAX / 2 || ldy > INT32_MAX / 2 || batch > 65535 * 4 ||
+        batch * ldy > (int64_t{1} << 40))
+        return fail(NQ_ERR_UNSUPPORTED, "%s: sizes too large", name);
+    if (batch == 0) return NQ_OK;
+    if (!w || !x || !y) return fail(NQ_ERR_INVALID_ARGUMENT, "%s: null pointer", name);
+    if (!aligned(w, 16) || !aligned(x, 16) || !aligned(y, 2))
+        return fail(NQ_ERR_ALIGNMENT, "%s: w and x must be 16-byte aligned, y 2-byte", name);
+    const auto* wp = static_cast<const uint16_t*>(w);
+    const auto* xp = static_cast<const uint16_t*>(x);
+    auto* yp = static_cast<uint16_t*>(y);
+    hipStream_t st = as_stream(stream);
+    if (dtype == NQ_F16)
+        launch_dense_gemv<F16>(wp, xp, yp, static_cast<int>(m), static_cast<int>(n), static_cast<int>(batch),
+                               static_cast<int>(ldy), st);
+    else
+        launch_dense_gemv<BF16>(wp, xp, yp, static_cast<int>(m), static_cast<int>(n), static_cast<int>(batch),
+                                static_cast<int>(ldy), st);
     return check_launch(name);
 }
 

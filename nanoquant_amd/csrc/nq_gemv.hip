@@ -258,11 +258,13 @@ struct S2Item {
     int m, wr, zpitch;
     int ystride;  // elements between batch rows of y and resid
     int blocks;  // blockIdx.x < blocks do the item's rows (each item has a grid plane, blockIdx.z)
-    int rope;         // kEpiRope: 1 rotate into y (queries), 2 rotate into cache (keys), 3 copy into cache (values)
+    int rope;         // kEpiRope: 0 store into y, 1 rotate into y (queries), 2 rotate into cache (keys),
+                      // 3 copy into cache (values)
     uint16_t* cache;  // kEpiRope, kinds 2 and 3: [batch, m / head_dim, max_len, head_dim]
 };
 
-// The rotary step of kEpiRope: position p = *pos (device), cos/sin rows [max_len, head_dim].
+// The rotary step of kEpiRope: position p = *pos (device), cos/sin rows [max_len, head_dim] (null when
+// no item rotates).
 struct S2Rope {
     const int64_t* pos;
     const uint16_t* cos;
@@ -944,7 +946,7 @@ __global__ __launch_bounds__(256) void s2t_kernel(const S2Table tab, int batch) 
     // the rotary cos/sin entries of this lane's epilogue rows (row p of the tables; p outside the
     // tables reads row 0, and those values are never used)
     uint16_t rcos[4] = {0, 0, 0, 0}, rsin[4] = {0, 0, 0, 0};
-    if (EPI == kEpiRope) {
+    if (EPI == kEpiRope && tab.rope.cos != nullptr) {
         const int D = tab.rope.head_dim;
         const size_t prow = p64 >= 0 && p64 < tab.rope.max_len ? static_cast<size_t>(p64) * D : 0;
 #pragma unroll
@@ -1097,7 +1099,9 @@ __global__ __launch_bounds__(256) void s2t_kernel(const S2Table tab, int batch) 
                                                    T::to_float(T::from_float(xr * T::to_float(rsin[i]))));
                 const bool p_ok = p64 >= 0 && p64 < tab.rope.max_len;
                 if (b_ok && row < m) {
-                    if (it.rope == 1) {
+                    if (it.rope == 0) {
+                        its[0].y[static_cast<size_t>(b0 + bcol) * its[0].ystride + row] = val;
+                    } else if (it.rope == 1) {
                         its[0].y[static_cast<size_t>(b0 + bcol) * its[0].ystride + row] = p_ok ? rot : uint16_t(0);
                     } else if (p_ok) {
                         const size_t at = ((static_cast<size_t>(b0 + bcol) * (m / D) + row / D) * tab.rope.max_len +
@@ -2603,11 +2607,13 @@ int nq_gemv_group_stage1(int dtype, int64_t count, const nq_gemv_item* items, co
 namespace nq {
 namespace {
 
-// The group stage 2 with any epilogue; `rope` (kEpiRope only) carries the rotary step and the caches.
+// The group stage 2 with any epilogue; `rope` (kEpiRope only) carries the rotary step, the caches
+// and what the store does with each of the three items (S2Item::rope).
 struct RopeArgs {
     S2Rope rope;
     uint16_t* k_cache;
     uint16_t* v_cache;
+    int kind[3];
 };
 
 int group_stage2(const char* name, int dtype, int64_t count, const nq_gemv_item* items, int64_t batch, int epilogue,
@@ -2660,6 +2666,35 @@ int nq_gemv_group_stage2_rope(int dtype, const nq_gemv_item* items, int64_t batc
     ra.rope.mask_groups = scores_mask ? static_cast<int>(items[0].m / items[1].m) : 1;
     ra.k_cache = static_cast<uint16_t*>(k_cache);
     ra.v_cache = static_cast<uint16_t*>(v_cache);
+    ra.kind[0] = 1;  // q rotated into its output
+    ra.kind[1] = 2;  // k rotated into the key cache
+    ra.kind[2] = 3;  // v copied into the value cache
+    return group_stage2(name, dtype, 3, items, batch, -1, &ra, workspace, workspace_bytes, stream);
+}
+
+int nq_gemv_group_stage2_kv(int dtype, const nq_gemv_item* items, int64_t batch, void* v_cache,
+                            const int64_t* position, int64_t head_dim, int64_t max_len, void* workspace,
+                            size_t workspace_bytes, nq_stream_t stream) {
+    const char* name = "nq_gemv_group_stage2_kv";
+    if (!items) return fail(NQ_ERR_INVALID_ARGUMENT, "%s: null items", name);
+    if (head_dim < 16 || head_dim % 16 || max_len <= 0 || max_len > INT32_MAX / 2)
+        return fail(NQ_ERR_INVALID_ARGUMENT, "%s: head_dim must be a positive multiple of 16 and max_len positive",
+                    name);
+    for (int k = 0; k < 3; ++k)
+        if (items[k].m % head_dim)
+            return fail(NQ_ERR_SHAPE, "%s: item %d: m %lld is not whole heads of %lld", name, k,
+                        (long long)items[k].m, (long long)head_dim);
+    if (batch > 0 && (!v_cache || !position)) return fail(NQ_ERR_INVALID_ARGUMENT, "%s: null pointer", name);
+    if (!aligned(v_cache, 2) || !aligned(position, 8)) return fail(NQ_ERR_ALIGNMENT, "%s: misaligned operand", name);
+    if (batch * (items[2].m / head_dim) * max_len * head_dim > ((int64_t)1 << 40))
+        return fail(NQ_ERR_UNSUPPORTED, "%s: cache too large", name);
+    RopeArgs ra;
+    ra.rope = S2Rope{position, nullptr, nullptr, static_cast<int>(head_dim), static_cast<int>(max_len), nullptr, 0u, 1};
+    ra.k_cache = nullptr;
+    ra.v_cache = static_cast<uint16_t*>(v_cache);
+    ra.kind[0] = 0;  // q stored into its output
+    ra.kind[1] = 0;  // k stored into its output
+    ra.kind[2] = 3;  // v copied into the value cache
     return group_stage2(name, dtype, 3, items, batch, -1, &ra, workspace, workspace_bytes, stream);
 }
 
@@ -2705,8 +2740,8 @@ int group_stage2(const char* name, int dtype, int64_t count, const nq_gemv_item*
         it.zpitch = g.plan[k].zpitch;
         it.ystride = static_cast<int>(in.y_stride);
         it.blocks = 0;
-        it.rope = rope == nullptr ? 0 : static_cast<int>(k) + 1;  // q, k, v
-        it.cache = rope == nullptr ? nullptr : (k == 1 ? rope->k_cache : k == 2 ? rope->v_cache : nullptr);
+        it.rope = rope == nullptr ? 0 : rope->kind[k];
+        it.cache = rope == nullptr ? nullptr : (it.rope == 2 ? rope->k_cache : it.rope == 3 ? rope->v_cache : nullptr);
     }
     // one launch per class of items that share the stage-2 word split (equal ranks always do)
     const int b = static_cast<int>(batch);

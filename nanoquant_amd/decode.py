@@ -160,21 +160,50 @@ def rotary_attention(shape: LlamaShape, layer: int, q, k, v, cos, sin, positions
     return torch.matmul(p, v_c).view(B, H, T, D).transpose(1, 2).reshape(B, T, H * D)
 
 
-def rotary_step_tables(cos, sin, positions, cache: StaticKVCache, dtype):
+_STEP_CONSTANTS = {}
+
+
+def step_constants(head_dim: int, dtype, device):
+    """The fixed parts of a one-token step's tables, made once per (head_dim, dtype, device): the
+    identity I and the rotate-half matrix P (x @ P == rotate_half(x)) in ``dtype``, and the two
+    values of the additive causal mask (0, -inf) as 0-d tensors."""
+    key = (head_dim, dtype, str(device))
+    if key not in _STEP_CONSTANTS:
+        h = head_dim // 2
+        eye = torch.eye(head_dim, device=device, dtype=dtype)
+        rot = torch.zeros(head_dim, head_dim, device=device, dtype=dtype)
+        idx = torch.arange(h, device=device)
+        rot[idx + h, idx] = -1.0  # out[j < h] takes -x[j + h]
+        rot[idx, idx + h] = 1.0   # out[j >= h] takes x[j - h]
+        _STEP_CONSTANTS[key] = (eye, rot, torch.zeros((), device=device, dtype=dtype),
+                                torch.full((), float("-inf"), device=device, dtype=dtype))
+    return _STEP_CONSTANTS[key]
+
+
+def step_mask(positions, cache: StaticKVCache, dtype, out=None):
+    """The additive causal mask of a one-token step at ``positions`` (one position, on the device):
+    [1, L, 1], 0 for cache rows up to the position and -inf past it; written into ``out`` (any
+    shape that broadcasts [1, L, 1], e.g. every layer's scores at once) when it is given."""
+    _, _, zero, ninf = step_constants(2, dtype, positions.device)
+    visible = cache.key_index.view(1, -1, 1) <= positions.view(1, 1, 1)
+    if out is None:
+        return torch.where(visible, zero, ninf)
+    # the condition takes out's full shape, so that the result is written in place, not resized
+    L = visible.shape[1]
+    visible = visible.view([1] * (out.dim() - 2) + [L, 1]).expand(out.shape)
+    return torch.where(visible, zero, ninf, out=out)
+
+
+def rotary_step_tables(cos, sin, positions, cache: StaticKVCache, dtype, with_mask: bool = True):
     """What every layer of a one-token step at ``positions`` (one position, on the device) shares:
     the rotary embedding as a [D, D] matrix R (x @ R == x * cos + rotate_half(x) * sin, with cos and
     sin [1, D] of that position) and the causal mask as an additive [1, L, 1] (0 for visible cache
-    rows, -inf past the position)."""
+    rows, -inf past the position; None without ``with_mask``). R = I * cos + P * sin column by
+    column: each entry is one of cos, +-sin or 0, exact in ``dtype``."""
     D = cos.shape[-1]
-    h = D // 2
-    c, s_ = cos.float().view(-1), sin.float().view(-1)
-    R = torch.diag_embed(c)
-    idx = torch.arange(h, device=cos.device)
-    R[idx + h, idx] = -s_[:h]  # out[j < h] takes -x[j + h] * sin[j]
-    R[idx, idx + h] = s_[h:]   # out[j >= h] takes x[j - h] * sin[j]
-    visible = cache.key_index.view(1, -1, 1) <= positions.view(1, 1, 1)
-    madd = torch.zeros(visible.shape, device=cos.device, dtype=dtype).masked_fill_(~visible, float("-inf"))
-    return R.to(dtype), madd
+    eye, rot, _, _ = step_constants(D, dtype, cos.device)
+    R = torch.addcmul(eye * cos.reshape(1, D).to(dtype), rot, sin.reshape(1, D).to(dtype))
+    return R, (step_mask(positions, cache, dtype) if with_mask else None)
 
 
 def attention_products_step(shape: LlamaShape, layer: int, q, madd, cache: StaticKVCache, out, scores=None):
@@ -208,14 +237,17 @@ def attention_products_step(shape: LlamaShape, layer: int, q, madd, cache: Stati
     return out
 
 
-def rotary_attention_step(shape: LlamaShape, layer: int, qk, v, tables, positions, cache: StaticKVCache, out=None):
+def rotary_attention_step(shape: LlamaShape, layer: int, qk, v, tables, positions, cache: StaticKVCache, out=None,
+                          scores=None):
     """``rotary_attention`` for one token per sequence in seven torch launches: RoPE of q and k as one
     matrix product, the two cache writes, the scores of each kv head's query group with the scale and
     the causal mask folded into one batched product, the softmax, the value product and the copy out.
 
-    qk [B, (H + KV) * D] (q heads then k heads, contiguous), v [B, KV * D]; ``tables`` from
-    ``rotary_step_tables``; returns [B, 1, H * D], written into ``out`` [B, H * D] when it is given
-    and each kv head serves one query head (the value product then needs no copy).
+    qk [B, (H + KV) * D] (q heads then k heads, contiguous), v [B, KV * D], or None when the value
+    row is already in the cache; ``tables`` from ``rotary_step_tables``; returns [B, 1, H * D],
+    written into ``out`` [B, H * D] when it is given and each kv head serves one query head (the
+    value product then needs no copy). With ``scores`` [B * KV, L, G] already holding the step's
+    additive causal mask, the scores product adds into it in place (the mask is not copied first).
     """
     H, KV, D = shape.heads, shape.kv_heads, shape.head_dim
     B, G = qk.shape[0], H // KV
@@ -224,10 +256,14 @@ def rotary_attention_step(shape: LlamaShape, layer: int, qk, v, tables, position
     L = k_c.shape[2]
     rot = torch.mm(qk.reshape(-1, D), R).view(B, H + KV, D)
     k_c.index_copy_(2, positions, rot[:, H:].unsqueeze(2).to(k_c.dtype))
-    v_c.index_copy_(2, positions, v.reshape(B, KV, 1, D).to(v_c.dtype))
+    if v is not None:
+        v_c.index_copy_(2, positions, v.reshape(B, KV, 1, D).to(v_c.dtype))
     # K [B*KV, L, D] @ Q^T [B*KV, D, G]: the right operand is a contiguous copy (free for one query per kv head)
     q_t = rot[:, :H].reshape(B * KV, G, D).transpose(1, 2).contiguous()
-    scores = torch.baddbmm(madd, k_c.view(B * KV, L, D), q_t.to(k_c.dtype), alpha=D ** -0.5)  # [B*KV, L, G]
+    if scores is None:
+        scores = torch.baddbmm(madd, k_c.view(B * KV, L, D), q_t.to(k_c.dtype), alpha=D ** -0.5)  # [B*KV, L, G]
+    else:
+        scores.baddbmm_(k_c.view(B * KV, L, D), q_t.to(k_c.dtype), alpha=D ** -0.5)
     p = torch.softmax(scores, dim=1)
     if out is not None and G == 1:
         torch.bmm(v_c.view(B * KV, L, D).transpose(1, 2), p, out=out.view(B * KV, D, 1))
@@ -455,16 +491,20 @@ class FusedDecoder(GraphDecoder):
     2. q, k, v stage 2 in one launch, into one [B, (heads + 2 kv_heads) * head_dim] buffer;
     3. rotary embedding, KV-cache write and attention: in torch ops (``attention="torch"``, the
        default, as the benchmark's end-to-end configuration keeps the non-linear ops in
-       PyTorch), or the rotary embedding and cache write folded into step 2's stores
-       (``nq_gemv_group_stage2_rope``) and the attention products in torch (``attention="rope"``),
-       or all of it in one HIP launch pair (``attention="hip"``, ``nq_attention_decode``);
+       PyTorch; step 2 then also writes the value row into its cache,
+       ``nq_gemv_group_stage2_kv``, and the step's causal mask goes into every layer's scores
+       buffer in one launch per step), or the rotary embedding and cache write folded into step
+       2's stores (``nq_gemv_group_stage2_rope``) and the attention products in torch
+       (``attention="rope"``), or all of it in one HIP launch pair (``attention="hip"``,
+       ``nq_attention_decode``);
     4, 5. o_proj, its stage 2 adding the residual;
     6. gate and up stage 1 in one launch, post_attention_layernorm folded in;
     7. gate and up stage 2 in one launch storing silu(gate) * up;
     8, 9. down_proj, its stage 2 adding the residual.
-    The embedding lookup, final norm, lm_head and argmax stay torch ops. Prefill runs the
-    unfused model (it fills the same cache layout). Needs the model packed for the ``gemv``
-    kernel in float16 or bfloat16 and head_dim 128.
+    The lm_head runs as one dense GEMV of the library (``nq_dense_gemv``: torch's linear reads
+    its weights, cold after the layers, at a fraction of the bandwidth); the embedding lookup,
+    final norm and argmax stay torch ops. Prefill runs the unfused model (it fills the same cache
+    layout). Needs the model packed for the ``gemv`` kernel in float16 or bfloat16 and head_dim 128.
     """
 
     def __init__(self, model: NanoQuantLlama, batch: int, max_len: int, steps_per_graph: int = 1,
@@ -501,9 +541,21 @@ class FusedDecoder(GraphDecoder):
         # attention scores of the rope step [B * KV, L, G]: the q/k/v launch writes the step's causal
         # mask into it, the scores product adds into it in place
         self.scores = torch.zeros(batch * KV, max_len, H // KV, device=dev, dtype=dt)
+        # the torch step's scores, one buffer per layer: the step's causal mask is copied into all of
+        # them by one launch, and each layer's scores product adds into its own in place
+        self.scores_all = (torch.zeros(s.layers, batch * KV, max_len, H // KV, device=dev, dtype=dt)
+                           if attention == "torch" else None)
+        head = model.lm_head
+        if head.weight.dtype != dt or head.in_features % 8:
+            raise ValueError("the fused decode step's lm_head needs the model dtype and in_features % 8 == 0")
+        self.head_weight = head.weight.detach().contiguous()
+        self.head_bias = None if head.bias is None else head.bias.detach()
+        self.logits16 = torch.zeros(batch, head.out_features, device=dev, dtype=dt)
         self.act = torch.zeros(batch, s.ffn, device=dev, dtype=dt)
         cos, sin = model.rope(torch.arange(max_len, device=dev), dt)
         self.rope_cos, self.rope_sin = cos.contiguous(), sin.contiguous()
+        self.rope_cs = torch.stack((self.rope_cos, self.rope_sin), dim=1).contiguous()  # [max_len, 2, D]
+        self.tok = torch.zeros(batch, dtype=torch.long, device=dev)  # the step's input token ids
         self._keep = []  # tensors whose addresses the item tables hold
         self.plans = [self._layer_plan(layer) for layer in model.model.layers]
         need = 0
@@ -570,12 +622,11 @@ class FusedDecoder(GraphDecoder):
         H, KV, D = s.heads, s.kv_heads, s.head_dim
         dt, ws, wsb = self.dcode, self.ws.data_ptr(), self.ws.numel()
         st = self._lib.stream_of(self.device)
-        tok = self.ids.index_select(1, self.pos).view(-1)
-        torch.index_select(self.model.model.embed_tokens.weight, 0, tok, out=self.x)
+        torch.index_select(self.model.model.embed_tokens.weight, 0, self.tok, out=self.x)
         if self.attention == "torch":
-            tables = rotary_step_tables(self.rope_cos.index_select(0, self.pos),
-                                        self.rope_sin.index_select(0, self.pos), self.pos, self.cache,
-                                        self.model.dtype)
+            cs = self.rope_cs.index_select(0, self.pos)  # [1, 2, D]: cos, sin of the position
+            tables = rotary_step_tables(cs[:, 0], cs[:, 1], self.pos, self.cache, self.model.dtype, with_mask=False)
+            step_mask(self.pos, self.cache, self.model.dtype, out=self.scores_all)
         x, h, qkv, attn, act = (t.data_ptr() for t in (self.x, self.h, self.qkv, self.attn, self.act))
         esz = self.qkv.element_size()
         for li, plan in enumerate(self.plans):
@@ -587,6 +638,9 @@ class FusedDecoder(GraphDecoder):
                     dt, items_r, B, self.cache.k[li].data_ptr(), self.cache.v[li].data_ptr(), self.rope_cos.data_ptr(),
                     self.rope_sin.data_ptr(), self.pos.data_ptr(), D, self.max_len, self.scores.data_ptr(), ws, wsb,
                     st), "qkv 2 rope")
+            elif self.attention == "torch":
+                self._check(lib.nq_gemv_group_stage2_kv(dt, items, B, self.cache.v[li].data_ptr(),
+                                                        self.pos.data_ptr(), D, self.max_len, ws, wsb, st), "qkv 2 kv")
             else:
                 self._check(lib.nq_gemv_group_stage2(dt, n, items, B, self._lib.NQ_EPI_STORE, ws, wsb, st), "qkv 2")
             if self.attention == "hip":
@@ -598,8 +652,8 @@ class FusedDecoder(GraphDecoder):
             elif self.attention == "rope":
                 attention_products_step(s, li, self.q_rot, None, self.cache, self.attn, scores=self.scores)
             else:
-                out = rotary_attention_step(s, li, self.qkv[:, :(H + KV) * D], self.qkv[:, (H + KV) * D:], tables,
-                                            self.pos, self.cache, out=self.attn)
+                out = rotary_attention_step(s, li, self.qkv[:, :(H + KV) * D], None, tables, self.pos, self.cache,
+                                            out=self.attn, scores=self.scores_all[li])
                 if out.data_ptr() != self.attn.data_ptr():
                     self.attn.copy_(out.view(B, H * D))
             items, n = plan["o"]
@@ -612,10 +666,21 @@ class FusedDecoder(GraphDecoder):
             self._check(lib.nq_gemv_group_stage1(dt, n, items, act, B, s.ffn, -1.0, ws, wsb, st), "down 1")
             self._check(lib.nq_gemv_group_stage2(dt, n, items, B, self._lib.NQ_EPI_RESIDUAL, ws, wsb, st),
                         "down 2")
-        logits = self.model.lm_head(self.model.model.norm(self.x)).float()
-        nxt = logits.argmax(dim=-1, keepdim=True)
+        xn = self.model.model.norm(self.x).contiguous()
+        self._check(lib.nq_dense_gemv(dt, self.head_weight.data_ptr(), xn.data_ptr(), self.logits16.data_ptr(), B,
+                                      self.head_weight.shape[1], self.head_weight.shape[0], self.logits16.shape[1],
+                                      st), "lm_head")
+        logits = self.logits16 if self.head_bias is None else self.logits16 + self.head_bias
+        logits = logits.float()
+        torch.argmax(logits, dim=-1, out=self.tok)
         self.pos.add_(1)
-        self.ids.index_copy_(1, self.pos, nxt)
+        self.ids.index_copy_(1, self.pos, self.tok.view(-1, 1))
+        return logits
+
+    @torch.no_grad()
+    def prefill(self, prompt: torch.Tensor) -> torch.Tensor:
+        logits = super().prefill(prompt)
+        self.tok.copy_(self.ids[:, prompt.shape[1]])  # the step's input token, kept on the device
         return logits
 
 

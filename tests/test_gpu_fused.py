@@ -331,3 +331,132 @@ def test_group_stage2_rope_equals_store_then_rope_kernel(lib, dtype, B, heads, k
     assert torch.equal(caches[1].view(torch.int16), caches_ref[1].view(torch.int16))
     if pos >= L:
         assert torch.equal(q_rot, torch.zeros_like(q_rot))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("B,heads,kv_heads,D,r_qkv,pos", [(1, 4, 4, 128, (96, 96, 96), 37), (2, 8, 2, 128, (160, 96, 96), 0),
+                                                          (3, 4, 1, 64, (64, 64, 64), 63), (1, 2, 2, 64, (96, 96, 96), 80)])
+def test_group_stage2_kv_equals_store_then_value_copy(lib, dtype, B, heads, kv_heads, D, r_qkv, pos):
+    """nq_gemv_group_stage2_kv (the q/k/v stage 2 storing q and k, and copying v into its cache row)
+    against nq_gemv_group_stage2 (NQ_EPI_STORE) on the same intermediate: q and k bit for bit, the
+    value cache's row at the position equal to the stored v, every other cache row and v's own
+    output untouched; ranks equal and unequal (two launches); a position past the cache (80 of 64
+    rows) writes no row."""
+    from nanoquant_amd import _lib
+    announce("group stage 2 kv", dtype, (B, heads, kv_heads, D, r_qkv, pos))
+    n, L = 256, 64
+    ms = (heads * D, kv_heads * D, kv_heads * D)
+    width = sum(ms)
+    rng = np.random.default_rng(B * 100 + heads + pos + 1)
+    x = torch.from_numpy((rng.normal(size=(B, n)) * 2.0).astype(np.float16)).cuda().to(dtype)
+    keep, its = [], []
+    ref = torch.zeros(B, width, dtype=dtype, device="cuda")
+    got = torch.full((B, width), 5.0, dtype=dtype, device="cuda")
+    off = 0
+    for i, (m, r) in enumerate(zip(ms, r_qkv)):
+        c = make_linear(80 + i, m, n, r, with_mid=(i == 1))
+        V, U = words(c["V"]), words(c["U"])
+        s_in = torch.from_numpy(c["s_in"]).cuda().to(dtype)
+        s_out = torch.from_numpy(c["s_out"]).cuda().to(dtype)
+        s_mid = None if c["s_mid"] is None else torch.from_numpy(c["s_mid"]).cuda().to(dtype)
+        keep += [V, U, s_in, s_out, s_mid]
+        its.append((V, s_in, s_mid, U, s_out, off, r, m))
+        off += m
+    arr_ref = (_lib.GemvItem * 3)(*[item(_lib, V, si, sm, U, so, ref, o, width, None, r, m)
+                                    for V, si, sm, U, so, o, r, m in its])
+    arr_kv = (_lib.GemvItem * 3)(*[item(_lib, V, si, sm, U, so, got, o, width, None, r, m)
+                                   for V, si, sm, U, so, o, r, m in its])
+    gen = torch.Generator(device="cuda").manual_seed(pos + 1)
+    v_cache = torch.randn(B, kv_heads, L, D, device="cuda", generator=gen).to(dtype)
+    v_ref = v_cache.clone()
+    position = torch.tensor([pos], dtype=torch.int64, device="cuda")
+    dc = _lib.dtype_code(dtype)
+    st = torch.cuda.current_stream().cuda_stream
+    need = lib.nq_gemv_group_workspace_bytes(3, arr_ref, B)
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    _lib.check(lib.nq_gemv_group_stage1(dc, 3, arr_ref, x.data_ptr(), B, n, -1.0, ws.data_ptr(), need, st), "s1")
+    _lib.check(lib.nq_gemv_group_stage2(dc, 3, arr_ref, B, _lib.NQ_EPI_STORE, ws.data_ptr(), need, st), "s2")
+    _lib.check(lib.nq_gemv_group_stage2_kv(dc, arr_kv, B, v_cache.data_ptr(), position.data_ptr(), D, L,
+                                           ws.data_ptr(), need, st), "s2 kv")
+    torch.cuda.synchronize()
+    qk = ms[0] + ms[1]
+    assert torch.equal(got[:, :qk].view(torch.int16), ref[:, :qk].view(torch.int16))
+    assert torch.equal(got[:, qk:], torch.full_like(got[:, qk:], 5.0))  # v's own output is not written
+    if pos < L:
+        v_ref[:, :, pos, :] = ref[:, qk:].view(B, kv_heads, D)
+    assert torch.equal(v_cache.view(torch.int16), v_ref.view(torch.int16))
+
+
+def test_group_stage2_kv_argument_errors(lib):
+    from nanoquant_amd import _lib
+    announce("group stage 2 kv errors")
+    t = torch.zeros(64, dtype=torch.int32, device="cuda")
+    it = _lib.GemvItem()
+    it.v_bits = it.u_bits = it.s_in = it.s_out = it.y = t.data_ptr()
+    it.r, it.m, it.y_stride = 32, 100, 100
+    arr = (_lib.GemvItem * 3)(it, it, it)
+    pos = torch.zeros(1, dtype=torch.int64, device="cuda")
+    assert lib.nq_gemv_group_stage2_kv(_lib.NQ_F16, arr, 1, t.data_ptr(), pos.data_ptr(), 64, 8, t.data_ptr(), 256,
+                                       None) == _lib.NQ_ERR_SHAPE  # m = 100 is not whole heads of 64
+    assert lib.nq_gemv_group_stage2_kv(_lib.NQ_F16, arr, 1, t.data_ptr(), pos.data_ptr(), 24, 8, t.data_ptr(), 256,
+                                       None) == _lib.NQ_ERR_INVALID_ARGUMENT  # head_dim not a multiple of 16
+    assert lib.nq_gemv_group_stage2_kv(_lib.NQ_F16, None, 1, t.data_ptr(), pos.data_ptr(), 64, 8, t.data_ptr(), 256,
+                                       None) == _lib.NQ_ERR_INVALID_ARGUMENT
+
+
+def half_ulp(v, bits):
+    """Half a unit in the last place of |v| for a float of `bits` significant bits."""
+    _, e = np.frexp(np.abs(v))
+    return np.ldexp(1.0, e - 1 - bits)
+
+
+DENSE_CASES = [  # m, n, batch, ldy
+    (32000, 4096, 1, 32000),  # the Llama-2-7B lm_head
+    (7, 8, 3, 7),             # one 16-byte chunk per row, a ragged block of rows
+    (1000, 4104, 5, 1000),    # a second, nearly empty 4096-column group; batch past one 4-row pass
+    (513, 8200, 2, 600),      # output rows wider than m (the gap is not written)
+    (64, 12288, 4, 64),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("m,n,batch,ldy", DENSE_CASES)
+def test_dense_gemv_against_fp32(lib, dtype, m, n, batch, ldy):
+    """nq_dense_gemv against a float32 torch product of the same dtype inputs: each output within half
+    a unit in the last place of the rounded exact value plus 1e-5 of the largest output (fp32
+    summation order); the padding of y past m untouched."""
+    from nanoquant_amd import _lib
+    announce("dense gemv", dtype, (m, n, batch, ldy))
+    gen = torch.Generator(device="cuda").manual_seed(m + n + batch)
+    w = (torch.randn(m, n, device="cuda", generator=gen) * 0.05).to(dtype)
+    x = torch.randn(batch, n, device="cuda", generator=gen).to(dtype)
+    y = torch.full((batch, ldy), 9.0, dtype=dtype, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    _lib.check(lib.nq_dense_gemv(_lib.dtype_code(dtype), w.data_ptr(), x.data_ptr(), y.data_ptr(), batch, n, m, ldy,
+                                 st), "dense gemv")
+    torch.cuda.synchronize()
+    ref = (x.double().cpu() @ w.double().cpu().T).numpy()
+    got = y[:, :m].double().cpu().numpy()
+    bits = 11 if dtype == torch.float16 else 8
+    # half a unit of the rounded value's binade (the larger one where rounding carried into the next)
+    allowed = np.maximum(half_ulp(ref, bits), half_ulp(got, bits))
+    excess = np.maximum(np.abs(got - ref) - allowed, 0.0).max() / np.abs(ref).max()
+    print(f"[dense] {dtype} {(m, n, batch)} excess={excess:.2e}", flush=True)
+    assert excess <= 1e-5, excess
+    if ldy > m:
+        assert torch.equal(y[:, m:], torch.full_like(y[:, m:], 9.0))
+
+
+def test_dense_gemv_argument_errors(lib):
+    from nanoquant_amd import _lib
+    announce("dense gemv errors")
+    w = torch.zeros(16, 64, dtype=torch.float16, device="cuda")
+    x = torch.zeros(2, 64, dtype=torch.float16, device="cuda")
+    y = torch.zeros(2, 16, dtype=torch.float16, device="cuda")
+    f = lib.nq_dense_gemv
+    assert f(_lib.NQ_F16, w.data_ptr(), x.data_ptr(), y.data_ptr(), 2, 60, 16, 16, None) == _lib.NQ_ERR_SHAPE
+    assert f(_lib.NQ_F16, w.data_ptr() + 2, x.data_ptr(), y.data_ptr(), 2, 64, 15, 16, None) == _lib.NQ_ERR_ALIGNMENT
+    assert f(_lib.NQ_F16, w.data_ptr(), x.data_ptr(), y.data_ptr(), 2, 64, 16, 15, None) == \
+        _lib.NQ_ERR_INVALID_ARGUMENT
+    assert f(7, w.data_ptr(), x.data_ptr(), y.data_ptr(), 2, 64, 16, 16, None) == _lib.NQ_ERR_DTYPE
+    assert f(_lib.NQ_F16, None, None, None, 0, 64, 16, 16, None) == _lib.NQ_OK  # empty batch
