@@ -313,14 +313,18 @@ int nq_rope_kv_write(int dtype, const void* qkv, int64_t qkv_stride, void* k_cac
 
 /* ---------------------------------------------------------------- dense GEMV */
 
-/* y[b, j] = dtype(sum_k w[j, k] x[b, k]) for b < batch, j < m: a dense linear of a few rows, the
- * lm_head of a decode step. w dtype [m, n] row-major, x dtype [batch, n] contiguous (both 16-byte
- * aligned), y dtype rows of ldy >= m elements. fp32 sum, rounded once to dtype (overflow to +-inf
- * as a torch linear does). n a multiple of 8. Each wave streams one row of w with 8 KB of loads in
- * flight, which is what reading a large w from HBM takes. No counterpart in the reference, whose
- * decode step runs the lm_head as torch's linear (kernel/test_decode.py:387-394). */
-int nq_dense_gemv(int dtype, const void* w, const void* x, void* y, int64_t batch, int64_t n, int64_t m, int64_t ldy,
-                  nq_stream_t stream);
+/* y[b, j] = dtype(sum_k w[j, k] xn[b, k]) for b < batch, j < m: a dense linear of a few rows, the
+ * lm_head of a decode step. w dtype [m, n] row-major, x dtype [batch, n] contiguous (16-byte aligned
+ * both). xn is x, or with norm_weight (dtype [n], 16-byte aligned; NULL for none) x's RMS norm as a
+ * Llama decoder rounds it: dtype(g[k] * dtype(x[k] * rsqrt(mean_k x^2 + eps))), mean and products in
+ * fp32. fp32 sum, rounded once to dtype (overflow to +-inf as a torch linear does); with y_float32
+ * the rounded values are stored widened to float32 (y then float [batch, ldy]), else y is dtype
+ * rows of ldy >= m elements. n a multiple of 8, at most 32256; batch at most 65535. Each wave
+ * streams one row of w with 8 KB of loads in flight, which is what reading a large w from HBM
+ * takes. No counterpart in the reference, whose decode step runs the final norm and the lm_head as
+ * torch ops (kernel/test_decode.py:387-394). */
+int nq_dense_gemv(int dtype, const void* w, const void* x, const void* norm_weight, float eps, void* y,
+                  int y_float32, int64_t batch, int64_t n, int64_t m, int64_t ldy, nq_stream_t stream);
 
 /* ---------------------------------------------------------------- measurement aid */
 

@@ -374,41 +374,105 @@ bool launch_attn_g(int g, const void* q, const void* k, const void* v, int64_t q
 
 // ---- dense GEMV: the lm_head of a decode step
 //
-// y[b][j] = T(sum_k W[j][k] x[b][k]) (fp32 sum, one rounding), W [m][n] row-major in T. A decode
-// step reaches its lm_head after its layers have streamed their weights through the caches, so W
-// comes from HBM, and streaming it at speed takes many bytes in flight per CU: each wave owns one
-// row of W and issues every 16-byte load of a 4096-column group of it at once (8 per lane,
-// non-temporal), x's matching chunks come from L2, and the wave's sum is reduced across lanes.
-// Loads past the row's end read zeros (buffer resource bounds), so n need only be a multiple of 8.
-// NB batch rows per block (grid.y covers the batch); blocks hold 4 rows of W.
-constexpr int kDenseCols = 4096;  // columns of W a wave has in flight: 64 lanes x 8 x 8 elements
+// y[b][j] = T(sum_k W[j][k] xn[b][k]) (fp32 sum, one rounding), W [m][n] row-major in T, where xn is
+// x itself or, with a norm weight g, its RMS norm as the decoder's torch path rounds it:
+// T(g[k] * T(x[k] * rsqrt(mean(x^2) + eps))) (mean and product in fp32). A decode step reaches its
+// lm_head after its layers have streamed their weights through the caches, so W comes from HBM, and
+// streaming it at speed takes many bytes in flight per CU: each wave owns one row of W and issues
+// every 16-byte load of a 4096-column group of it at once (8 per lane, non-temporal); the first
+// group's loads go out before the block stages its NB batch rows of x (or xn) in LDS, so their
+// latency covers the staging. Loads past the row's end read zeros (buffer resource bounds), so n
+// need only be a multiple of 8. Blocks hold 4 rows of W; grid.y covers the batch.
+constexpr int kDenseCols = 4096;      // columns of W a wave has in flight: 64 lanes x 8 x 8 elements
+constexpr int kDenseLdsBytes = 64512;  // staged rows of x, NB * n * 2 bytes: within 64 KB with the static part
 
-template <typename T, int NB>
+template <typename T, int NB, bool NORM>
 __global__ __launch_bounds__(256) void dense_gemv_kernel(const uint16_t* __restrict__ w, const uint16_t* __restrict__ x,
-                                                         uint16_t* __restrict__ y, int m, int n, int batch, int ldy) {
-    const int lane = threadIdx.x & 63;
-    const int row = static_cast<int>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-    if (row >= m) return;  // a whole wave (the kernel has no barrier)
+                                                         const uint16_t* __restrict__ norm_w, float eps,
+                                                         void* __restrict__ y, int y_f32, int m, int n, int batch,
+                                                         int ldy) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // [NB][n]
+    __shared__ float part[NB][4];
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int row_out = static_cast<int>(blockIdx.x) * 4 + wave;
+    const int row = min(row_out, m - 1);  // every wave stages its share of x, so none leaves early
     const int b0 = static_cast<int>(blockIdx.y) * NB;
-    const uint32_t row_bytes = static_cast<uint32_t>(n) * 2u;
-    const rsrc_t wr = make_rsrc(w + static_cast<size_t>(row) * static_cast<size_t>(n), row_bytes);
-    rsrc_t xr[NB];
+    const rsrc_t wr = make_rsrc(w + static_cast<size_t>(row) * static_cast<size_t>(n), static_cast<uint32_t>(n) * 2u);
+    u32x4 wv[8];
 #pragma unroll
-    for (int b = 0; b < NB; ++b)
-        xr[b] = make_rsrc(x + static_cast<size_t>(min(b0 + b, batch - 1)) * static_cast<size_t>(n), row_bytes);
+    for (int k = 0; k < 8; ++k) wv[k] = load_b128_stream(wr, static_cast<uint32_t>((k * 64 + lane) * 16));
+
+    // x's batch rows into LDS (16-byte chunks; every thread keeps to its own chunks throughout)
+    const int chunks = n / 8;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const uint16_t* xr = x + static_cast<size_t>(min(b0 + b, batch - 1)) * static_cast<size_t>(n);
+        float ss = 0.0f;
+        for (int c = t; c < chunks; c += 256) {
+            const u32x4 v = *reinterpret_cast<const u32x4*>(xr + c * 8);
+            *reinterpret_cast<u32x4*>(xs + b * n + c * 8) = v;
+            if (NORM) {
+                const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float lo = T::to_float(static_cast<uint16_t>(d[q] & 0xFFFFu));
+                    const float hi = T::to_float(static_cast<uint16_t>(d[q] >> 16));
+                    ss += lo * lo;
+                    ss += hi * hi;
+                }
+            }
+        }
+        if (NORM) {
+            ss = wave_sum(ss);
+            if (lane == 0) part[b][wave] = ss;
+        }
+    }
+    if (NORM) {
+        __syncthreads();
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const float r = rsqrtf((part[b][0] + part[b][1] + part[b][2] + part[b][3]) / static_cast<float>(n) + eps);
+            for (int c = t; c < chunks; c += 256) {
+                u32x4 v = *reinterpret_cast<const u32x4*>(xs + b * n + c * 8);
+                const u32x4 g = *reinterpret_cast<const u32x4*>(norm_w + c * 8);
+                uint32_t d[4] = {v.x, v.y, v.z, v.w};
+                const uint32_t gd[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    uint16_t h[2];
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        const uint16_t xe = static_cast<uint16_t>(d[q] >> (16 * e));
+                        const uint16_t ge = static_cast<uint16_t>(gd[q] >> (16 * e));
+                        const float xn = T::to_float(T::from_float(T::to_float(xe) * r));
+                        h[e] = T::from_float(T::to_float(ge) * xn);
+                    }
+                    d[q] = static_cast<uint32_t>(h[0]) | (static_cast<uint32_t>(h[1]) << 16);
+                }
+                v = u32x4{d[0], d[1], d[2], d[3]};
+                *reinterpret_cast<u32x4*>(xs + b * n + c * 8) = v;
+            }
+        }
+    }
+    __syncthreads();
+
     float acc[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) acc[b] = 0.0f;
     for (int c0 = 0; c0 < n; c0 += kDenseCols) {
-        u32x4 wv[8];
+        if (c0 > 0) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
-            wv[k] = load_b128_stream(wr, static_cast<uint32_t>(c0 + (k * 64 + lane) * 8) * 2u);
+            for (int k = 0; k < 8; ++k)
+                wv[k] = load_b128_stream(wr, static_cast<uint32_t>(c0 + (k * 64 + lane) * 8) * 2u);
+        }
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
-                const u32x4 xv = load_b128(xr[b], static_cast<uint32_t>(c0 + (k * 64 + lane) * 8) * 2u);
+                const int col = c0 + (k * 64 + lane) * 8;
+                const u32x4 xv = col < n ? *reinterpret_cast<const u32x4*>(xs + b * n + col) : u32x4{0u, 0u, 0u, 0u};
                 acc[b] = T::dot2(wv[k].x, xv.x, acc[b]);
                 acc[b] = T::dot2(wv[k].y, xv.y, acc[b]);
                 acc[b] = T::dot2(wv[k].z, xv.z, acc[b]);
@@ -419,18 +483,31 @@ __global__ __launch_bounds__(256) void dense_gemv_kernel(const uint16_t* __restr
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
         const float s = wave_sum(acc[b]);
-        if (lane == 0 && b0 + b < batch) y[static_cast<size_t>(b0 + b) * ldy + row] = T::from_float(s);
+        if (lane == 0 && row_out < m && b0 + b < batch) {
+            const uint16_t v = T::from_float(s);
+            const size_t at = static_cast<size_t>(b0 + b) * static_cast<size_t>(ldy) + static_cast<size_t>(row_out);
+            if (y_f32) static_cast<float*>(y)[at] = T::to_float(v);
+            else static_cast<uint16_t*>(y)[at] = v;
+        }
     }
 }
 
-template <typename T>
-void launch_dense_gemv(const uint16_t* w, const uint16_t* x, uint16_t* y, int m, int n, int batch, int ldy,
-                       hipStream_t st) {
-    const int nb = batch >= 4 ? 4 : (batch >= 2 ? 2 : 1);
+// Batch rows per block: up to 4, as many as the batch has, as fit the staging LDS.
+inline int dense_rows_per_block(int64_t batch, int64_t n) {
+    int nb = batch >= 4 ? 4 : (batch >= 2 ? 2 : 1);
+    while (nb > 1 && static_cast<int64_t>(nb) * n * 2 > kDenseLdsBytes) nb /= 2;
+    return nb;
+}
+
+template <typename T, bool NORM>
+void launch_dense_gemv(const uint16_t* w, const uint16_t* x, const uint16_t* g, float eps, void* y, int y_f32, int m,
+                       int n, int batch, int ldy, hipStream_t st) {
+    const int nb = dense_rows_per_block(batch, n);
     const dim3 grid(static_cast<unsigned>(ceil_div(m, 4)), static_cast<unsigned>(ceil_div(batch, nb)));
-    if (nb == 4) dense_gemv_kernel<T, 4><<<grid, 256, 0, st>>>(w, x, y, m, n, batch, ldy);
-    else if (nb == 2) dense_gemv_kernel<T, 2><<<grid, 256, 0, st>>>(w, x, y, m, n, batch, ldy);
-    else dense_gemv_kernel<T, 1><<<grid, 256, 0, st>>>(w, x, y, m, n, batch, ldy);
+    const size_t lds = static_cast<size_t>(nb) * n * 2;
+    if (nb == 4) dense_gemv_kernel<T, 4, NORM><<<grid, 256, lds, st>>>(w, x, g, eps, y, y_f32, m, n, batch, ldy);
+    else if (nb == 2) dense_gemv_kernel<T, 2, NORM><<<grid, 256, lds, st>>>(w, x, g, eps, y, y_f32, m, n, batch, ldy);
+    else dense_gemv_kernel<T, 1, NORM><<<grid, 256, lds, st>>>(w, x, g, eps, y, y_f32, m, n, batch, ldy);
 }
 
 }  // namespace
@@ -529,31 +606,37 @@ int nq_rope_kv_write(int dtype, const void* qkv, int64_t qkv_stride, void* k_cac
     return check_launch(name);
 }
 
-int nq_dense_gemv(int dtype, const void* w, const void* x, void* y, int64_t batch, int64_t n, int64_t m, int64_t ldy,
-                  nq_stream_t stream) {
+int nq_dense_gemv(int dtype, const void* w, const void* x, const void* norm_weight, float eps, void* y,
+                  int y_float32, int64_t batch, int64_t n, int64_t m, int64_t ldy, nq_stream_t stream) {
     const char* name = "nq_dense_gemv";
     if (dtype != NQ_F16 && dtype != NQ_BF16) return fail(NQ_ERR_DTYPE, "%s: unsupported dtype %d", name, dtype);
     if (batch < 0 || n <= 0 || m <= 0 || ldy < m)
         return fail(NQ_ERR_INVALID_ARGUMENT, "%s: bad sizes (batch %lld, n %lld, m %lld, ldy %lld)", name,
                     (long long)batch, (long long)n, (long long)m, (long long)ldy);
     if (n % 8) return fail(NQ_ERR_SHAPE, "%s: n must be a multiple of 8, got %lld", name, (long long)n);
-    if (n > (int64_t{1} << 28) || m > INT32_MAX / 2 || ldy > INT32_MAX / 2 || batch > 65535 * 4 ||
+    if (n * 2 > kDenseLdsBytes || m > INT32_MAX / 2 || ldy > INT32_MAX / 2 || batch > 65535 ||
         batch * ldy > (int64_t{1} << 40))
-        return fail(NQ_ERR_UNSUPPORTED, "%s: sizes too large", name);
+        return fail(NQ_ERR_UNSUPPORTED, "%s: sizes too large (n at most %d)", name, kDenseLdsBytes / 2);
     if (batch == 0) return NQ_OK;
     if (!w || !x || !y) return fail(NQ_ERR_INVALID_ARGUMENT, "%s: null pointer", name);
-    if (!aligned(w, 16) || !aligned(x, 16) || !aligned(y, 2))
-        return fail(NQ_ERR_ALIGNMENT, "%s: w and x must be 16-byte aligned, y 2-byte", name);
+    if (!aligned(w, 16) || !aligned(x, 16) || (norm_weight && !aligned(norm_weight, 16)) ||
+        !aligned(y, y_float32 ? 4 : 2))
+        return fail(NQ_ERR_ALIGNMENT, "%s: w, x and norm_weight must be 16-byte aligned, y aligned to its type",
+                    name);
     const auto* wp = static_cast<const uint16_t*>(w);
     const auto* xp = static_cast<const uint16_t*>(x);
-    auto* yp = static_cast<uint16_t*>(y);
+    const auto* gp = static_cast<const uint16_t*>(norm_weight);
+    const int yf = y_float32 ? 1 : 0;
+    const int mi = static_cast<int>(m), ni = static_cast<int>(n), bi = static_cast<int>(batch);
+    const int li = static_cast<int>(ldy);
     hipStream_t st = as_stream(stream);
-    if (dtype == NQ_F16)
-        launch_dense_gemv<F16>(wp, xp, yp, static_cast<int>(m), static_cast<int>(n), static_cast<int>(batch),
-                               static_cast<int>(ldy), st);
-    else
-        launch_dense_gemv<BF16>(wp, xp, yp, static_cast<int>(m), static_cast<int>(n), static_cast<int>(batch),
-                                static_cast<int>(ldy), st);
+    if (dtype == NQ_F16) {
+        if (gp) launch_dense_gemv<F16, true>(wp, xp, gp, eps, y, yf, mi, ni, bi, li, st);
+        else launch_dense_gemv<F16, false>(wp, xp, gp, eps, y, yf, mi, ni, bi, li, st);
+    } else {
+        if (gp) launch_dense_gemv<BF16, true>(wp, xp, gp, eps, y, yf, mi, ni, bi, li, st);
+        else launch_dense_gemv<BF16, false>(wp, xp, gp, eps, y, yf, mi, ni, bi, li, st);
+    }
     return check_launch(name);
 }
 

@@ -258,13 +258,13 @@ struct S2Item {
     int m, wr, zpitch;
     int ystride;  // elements between batch rows of y and resid
     int blocks;  // blockIdx.x < blocks do the item's rows (each item has a grid plane, blockIdx.z)
-    int rope;         // kEpiRope: 0 store into y, 1 rotate into y (queries), 2 rotate into cache (keys),
-                      // 3 copy into cache (values)
-    uint16_t* cache;  // kEpiRope, kinds 2 and 3: [batch, m / head_dim, max_len, head_dim]
+    int rope;         // kEpiRope, kEpiKv: 0 store into y, 1 rotate into y (queries), 2 rotate into cache
+                      // (keys), 3 copy into cache (values)
+    uint16_t* cache;  // kinds 2 and 3: [batch, m / head_dim, max_len, head_dim]
 };
 
-// The rotary step of kEpiRope: position p = *pos (device), cos/sin rows [max_len, head_dim] (null when
-// no item rotates).
+// The rotary step of kEpiRope: position p = *pos (device), cos/sin rows [max_len, head_dim] (null for
+// kEpiKv, which rotates nothing).
 struct S2Rope {
     const int64_t* pos;
     const uint16_t* cos;
@@ -281,12 +281,25 @@ struct S2Table {
     S2Rope rope;
 };
 
+// The step position of kEpiRope and kEpiKv as a vector (buffer) load. Scalar loads may return out of order,
+// so the compiler waits for every outstanding one at the first use of any: this load, which
+// follows a pointer from the kernel arguments, would hold up the block's first reads of its item.
+// Vector loads are counted in order, and the wait for this one falls where its value is used.
+__device__ inline int64_t load_position(const int64_t* pos) {
+    const rsrc_t rs = make_rsrc(pos, 8);
+    const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b32(rs, 0, 0, 0);
+    const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b32(rs, 4, 0, 0);
+    return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 // Stage-2 epilogues: y = sat(s_out * acc); y = resid + that (rounded as two T operations);
 // gated pair (items 0 and 1 over the same rows): y0 = silu(gate) * up, each a T value;
 // kEpiStoreOne is kEpiStore for a one-item table (no item lookup); kEpiRope: the q, k, v
 // projections of a decode step with the rotary embedding at position p applied to q and k, q stored
 // to y, k and v written into their caches at row p.
-enum Epilogue { kEpiStore = 0, kEpiResidual = 1, kEpiGated = 2, kEpiStoreOne = 3, kEpiRope = 4 };
+// kEpiKv: the same three projections with no rotation, q and k stored to y, v written into its
+// cache at row p (S2Item::rope 0 and 3).
+enum Epilogue { kEpiStore = 0, kEpiResidual = 1, kEpiGated = 2, kEpiStoreOne = 3, kEpiRope = 4, kEpiKv = 5 };
 
 // The item of this block: a table launch gives each item a grid plane of its own (blockIdx.z), so
 // the item's fields are one round of scalar loads at an offset known when the wave starts. (A
@@ -842,24 +855,29 @@ __global__ __launch_bounds__(256) void s2t_kernel(const S2Table tab, int batch) 
     const int wave = t >> 6;
     const int c = lane & 15;
     const int g = lane >> 4;
-    if (EPI == kEpiRope && tab.rope.mask != nullptr) {
-        // the additive causal mask of the step into the attention scores: element (row, p, group)
-        // is 0 for a cache position p <= the step's position and -inf after it; every thread of the
-        // grid takes every nthr-th element, before any block leaves
-        const int64_t pm = *tab.rope.pos;
+    S2Item its[P];
+    its[0] = (EPI == kEpiGated || EPI == kEpiStoreOne) ? tab.item[0] : pick_item<S2Item>(tab);
+    if (P == 2) its[P - 1] = tab.item[1];
+    const int64_t p64 = EPI == kEpiRope || EPI == kEpiKv ? load_position(tab.rope.pos) : 0;
+    // kEpiRope: the additive causal mask of the step into the attention scores, element (row, p,
+    // group) 0 for a cache position p <= the step's position and -inf after it; every thread of
+    // the grid takes every nthr-th element, once its block's own stores are issued (a block with no
+    // rows of its item does it at once)
+    auto write_mask = [&]() {
+        if (EPI != kEpiRope || tab.rope.mask == nullptr) return;
         const uint32_t nthr = gridDim.x * gridDim.y * gridDim.z * 256u;
         const uint32_t gid = ((blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * 256u + threadIdx.x;
         const uint16_t neg_inf = T::from_float(-__builtin_huge_valf());
         for (uint32_t e = gid; e < tab.rope.mask_total; e += nthr) {
             const int p = static_cast<int>((e / static_cast<uint32_t>(tab.rope.mask_groups)) %
                                            static_cast<uint32_t>(tab.rope.max_len));
-            tab.rope.mask[e] = p <= pm ? uint16_t(0) : neg_inf;
+            tab.rope.mask[e] = p <= p64 ? uint16_t(0) : neg_inf;
         }
+    };
+    if (EPI != kEpiGated && EPI != kEpiStoreOne && item_done(its[0])) {
+        write_mask();
+        return;
     }
-    S2Item its[P];
-    its[0] = (EPI == kEpiGated || EPI == kEpiStoreOne) ? tab.item[0] : pick_item<S2Item>(tab);
-    if (P == 2) its[P - 1] = tab.item[1];
-    if (EPI != kEpiGated && EPI != kEpiStoreOne && item_done(its[0])) return;
     const int m = its[0].m;
     const int wr = its[0].wr;  // gated items share m and wr
     const int i0 = static_cast<int>(blockIdx.x) * kRows;
@@ -878,7 +896,6 @@ __global__ __launch_bounds__(256) void s2t_kernel(const S2Table tab, int batch) 
     }
     auto feat = [&](int r) { return f0 + (r & 7) + (r >> 3) * fhalf; };  // row of U of tile row r
     const int re = 16 * min(wave, RT - 1);  // first tile row whose epilogue this wave may run
-    const int64_t p64 = EPI == kEpiRope ? *tab.rope.pos : 0;
     NQ_STAMP(0);
 
     // 1. every global load: the tiles' words as 16-byte pieces, h, the output scales
@@ -946,7 +963,7 @@ __global__ __launch_bounds__(256) void s2t_kernel(const S2Table tab, int batch) 
     // the rotary cos/sin entries of this lane's epilogue rows (row p of the tables; p outside the
     // tables reads row 0, and those values are never used)
     uint16_t rcos[4] = {0, 0, 0, 0}, rsin[4] = {0, 0, 0, 0};
-    if (EPI == kEpiRope && tab.rope.cos != nullptr) {
+    if (EPI == kEpiRope) {
         const int D = tab.rope.head_dim;
         const size_t prow = p64 >= 0 && p64 < tab.rope.max_len ? static_cast<size_t>(p64) * D : 0;
 #pragma unroll
@@ -1111,6 +1128,19 @@ __global__ __launch_bounds__(256) void s2t_kernel(const S2Table tab, int batch) 
                 }
                 continue;
             }
+            if (EPI == kEpiKv) {
+                if (b_ok && row < m) {
+                    const uint16_t val = saturate_to<T>(out[0], T::SAT);
+                    if (its[0].rope != 3) {
+                        its[0].y[static_cast<size_t>(b0 + bcol) * its[0].ystride + row] = val;
+                    } else if (p64 >= 0 && p64 < tab.rope.max_len) {
+                        const int D = tab.rope.head_dim;
+                        its[0].cache[((static_cast<size_t>(b0 + bcol) * (m / D) + row / D) * tab.rope.max_len +
+                                      static_cast<size_t>(p64)) * D + row % D] = val;
+                    }
+                }
+                continue;
+            }
             if (b_ok && row < m) {
                 uint16_t val = saturate_to<T>(out[0], T::SAT);
                 if (EPI == kEpiResidual) {
@@ -1124,6 +1154,7 @@ __global__ __launch_bounds__(256) void s2t_kernel(const S2Table tab, int batch) 
             }
         }
     }
+    write_mask();
     NQ_STAMP(3);
 }
 
@@ -2607,7 +2638,7 @@ int nq_gemv_group_stage1(int dtype, int64_t count, const nq_gemv_item* items, co
 namespace nq {
 namespace {
 
-// The group stage 2 with any epilogue; `rope` (kEpiRope only) carries the rotary step, the caches
+// The group stage 2 with any epilogue; `rope` (kEpiRope, kEpiKv) carries the rotary step, the caches
 // and what the store does with each of the three items (S2Item::rope).
 struct RopeArgs {
     S2Rope rope;
@@ -2759,7 +2790,10 @@ int group_stage2(const char* name, int dtype, int64_t count, const nq_gemv_item*
                 done[k] = true;
             }
         bool ok;
-        if (rope != nullptr) {
+        if (rope != nullptr && rope->rope.cos == nullptr) {  // nq_gemv_group_stage2_kv
+            ok = dtype == NQ_F16 ? launch_s2t_qw<F16, kEpiKv>(tab, qw, b, st)
+                                 : launch_s2t_qw<BF16, kEpiKv>(tab, qw, b, st);
+        } else if (rope != nullptr) {
             ok = dtype == NQ_F16 ? launch_s2t_qw<F16, kEpiRope>(tab, qw, b, st)
                                  : launch_s2t_qw<BF16, kEpiRope>(tab, qw, b, st);
         } else if (dtype == NQ_F16) {

@@ -501,9 +501,10 @@ class FusedDecoder(GraphDecoder):
     6. gate and up stage 1 in one launch, post_attention_layernorm folded in;
     7. gate and up stage 2 in one launch storing silu(gate) * up;
     8, 9. down_proj, its stage 2 adding the residual.
-    The lm_head runs as one dense GEMV of the library (``nq_dense_gemv``: torch's linear reads
-    its weights, cold after the layers, at a fraction of the bandwidth); the embedding lookup,
-    final norm and argmax stay torch ops. Prefill runs the unfused model (it fills the same cache
+    The final norm and the lm_head run as one dense GEMV of the library (``nq_dense_gemv`` with
+    its RMS-norm prologue: torch's linear reads the head's weights, cold after the layers, at a
+    fraction of the bandwidth), which writes the float32 logits; the embedding lookup and argmax
+    stay torch ops. The logits a step returns live in a buffer the next step overwrites. Prefill runs the unfused model (it fills the same cache
     layout). Needs the model packed for the ``gemv`` kernel in float16 or bfloat16 and head_dim 128.
     """
 
@@ -551,6 +552,11 @@ class FusedDecoder(GraphDecoder):
         self.head_weight = head.weight.detach().contiguous()
         self.head_bias = None if head.bias is None else head.bias.detach()
         self.logits16 = torch.zeros(batch, head.out_features, device=dev, dtype=dt)
+        self.logits = torch.zeros(batch, head.out_features, device=dev, dtype=torch.float32)
+        norm = model.model.norm
+        if norm.weight.dtype != dt:
+            raise ValueError("the fused decode step folds the final norm into the lm_head: its weight needs the model dtype")
+        self.norm_weight = norm.weight.detach().contiguous()
         self.act = torch.zeros(batch, s.ffn, device=dev, dtype=dt)
         cos, sin = model.rope(torch.arange(max_len, device=dev), dt)
         self.rope_cos, self.rope_sin = cos.contiguous(), sin.contiguous()
@@ -666,12 +672,15 @@ class FusedDecoder(GraphDecoder):
             self._check(lib.nq_gemv_group_stage1(dt, n, items, act, B, s.ffn, -1.0, ws, wsb, st), "down 1")
             self._check(lib.nq_gemv_group_stage2(dt, n, items, B, self._lib.NQ_EPI_RESIDUAL, ws, wsb, st),
                         "down 2")
-        xn = self.model.model.norm(self.x).contiguous()
-        self._check(lib.nq_dense_gemv(dt, self.head_weight.data_ptr(), xn.data_ptr(), self.logits16.data_ptr(), B,
-                                      self.head_weight.shape[1], self.head_weight.shape[0], self.logits16.shape[1],
-                                      st), "lm_head")
-        logits = self.logits16 if self.head_bias is None else self.logits16 + self.head_bias
-        logits = logits.float()
+        # the final RMS norm folded into the lm_head launch; float32 logits straight from it (with a
+        # bias, the dtype logits, the bias added in dtype, then widened, as the torch head rounds)
+        norm = self.model.model.norm
+        hw = self.head_weight
+        out = self.logits if self.head_bias is None else self.logits16
+        self._check(lib.nq_dense_gemv(dt, hw.data_ptr(), self.x.data_ptr(), self.norm_weight.data_ptr(), norm.eps,
+                                      out.data_ptr(), int(self.head_bias is None), B, hw.shape[1], hw.shape[0],
+                                      out.shape[1], st), "lm_head")
+        logits = self.logits if self.head_bias is None else (self.logits16 + self.head_bias).float()
         torch.argmax(logits, dim=-1, out=self.tok)
         self.pos.add_(1)
         self.ids.index_copy_(1, self.pos, self.tok.view(-1, 1))

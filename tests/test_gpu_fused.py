@@ -415,34 +415,48 @@ DENSE_CASES = [  # m, n, batch, ldy
     (7, 8, 3, 7),             # one 16-byte chunk per row, a ragged block of rows
     (1000, 4104, 5, 1000),    # a second, nearly empty 4096-column group; batch past one 4-row pass
     (513, 8200, 2, 600),      # output rows wider than m (the gap is not written)
-    (64, 12288, 4, 64),
+    (64, 12288, 4, 64),       # three column groups; two batch rows per block (LDS)
 ]
+
+
+def dense_call(lib, dtype, w, x, g, eps, y, y_f32, batch, n, m, ldy):
+    from nanoquant_amd import _lib
+    st = torch.cuda.current_stream().cuda_stream
+    _lib.check(lib.nq_dense_gemv(_lib.dtype_code(dtype), w.data_ptr(), x.data_ptr(), None if g is None else g.data_ptr(),
+                                 eps, y.data_ptr(), int(y_f32), batch, n, m, ldy, st), "dense gemv")
+    torch.cuda.synchronize()
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
 @pytest.mark.parametrize("m,n,batch,ldy", DENSE_CASES)
-def test_dense_gemv_against_fp32(lib, dtype, m, n, batch, ldy):
-    """nq_dense_gemv against a float32 torch product of the same dtype inputs: each output within half
-    a unit in the last place of the rounded exact value plus 1e-5 of the largest output (fp32
-    summation order); the padding of y past m untouched."""
-    from nanoquant_amd import _lib
-    announce("dense gemv", dtype, (m, n, batch, ldy))
+@pytest.mark.parametrize("norm", [False, True], ids=["plain", "rmsnorm"])
+def test_dense_gemv_against_fp32(lib, dtype, m, n, batch, ldy, norm):
+    """nq_dense_gemv against a float64 product of the same dtype inputs: each output within half a
+    unit in the last place of the rounded exact value plus 1e-5 of the largest output (fp32
+    summation order); with the norm prologue the input is the decoder's RMSNorm of x computed by
+    torch (an element of it may differ by a unit in the last place: the mean's summation order),
+    bar 5e-5. float32 outputs (norm cases) hold the dtype-rounded values exactly; the padding of y
+    past m is untouched."""
+    announce("dense gemv", dtype, (m, n, batch, ldy), "norm" if norm else "")
     gen = torch.Generator(device="cuda").manual_seed(m + n + batch)
     w = (torch.randn(m, n, device="cuda", generator=gen) * 0.05).to(dtype)
-    x = torch.randn(batch, n, device="cuda", generator=gen).to(dtype)
-    y = torch.full((batch, ldy), 9.0, dtype=dtype, device="cuda")
-    st = torch.cuda.current_stream().cuda_stream
-    _lib.check(lib.nq_dense_gemv(_lib.dtype_code(dtype), w.data_ptr(), x.data_ptr(), y.data_ptr(), batch, n, m, ldy,
-                                 st), "dense gemv")
-    torch.cuda.synchronize()
-    ref = (x.double().cpu() @ w.double().cpu().T).numpy()
+    x = (torch.randn(batch, n, device="cuda", generator=gen) * 3.0).to(dtype)
+    g = (torch.rand(n, device="cuda", generator=gen) + 0.5).to(dtype) if norm else None
+    eps = 1e-5
+    y_f32 = norm  # the decode step's use: norm folded in, float32 logits
+    y = torch.full((batch, ldy), 9.0, dtype=torch.float32 if y_f32 else dtype, device="cuda")
+    dense_call(lib, dtype, w, x, g, eps, y, y_f32, batch, n, m, ldy)
+    xin = (g * torch.nn.functional.rms_norm(x.float(), (n,), eps=eps).to(dtype)) if norm else x
+    ref = (xin.double().cpu() @ w.double().cpu().T).numpy()
     got = y[:, :m].double().cpu().numpy()
+    if y_f32:  # float32 outputs carry values already rounded to dtype
+        assert torch.equal(y[:, :m].to(dtype).float(), y[:, :m])
     bits = 11 if dtype == torch.float16 else 8
     # half a unit of the rounded value's binade (the larger one where rounding carried into the next)
     allowed = np.maximum(half_ulp(ref, bits), half_ulp(got, bits))
     excess = np.maximum(np.abs(got - ref) - allowed, 0.0).max() / np.abs(ref).max()
-    print(f"[dense] {dtype} {(m, n, batch)} excess={excess:.2e}", flush=True)
-    assert excess <= 1e-5, excess
+    print(f"[dense] {dtype} {(m, n, batch)} norm={norm} excess={excess:.2e}", flush=True)
+    assert excess <= (5e-5 if norm else 1e-5), excess
     if ldy > m:
         assert torch.equal(y[:, m:], torch.full_like(y[:, m:], 9.0))
 
@@ -454,9 +468,13 @@ def test_dense_gemv_argument_errors(lib):
     x = torch.zeros(2, 64, dtype=torch.float16, device="cuda")
     y = torch.zeros(2, 16, dtype=torch.float16, device="cuda")
     f = lib.nq_dense_gemv
-    assert f(_lib.NQ_F16, w.data_ptr(), x.data_ptr(), y.data_ptr(), 2, 60, 16, 16, None) == _lib.NQ_ERR_SHAPE
-    assert f(_lib.NQ_F16, w.data_ptr() + 2, x.data_ptr(), y.data_ptr(), 2, 64, 15, 16, None) == _lib.NQ_ERR_ALIGNMENT
-    assert f(_lib.NQ_F16, w.data_ptr(), x.data_ptr(), y.data_ptr(), 2, 64, 16, 15, None) == \
-        _lib.NQ_ERR_INVALID_ARGUMENT
-    assert f(7, w.data_ptr(), x.data_ptr(), y.data_ptr(), 2, 64, 16, 16, None) == _lib.NQ_ERR_DTYPE
-    assert f(_lib.NQ_F16, None, None, None, 0, 64, 16, 16, None) == _lib.NQ_OK  # empty batch
+    F16 = _lib.NQ_F16
+    wp, xp, yp = w.data_ptr(), x.data_ptr(), y.data_ptr()
+    assert f(F16, wp, xp, None, 0.0, yp, 0, 2, 60, 16, 16, None) == _lib.NQ_ERR_SHAPE
+    assert f(F16, wp + 2, xp, None, 0.0, yp, 0, 2, 64, 15, 16, None) == _lib.NQ_ERR_ALIGNMENT
+    assert f(F16, wp, xp, xp + 2, 0.0, yp, 0, 2, 64, 16, 16, None) == _lib.NQ_ERR_ALIGNMENT  # norm weight
+    assert f(F16, wp, xp, None, 0.0, yp + 2, 1, 2, 64, 16, 16, None) == _lib.NQ_ERR_ALIGNMENT  # float32 y
+    assert f(F16, wp, xp, None, 0.0, yp, 0, 2, 64, 16, 15, None) == _lib.NQ_ERR_INVALID_ARGUMENT
+    assert f(F16, wp, xp, None, 0.0, yp, 0, 2, 40000, 16, 16, None) == _lib.NQ_ERR_UNSUPPORTED  # n past the LDS
+    assert f(7, wp, xp, None, 0.0, yp, 0, 2, 64, 16, 16, None) == _lib.NQ_ERR_DTYPE
+    assert f(F16, None, None, None, 0.0, None, 0, 0, 64, 16, 16, None) == _lib.NQ_OK  # empty batch
