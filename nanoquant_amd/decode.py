@@ -21,6 +21,7 @@ from __future__ import annotations
 
 import math
 import time
+import warnings
 from dataclasses import dataclass
 
 import torch
@@ -30,6 +31,11 @@ import torch.nn.functional as F
 from .modules.linear import NanoQuantLinear
 
 LINEAR_NAMES = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
+
+# The fused step's complex rotary product runs on complex32 tensors, whose first allocation makes
+# torch warn that ComplexHalf support is experimental; its multiply is what the step uses, and the
+# step is checked against the unfused path.
+warnings.filterwarnings("ignore", message="ComplexHalf support is experimental", category=UserWarning)
 
 
 @dataclass(frozen=True)
@@ -250,11 +256,22 @@ def rotary_attention_step(shape: LlamaShape, layer: int, qk, v, tables, position
     additive causal mask, the scores product adds into it in place (the mask is not copied first).
     """
     H, KV, D = shape.heads, shape.kv_heads, shape.head_dim
-    B, G = qk.shape[0], H // KV
     R, madd = tables
+    rot = torch.mm(qk.reshape(-1, D), R).view(qk.shape[0], H + KV, D)
+    return attention_after_rotary(shape, layer, rot, v, positions, cache, madd, out=out, scores=scores)
+
+
+def attention_after_rotary(shape: LlamaShape, layer: int, rot, v, positions, cache: StaticKVCache, madd, out=None,
+                           scores=None):
+    """The rest of ``rotary_attention_step`` once q and k are rotated: rot [B, H + KV, D] (q heads then
+    k heads); the key and value cache writes (v None: the value row is already in the cache), the
+    scores with the scale and mask folded into one batched product (``madd`` the additive mask, or
+    ``scores`` already holding it), the softmax and the value product (into ``out`` when given and
+    each kv head serves one query head)."""
+    H, KV, D = shape.heads, shape.kv_heads, shape.head_dim
+    B, G = rot.shape[0], H // KV
     k_c, v_c = cache.k[layer], cache.v[layer]
     L = k_c.shape[2]
-    rot = torch.mm(qk.reshape(-1, D), R).view(B, H + KV, D)
     k_c.index_copy_(2, positions, rot[:, H:].unsqueeze(2).to(k_c.dtype))
     if v is not None:
         v_c.index_copy_(2, positions, v.reshape(B, KV, 1, D).to(v_c.dtype))
@@ -562,6 +579,18 @@ class FusedDecoder(GraphDecoder):
         self.rope_cos, self.rope_sin = cos.contiguous(), sin.contiguous()
         self.rope_cs = torch.stack((self.rope_cos, self.rope_sin), dim=1).contiguous()  # [max_len, 2, D]
         self.tok = torch.zeros(batch, dtype=torch.long, device=dev)  # the step's input token ids
+        # the torch step in float16 rotates q and k as one complex product: their features in pair
+        # order (feature j of a head, then j + D/2, ...), the cache's keys too (dot products do not
+        # change under a common reordering); bfloat16 has no complex type and keeps the [D, D] product
+        self.pair_order = attention == "torch" and dt == torch.float16
+        if self.pair_order:
+            j = torch.arange(D, device=dev)
+            self.head_order = (j // 2) + (j % 2) * (D // 2)  # position i of a head holds feature head_order[i]
+            self.q_order = (torch.arange(H, device=dev)[:, None] * D + self.head_order).reshape(-1)
+            self.k_order = (torch.arange(KV, device=dev)[:, None] * D + self.head_order).reshape(-1)
+            half = torch.stack((self.rope_cos[:, : D // 2], self.rope_sin[:, : D // 2]), dim=-1).contiguous()
+            self.rope_freqs = torch.view_as_complex(half)  # [max_len, D / 2] complex32: cos + i sin
+            self.rot = torch.zeros(batch, H + KV, D, device=dev, dtype=dt)
         self._keep = []  # tensors whose addresses the item tables hold
         self.plans = [self._layer_plan(layer) for layer in model.model.layers]
         need = 0
@@ -585,15 +614,24 @@ class FusedDecoder(GraphDecoder):
         return s_in
 
     def _items(self, entries):
+        """Item table of (linear, norm weight, y, offset, stride, residual[, output row order]): with a
+        row order (an index tensor over the outputs), the item holds copies of U's rows and s_out in
+        that order, so output j of the item is output order[j] of the linear."""
         arr = (self._lib.GemvItem * len(entries))()
-        for i, (lin, norm_weight, y, y_off, y_stride, resid) in enumerate(entries):
+        for i, entry in enumerate(entries):
+            lin, norm_weight, y, y_off, y_stride, resid = entry[:6]
+            order = entry[6] if len(entry) > 6 else None
+            u_words, s_out = lin.U_int8, lin.scale_post
+            if order is not None:
+                u_words, s_out = u_words.index_select(0, order).contiguous(), s_out.index_select(0, order).contiguous()
+                self._keep += [u_words, s_out]
             it = arr[i]
             it.v_bits = lin.V_int8.data_ptr()
             it.s_in = self._scale_in(lin, norm_weight).data_ptr()
             mid = getattr(lin, "scale_mid", None)
             it.s_mid = None if mid is None else mid.data_ptr()
-            it.u_bits = lin.U_int8.data_ptr()
-            it.s_out = lin.scale_post.data_ptr()
+            it.u_bits = u_words.data_ptr()
+            it.s_out = s_out.data_ptr()
             it.y = y.data_ptr() + y_off * y.element_size()
             it.resid = None if resid is None else resid.data_ptr()
             it.r = lin.V_int8.shape[0]
@@ -607,8 +645,11 @@ class FusedDecoder(GraphDecoder):
         a, mlp = layer.self_attn, layer.mlp
         w1, w2 = layer.input_layernorm.weight, layer.post_attention_layernorm.weight
         W = self.qkv_width
+        # in pair order (the torch step's complex rotary product) q and k come out with each head's
+        # features j and j + D/2 side by side
+        qo, ko = (self.q_order, self.k_order) if self.pair_order else (None, None)
         return {
-            "qkv": self._items([(a.q_proj, w1, self.qkv, 0, W, None), (a.k_proj, w1, self.qkv, H * D, W, None),
+            "qkv": self._items([(a.q_proj, w1, self.qkv, 0, W, None, qo), (a.k_proj, w1, self.qkv, H * D, W, None, ko),
                                 (a.v_proj, w1, self.qkv, (H + KV) * D, W, None)]),
             # the same three items with q stored rotated into q_rot (k and v go to the caches)
             "qkv_rope": self._items([(a.q_proj, w1, self.q_rot, 0, H * D, None), (a.k_proj, w1, self.qkv, 0, W, None),
@@ -630,8 +671,12 @@ class FusedDecoder(GraphDecoder):
         st = self._lib.stream_of(self.device)
         torch.index_select(self.model.model.embed_tokens.weight, 0, self.tok, out=self.x)
         if self.attention == "torch":
-            cs = self.rope_cs.index_select(0, self.pos)  # [1, 2, D]: cos, sin of the position
-            tables = rotary_step_tables(cs[:, 0], cs[:, 1], self.pos, self.cache, self.model.dtype, with_mask=False)
+            if self.pair_order:
+                freqs = self.rope_freqs.index_select(0, self.pos)  # [1, D / 2]: cos + i sin of the position
+            else:
+                cs = self.rope_cs.index_select(0, self.pos)  # [1, 2, D]: cos, sin of the position
+                tables = rotary_step_tables(cs[:, 0], cs[:, 1], self.pos, self.cache, self.model.dtype,
+                                            with_mask=False)
             step_mask(self.pos, self.cache, self.model.dtype, out=self.scores_all)
         x, h, qkv, attn, act = (t.data_ptr() for t in (self.x, self.h, self.qkv, self.attn, self.act))
         esz = self.qkv.element_size()
@@ -658,8 +703,15 @@ class FusedDecoder(GraphDecoder):
             elif self.attention == "rope":
                 attention_products_step(s, li, self.q_rot, None, self.cache, self.attn, scores=self.scores)
             else:
-                out = rotary_attention_step(s, li, self.qkv[:, :(H + KV) * D], None, tables, self.pos, self.cache,
-                                            out=self.attn, scores=self.scores_all[li])
+                qk = self.qkv[:, :(H + KV) * D]
+                if self.pair_order:
+                    pairs = torch.view_as_complex(qk.reshape(B, H + KV, D // 2, 2))
+                    torch.mul(pairs, freqs, out=torch.view_as_complex(self.rot.view(B, H + KV, D // 2, 2)))
+                    out = attention_after_rotary(s, li, self.rot, None, self.pos, self.cache, None, out=self.attn,
+                                                 scores=self.scores_all[li])
+                else:
+                    out = rotary_attention_step(s, li, qk, None, tables, self.pos, self.cache, out=self.attn,
+                                                scores=self.scores_all[li])
                 if out.data_ptr() != self.attn.data_ptr():
                     self.attn.copy_(out.view(B, H * D))
             items, n = plan["o"]
@@ -690,6 +742,9 @@ class FusedDecoder(GraphDecoder):
     def prefill(self, prompt: torch.Tensor) -> torch.Tensor:
         logits = super().prefill(prompt)
         self.tok.copy_(self.ids[:, prompt.shape[1]])  # the step's input token, kept on the device
+        if self.pair_order:  # the prompt's keys into the step's pair order
+            for k_c in self.cache.k:
+                k_c.copy_(k_c.index_select(3, self.head_order))
         return logits
 
 
