@@ -166,50 +166,47 @@ def rotary_attention(shape: LlamaShape, layer: int, q, k, v, cos, sin, positions
     return torch.matmul(p, v_c).view(B, H, T, D).transpose(1, 2).reshape(B, T, H * D)
 
 
-_STEP_CONSTANTS = {}
-
-
 def step_constants(head_dim: int, dtype, device):
-    """The fixed parts of a one-token step's tables, made once per (head_dim, dtype, device): the
-    identity I and the rotate-half matrix P (x @ P == rotate_half(x)) in ``dtype``, and the two
-    values of the additive causal mask (0, -inf) as 0-d tensors."""
-    key = (head_dim, dtype, str(device))
-    if key not in _STEP_CONSTANTS:
-        h = head_dim // 2
-        eye = torch.eye(head_dim, device=device, dtype=dtype)
-        rot = torch.zeros(head_dim, head_dim, device=device, dtype=dtype)
-        idx = torch.arange(h, device=device)
-        rot[idx + h, idx] = -1.0  # out[j < h] takes -x[j + h]
-        rot[idx, idx + h] = 1.0   # out[j >= h] takes x[j - h]
-        _STEP_CONSTANTS[key] = (eye, rot, torch.zeros((), device=device, dtype=dtype),
-                                torch.full((), float("-inf"), device=device, dtype=dtype))
-    return _STEP_CONSTANTS[key]
+    """The fixed parts of a one-token step's tables: the identity I and the rotate-half matrix P
+    (x @ P == rotate_half(x)) [D, D] in ``dtype``, and the two values of the additive causal mask
+    (0, -inf) as a [2] tensor. Callers make them once and keep them (the model as buffers): tensors
+    made inside a captured or compiled step would be overwritten by the graph's next run."""
+    h = head_dim // 2
+    eye = torch.eye(head_dim, device=device, dtype=dtype)
+    rot = torch.zeros(head_dim, head_dim, device=device, dtype=dtype)
+    idx = torch.arange(h, device=device)
+    rot[idx + h, idx] = -1.0  # out[j < h] takes -x[j + h]
+    rot[idx, idx + h] = 1.0   # out[j >= h] takes x[j - h]
+    values = torch.tensor([0.0, float("-inf")], device=device, dtype=dtype)
+    return eye, rot, values
 
 
-def step_mask(positions, cache: StaticKVCache, dtype, out=None):
+def step_mask(positions, cache: StaticKVCache, values, out=None):
     """The additive causal mask of a one-token step at ``positions`` (one position, on the device):
-    [1, L, 1], 0 for cache rows up to the position and -inf past it; written into ``out`` (any
-    shape that broadcasts [1, L, 1], e.g. every layer's scores at once) when it is given."""
-    _, _, zero, ninf = step_constants(2, dtype, positions.device)
+    [1, L, 1], values[0] (0) for cache rows up to the position and values[1] (-inf) past it; written
+    into ``out`` (any shape that broadcasts [1, L, 1], e.g. every layer's scores at once) when it
+    is given."""
     visible = cache.key_index.view(1, -1, 1) <= positions.view(1, 1, 1)
     if out is None:
-        return torch.where(visible, zero, ninf)
+        return torch.where(visible, values[0], values[1])
     # the condition takes out's full shape, so that the result is written in place, not resized
     L = visible.shape[1]
     visible = visible.view([1] * (out.dim() - 2) + [L, 1]).expand(out.shape)
-    return torch.where(visible, zero, ninf, out=out)
+    return torch.where(visible, values[0], values[1], out=out)
 
 
-def rotary_step_tables(cos, sin, positions, cache: StaticKVCache, dtype, with_mask: bool = True):
+def rotary_step_tables(cos, sin, positions, cache: StaticKVCache, dtype, with_mask: bool = True, consts=None):
     """What every layer of a one-token step at ``positions`` (one position, on the device) shares:
     the rotary embedding as a [D, D] matrix R (x @ R == x * cos + rotate_half(x) * sin, with cos and
     sin [1, D] of that position) and the causal mask as an additive [1, L, 1] (0 for visible cache
     rows, -inf past the position; None without ``with_mask``). R = I * cos + P * sin column by
-    column: each entry is one of cos, +-sin or 0, exact in ``dtype``."""
+    column: each entry is one of cos, +-sin or 0, exact in ``dtype``. ``consts``: the
+    ``step_constants`` to use (made here when None)."""
     D = cos.shape[-1]
-    eye, rot, _, _ = step_constants(D, dtype, cos.device)
+    eye, rot, values = consts if consts is not None else step_constants(D, dtype, cos.device)
+    eye, rot, values = eye.to(dtype), rot.to(dtype), values.to(dtype)
     R = torch.addcmul(eye * cos.reshape(1, D).to(dtype), rot, sin.reshape(1, D).to(dtype))
-    return R, (step_mask(positions, cache, dtype) if with_mask else None)
+    return R, (step_mask(positions, cache, values) if with_mask else None)
 
 
 def attention_products_step(shape: LlamaShape, layer: int, q, madd, cache: StaticKVCache, out, scores=None):
@@ -349,6 +346,10 @@ class NanoQuantLlama(nn.Module):
         d = shape.head_dim
         inv_freq = 1.0 / (shape.rope_theta ** (torch.arange(0, d, 2, dtype=torch.float32, device=device) / d))
         self.register_buffer("inv_freq", inv_freq, persistent=False)
+        eye, rot, values = step_constants(d, dtype, device)
+        self.register_buffer("step_eye", eye, persistent=False)
+        self.register_buffer("step_rot", rot, persistent=False)
+        self.register_buffer("step_mask_values", values, persistent=False)
 
     def linears(self):
         for layer in self.model.layers:
@@ -364,7 +365,8 @@ class NanoQuantLlama(nn.Module):
     def forward(self, ids, positions, cache: StaticKVCache):
         x = self.model.embed_tokens(ids)
         cos, sin = self.rope(positions, x.dtype)
-        tables = rotary_step_tables(cos, sin, positions, cache, x.dtype) if ids.shape[1] == 1 else None
+        consts = (self.step_eye, self.step_rot, self.step_mask_values)
+        tables = rotary_step_tables(cos, sin, positions, cache, x.dtype, consts=consts) if ids.shape[1] == 1 else None
         for layer in self.model.layers:
             x = layer(x, cos, sin, positions, cache, tables)
         x = self.model.norm(x)
@@ -384,6 +386,8 @@ class NanoQuantLlama(nn.Module):
             layer.input_layernorm.to(dtype)
             layer.post_attention_layernorm.to(dtype)
         self.lm_head.to(dtype)
+        for name in ("step_eye", "step_rot", "step_mask_values"):  # the one-token step's tables
+            setattr(self, name, getattr(self, name).to(dtype))
         self.dtype = dtype
         return self
 
@@ -579,6 +583,7 @@ class FusedDecoder(GraphDecoder):
         self.rope_cos, self.rope_sin = cos.contiguous(), sin.contiguous()
         self.rope_cs = torch.stack((self.rope_cos, self.rope_sin), dim=1).contiguous()  # [max_len, 2, D]
         self.tok = torch.zeros(batch, dtype=torch.long, device=dev)  # the step's input token ids
+        self.step_consts = step_constants(D, dt, dev)
         # the torch step in float16 rotates q and k as one complex product: their features in pair
         # order (feature j of a head, then j + D/2, ...), the cache's keys too (dot products do not
         # change under a common reordering); bfloat16 has no complex type and keeps the [D, D] product
@@ -676,8 +681,8 @@ class FusedDecoder(GraphDecoder):
             else:
                 cs = self.rope_cs.index_select(0, self.pos)  # [1, 2, D]: cos, sin of the position
                 tables = rotary_step_tables(cs[:, 0], cs[:, 1], self.pos, self.cache, self.model.dtype,
-                                            with_mask=False)
-            step_mask(self.pos, self.cache, self.model.dtype, out=self.scores_all)
+                                            with_mask=False, consts=self.step_consts)
+            step_mask(self.pos, self.cache, self.step_consts[2], out=self.scores_all)
         x, h, qkv, attn, act = (t.data_ptr() for t in (self.x, self.h, self.qkv, self.attn, self.act))
         esz = self.qkv.element_size()
         for li, plan in enumerate(self.plans):
