@@ -581,7 +581,9 @@ def bench_decode(args, dev):
             "ms_per_token": round(prof["ms_per_token"], 4),
             "step": head if head != "fused_torch_attention" else
                     ("fused linears (q/k/v and gate/up stage 1 each one launch with RMSNorm folded in, SiLU*mul "
-                     "and residual epilogues) with RoPE, KV write and attention in torch ops; HIP graph"),
+                     "and residual epilogues; the q/k/v stage 2 writes the value cache row) with the rotary "
+                     "embedding (one complex product), key-cache write, causal mask, scores, softmax and value "
+                     "product in torch ops; final norm and lm_head one dense GEMV launch; HIP graph"),
             "variants": {"fused_torch_attention": "the step above (config 5 as written: non-linear ops of the "
                                                   "attention in torch)",
                          "fused_torch_attention_spg1": "the same, one step per graph",
