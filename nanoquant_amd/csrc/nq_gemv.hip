@@ -650,6 +650,158 @@ __global__ __launch_bounds__(G * WR * 64) void s1l_kernel(const S1Table tab, con
     NQ_STAMP(3);
 }
 
+// s1b_kernel: s1l_kernel for NB = 2..4 batch rows. Each sign word's decode (the 64-bit shift of a
+// row pair and the xor of the pair signs onto the s_in pair) is done once and feeds one v_dot2 per
+// batch row, so a batch row costs one dot2 per pair and row on top of the decode (1.5 VALU) instead
+// of a pass of its own. LDS per word: s_in pieces 0..3, x pieces 0..3 of each batch row, one pad:
+// 4 NB + 5 slots, an odd stride, so the quarter-wave reads stay in distinct slots. The LDS reads go
+// a quarter word (one piece of s_in and of each batch row) ahead of the arithmetic.
+__host__ __device__ inline int s1b_word_slots(int nb) { return 4 * nb + 5; }
+__host__ __device__ inline int s1b_zero_slot(int wn, int nb) { return (s1b_word_slots(nb) * wn + 63) / 64 * 64; }
+inline size_t s1b_lds_bytes(int wn, int nb) {
+    return static_cast<size_t>(s1b_zero_slot(wn, nb) + s1b_word_slots(nb)) * 16;
+}
+
+template <typename T, int WPL, int R, int G, int WR, int NB, bool kNorm, bool kOne>
+__global__ __launch_bounds__(G * WR * 64) void s1b_kernel(const S1Table tab, const uint16_t* __restrict__ x, int n,
+                                                          int wn, float eps) {
+    static_assert(R % 2 == 0, "rows go in pairs");
+    static_assert(NB >= 2 && NB <= 4, "two to four batch rows");
+    constexpr int S = 4 * NB + 5;  // LDS slots per word
+    extern __shared__ __attribute__((aligned(16))) uint32_t sx[];
+    __shared__ float part[(G * R + 1) * NB * WR];
+    static_assert(sizeof(part) <= 1024, "the static LDS the launch leaves aside");
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int grp = wave / WR, h = wave % WR;
+    const S1Item it = kOne ? tab.item[0] : pick_item<S1Item>(tab);
+    if (!kOne && item_done(it)) return;
+    const int r = it.r;
+    const int j0 = static_cast<int>(blockIdx.x) * (G * R) + grp * R;
+    const int zslot = s1b_zero_slot(wn, NB);
+
+    // V's words of this wave's rows (as s1l_kernel)
+    const rsrc_t v_rs = make_rsrc(it.v_bits, static_cast<uint32_t>(r) * static_cast<uint32_t>(wn) * 4u);
+    uint32_t vb[WPL][R];
+#pragma unroll
+    for (int w = 0; w < WPL; ++w)
+#pragma unroll
+        for (int k = 0; k < R; ++k)
+            vb[w][k] = load_b32_stream(v_rs, (static_cast<uint32_t>(j0 + k) * static_cast<uint32_t>(wn) +
+                                              static_cast<uint32_t>(h * 64 + lane + 64 * WR * w)) * 4u);
+    uint16_t mid[R];
+    const uint16_t* msrc = it.s_mid != nullptr ? it.s_mid : it.s_in;
+    const int mlim = (it.s_mid != nullptr ? r : n) - 1;
+#pragma unroll
+    for (int k = 0; k < R; ++k) mid[k] = msrc[min(j0 + k, mlim)];
+    // the DMA of s_in and the batch rows of x: slot l = S q + v (each wave's lanes fill 64
+    // consecutive slots; the last round's lanes past the region repeat its last piece into slots
+    // below zslot)
+    const int slots = S * wn;
+    const uint32_t magic = div_magic(S);
+    for (int l0 = wave * 64; l0 < slots; l0 += G * WR * 64) {
+        const int l = min(l0 + lane, slots - 1);
+        const int q = static_cast<int>(__umulhi(static_cast<uint32_t>(l), magic));
+        const int v = l - S * q;
+        const uint16_t* src;
+        if (v < 4) src = it.s_in + 32 * q + 8 * v;
+        else if (v < 4 + 4 * NB) src = x + static_cast<size_t>((v - 4) >> 2) * n + 32 * q + 8 * ((v - 4) & 3);
+        else src = x + 32 * q;  // the pad slot: any valid piece
+        dma16(src, sx + 4 * l0);
+    }
+    if (t < 4 * S) sx[4 * zslot + t] = 0u;
+    wait_vmcnt<0>();
+    barrier_keep_dma();
+
+    const uint32_t mask = kSignPair;
+    float acc[2][R][NB];
+    float ss[2][NB];
+#pragma unroll
+    for (int k = 0; k < R; ++k)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) acc[0][k][b] = acc[1][k][b] = 0.0f;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) ss[0][b] = ss[1][b] = 0.0f;
+    // one quarter word: piece v of s_in and of each batch row's x
+    u32x4 cs, cx[NB], ns, nx[NB];
+    auto fetch = [&](u32x4& ds, u32x4* dx, int w, int v) {
+        const int q = h * 64 + lane + 64 * WR * w;
+        const u32x4* p = reinterpret_cast<const u32x4*>(sx) + (q < wn ? S * q : zslot);
+        ds = p[v];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) dx[b] = p[4 + 4 * b + v];
+    };
+    fetch(cs, cx, 0, 0);
+#pragma unroll
+    for (int w = 0; w < WPL; ++w) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            if (v + 1 < 4) fetch(ns, nx, w, v + 1);
+            else if (w + 1 < WPL) fetch(ns, nx, w + 1, 0);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int pp = 4 * v + e;
+                const uint32_t sp = cs[e];
+#pragma unroll
+                for (int k = 0; k < R; k += 2) {
+                    const uint64_t sh = ((static_cast<uint64_t>(vb[w][k + 1]) << 32) | vb[w][k]) << pp;
+                    const uint32_t a0 = (static_cast<uint32_t>(sh) & mask) ^ sp;
+                    const uint32_t a1 = (static_cast<uint32_t>(sh >> 32) & mask) ^ sp;
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) {
+                        acc[pp & 1][k][b] = T::dot2(a0, cx[b][e], acc[pp & 1][k][b]);
+                        acc[pp & 1][k + 1][b] = T::dot2(a1, cx[b][e], acc[pp & 1][k + 1][b]);
+                    }
+                }
+                if (kNorm && grp == 0) {
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) ss[pp & 1][b] = T::dot2(cx[b][e], cx[b][e], ss[pp & 1][b]);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            cs = ns;
+#pragma unroll
+            for (int b = 0; b < NB; ++b) cx[b] = nx[b];
+        }
+    }
+
+    // the waves' sums per (row, batch row) and group 0's x^2 sums per batch row, through LDS
+#pragma unroll
+    for (int k = 0; k < R; ++k)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const float v = wave_sum_dpp(acc[0][k][b] + acc[1][k][b]);
+            if (lane == 0) part[((grp * R + k) * NB + b) * WR + h] = v;
+        }
+    if (kNorm && grp == 0) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const float v = wave_sum_dpp(ss[0][b] + ss[1][b]);
+            if (lane == 0) part[(G * R * NB + b) * WR + h] = v;
+        }
+    }
+    __syncthreads();
+    if (h == 0 && lane < R * NB) {
+        const int k = lane / NB, b = lane - (lane / NB) * NB;  // row j0 + k of the group, batch row b
+        const int j = j0 + k;
+        float v = 0.0f, sq = 0.0f;
+#pragma unroll
+        for (int s2 = 0; s2 < WR; ++s2) {
+            v += part[((grp * R + k) * NB + b) * WR + s2];
+            if (kNorm) sq += part[(G * R * NB + b) * WR + s2];
+        }
+        if (kNorm) v *= rsqrtf(sq / static_cast<float>(n) + eps);
+        uint16_t mk = mid[0];
+#pragma unroll
+        for (int kk = 1; kk < R; ++kk) mk = k == kk ? mid[kk] : mk;
+        const float mf = it.s_mid != nullptr ? T::to_float(mk) : 1.0f;
+        if (j < it.kpad) store_h(it.z_hi, it.z_lo, it.zpitch, b, j, j < r ? v * mf : 0.0f);
+    }
+    if (blockIdx.x == 0) zero_h_pad(it.z_hi, it.z_lo, it.zpitch, it.kpad, 0, NB, NB);
+}
+
 // --------------------------------------------------------------------------- stage 1, MFMA (batches)
 //
 // For three or more batch rows: v_mfma_f32_16x16x32_{f16,bf16} with A = 16 rows of V x 32 k of
@@ -1872,12 +2024,72 @@ void launch_s1l_cfg(const S1lShape& sh, const S1Table& tab, int blocks, const ui
 // are 16-byte aligned), up to kS1lMaxWords words.
 inline bool s1l_applies(int batch, int n, int wn) { return batch == 1 && n % 32 == 0 && wn <= kS1lMaxWords; }
 
+inline hipError_t allow_lds_bytes(const void* kernel, int bytes);
+
+// Whether s1b_kernel takes the stage (same-box A/B of the GEMV op against the kernels it replaces,
+// 32 rotating weight copies, us): rows of up to 128 words at two to four batch rows (n = 4096, gate
+// at 2 / 3 / 4 rows 8.31 / 9.65 / 10.17 -> 7.79 / 8.75 / 9.23, q/k/v/o at 2 / 4 rows 6.76 / 8.57 ->
+// 6.45 / 7.59), and rows of 257-384 words at two (down_proj, n = 11008: 9.27 -> 8.03). Elsewhere it
+// lost: on 8192-wide rows each block of 4 rows of V stages all of x for its batch rows (Llama-3-70B
+// q/o at 4 rows 12.0 -> 15.8 us, k/v 6.7 -> 7.3, gate 19.8 -> 27.2, q/o at 2 rows 10.09 -> 10.24),
+// and on 257-384-word rows at 3-4 batch rows the 12-wave shape runs out of its 168 registers and
+// spills (11008-wide rows at 3 / 4: 12.6 / 12.8 -> 25.1 / 32.5 us).
+// (The kernel's static LDS, its partial sums, takes at most 432 bytes of the 1 KB left aside.)
+constexpr int kS1bLdsBytes = kSbLdsBytes - 1024;
+inline bool s1b_applies(int batch, int n, int wn) {
+    if (batch < 2 || batch > 4 || n % 32 != 0) return false;
+    if (!(wn <= 128 || (batch == 2 && wn > 256 && wn <= kS1lMaxWords))) return false;
+    return s1b_lds_bytes(wn, batch) <= static_cast<size_t>(kS1bLdsBytes);
+}
+
+template <typename T, int NB, bool kNorm, bool kOne>
+void launch_s1b_cfg(const S1lShape& sh, const S1Table& tab, int blocks, const uint16_t* x, int n, int wn, float eps,
+                    hipStream_t st) {
+    const size_t lds = s1b_lds_bytes(wn, NB);
+    // (blocks may take more than 64 KB of LDS: the limit is raised once per kernel)
+#define NQ_S1B_CASE(WPL, R, G, WR)                                                                               \
+    if (sh.wpl == WPL && sh.r == R && sh.g == G && sh.wr == WR) {                                                \
+        static const hipError_t attr = allow_lds_bytes(                                                          \
+            reinterpret_cast<const void*>(&s1b_kernel<T, WPL, R, G, WR, NB, kNorm, kOne>), kS1bLdsBytes);        \
+        (void)attr; /* a refusal surfaces as the launch's error */                                              \
+        s1b_kernel<T, WPL, R, G, WR, NB, kNorm, kOne>                                                            \
+            <<<dim3(blocks, 1, tab.count), G * WR * 64, lds, st>>>(tab, x, n, wn, eps);                          \
+        return;                                                                                                  \
+    }
+    NQ_S1B_CASE(1, 2, 4, 1)
+    NQ_S1B_CASE(2, 2, 4, 1)
+    if constexpr (NB == 2) {  // (wider rows take two batch rows only, see s1b_applies)
+        NQ_S1B_CASE(2, 2, 4, 3)
+    }
+#undef NQ_S1B_CASE
+}
+
+template <typename T, int NB>
+void launch_s1b_table(const S1lShape& sh, const S1Table& tab, int blocks, const uint16_t* x, int n, int wn, bool norm,
+                      float eps, hipStream_t st) {
+    if (tab.count == 1) {
+        if (norm) launch_s1b_cfg<T, NB, true, true>(sh, tab, blocks, x, n, wn, eps, st);
+        else launch_s1b_cfg<T, NB, false, true>(sh, tab, blocks, x, n, wn, eps, st);
+    } else {
+        if (norm) launch_s1b_cfg<T, NB, true, false>(sh, tab, blocks, x, n, wn, eps, st);
+        else launch_s1b_cfg<T, NB, false, false>(sh, tab, blocks, x, n, wn, eps, st);
+    }
+}
+
 // One launch over every item of `tab` (block ranges filled in here). The caller checked that
 // the fast stage 1 applies: n >= 8, n % 8 == 0, wn <= 1024, x and each s_in 16-byte aligned,
 // every r > 0.
 template <typename T>
 void launch_s1w_table(S1Table& tab, const uint16_t* x, int batch, int n, int wn, bool norm, float eps,
                       hipStream_t st) {
+    if (s1b_applies(batch, n, wn)) {
+        const S1lShape sh = s1l_shape(wn);
+        const int blocks = item_planes(tab, sh.r * sh.g);
+        if (batch == 2) launch_s1b_table<T, 2>(sh, tab, blocks, x, n, wn, norm, eps, st);
+        else if (batch == 3) launch_s1b_table<T, 3>(sh, tab, blocks, x, n, wn, norm, eps, st);
+        else launch_s1b_table<T, 4>(sh, tab, blocks, x, n, wn, norm, eps, st);
+        return;
+    }
     if (s1l_applies(batch, n, wn)) {
         const S1lShape sh = s1l_shape(wn);
         const int blocks = item_planes(tab, sh.r * sh.g);
@@ -2011,7 +2223,7 @@ void launch_stage1_table(S1Table& tab, const uint16_t* x, int batch, int n, int 
     const bool valu_rows = batch <= 2 || (batch <= 4 && wn <= 256 && v_words < 256 * 1024) ||
                            (batch == 3 && wn <= 256 && r_max <= 2496);
     // past 512 words the VALU shape covers one batch row (four words per lane)
-    if ((!valu_rows || wn > 1024 || (wn > 512 && batch > 1)) && s1m_fits(n, wn))
+    if (!s1b_applies(batch, n, wn) && (!valu_rows || wn > 1024 || (wn > 512 && batch > 1)) && s1m_fits(n, wn))
         launch_s1m_table<T>(tab, x, batch, n, wn, norm, eps, st);
     else
         launch_s1w_table<T>(tab, x, batch, n, wn, norm, eps, st);

@@ -103,11 +103,12 @@ def rel(y, y64):
     return float(np.abs(y - y64).max() / np.abs(y64).max())
 
 
-# n = 512: VALU stage 1 for 1-2 rows, MFMA stage 1 from 3; n = 20000 (625-word rows): the VALU
-# shape with four words per lane over four waves at one row, the MFMA stage 1 from 2; n = 32768
-# (1024-word rows): the same, the MFMA stage 1 with its tile of V at the unpadded stride
+# n = 512: VALU stage 1 for 1-4 rows (2-4 rows decoding each sign word once for all of them), MFMA
+# stage 1 from 5; n = 20000 (625-word rows): the VALU shape with four words per lane over four waves
+# at one row, the MFMA stage 1 from 2; n = 32768 (1024-word rows): the same, the MFMA stage 1 with
+# its tile of V at the unpadded stride
 @pytest.mark.parametrize("n", [512, 20000, 32768])
-@pytest.mark.parametrize("batch", [1, 2, 5, 18])
+@pytest.mark.parametrize("batch", [1, 2, 4, 5, 18])
 def test_group_norm_and_residual(lib, batch, n):
     from nanoquant_amd import _lib
     announce("group norm + residual", batch, n)

@@ -276,6 +276,18 @@ GEMV_CASES = [
     ("sb_rounds_b48_n28672", 300, 28672, 3000, 48, True),
     ("sb_rounds_b128_n11008", 500, 11008, 2976, 128, False),
     ("sb_rounds_b100_n28672", 200, 28672, 2900, 100, True),
+    # the VALU stage 1 that decodes each sign word once for all batch rows: two to four rows on rows of
+    # up to 128 words (each launch shape's width bucket), two rows on rows of 257-384 words; ragged
+    # ranks and row ends, s_mid, a rank of 1; and the rows next to its bounds, which other kernels take
+    ("s1b_b2_n1024_mid_ragged", 300, 1024, 70, 2, True),
+    ("s1b_b4_n2048_mid", 600, 2048, 250, 4, True),
+    ("s1b_b3_n4096_ragged", 500, 4096, 333, 3, False),
+    ("s1b_b4_n4064_mid", 400, 4064, 130, 4, True),
+    ("s1b_b2_n11008", 700, 11008, 1632, 2, False),
+    ("s1b_b2_n12288_mid", 400, 12288, 130, 2, True),
+    ("s1b_b2_n11008_r1", 64, 11008, 1, 2, True),
+    ("not_s1b_b4_n8192_mid", 600, 8192, 250, 4, True),
+    ("not_s1b_b3_n11008", 700, 11008, 1632, 3, False),
 ]
 
 
