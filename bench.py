@@ -25,6 +25,8 @@ The JSON line carries:
   shapes, TFLOP/s = 2*B*r*(n+m) / time against 2.5 PFLOP/s dense fp16;
 * ``pack``: sign packing, unpacking, reordering and Marlin packing of the down factors, GB/s of
   bytes read plus written against 8 TB/s;
+* ``dense``: the fused decode step's final norm and lm_head (``nq_dense_gemv``, 32000 x 4096 fp16)
+  at batch 1 and 4 on cold weights, GB/s on the weight bytes against 8 TB/s;
 * ``decode_e2e``: greedy decode of a random-init Llama-2-7B-architecture model with every linear
   NanoQuant-factorised at 0.55 bpw (prompt 128, 256 new tokens, batch 1): the fused-linears step
   with attention in torch (the headline), the unfused step, the step whose q/k/v launch also
@@ -38,8 +40,9 @@ The JSON line carries:
 
 ``--floor`` prints the ``floor`` section alone; ``--sweep`` prints one line per config shape (GEMV
 at batch 1/4/16, GEMM at 256/2048); ``--batch-sweep`` the GEMV and the GEMM at batch 1..256 on the
-7B gate and down shapes (every config shape with ``--batch-sweep-shapes configs``); ``--gemv-only``, ``--decode-only`` (with ``--decode-variants``) and the
-``--skip-*`` switches narrow a run for kernel traces.
+7B gate and down shapes (every config shape with ``--batch-sweep-shapes configs``); ``--gemv-only``,
+``--decode-only`` (with ``--decode-variants``), ``--dense-only`` and the ``--skip-*`` switches narrow a
+run for kernel traces.
 Multi-GPU runs are not part of this build: ``--gpus`` above 1 exits with a message.
 """
 from __future__ import annotations
@@ -367,6 +370,46 @@ def bench_gemm(name, args, dev):
                          "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
                          "traffic": measured_traffic(f"gemm_{name}", (m, n, r, B))[0],
                          "traffic_unit": "HBM bytes per call (both launches)"}}, c, y
+
+
+def bench_dense(dev, copies=3):
+    """The decode step's lm_head as the fused step runs it: ``nq_dense_gemv`` with its RMS-norm prologue
+    and float32 logits, Llama-2-7B shapes (32000 x 4096 fp16), batch 1 and 4, over ``copies``
+    rotating weight copies (786 MB: more than the Infinity Cache holds, so every read is cold),
+    graph-replayed. GB/s on the weight bytes; the logits are checked against torch's RMS norm and
+    linear in float64 on the first copy."""
+    from nanoquant_amd import _lib
+    lib = _lib.load()
+    m, n, eps = 32000, 4096, 1e-5
+    gen = torch.Generator(device=dev).manual_seed(9)
+    stream = torch.cuda.Stream(device=dev)
+    ws = [(torch.randn(m, n, device=dev, generator=gen) * 0.02).half() for _ in range(copies)]
+    g = (torch.rand(n, device=dev, generator=gen) + 0.5).half()
+    out = {}
+    for B in (1, 4):
+        x = (torch.randn(B, n, device=dev, generator=gen) * 3.0).half()
+        y = torch.empty(B, m, device=dev, dtype=torch.float32)
+
+        def fn():
+            st = torch.cuda.current_stream().cuda_stream
+            for i in range(copies):
+                _lib.check(lib.nq_dense_gemv(_lib.NQ_F16, ws[i].data_ptr(), x.data_ptr(), g.data_ptr(), eps,
+                                             y.data_ptr(), 1, B, n, m, m, st), "dense gemv")
+        ms, graph, _ = steady_ms(fn, copies, stream, replays=16)
+        del graph
+        # the last replay's call was copy copies - 1; one more call on copy 0 for the check
+        _lib.check(lib.nq_dense_gemv(_lib.NQ_F16, ws[0].data_ptr(), x.data_ptr(), g.data_ptr(), eps, y.data_ptr(), 1,
+                                     B, n, m, m, torch.cuda.current_stream().cuda_stream), "dense gemv")
+        xn = (g * torch.nn.functional.rms_norm(x.float(), (n,), eps=eps).half()).double()
+        ref = xn @ ws[0].double().T
+        rel = float((y.double() - ref).abs().max() / ref.abs().max())
+        nbytes = m * n * 2
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[f"b{B}"] = {"us": round(ms * 1e3, 3), "weight_bytes": nbytes, "achieved": round(gbs, 1),
+                        "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "rel_err_vs_f64": rel}
+    out["what"] = ("lm_head of the fused decode step: RMS norm + 32000 x 4096 fp16 linear, float32 logits "
+                   f"(nq_dense_gemv), {copies} rotating weight copies")
+    return out
 
 
 def bench_pack(dev):
@@ -764,6 +807,7 @@ def main():
     ap.add_argument("--cpu-pack-seconds", type=float, default=3.0, help="bounded CPU sample per packer")
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--skip-decode", action="store_true", help="skip the end-to-end decode measurement")
+    ap.add_argument("--dense-only", action="store_true", help="measure the decode step's lm_head GEMV alone")
     ap.add_argument("--sweep", action="store_true",
                     help="measure GEMV (batch 1/4/16) and GEMM (batch 256/2048) on every config shape instead")
     ap.add_argument("--batch-sweep", action="store_true",
@@ -813,6 +857,9 @@ def main():
         return 0
     if args.floor:  # the launch and cold-read floor alone
         print(json.dumps({"floor": bench_floor(dev)}), flush=True)
+        return 0
+    if args.dense_only:  # profiling aid: only the decode step's lm_head GEMV
+        print(json.dumps({"dense": bench_dense(dev)}), flush=True)
         return 0
     if args.decode_only:  # profiling aid: only the end-to-end decode, reported on its own line
         log(f"[bench] decode e2e B={args.e2e_batch} prompt={args.e2e_prompt} new={args.e2e_new}")
@@ -869,6 +916,11 @@ def main():
         log(f"[bench] pack {json.dumps(pack)}")
         torch.cuda.empty_cache()
 
+    log("[bench] dense (lm_head)")
+    dense = bench_dense(dev)
+    log(f"[bench] dense {json.dumps(dense)}")
+    torch.cuda.empty_cache()
+
     decode = None
     if not args.skip_decode:
         log(f"[bench] decode e2e B={args.e2e_batch} prompt={args.e2e_prompt} new={args.e2e_new}")
@@ -912,6 +964,7 @@ def main():
         "floor": floor,
         "gemm": gemm,
         "pack": pack,
+        "dense": dense,
         "decode_e2e": decode,
         "cpu_baseline": cpu,
         "parity": {**parity, "gemv_graph_matches_eager": graph_ok, "bar": 1e-3},

@@ -320,8 +320,8 @@ int nq_rope_kv_write(int dtype, const void* qkv, int64_t qkv_stride, void* k_cac
  * fp32. fp32 sum, rounded once to dtype (overflow to +-inf as a torch linear does); with y_float32
  * the rounded values are stored widened to float32 (y then float [batch, ldy]), else y is dtype
  * rows of ldy >= m elements. n a multiple of 8, at most 32256; batch at most 65535. Each wave
- * streams one row of w with 8 KB of loads in flight, which is what reading a large w from HBM
- * takes. No counterpart in the reference, whose decode step runs the final norm and the lm_head as
+ * streams rows of w with the next 8 KB of loads in flight during the current row's arithmetic,
+ * which is what reading a large w from HBM takes. No counterpart in the reference, whose decode step runs the final norm and the lm_head as
  * torch ops (kernel/test_decode.py:387-394). */
 int nq_dense_gemv(int dtype, const void* w, const void* x, const void* norm_weight, float eps, void* y,
                   int y_float32, int64_t batch, int64_t n, int64_t m, int64_t ldy, nq_stream_t stream);

@@ -378,15 +378,16 @@ bool launch_attn_g(int g, const void* q, const void* k, const void* v, int64_t q
 // x itself or, with a norm weight g, its RMS norm as the decoder's torch path rounds it:
 // T(g[k] * T(x[k] * rsqrt(mean(x^2) + eps))) (mean and product in fp32). A decode step reaches its
 // lm_head after its layers have streamed their weights through the caches, so W comes from HBM, and
-// streaming it at speed takes many bytes in flight per CU: each wave owns one row of W and issues
-// every 16-byte load of a 4096-column group of it at once (8 per lane, non-temporal); the first
-// group's loads go out before the block stages its NB batch rows of x (or xn) in LDS, so their
-// latency covers the staging. Loads past the row's end read zeros (buffer resource bounds), so n
-// need only be a multiple of 8. Blocks hold 4 rows of W; grid.y covers the batch.
+// streaming it at speed takes many bytes in flight per CU: a wave takes RPW rows of W one after the
+// other and issues every 16-byte load of a 4096-column group at once (8 per lane, non-temporal),
+// the next group's (or next row's) before the current one's arithmetic; the first row's loads go
+// out before the block stages its NB batch rows of x (or xn) in LDS, so their latency covers the
+// staging, which serves the block's 4 RPW rows. Loads past the row's end read zeros (buffer resource
+// bounds), so n need only be a multiple of 8. grid.y covers the batch.
 constexpr int kDenseCols = 4096;      // columns of W a wave has in flight: 64 lanes x 8 x 8 elements
 constexpr int kDenseLdsBytes = 64512;  // staged rows of x, NB * n * 2 bytes: within 64 KB with the static part
 
-template <typename T, int NB, bool NORM>
+template <typename T, int NB, bool NORM, int RPW>
 __global__ __launch_bounds__(256) void dense_gemv_kernel(const uint16_t* __restrict__ w, const uint16_t* __restrict__ x,
                                                          const uint16_t* __restrict__ norm_w, float eps,
                                                          void* __restrict__ y, int y_f32, int m, int n, int batch,
@@ -396,13 +397,21 @@ __global__ __launch_bounds__(256) void dense_gemv_kernel(const uint16_t* __restr
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
-    const int row_out = static_cast<int>(blockIdx.x) * 4 + wave;
-    const int row = min(row_out, m - 1);  // every wave stages its share of x, so none leaves early
+    // wave w of the block takes rows row0 + 4 rr (rr < RPW), one after the other, the next row's
+    // loads in flight during the current row's arithmetic; every wave stages its share of x, so
+    // none leaves early
+    const int row0 = static_cast<int>(blockIdx.x) * 4 * RPW + wave;
     const int b0 = static_cast<int>(blockIdx.y) * NB;
-    const rsrc_t wr = make_rsrc(w + static_cast<size_t>(row) * static_cast<size_t>(n), static_cast<uint32_t>(n) * 2u);
-    u32x4 wv[8];
+    // the 8 loads of one 4096-column group of a row (rows past m read row m - 1 and store nothing)
+    auto issue = [&](u32x4 (&dst)[8], int row, int c0) {
+        const rsrc_t wr = make_rsrc(w + static_cast<size_t>(min(row, m - 1)) * static_cast<size_t>(n),
+                                    static_cast<uint32_t>(n) * 2u);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) wv[k] = load_b128_stream(wr, static_cast<uint32_t>((k * 64 + lane) * 16));
+        for (int k = 0; k < 8; ++k)
+            dst[k] = load_b128_stream(wr, static_cast<uint32_t>(c0 + (k * 64 + lane) * 8) * 2u);
+    };
+    u32x4 wv[8], wq[8];
+    issue(wv, row0, 0);
 
     // x's batch rows into LDS (16-byte chunks; every thread keeps to its own chunks throughout)
     const int chunks = n / 8;
@@ -458,36 +467,46 @@ __global__ __launch_bounds__(256) void dense_gemv_kernel(const uint16_t* __restr
     }
     __syncthreads();
 
-    float acc[NB];
+#pragma unroll 1
+    for (int rr = 0; rr < RPW; ++rr) {
+        const int row = row0 + 4 * rr;
+        float acc[NB];
 #pragma unroll
-    for (int b = 0; b < NB; ++b) acc[b] = 0.0f;
-    for (int c0 = 0; c0 < n; c0 += kDenseCols) {
-        if (c0 > 0) {
+        for (int b = 0; b < NB; ++b) acc[b] = 0.0f;
+        for (int c0 = 0; c0 < n; c0 += kDenseCols) {
+            // the next group's loads go out before this group's arithmetic: the rest of this row,
+            // else the start of the wave's next row
+            const bool next_group = c0 + kDenseCols < n;
+            const bool next_row = !next_group && rr + 1 < RPW;
+            if (next_group) issue(wq, row, c0 + kDenseCols);
+            else if (next_row) issue(wq, row + 4, 0);
 #pragma unroll
-            for (int k = 0; k < 8; ++k)
-                wv[k] = load_b128_stream(wr, static_cast<uint32_t>(c0 + (k * 64 + lane) * 8) * 2u);
+            for (int b = 0; b < NB; ++b) {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const int col = c0 + (k * 64 + lane) * 8;
+                    const u32x4 xv =
+                        col < n ? *reinterpret_cast<const u32x4*>(xs + b * n + col) : u32x4{0u, 0u, 0u, 0u};
+                    acc[b] = T::dot2(wv[k].x, xv.x, acc[b]);
+                    acc[b] = T::dot2(wv[k].y, xv.y, acc[b]);
+                    acc[b] = T::dot2(wv[k].z, xv.z, acc[b]);
+                    acc[b] = T::dot2(wv[k].w, xv.w, acc[b]);
+                }
+            }
+            if (next_group || next_row) {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) wv[k] = wq[k];
+            }
         }
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const int col = c0 + (k * 64 + lane) * 8;
-                const u32x4 xv = col < n ? *reinterpret_cast<const u32x4*>(xs + b * n + col) : u32x4{0u, 0u, 0u, 0u};
-                acc[b] = T::dot2(wv[k].x, xv.x, acc[b]);
-                acc[b] = T::dot2(wv[k].y, xv.y, acc[b]);
-                acc[b] = T::dot2(wv[k].z, xv.z, acc[b]);
-                acc[b] = T::dot2(wv[k].w, xv.w, acc[b]);
+            const float s = wave_sum(acc[b]);
+            if (lane == 0 && row < m && b0 + b < batch) {
+                const uint16_t v = T::from_float(s);
+                const size_t at = static_cast<size_t>(b0 + b) * static_cast<size_t>(ldy) + static_cast<size_t>(row);
+                if (y_f32) static_cast<float*>(y)[at] = T::to_float(v);
+                else static_cast<uint16_t*>(y)[at] = v;
             }
-        }
-    }
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-        const float s = wave_sum(acc[b]);
-        if (lane == 0 && row_out < m && b0 + b < batch) {
-            const uint16_t v = T::from_float(s);
-            const size_t at = static_cast<size_t>(b0 + b) * static_cast<size_t>(ldy) + static_cast<size_t>(row_out);
-            if (y_f32) static_cast<float*>(y)[at] = T::to_float(v);
-            else static_cast<uint16_t*>(y)[at] = v;
         }
     }
 }
@@ -499,15 +518,33 @@ inline int dense_rows_per_block(int64_t batch, int64_t n) {
     return nb;
 }
 
+// Rows of W per wave (each block stages x's batch rows once for 4 RPW rows of W). Same-box A/B on the
+// Llama-2-7B lm_head (32000 x 4096 fp16, norm prologue, float32 out, 3 rotating weight copies; us at
+// batch 1 / 2 / 4 / 8): one row per wave, every block staging x for its 4 rows, 44.5 / 60.4 / 133.6 /
+// 260.1; 4 rows 43.5 / 50.2 / 76.3 / 148.1; 8 rows 43.9 / 52.3 / 62.7 / 123.4. Taking a wave's rows
+// at once instead (each x chunk read from LDS feeding them all, no next-row prefetch) measured
+// slower: 4 rows 46.5 / 54.9 / 108.5 / 207.1.
+inline int dense_rows_per_wave(int64_t batch) { return batch >= 3 ? 8 : 4; }
+
+template <typename T, bool NORM, int NB>
+void launch_dense_rpw(int rpw, const uint16_t* w, const uint16_t* x, const uint16_t* g, float eps, void* y, int y_f32,
+                      int m, int n, int batch, int ldy, hipStream_t st) {
+    const dim3 grid(static_cast<unsigned>(ceil_div(m, 4 * rpw)), static_cast<unsigned>(ceil_div(batch, NB)));
+    const size_t lds = static_cast<size_t>(NB) * n * 2;
+    if (rpw == 8) dense_gemv_kernel<T, NB, NORM, 8><<<grid, 256, lds, st>>>(w, x, g, eps, y, y_f32, m, n, batch, ldy);
+    else if (rpw == 4) dense_gemv_kernel<T, NB, NORM, 4><<<grid, 256, lds, st>>>(w, x, g, eps, y, y_f32, m, n, batch, ldy);
+    else if (rpw == 2) dense_gemv_kernel<T, NB, NORM, 2><<<grid, 256, lds, st>>>(w, x, g, eps, y, y_f32, m, n, batch, ldy);
+    else dense_gemv_kernel<T, NB, NORM, 1><<<grid, 256, lds, st>>>(w, x, g, eps, y, y_f32, m, n, batch, ldy);
+}
+
 template <typename T, bool NORM>
 void launch_dense_gemv(const uint16_t* w, const uint16_t* x, const uint16_t* g, float eps, void* y, int y_f32, int m,
                        int n, int batch, int ldy, hipStream_t st) {
     const int nb = dense_rows_per_block(batch, n);
-    const dim3 grid(static_cast<unsigned>(ceil_div(m, 4)), static_cast<unsigned>(ceil_div(batch, nb)));
-    const size_t lds = static_cast<size_t>(nb) * n * 2;
-    if (nb == 4) dense_gemv_kernel<T, 4, NORM><<<grid, 256, lds, st>>>(w, x, g, eps, y, y_f32, m, n, batch, ldy);
-    else if (nb == 2) dense_gemv_kernel<T, 2, NORM><<<grid, 256, lds, st>>>(w, x, g, eps, y, y_f32, m, n, batch, ldy);
-    else dense_gemv_kernel<T, 1, NORM><<<grid, 256, lds, st>>>(w, x, g, eps, y, y_f32, m, n, batch, ldy);
+    const int rpw = dense_rows_per_wave(batch);
+    if (nb == 4) launch_dense_rpw<T, NORM, 4>(rpw, w, x, g, eps, y, y_f32, m, n, batch, ldy, st);
+    else if (nb == 2) launch_dense_rpw<T, NORM, 2>(rpw, w, x, g, eps, y, y_f32, m, n, batch, ldy, st);
+    else launch_dense_rpw<T, NORM, 1>(rpw, w, x, g, eps, y, y_f32, m, n, batch, ldy, st);
 }
 
 }  // namespace

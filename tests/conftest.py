@@ -10,6 +10,7 @@ if ROOT not in sys.path:
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) and the built HIP library")
+    config.addinivalue_line("filterwarnings", "ignore:ComplexHalf support is experimental:UserWarning")
 
 
 def _gpu_available() -> bool:
