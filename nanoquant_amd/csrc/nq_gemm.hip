@@ -191,8 +191,8 @@ int launch_onebit(const void* A, const uint32_t* W, const void* s_in, const void
 // ------------------------------------------------------------------ LDS-DMA natural-k kernel
 //
 // The natural-k product with every operand of a 64-k step fetched by global_load_lds (16 bytes
-// a lane for the A tile, 4 for sign words and s_in) straight into one of three LDS buffers,
-// two steps ahead, so no register holds a tile in flight. A wave's DMA writes 64 consecutive
+// a lane for the A tile, 4 for sign words and s_in) straight into one of NBUF LDS buffers (three
+// to eight), NBUF - 1 steps ahead, so no register holds a tile in flight. A wave's DMA writes 64 consecutive
 // LDS slots, so the A tile is unpadded (128-byte rows) and bank conflicts are avoided by where
 // each lane fetches from: LDS chunk p of row r holds the row's 16-byte chunk p ^ ((r / 2) % 8). s_in
 // is fetched in the order the operands read it (every wave keeps its own copy, so every wave
@@ -210,7 +210,7 @@ int launch_onebit(const void* A, const uint32_t* W, const void* s_in, const void
 // split_steps steps, and each block stores its raw fp32 sums to its plane of `part`
 // [splits][M][N]; gemm_split_finish_kernel adds the planes in order and applies the epilogue.
 template <typename T, bool kSin, bool kSout, int BP, int BQ, int WP, int WQ, int WPE, int KS, bool kSplit,
-          int BKK = 64>
+          int NBUF = 3, int BKK = 64>
 __global__ __launch_bounds__((BP / WP) * (BQ / WQ) * 64 * KS) __attribute__((amdgpu_waves_per_eu(WPE)))
 void gemm_dm_kernel(
     const uint16_t* __restrict__ A, const uint32_t* __restrict__ W, const uint16_t* __restrict__ s_in,
@@ -243,15 +243,16 @@ void gemm_dm_kernel(
     static_assert(WP % 64 == 0 && BP % 64 == 0, "features come in whole 64-feature word groups");
     static_assert(KS == 1 || KS == 2 || KS == 4, "one, two or four k groups");
     static_assert(!kSplit || (KS == 1 && !kSout), "a k range of the grid is one wave group, scaled later");
-    __shared__ __attribute__((aligned(16))) uint16_t xsall[3][KS][BQ * BKK];
+    // NBUF step buffers, each step's DMAs issued NBUF - 1 steps ahead
+    static_assert(NBUF >= 3 && (NBUF - 2) * kIssued < 64, "the DMAs in flight fit the 6-bit vmcnt");
+    __shared__ __attribute__((aligned(16))) uint16_t xsall[NBUF][KS][BQ * BKK];
     auto& xs0 = xsall[0];
     auto& xs1 = xsall[1];
-    auto& xs2 = xsall[2];
-    __shared__ __attribute__((aligned(16))) uint32_t ws0[KS][WWORDS], ws1[KS][WWORDS], ws2[KS][WWORDS];
-    __shared__ __attribute__((aligned(16))) uint32_t ss0[kSin ? NT : 4], ss1[kSin ? NT : 4], ss2[kSin ? NT : 4];
+    __shared__ __attribute__((aligned(16))) uint32_t wsall[NBUF][KS][WWORDS];
+    __shared__ __attribute__((aligned(16))) uint32_t ssall[NBUF][kSin ? NT : 4];
     __shared__ float red_arr[KS == 2 ? kAcc * NTG : 1];
     // with four groups one group's sums at a time pass through the step buffers, free by then
-    static_assert(KS != 4 || 3 * KS * BQ * BKK * 2 >= kAcc * NTG * 4, "the step buffers hold one group's sums");
+    static_assert(KS != 4 || NBUF * KS * BQ * BKK * 2 >= kAcc * NTG * 4, "the step buffers hold one group's sums");
     float* red = KS == 4 ? reinterpret_cast<float*>(&xsall[0][0][0]) : red_arr;
     __shared__ uint16_t sos[BP];
 
@@ -329,18 +330,13 @@ void gemm_dm_kernel(
 #pragma unroll
     for (int j = 0; j < WPT; ++j) wsrcb[j] = 4u * wsrc[j];
     const uint32_t sidxb = 4u * static_cast<uint32_t>(sidx);
-    // LDS byte addresses of this wave's DMA destinations in each of the three step buffers
-    uint32_t lx[3], lw[3], ls[3];
-    {
-        const void* xb[3] = {xs0[grp], xs1[grp], xs2[grp]};
-        const void* wb[3] = {ws0[grp], ws1[grp], ws2[grp]};
-        const void* sb[3] = {ss0, ss1, ss2};
+    // LDS byte addresses of this wave's DMA destinations in each step buffer
+    uint32_t lx[NBUF], lw[NBUF], ls[NBUF];
 #pragma unroll
-        for (int b = 0; b < 3; ++b) {
-            lx[b] = __builtin_amdgcn_readfirstlane(lds_addr(xb[b]) + static_cast<uint32_t>(gw) * 1024u);
-            lw[b] = __builtin_amdgcn_readfirstlane(lds_addr(wb[b]) + static_cast<uint32_t>(gw) * 256u);
-            ls[b] = __builtin_amdgcn_readfirstlane(lds_addr(sb[b]) + static_cast<uint32_t>(wave) * 256u);
-        }
+    for (int b = 0; b < NBUF; ++b) {
+        lx[b] = __builtin_amdgcn_readfirstlane(lds_addr(xsall[b][grp]) + static_cast<uint32_t>(gw) * 1024u);
+        lw[b] = __builtin_amdgcn_readfirstlane(lds_addr(wsall[b][grp]) + static_cast<uint32_t>(gw) * 256u);
+        ls[b] = __builtin_amdgcn_readfirstlane(lds_addr(ssall[b]) + static_cast<uint32_t>(wave) * 256u);
     }
     auto issue = [&](int iter, int b) {
         const uint32_t k0 = static_cast<uint32_t>((k_first + iter) * BKK);
@@ -397,11 +393,15 @@ void gemm_dm_kernel(
             for (int tq = 0; tq < TQ; ++tq) acc[tp][tq] = mfma32x32x16<T>(a, f.x[tq], acc[tp][tq]);
         }
     };
-    // One step: DMA step it + 2 into the buffer step it - 1 used, run the MFMAs of step it (each k
-    // tile's reads issued before the previous tile's MFMAs), wait for this wave's DMAs of step
-    // it + 1, barrier. The tail re-fetches the last step into the free buffer.
-    auto step = [&](const uint16_t* xc, const uint32_t* wc, const uint32_t* sc, int bf, int it) {
-        issue(min(it + 2, k_iters - 1), bf);
+    // One step out of buffer b: DMA step it + NBUF - 1 into the buffer step it - 1 used, run the
+    // MFMAs of step it (each k tile's reads issued before the previous tile's MFMAs), wait for this
+    // wave's DMAs of step it + 1, barrier. The tail re-fetches the last step into free buffers, so
+    // that every step issues the same DMAs.
+    auto step = [&](int b, int it) {
+        const uint16_t* xc = xsall[b][grp];
+        const uint32_t* wc = wsall[b][grp];
+        const uint32_t* sc = ssall[b];
+        issue(min(it + NBUF - 1, k_iters - 1), (b + NBUF - 1) % NBUF);
         __builtin_amdgcn_sched_barrier(0);  // the DMAs go out first, not after the step's MFMAs
         Frag f[2];
         read_kt(f[0], xc, wc, sc, 0);
@@ -410,18 +410,12 @@ void gemm_dm_kernel(
             if (kt + 1 < KT) read_kt(f[(kt + 1) & 1], xc, wc, sc, kt + 1);
             compute_kt(f[kt & 1]);
         }
-        wait_vmcnt<kIssued>();
+        wait_vmcnt<(NBUF - 2) * kIssued>();
         barrier_keep_dma();
     };
 
-    uint16_t* x0 = xs0[grp];
-    uint16_t* x1 = xs1[grp];
-    uint16_t* x2 = xs2[grp];
-    uint32_t* w0 = ws0[grp];
-    uint32_t* w1 = ws1[grp];
-    uint32_t* w2 = ws2[grp];
-    issue(0, 0);
-    issue(min(1, k_iters - 1), 1);
+#pragma unroll
+    for (int b = 0; b + 1 < NBUF; ++b) issue(min(b, k_iters - 1), b);
     if (k_trim) {
         int last = -1;  // the last nonzero entry this thread holds (zeros past K)
 #pragma unroll
@@ -435,7 +429,7 @@ void gemm_dm_kernel(
         for (int off = 32; off > 0; off >>= 1) last = max(last, __shfl_xor(last, off, 64));
         if (lane == 0) klast[wave] = last;
     }
-    wait_vmcnt<kIssued>();
+    wait_vmcnt<(NBUF - 2) * kIssued>();
     __syncthreads();
     if (k_trim) {
         int last = -1;
@@ -444,15 +438,13 @@ void gemm_dm_kernel(
         k_iters = max(1, min(k_iters, (last + BKK) / BKK));  // steps up to the one holding `last`
     }
     int it = 0;
-    for (; it + 3 <= k_iters; it += 3) {
-        step(x0, w0, ss0, 2, it);
-        step(x1, w1, ss1, 0, it + 1);
-        step(x2, w2, ss2, 1, it + 2);
+    for (; it + NBUF <= k_iters; it += NBUF) {
+#pragma unroll
+        for (int b = 0; b < NBUF; ++b) step(b, it + b);
     }
-    if (it < k_iters) {
-        step(x0, w0, ss0, 2, it);
-        if (it + 1 < k_iters) step(x1, w1, ss1, 0, it + 1);
-    }
+#pragma unroll
+    for (int b = 0; b + 1 < NBUF; ++b)
+        if (it + b < k_iters) step(b, it + b);
     wait_vmcnt<0>();  // the tail's re-fetches land before the block's LDS is reused or released
 
     if (KS == 4) {  // groups 1, 2 and 3 join group 0's sums in that order (deterministic)
@@ -580,7 +572,7 @@ void gemm_dm_kernel(
         }
 }
 
-template <typename T, int BP, int BQ, int WP, int WQ, int WPE, int KS>
+template <typename T, int BP, int BQ, int WP, int WQ, int WPE, int KS, int NBUF = 3>
 void launch_dm(const void* A, const uint32_t* W, const void* s_in, const void* s_out, void* C, int64_t M, int64_t K,
                int64_t N, hipStream_t stream, const void* k_scale = nullptr) {
     const auto* ksc = static_cast<const uint16_t*>(k_scale);
@@ -594,16 +586,16 @@ void launch_dm(const void* A, const uint32_t* W, const void* s_in, const void* s
     auto* c = static_cast<uint16_t*>(C);
     const int m = static_cast<int>(M), k = static_cast<int>(K), n = static_cast<int>(N);
     if (s_in && s_out)
-        gemm_dm_kernel<T, true, true, BP, BQ, WP, WQ, WPE, KS, false>
+        gemm_dm_kernel<T, true, true, BP, BQ, WP, WQ, WPE, KS, false, NBUF>
             <<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles, p_tiles, nullptr, 0, ksc);
     else if (s_in)
-        gemm_dm_kernel<T, true, false, BP, BQ, WP, WQ, WPE, KS, false>
+        gemm_dm_kernel<T, true, false, BP, BQ, WP, WQ, WPE, KS, false, NBUF>
             <<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles, p_tiles, nullptr, 0, ksc);
     else if (s_out)
-        gemm_dm_kernel<T, false, true, BP, BQ, WP, WQ, WPE, KS, false>
+        gemm_dm_kernel<T, false, true, BP, BQ, WP, WQ, WPE, KS, false, NBUF>
             <<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles, p_tiles, nullptr, 0, ksc);
     else
-        gemm_dm_kernel<T, false, false, BP, BQ, WP, WQ, WPE, KS, false>
+        gemm_dm_kernel<T, false, false, BP, BQ, WP, WQ, WPE, KS, false, NBUF>
             <<<grid, NT, 0, stream>>>(a, W, si, so, c, m, k, n, q_tiles, p_tiles, nullptr, 0, ksc);
 }
 
@@ -648,7 +640,7 @@ __global__ __launch_bounds__(256) void gemm_split_finish_kernel(const float* __r
 
 // K split over `splits` ranges of the grid: the ranges' raw sums into part [splits][M][N] fp32,
 // then the finishing launch.
-template <typename T, int BP, int BQ, int WP, int WQ, int WPE>
+template <typename T, int BP, int BQ, int WP, int WQ, int WPE, int NBUF = 3>
 void launch_dm_split(const void* A, const uint32_t* W, const void* s_in, const void* s_out, void* C, int64_t M,
                      int64_t K, int64_t N, float* part, int splits, int split_steps, hipStream_t stream) {
     const int q_tiles = static_cast<int>(ceil_div(M, BQ));
@@ -661,10 +653,10 @@ void launch_dm_split(const void* A, const uint32_t* W, const void* s_in, const v
     auto* c = static_cast<uint16_t*>(C);
     const int m = static_cast<int>(M), k = static_cast<int>(K), n = static_cast<int>(N);
     if (s_in)
-        gemm_dm_kernel<T, true, false, BP, BQ, WP, WQ, WPE, 1, true>
+        gemm_dm_kernel<T, true, false, BP, BQ, WP, WQ, WPE, 1, true, NBUF>
             <<<grid, NT, 0, stream>>>(a, W, si, nullptr, c, m, k, n, q_tiles, p_tiles, part, split_steps, nullptr);
     else
-        gemm_dm_kernel<T, false, false, BP, BQ, WP, WQ, WPE, 1, true>
+        gemm_dm_kernel<T, false, false, BP, BQ, WP, WQ, WPE, 1, true, NBUF>
             <<<grid, NT, 0, stream>>>(a, W, nullptr, nullptr, c, m, k, n, q_tiles, p_tiles, part, split_steps, nullptr);
     const int64_t quads = M * (N / 4);
     const dim3 fgrid(static_cast<unsigned>(ceil_div(quads, 256)));
@@ -703,6 +695,16 @@ void launch_dm_split(const void* A, const uint32_t* W, const void* s_in, const v
 constexpr int64_t kSplitTarget = 256;    // blocks a split grid aims at (one per CU; two for long K)
 constexpr int64_t kSplitMinSteps = 8;    // 64-k steps of the shortest range
 constexpr int64_t kSplitLongSteps = 128; // beyond this many steps K counts as long
+// Step buffers (the DMAs of a step go out that many steps less one ahead): three, except K over
+// two wave groups on 64-row tiles (four: 152 KB of LDS with the groups' hand-over) and ranges of 16
+// or more steps split across the grid on 32-row tiles (eight). Interleaved same-box A/B through the
+// op, fp16, bit-identical, minimum of 8 rounds: B = 256 gate 30.7 -> 29.5 us (each of the two
+// changes alone about half of it), Llama-3-70B gate 83.2 -> 80.3; every other Llama-2-7B and
+// Llama-3-70B cell at B = 64-2048 within 1%. Deeper buffers elsewhere measured no better (B = 2048
+// stage 2 within 0.5%) or slower (the long-K split on 64-row tiles at six or eight: B = 256 down
+// 36.0 -> 37.1 / 40.3 us, two blocks a CU no longer fitting at eight; ten-step ranges at eight:
+// B = 128 down 34.5 -> 35.0).
+constexpr int kBufGroups = 4, kBufSplit32Long = 8, kSplit32LongSteps = 16;
 enum GemmMode { kModeOnebit, kModeTile, kModeTile128, kModeGroups, kModeGroups32, kModeSplit, kModeSplit32 };
 struct GemmPlan {
     GemmMode mode = kModeOnebit;
@@ -766,7 +768,7 @@ int launch_gemm(const char* name, const void* A, const uint32_t* W, const void* 
             if ((K / 64) % 4 == 0 && K / 64 >= 128)
                 launch_dm<T, 256, 64, 64, 64, 4, 4>(A, W, s_in, s_out, C, M, K, N, stream);
             else
-                launch_dm<T, 256, 64, 64, 64, 2, 2>(A, W, s_in, s_out, C, M, K, N, stream);
+                launch_dm<T, 256, 64, 64, 64, 2, 2, kBufGroups>(A, W, s_in, s_out, C, M, K, N, stream);
             break;
         case kModeGroups32:
             launch_dm<T, 256, 32, 64, 32, 2, 2>(A, W, s_in, s_out, C, M, K, N, stream);
@@ -776,8 +778,12 @@ int launch_gemm(const char* name, const void* A, const uint32_t* W, const void* 
                                                    p.splits, p.split_steps, stream);
             break;
         case kModeSplit32:
-            launch_dm_split<T, 256, 32, 64, 32, 2>(A, W, s_in, s_out, C, M, K, N, static_cast<float*>(workspace),
-                                                   p.splits, p.split_steps, stream);
+            if (p.split_steps >= kSplit32LongSteps)
+                launch_dm_split<T, 256, 32, 64, 32, 2, kBufSplit32Long>(
+                    A, W, s_in, s_out, C, M, K, N, static_cast<float*>(workspace), p.splits, p.split_steps, stream);
+            else
+                launch_dm_split<T, 256, 32, 64, 32, 2>(A, W, s_in, s_out, C, M, K, N, static_cast<float*>(workspace),
+                                                       p.splits, p.split_steps, stream);
             break;
     }
     return check_launch(name);
