@@ -206,9 +206,12 @@ int launch_onebit(const void* A, const uint32_t* W, const void* s_in, const void
 // With KS = 2 the block holds two groups of waves with buffers of their own, each over half of
 // the k steps (for outputs too few to give every SIMD two waves); group 1 hands its accumulators
 // to group 0 through LDS at the end. With KS = 4 (long K) four groups each take a quarter of the
-// steps and hand their sums to group 0 one group at a time through the step buffers. With kSplit the grid repeats the tiles once per k range of
-// split_steps steps, and each block stores its raw fp32 sums to its plane of `part`
-// [splits][M][N]; gemm_split_finish_kernel adds the planes in order and applies the epilogue.
+// steps and hand their sums to group 0 one group at a time through the step buffers. With kSplit
+// the grid repeats the tiles once per k range of split_steps steps, and each block stores its raw
+// fp32 sums to its plane of `part` [splits][M][N]; gemm_split_finish_kernel adds the planes in
+// order and applies the epilogue. A k range may also be shared by KS groups: contiguous runs of
+// steps, the first len % KS groups one step longer; every group runs as many steps as the
+// longest (the block's barriers are common), a shorter group's last one without its MFMAs.
 template <typename T, bool kSin, bool kSout, int BP, int BQ, int WP, int WQ, int WPE, int KS, bool kSplit,
           int NBUF = 3, int BKK = 64>
 __global__ __launch_bounds__((BP / WP) * (BQ / WQ) * 64 * KS) __attribute__((amdgpu_waves_per_eu(WPE)))
@@ -242,7 +245,7 @@ void gemm_dm_kernel(
     static_assert(XCH % NTG == 0 && WWORDS % NTG == 0, "tile pieces must divide evenly");
     static_assert(WP % 64 == 0 && BP % 64 == 0, "features come in whole 64-feature word groups");
     static_assert(KS == 1 || KS == 2 || KS == 4, "one, two or four k groups");
-    static_assert(!kSplit || (KS == 1 && !kSout), "a k range of the grid is one wave group, scaled later");
+    static_assert(!kSplit || !kSout, "k ranges of the grid are scaled later");
     // NBUF step buffers, each step's DMAs issued NBUF - 1 steps ahead
     static_assert(NBUF >= 3 && (NBUF - 2) * kIssued < 64, "the DMAs in flight fit the 6-bit vmcnt");
     __shared__ __attribute__((aligned(16))) uint16_t xsall[NBUF][KS][BQ * BKK];
@@ -275,8 +278,23 @@ void gemm_dm_kernel(
     const uint32_t half_n = static_cast<uint32_t>(N) >> 1;
     // steps of this block's k group or k range (the host makes K / 64 divide by KS and leaves no
     // k range empty), and the first of them
-    int k_iters = kSplit ? min(split_steps, K / BKK - split * split_steps) : K / BKK / KS;
-    const int k_first = kSplit ? split * split_steps : grp * k_iters;
+    // steps of this wave group (k_iters), the first of them (k_first) and the steps every group of
+    // the block runs (k_all). Without kSplit the host makes K / 64 divide by KS. With it, a k range
+    // holds len >= 1 steps (the host leaves none empty); with len < KS a group gets none, and its
+    // DMAs, clamped to step k_iters - 1 = -1 of its run, re-fetch the range's last step.
+    int k_iters, k_first, k_all;
+    if (kSplit) {
+        const int r0 = split * split_steps;
+        const int len = min(split_steps, K / BKK - r0);
+        const int q = len / KS, rem = len % KS;
+        k_iters = q + (grp < rem ? 1 : 0);
+        k_first = r0 + grp * q + min(grp, rem);
+        k_all = q + (rem > 0 ? 1 : 0);
+    } else {
+        k_iters = K / BKK / KS;
+        k_first = grp * k_iters;
+        k_all = k_iters;
+    }
     // k_scale (one block over all of K, K <= 32 * NT): A's columns whose k_scale entry is zero are
     // exact zeros (the previous stage multiplied them by it; the padded rank of the NanoQuant
     // factorisation), so the 64-k steps after the last nonzero entry add nothing and are not run.
@@ -403,12 +421,14 @@ void gemm_dm_kernel(
         const uint32_t* sc = ssall[b];
         issue(min(it + NBUF - 1, k_iters - 1), (b + NBUF - 1) % NBUF);
         __builtin_amdgcn_sched_barrier(0);  // the DMAs go out first, not after the step's MFMAs
-        Frag f[2];
-        read_kt(f[0], xc, wc, sc, 0);
+        if (!(kSplit && KS > 1) || it < k_iters) {  // uniform over the wave group
+            Frag f[2];
+            read_kt(f[0], xc, wc, sc, 0);
 #pragma unroll
-        for (int kt = 0; kt < KT; ++kt) {
-            if (kt + 1 < KT) read_kt(f[(kt + 1) & 1], xc, wc, sc, kt + 1);
-            compute_kt(f[kt & 1]);
+            for (int kt = 0; kt < KT; ++kt) {
+                if (kt + 1 < KT) read_kt(f[(kt + 1) & 1], xc, wc, sc, kt + 1);
+                compute_kt(f[kt & 1]);
+            }
         }
         wait_vmcnt<(NBUF - 2) * kIssued>();
         barrier_keep_dma();
@@ -436,15 +456,16 @@ void gemm_dm_kernel(
 #pragma unroll
         for (int w = 0; w < NT / 64; ++w) last = max(last, klast[w]);
         k_iters = max(1, min(k_iters, (last + BKK) / BKK));  // steps up to the one holding `last`
+        k_all = k_iters;
     }
     int it = 0;
-    for (; it + NBUF <= k_iters; it += NBUF) {
+    for (; it + NBUF <= k_all; it += NBUF) {
 #pragma unroll
         for (int b = 0; b < NBUF; ++b) step(b, it + b);
     }
 #pragma unroll
     for (int b = 0; b + 1 < NBUF; ++b)
-        if (it + b < k_iters) step(b, it + b);
+        if (it + b < k_all) step(b, it + b);
     wait_vmcnt<0>();  // the tail's re-fetches land before the block's LDS is reused or released
 
     if (KS == 4) {  // groups 1, 2 and 3 join group 0's sums in that order (deterministic)
@@ -638,25 +659,25 @@ __global__ __launch_bounds__(256) void gemm_split_finish_kernel(const float* __r
     *reinterpret_cast<uint2*>(C + static_cast<size_t>(q) * N + o) = v;
 }
 
-// K split over `splits` ranges of the grid: the ranges' raw sums into part [splits][M][N] fp32,
-// then the finishing launch.
-template <typename T, int BP, int BQ, int WP, int WQ, int WPE, int NBUF = 3>
+// K split over `splits` ranges of the grid, each range over KS wave groups of a block: the
+// ranges' raw sums into part [splits][M][N] fp32, then the finishing launch.
+template <typename T, int BP, int BQ, int WP, int WQ, int WPE, int NBUF = 3, int KS = 1>
 void launch_dm_split(const void* A, const uint32_t* W, const void* s_in, const void* s_out, void* C, int64_t M,
                      int64_t K, int64_t N, float* part, int splits, int split_steps, hipStream_t stream) {
     const int q_tiles = static_cast<int>(ceil_div(M, BQ));
     const int p_tiles = static_cast<int>(ceil_div(N, BP));
     const dim3 grid(static_cast<unsigned>(q_tiles * p_tiles * splits));
-    constexpr int NT = (BP / WP) * (BQ / WQ) * 64;
+    constexpr int NT = (BP / WP) * (BQ / WQ) * 64 * KS;
     const auto* a = static_cast<const uint16_t*>(A);
     const auto* si = static_cast<const uint16_t*>(s_in);
     const auto* so = static_cast<const uint16_t*>(s_out);
     auto* c = static_cast<uint16_t*>(C);
     const int m = static_cast<int>(M), k = static_cast<int>(K), n = static_cast<int>(N);
     if (s_in)
-        gemm_dm_kernel<T, true, false, BP, BQ, WP, WQ, WPE, 1, true, NBUF>
+        gemm_dm_kernel<T, true, false, BP, BQ, WP, WQ, WPE, KS, true, NBUF>
             <<<grid, NT, 0, stream>>>(a, W, si, nullptr, c, m, k, n, q_tiles, p_tiles, part, split_steps, nullptr);
     else
-        gemm_dm_kernel<T, false, false, BP, BQ, WP, WQ, WPE, 1, true, NBUF>
+        gemm_dm_kernel<T, false, false, BP, BQ, WP, WQ, WPE, KS, true, NBUF>
             <<<grid, NT, 0, stream>>>(a, W, nullptr, nullptr, c, m, k, n, q_tiles, p_tiles, part, split_steps, nullptr);
     const int64_t quads = M * (N / 4);
     const dim3 fgrid(static_cast<unsigned>(ceil_div(quads, 256)));
@@ -689,9 +710,10 @@ void launch_dm_split(const void* A, const uint32_t* W, const void* s_in, const v
 //     workspace, then a finishing launch. Up to 128 steps: about one block per CU, on 32-row tiles
 //     below 64 tiles of 64 rows (B = 256, K = 4096, N = 1792: 8 ranges of 28 tiles 19.6 us -> 4
 //     ranges of 56 tiles 15.8 us; B = 2048, K = 8192, N = 512: 8 ranges 34.6 -> 4 ranges 30.2 us).
-//     Longer K: about two blocks per CU on 64-row tiles (B = 256, K = 28672, N = 3584: 9 ranges of
-//     56 tiles 66.8 us, against 93.2 us for 2 ranges of 112 32-row tiles). Without that workspace,
-//     as the grid's K groups above.
+//     Longer K: one block of four wave groups per CU on 32-row tiles while its ranges hold at most
+//     96 steps (below), else about two blocks per CU on 64-row tiles (B = 256, K = 28672, N = 3584:
+//     9 ranges of 56 tiles 66.8 us, against 93.2 us for 2 ranges of 112 32-row tiles in one wave
+//     group). Without that workspace, as the grid's K groups above.
 constexpr int64_t kSplitTarget = 256;    // blocks a split grid aims at (one per CU; two for long K)
 constexpr int64_t kSplitMinSteps = 8;    // 64-k steps of the shortest range
 constexpr int64_t kSplitLongSteps = 128; // beyond this many steps K counts as long
@@ -705,7 +727,25 @@ constexpr int64_t kSplitLongSteps = 128; // beyond this many steps K counts as l
 // 36.0 -> 37.1 / 40.3 us, two blocks a CU no longer fitting at eight; ten-step ranges at eight:
 // B = 128 down 34.5 -> 35.0).
 constexpr int kBufGroups = 4, kBufSplit32Long = 8, kSplit32LongSteps = 16;
-enum GemmMode { kModeOnebit, kModeTile, kModeTile128, kModeGroups, kModeGroups32, kModeSplit, kModeSplit32 };
+// Long K on small grids: 32-row tiles, one block of 16 waves per CU, each k range over four wave
+// groups, when the ranges hold at most kSplitGroupMaxSteps steps (each group at least
+// kSplitGroupMinSteps). It writes a quarter to a half of the fp32 partials of the 64-row plan
+// below (7B down_proj at B = 256: 4 ranges, 7.3 MB, against 18 ranges, 33 MB). Interleaved same-box
+// A/B through the op, fp16: Llama-2-7B down_proj at 0.55 bpw B = 256 33.9 -> 29.1 us, B = 128 34.1
+// -> 28.9, B = 64 26.8 -> 24.0, at 1.0 bpw B = 256 42.4 -> 40.3 (2 ranges of 86 steps). With 224-step
+// ranges (Llama-3-70B down_proj at B = 256) it was slower, 74.4 -> 78.4 and 66.1 -> 71.9 (mixed
+// rank): there the 64-row tiles' MFMA efficiency outweighs the partials' traffic.
+constexpr int64_t kSplitGroupMinSteps = 4, kSplitGroupMaxSteps = 96;
+enum GemmMode {
+    kModeOnebit,
+    kModeTile,
+    kModeTile128,
+    kModeGroups,
+    kModeGroups32,
+    kModeSplit,
+    kModeSplit32,
+    kModeSplitGroups32
+};
 struct GemmPlan {
     GemmMode mode = kModeOnebit;
     int splits = 1;
@@ -730,6 +770,18 @@ GemmPlan plan_gemm(int64_t M, int64_t K, int64_t N) {
     }
     if (tiles >= 128) return p;
     const bool long_k = steps > kSplitLongSteps;
+    if (long_k) {  // 32-row tiles, a block per CU, each k range over four wave groups
+        const int64_t want = std::min<int64_t>(kSplitTarget / tiles32, steps / (4 * kSplitGroupMinSteps));
+        if (want >= 2 && ceil_div(steps, want) <= kSplitGroupMaxSteps) {
+            p.split_steps = static_cast<int>(ceil_div(steps, want));
+            p.splits = static_cast<int>(ceil_div(steps, p.split_steps));
+            if (p.splits >= 2) {
+                p.mode = kModeSplitGroups32;
+                p.workspace_bytes = static_cast<size_t>(p.splits) * static_cast<size_t>(M) * static_cast<size_t>(N) * 4;
+                return p;
+            }
+        }
+    }
     const bool rows32 = !long_k && tiles < 64;
     const int64_t grid_tiles = rows32 ? tiles32 : tiles;
     const int64_t want = std::min<int64_t>((long_k ? 2 : 1) * kSplitTarget / grid_tiles, steps / kSplitMinSteps);
@@ -749,7 +801,7 @@ int launch_gemm(const char* name, const void* A, const uint32_t* W, const void* 
                 const void* k_scale = nullptr) {
     GemmPlan p = plan_gemm(M, K, N);
     if (p.mode != kModeOnebit && !aligned(C, 16)) p.mode = kModeOnebit;
-    if ((p.mode == kModeSplit || p.mode == kModeSplit32) &&
+    if ((p.mode == kModeSplit || p.mode == kModeSplit32 || p.mode == kModeSplitGroups32) &&
         (!workspace || workspace_bytes < p.workspace_bytes || !aligned(workspace, 16)))
         p.mode = (K / 64) % 2 == 0 ? kModeGroups : kModeTile;
     switch (p.mode) {
@@ -784,6 +836,10 @@ int launch_gemm(const char* name, const void* A, const uint32_t* W, const void* 
             else
                 launch_dm_split<T, 256, 32, 64, 32, 2>(A, W, s_in, s_out, C, M, K, N, static_cast<float*>(workspace),
                                                        p.splits, p.split_steps, stream);
+            break;
+        case kModeSplitGroups32:
+            launch_dm_split<T, 256, 32, 64, 32, 4, 3, 4>(A, W, s_in, s_out, C, M, K, N, static_cast<float*>(workspace),
+                                                         p.splits, p.split_steps, stream);
             break;
     }
     return check_launch(name);

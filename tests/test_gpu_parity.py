@@ -539,9 +539,13 @@ def test_gemm_onebit_scale_variants(nq, scales, K):
     assert err <= 1e-3, err
 
 
-# 72 tiles of 64 rows with an odd 65 steps (so no split over wave groups) split on 64-row tiles
-@pytest.mark.parametrize("B,K,N", [(256, 4096, 1280), (100, 11008, 512), (1100, 4160, 1024)],
-                         ids=["b256_k4096_rows32", "b100_k11008_long_k", "b1100_k4160_rows64"])
+# Plans: 40 tiles of 32 rows in 6 ranges; long K (172 steps) in 10 ranges of 18 steps, each over four
+# wave groups of 5, 5, 4 and 4 steps, on a partial row tile; 72 tiles of 64 rows with an odd 65 steps
+# (so no split over wave groups) split on 64-row tiles; 257 steps in 16 ranges of 17 and a last range
+# of 2, so two of its four wave groups run no step of their own
+@pytest.mark.parametrize("B,K,N", [(256, 4096, 1280), (100, 11008, 512), (1100, 4160, 1024), (64, 16448, 512)],
+                         ids=["b256_k4096_rows32", "b100_k11008_long_k", "b1100_k4160_rows64",
+                              "b64_k16448_short_last_range"])
 def test_gemm_split_k(nq, B, K, N):
     """Small grids split K across blocks (fp32 planes in the workspace the op allocates, added
     by a finishing launch); the same call through the C ABI without a workspace runs unsplit.
