@@ -710,8 +710,9 @@ void launch_dm_split(const void* A, const uint32_t* W, const void* s_in, const v
 //     workspace, then a finishing launch. Up to 128 steps: about one block per CU, on 32-row tiles
 //     below 64 tiles of 64 rows (B = 256, K = 4096, N = 1792: 8 ranges of 28 tiles 19.6 us -> 4
 //     ranges of 56 tiles 15.8 us; B = 2048, K = 8192, N = 512: 8 ranges 34.6 -> 4 ranges 30.2 us).
-//     Longer K: one block of four wave groups per CU on 32-row tiles while its ranges hold at most
-//     96 steps (below), else about two blocks per CU on 64-row tiles (B = 256, K = 28672, N = 3584:
+//     Where the ranges of one block per CU on 32-row tiles hold 32-96 steps, each range runs over
+//     four wave groups (below). Longer K: the same while its ranges hold at most 96 steps, else
+//     about two blocks per CU on 64-row tiles (B = 256, K = 28672, N = 3584:
 //     9 ranges of 56 tiles 66.8 us, against 93.2 us for 2 ranges of 112 32-row tiles in one wave
 //     group). Without that workspace, as the grid's K groups above.
 constexpr int64_t kSplitTarget = 256;    // blocks a split grid aims at (one per CU; two for long K)
@@ -734,8 +735,12 @@ constexpr int kBufGroups = 4, kBufSplit32Long = 8, kSplit32LongSteps = 16;
 // A/B through the op, fp16: Llama-2-7B down_proj at 0.55 bpw B = 256 33.9 -> 29.1 us, B = 128 34.1
 // -> 28.9, B = 64 26.8 -> 24.0, at 1.0 bpw B = 256 42.4 -> 40.3 (2 ranges of 86 steps). With 224-step
 // ranges (Llama-3-70B down_proj at B = 256) it was slower, 74.4 -> 78.4 and 66.1 -> 71.9 (mixed
-// rank): there the 64-row tiles' MFMA efficiency outweighs the partials' traffic.
-constexpr int64_t kSplitGroupMinSteps = 4, kSplitGroupMaxSteps = 96;
+// rank): there the 64-row tiles' MFMA efficiency outweighs the partials' traffic. For K of up to
+// 128 steps it runs where its ranges hold 32-96 steps, as many ranges as the one-group plan: B = 256
+// Llama-3-70B gate/up 72.8 -> 69.2 us, q/o 32.6 -> 30.3, Llama-2-7B gate/up at 1.0 bpw 38.6 -> 36.6,
+// B = 2048 Llama-3-70B k/v 32.7 -> 31.1. Shorter ranges lost (B = 64 gate/up 23.6 -> 24.7,
+// q/k/v/o 19.5 -> 21.0, where four steps a group halve the ranges).
+constexpr int64_t kSplitGroupMinSteps = 4, kSplitGroupMaxSteps = 96, kSplitGroupShortMinSteps = 32;
 enum GemmMode {
     kModeOnebit,
     kModeTile,
@@ -770,9 +775,10 @@ GemmPlan plan_gemm(int64_t M, int64_t K, int64_t N) {
     }
     if (tiles >= 128) return p;
     const bool long_k = steps > kSplitLongSteps;
-    if (long_k) {  // 32-row tiles, a block per CU, each k range over four wave groups
+    {  // 32-row tiles, a block per CU, each k range over four wave groups
         const int64_t want = std::min<int64_t>(kSplitTarget / tiles32, steps / (4 * kSplitGroupMinSteps));
-        if (want >= 2 && ceil_div(steps, want) <= kSplitGroupMaxSteps) {
+        const int64_t run = want >= 2 ? ceil_div(steps, want) : 0;  // steps of a range
+        if (run > 0 && run <= kSplitGroupMaxSteps && (long_k || run >= kSplitGroupShortMinSteps)) {
             p.split_steps = static_cast<int>(ceil_div(steps, want));
             p.splits = static_cast<int>(ceil_div(steps, p.split_steps));
             if (p.splits >= 2) {
