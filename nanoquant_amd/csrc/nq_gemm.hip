@@ -712,9 +712,9 @@ void launch_dm_split(const void* A, const uint32_t* W, const void* s_in, const v
 //     ranges of 56 tiles 15.8 us; B = 2048, K = 8192, N = 512: 8 ranges 34.6 -> 4 ranges 30.2 us).
 //     Where the ranges of one block per CU on 32-row tiles hold 32-96 steps, each range runs over
 //     four wave groups (below). Longer K: the same while its ranges hold at most 96 steps, else
-//     about two blocks per CU on 64-row tiles (B = 256, K = 28672, N = 3584:
-//     9 ranges of 56 tiles 66.8 us, against 93.2 us for 2 ranges of 112 32-row tiles in one wave
-//     group). Without that workspace, as the grid's K groups above.
+//     the same on 64-row tiles (once about two blocks per CU on 64-row tiles in one wave group:
+//     B = 256, K = 28672, N = 3584, 9 ranges of 56 tiles 66.8 us, against 93.2 us for 2 ranges of
+//     112 32-row tiles in one group). Without that workspace, as the grid's K groups above.
 constexpr int64_t kSplitTarget = 256;    // blocks a split grid aims at (one per CU; two for long K)
 constexpr int64_t kSplitMinSteps = 8;    // 64-k steps of the shortest range
 constexpr int64_t kSplitLongSteps = 128; // beyond this many steps K counts as long
@@ -739,7 +739,11 @@ constexpr int kBufGroups = 4, kBufSplit32Long = 8, kSplit32LongSteps = 16;
 // 128 steps it runs where its ranges hold 32-96 steps, as many ranges as the one-group plan: B = 256
 // Llama-3-70B gate/up 72.8 -> 69.2 us, q/o 32.6 -> 30.3, Llama-2-7B gate/up at 1.0 bpw 38.6 -> 36.6,
 // B = 2048 Llama-3-70B k/v 32.7 -> 31.1. Shorter ranges lost (B = 64 gate/up 23.6 -> 24.7,
-// q/k/v/o 19.5 -> 21.0, where four steps a group halve the ranges).
+// q/k/v/o 19.5 -> 21.0, where four steps a group halve the ranges). Long K with longer ranges runs
+// the same split on 64-row tiles (each sign fragment feeding twice the MFMAs): Llama-3-70B
+// down_proj at B = 256 (4 ranges of 112 steps, 14.7 MB of partials, against 9 ranges and 33 MB on
+// one group) 78.9 -> 76.4 us, mixed rank 69.5 -> 67.6. Where the 32-row split applies it stays
+// ahead (7B down_proj B = 256 30.4 against 33.3 us on 64-row tiles).
 constexpr int64_t kSplitGroupMinSteps = 4, kSplitGroupMaxSteps = 96, kSplitGroupShortMinSteps = 32;
 enum GemmMode {
     kModeOnebit,
@@ -749,7 +753,8 @@ enum GemmMode {
     kModeGroups32,
     kModeSplit,
     kModeSplit32,
-    kModeSplitGroups32
+    kModeSplitGroups32,
+    kModeSplitGroups64
 };
 struct GemmPlan {
     GemmMode mode = kModeOnebit;
@@ -788,6 +793,18 @@ GemmPlan plan_gemm(int64_t M, int64_t K, int64_t N) {
             }
         }
     }
+    if (long_k) {  // longer ranges: 64-row tiles, a block per CU, each k range over four wave groups
+        const int64_t want = std::min<int64_t>(kSplitTarget / tiles, steps / (4 * kSplitGroupMinSteps));
+        if (want >= 2) {
+            p.split_steps = static_cast<int>(ceil_div(steps, want));
+            p.splits = static_cast<int>(ceil_div(steps, p.split_steps));
+            if (p.splits >= 2) {
+                p.mode = kModeSplitGroups64;
+                p.workspace_bytes = static_cast<size_t>(p.splits) * static_cast<size_t>(M) * static_cast<size_t>(N) * 4;
+                return p;
+            }
+        }
+    }
     const bool rows32 = !long_k && tiles < 64;
     const int64_t grid_tiles = rows32 ? tiles32 : tiles;
     const int64_t want = std::min<int64_t>((long_k ? 2 : 1) * kSplitTarget / grid_tiles, steps / kSplitMinSteps);
@@ -807,7 +824,8 @@ int launch_gemm(const char* name, const void* A, const uint32_t* W, const void* 
                 const void* k_scale = nullptr) {
     GemmPlan p = plan_gemm(M, K, N);
     if (p.mode != kModeOnebit && !aligned(C, 16)) p.mode = kModeOnebit;
-    if ((p.mode == kModeSplit || p.mode == kModeSplit32 || p.mode == kModeSplitGroups32) &&
+    if ((p.mode == kModeSplit || p.mode == kModeSplit32 || p.mode == kModeSplitGroups32 ||
+         p.mode == kModeSplitGroups64) &&
         (!workspace || workspace_bytes < p.workspace_bytes || !aligned(workspace, 16)))
         p.mode = (K / 64) % 2 == 0 ? kModeGroups : kModeTile;
     switch (p.mode) {
@@ -842,6 +860,10 @@ int launch_gemm(const char* name, const void* A, const uint32_t* W, const void* 
             else
                 launch_dm_split<T, 256, 32, 64, 32, 2>(A, W, s_in, s_out, C, M, K, N, static_cast<float*>(workspace),
                                                        p.splits, p.split_steps, stream);
+            break;
+        case kModeSplitGroups64:
+            launch_dm_split<T, 256, 64, 64, 64, 4, 3, 4>(A, W, s_in, s_out, C, M, K, N, static_cast<float*>(workspace),
+                                                         p.splits, p.split_steps, stream);
             break;
         case kModeSplitGroups32:
             launch_dm_split<T, 256, 32, 64, 32, 4, 3, 4>(A, W, s_in, s_out, C, M, K, N, static_cast<float*>(workspace),

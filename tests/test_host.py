@@ -271,8 +271,8 @@ def test_gemm_split_workspace_sizes():
     # ceil(172 / 4) = 43 steps (at most 96: each over four wave groups), and 4 ranges cover the steps
     assert lib.nq_gemm_onebit_workspace_bytes(256, 11008, 1792) == 4 * 256 * 1792 * 4
     # B=256, K=28672 (448 steps), N=3584: 112 tiles of 32 rows -> 2 ranges of 224 steps, too long for
-    # the wave groups; 56 tiles of 64 rows -> 2 * 256 // 56 = 9 ranges of ceil(448 / 9) = 50 steps
-    assert lib.nq_gemm_onebit_workspace_bytes(256, 28672, 3584) == 9 * 256 * 3584 * 4
+    # the 32-row wave groups; 56 tiles of 64 rows -> 256 // 56 = 4 ranges of 112 steps over four groups
+    assert lib.nq_gemm_onebit_workspace_bytes(256, 28672, 3584) == 4 * 256 * 3584 * 4
     # two stages share the workspace: the larger need
     s1 = lib.nq_gemm_onebit_workspace_bytes(256, 11008, 1792)
     s2 = lib.nq_gemm_onebit_workspace_bytes(256, 4096, 1792)  # 28 tiles, 56 of 32 rows: 4 ranges of 16
