@@ -574,6 +574,61 @@ def test_gemm_split_k(nq, B, K, N):
         assert err <= 1e-3, err
 
 
+# Split plans: 32-row tiles in one wave group (6 ranges); 32-row tiles over four wave groups (4
+# ranges of 43 steps; 10 of 18 on a partial row tile); 64-row tiles over four wave groups (193 steps,
+# too long for two 32-row ranges: 4 ranges of 49)
+@pytest.mark.parametrize("B,K,N", [(256, 4096, 1280), (256, 11008, 1792), (100, 11008, 512), (256, 12352, 4096)],
+                         ids=["rows32", "groups32", "groups32_partial_rows", "groups64"])
+def test_gemm_split_scratch_and_replays(nq, B, K, N):
+    """A split GEMM's results do not depend on what its scratch held: a workspace of random bytes,
+    calls one after another and replays of a captured graph (with eager calls between them) give
+    the same bits, within 1e-3 of float64."""
+    from nanoquant_amd import _lib
+    lib = _lib.load()
+    nbytes = lib.nq_gemm_onebit_workspace_bytes(B, K, N)
+    announce("gemm split scratch", B, K, N, nbytes)
+    assert nbytes > 0
+    rng = np.random.default_rng(21)
+    w = np.where(rng.random((N, K)) < 0.5, -1, 1).astype(np.int8)
+    s_in = np.abs(rng.normal(1, 0.2, K)).astype(np.float16)
+    s_out = (np.abs(rng.normal(1, 0.2, N)) / 16).astype(np.float16)
+    x = rng.normal(size=(B, K)).astype(np.float16)
+    words, p_in, p_out, _ = nq.pack_binary_marlin(dev_t(w), dev_t(s_in), dev_t(s_out))
+    xd = dev_t(x)
+    ws = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device="cuda")  # whatever the scratch held
+
+    def call(y):
+        st = lib.nq_gemm_onebit(_lib.NQ_F16, xd.data_ptr(), words.data_ptr(), p_in.data_ptr(), p_out.data_ptr(),
+                                y.data_ptr(), B, K, N, ws.data_ptr(), nbytes, _lib.stream_of(xd.device))
+        assert st == 0
+
+    y_first = torch.empty(B, N, dtype=torch.float16, device="cuda")
+    y_again = torch.empty_like(y_first)
+    call(y_first)
+    call(y_again)
+    torch.cuda.synchronize()
+    assert torch.equal(y_again, y_first)
+    y64 = ((x.astype(np.float64) * s_in.astype(np.float64)) @ w.T.astype(np.float64)) * s_out.astype(np.float64)
+    err, _ = rel_err(y_first, y64, "gemm", torch.float16)
+    assert err <= 1e-3, err
+    # a captured graph of two calls, replayed with eager calls in between
+    y_graph = torch.empty_like(y_first)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        call(y_graph)
+        call(y_graph)
+    for _ in range(3):
+        y_graph.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y_graph, y_first)
+        call(y_again)
+        torch.cuda.synchronize()
+        assert torch.equal(y_again, y_first)
+
+
 # --------------------------------------------------------------------------- Llama-3-70B shapes
 
 def mixed_rank(base: int, seed: int) -> int:
