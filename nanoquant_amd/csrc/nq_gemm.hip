@@ -192,11 +192,11 @@ int launch_onebit(const void* A, const uint32_t* W, const void* s_in, const void
 //
 // The natural-k product with every operand of a 64-k step fetched by global_load_lds (16 bytes
 // a lane for the A tile, 4 for sign words and s_in) straight into one of NBUF LDS buffers (three
-// to eight), NBUF - 1 steps ahead, so no register holds a tile in flight. A wave's DMA writes 64 consecutive
-// LDS slots, so the A tile is unpadded (128-byte rows) and bank conflicts are avoided by where
-// each lane fetches from: LDS chunk p of row r holds the row's 16-byte chunk p ^ ((r / 2) % 8). s_in
-// is fetched in the order the operands read it (every wave keeps its own copy, so every wave
-// issues the same number of DMAs per step). The DMAs are issued from inline assembly
+// to eight), NBUF - 1 steps ahead, so no register holds a tile in flight. A wave's DMA writes 64
+// consecutive LDS slots, so the A tile is unpadded (128-byte rows) and bank conflicts are avoided
+// by where each lane fetches from: LDS chunk p of row r holds the row's 16-byte chunk
+// p ^ ((r / 2) % 8). s_in is fetched in the order the operands read it (every wave keeps its own
+// copy, so every wave issues the same number of DMAs per step). The DMAs are issued from inline assembly
 // (dma16_lds / dma4_lds), from a per-step scalar base and a fixed byte offset per lane, so the
 // compiler does not track them and waits for the LDS reads of a k tile only as far as they are
 // needed (with the builtin it waited for every outstanding read at each first use; 5.8% / 5.9% /
