@@ -326,6 +326,14 @@ int nq_rope_kv_write(int dtype, const void* qkv, int64_t qkv_stride, void* k_cac
 int nq_dense_gemv(int dtype, const void* w, const void* x, const void* norm_weight, float eps, void* y,
                   int y_float32, int64_t batch, int64_t n, int64_t m, int64_t ldy, nq_stream_t stream);
 
+/* Greedy token choice of the decode step: out[b] = the index of the largest of the n float32
+ * logits in row b (x + b * ldx), the first one of equal values, the first NaN if there is one
+ * (torch.argmax's order). One launch of one block per row; rows <= 2097120, n < 2^30; x 4-byte and
+ * out 8-byte aligned. Replaces the argmax of the reference's decode harness
+ * (src/nanoquant/kernel/test_decode.py:350-353, greedy here in place of its top-k sampling),
+ * which torch runs as its own reduction launches. */
+int nq_argmax_rows(const float* x, int64_t rows, int64_t n, int64_t ldx, int64_t* out, nq_stream_t stream);
+
 /* ---------------------------------------------------------------- measurement aid */
 
 /* Enqueue a one-thread kernel that writes the GPU's constant-rate wall clock to *dst (device

@@ -79,6 +79,7 @@ SIGNATURES = {
     "nq_rope_kv_write": (_int, [_int, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
                                  _vp]),
     "nq_dense_gemv": (_int, [_int, _vp, _vp, _vp, ctypes.c_float, _vp, _int, _i64, _i64, _i64, _i64, _vp]),
+    "nq_argmax_rows": (_int, [_vp, _i64, _i64, _i64, _vp, _vp]),
     "nq_gemm_onebit_workspace_bytes": (_size, [_i64, _i64, _i64]),
     "nq_gemm_onebit": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _size, _vp]),
     "nq_gemm_nanoquant_workspace_bytes": (_size, [_i64, _i64, _i64, _i64]),

@@ -547,6 +547,61 @@ void launch_dense_gemv(const uint16_t* w, const uint16_t* x, const uint16_t* g, 
     else launch_dense_rpw<T, NORM, 1>(rpw, w, x, g, eps, y, y_f32, m, n, batch, ldy, st);
 }
 
+// ------------------------------------------------------------------ greedy argmax over the logits
+//
+// One block per batch row: each thread scans every kArgmaxThreads-th logit, then the wave and the
+// block reduce (value, index) pairs. The order is torch.argmax's: a NaN beats every number (the
+// first NaN wins), otherwise the larger value, and of equal values (-0 equal to +0) the smaller
+// index, so the result is the first maximal logit. One 32000-logit row: 8.4 us graph-replayed
+// against 10.5 us for torch.argmax (a variant issuing each thread's 32 loads at once took 9.0).
+constexpr int kArgmaxThreads = 1024;
+
+__device__ inline bool argmax_before(float a, int ia, float b, int ib) {
+    const bool na = a != a, nb = b != b;
+    if (na || nb) return na && (!nb || ia < ib);
+    return a > b || (a == b && ia < ib);
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_rows_kernel(const float* __restrict__ x, int n, int64_t ldx,
+                                                                     int64_t* __restrict__ out) {
+    const float* row = x + static_cast<int64_t>(blockIdx.x) * ldx;
+    float bv = -INFINITY;
+    int bi = INT32_MAX;  // loses to every element, a -inf one included (equal value, smaller index)
+#pragma unroll 8
+    for (int i = static_cast<int>(threadIdx.x); i < n; i += kArgmaxThreads) {
+        const float v = row[i];
+        if (argmax_before(v, i, bv, bi)) {
+            bv = v;
+            bi = i;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off, 64);
+        const int oi = __shfl_xor(bi, off, 64);
+        if (argmax_before(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    __shared__ float wv[kArgmaxThreads / 64];
+    __shared__ int wi[kArgmaxThreads / 64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        wv[wave] = bv;
+        wi[wave] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < kArgmaxThreads / 64; ++w)
+            if (argmax_before(wv[w], wi[w], bv, bi)) {
+                bv = wv[w];
+                bi = wi[w];
+            }
+        out[blockIdx.x] = bi;
+    }
+}
+
 }  // namespace
 }  // namespace nq
 
@@ -674,6 +729,20 @@ int nq_dense_gemv(int dtype, const void* w, const void* x, const void* norm_weig
         if (gp) launch_dense_gemv<BF16, true>(wp, xp, gp, eps, y, yf, mi, ni, bi, li, st);
         else launch_dense_gemv<BF16, false>(wp, xp, gp, eps, y, yf, mi, ni, bi, li, st);
     }
+    return check_launch(name);
+}
+
+int nq_argmax_rows(const float* x, int64_t rows, int64_t n, int64_t ldx, int64_t* out, nq_stream_t stream) {
+    const char* name = "nq_argmax_rows";
+    if (rows < 0 || n <= 0 || ldx < n)
+        return fail(NQ_ERR_INVALID_ARGUMENT, "%s: bad sizes (rows %lld, n %lld, ldx %lld)", name, (long long)rows,
+                    (long long)n, (long long)ldx);
+    if (n > INT32_MAX / 2 || rows > 65535 * 32) return fail(NQ_ERR_UNSUPPORTED, "%s: sizes too large", name);
+    if (rows == 0) return NQ_OK;
+    if (!x || !out) return fail(NQ_ERR_INVALID_ARGUMENT, "%s: null pointer", name);
+    if (!aligned(x, 4) || !aligned(out, 8)) return fail(NQ_ERR_ALIGNMENT, "%s: misaligned x or out", name);
+    argmax_rows_kernel<<<static_cast<unsigned>(rows), kArgmaxThreads, 0, as_stream(stream)>>>(
+        x, static_cast<int>(n), ldx, out);
     return check_launch(name);
 }
 

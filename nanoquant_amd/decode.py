@@ -738,7 +738,8 @@ class FusedDecoder(GraphDecoder):
                                       out.data_ptr(), int(self.head_bias is None), B, hw.shape[1], hw.shape[0],
                                       out.shape[1], st), "lm_head")
         logits = self.logits if self.head_bias is None else (self.logits16 + self.head_bias).float()
-        torch.argmax(logits, dim=-1, out=self.tok)
+        self._check(lib.nq_argmax_rows(logits.data_ptr(), B, logits.shape[1], logits.stride(0), self.tok.data_ptr(),
+                                       st), "argmax")
         self.pos.add_(1)
         self.ids.index_copy_(1, self.pos, self.tok.view(-1, 1))
         return logits

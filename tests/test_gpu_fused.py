@@ -479,3 +479,44 @@ def test_dense_gemv_argument_errors(lib):
     assert f(F16, wp, xp, None, 0.0, yp, 0, 2, 40000, 16, 16, None) == _lib.NQ_ERR_UNSUPPORTED  # n past the LDS
     assert f(7, wp, xp, None, 0.0, yp, 0, 2, 64, 16, 16, None) == _lib.NQ_ERR_DTYPE
     assert f(F16, None, None, None, 0.0, None, 0, 0, 64, 16, 16, None) == _lib.NQ_OK  # empty batch
+
+
+@pytest.mark.parametrize("rows,n,ldx", [(1, 32000, 32000), (4, 32000, 32000), (3, 1000, 1024), (2, 1, 1),
+                                        (5, 128256, 128256), (3, 1001, 1001)])
+def test_argmax_rows_is_torch_argmax(lib, rows, n, ldx):
+    """The decode step's greedy choice: the same index as torch.argmax on every row, including
+    repeated maxima (the first wins), NaNs (the first NaN wins), rows of -inf only, and rows read
+    at a stride larger than their length."""
+    from nanoquant_amd import _lib
+    announce("argmax rows", rows, n, ldx)
+    g = torch.Generator(device="cuda").manual_seed(rows * 7 + n)
+    x = torch.randn(rows, ldx, generator=g, device="cuda", dtype=torch.float32)
+    x[:, n:] = 1e30  # past the row: never read
+    if n > 8:
+        x[0, n // 3] = x[0, n - 2] = x[0, :n].max() + 1.0  # a repeated maximum: the first one
+    if rows > 1 and n > 4:
+        x[1, n - 3] = float("nan")
+        x[1, n // 2] = float("nan")  # two NaNs: the first one
+    if rows > 2:
+        x[2, :n] = float("-inf")  # index 0
+    out = torch.full((rows,), -1, dtype=torch.int64, device="cuda")
+    st = lib.nq_argmax_rows(x.data_ptr(), rows, n, ldx, out.data_ptr(), _lib.stream_of(x.device))
+    assert st == 0
+    torch.cuda.synchronize()
+    want = torch.argmax(x[:, :n], dim=-1)
+    assert torch.equal(out, want), (out.tolist(), want.tolist())
+
+
+def test_argmax_rows_argument_errors(lib):
+    from nanoquant_amd import _lib
+    announce("argmax rows errors")
+    x = torch.zeros(2, 64, dtype=torch.float32, device="cuda")
+    out = torch.zeros(2, dtype=torch.int64, device="cuda")
+    f = lib.nq_argmax_rows
+    xp, op = x.data_ptr(), out.data_ptr()
+    assert f(xp, 2, 0, 64, op, None) == _lib.NQ_ERR_INVALID_ARGUMENT  # no logits
+    assert f(xp, 2, 64, 32, op, None) == _lib.NQ_ERR_INVALID_ARGUMENT  # stride shorter than a row
+    assert f(xp + 2, 2, 62, 64, op, None) == _lib.NQ_ERR_ALIGNMENT
+    assert f(xp, 2, 64, 64, op + 4, None) == _lib.NQ_ERR_ALIGNMENT
+    assert f(None, 2, 64, 64, op, None) == _lib.NQ_ERR_INVALID_ARGUMENT
+    assert f(None, 0, 64, 64, None, None) == _lib.NQ_OK  # no rows

@@ -90,6 +90,10 @@ def test_c_abi_argument_errors_need_no_gpu():
     assert rope(0, 127, 96 * 127) == _lib.NQ_ERR_INVALID_ARGUMENT  # odd head_dim
     assert rope(0, 128, 95 * 128) == _lib.NQ_ERR_SHAPE  # row too short for q, k and v
     assert rope(0, 128, 96 * 128) == _lib.NQ_ERR_INVALID_ARGUMENT  # null pointers
+    # the decode step's argmax
+    assert lib.nq_argmax_rows(None, 2, 0, 64, None, None) == _lib.NQ_ERR_INVALID_ARGUMENT  # no logits
+    assert lib.nq_argmax_rows(None, 2, 64, 64, None, None) == _lib.NQ_ERR_INVALID_ARGUMENT  # null pointers
+    assert lib.nq_argmax_rows(None, 0, 64, 64, None, None) == 0  # no rows
 
 
 # The schema strings of the reference extension (kernel/pybind.cpp:85-104), written out here as
