@@ -473,6 +473,9 @@ GEMM_CASES = [
     ("llama7b_gate_055_b256", 256, 4096, 1632, 11008, False),
     ("llama7b_down_055_b256", 256, 11008, 1632, 4096, False),
     ("llama7b_gate_055_b2048", 2048, 4096, 1632, 11008, False),
+    # stage 1 of 193 64-k steps on 8 x 16 tiles of 32 rows: too long for two 32-row ranges, so its
+    # k ranges (4 of 49 steps) run over four wave groups on 64-row tiles
+    ("long_k_groups64_b256", 256, 12352, 4096, 256, False),
     # stage 2 counts 1024 tiles of 64 rows x 256 features, so it runs 512 blocks of 128 rows x 256
     # features (waves of 64 x 128), the last row block ragged: 1000 = 7 * 128 + 104
     ("wide_ragged_rows", 1000, 256, 128, 16384, True),
