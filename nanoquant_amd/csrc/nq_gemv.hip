@@ -1863,7 +1863,14 @@ inline bool sb_plan(int64_t batch, int64_t rows, int64_t wpr, int64_t kpad, SbPl
     return sb_plan_any(batch, rows, wpr, kpad, p);
 }
 // The search over grids of up to max_rounds rounds of blocks.
+// Up to 32 batch rows a round counts two blocks per CU where their LDS fits (a block's DMA of
+// its slice then runs beside the other's MFMAs): interleaved same-box A/B, fp16, bit-identical
+// outputs (the plans differ in their row tiles only): down_proj at 8 / 16 / 32 rows 12.91 -> 12.35 /
+// 13.72 -> 13.19 / 16.60 -> 16.16 us, Llama-3-70B q/o at 16 / 32 rows 16.27 -> 15.78 / 19.79 ->
+// 19.36, gate/up at 16 rows 25.22 -> 23.67, down 29.33 -> 28.89. At 64 rows the plan it picks
+// (other k ranges) was slower (21.58 -> 22.62), and four blocks per CU were no better.
 inline bool sb_plan_rounds(int64_t batch, int64_t rows, int64_t wpr, int64_t kpad, int max_rounds, SbPlan& p) {
+    const int64_t occupancy = batch <= 32 ? 2 : 1;  // blocks per CU a round may count
     const int ct = static_cast<int>(std::min<int64_t>(8, ceil_div(batch, 16)));
     const int passes = static_cast<int>(ceil_div(batch, 16LL * ct));
     const int xcols = 16 * ct + 1;
@@ -1875,15 +1882,16 @@ inline bool sb_plan_rounds(int64_t batch, int64_t rows, int64_t wpr, int64_t kpa
             const int64_t kw = std::max<int64_t>(2, (ceil_div(wpr, want) + 1) & ~int64_t{1});
             const int64_t ks = ceil_div(wpr, kw);
             const int64_t blocks = row_blocks * ks * passes;
-            if (blocks > int64_t{kSbMaxBlocks} * max_rounds) break;
+            if (blocks > int64_t{kSbMaxBlocks} * occupancy * max_rounds) break;
             const size_t lds = std::max<size_t>(
                 static_cast<size_t>(sb_xs_dwords(xcols, static_cast<int>(kw)) + sb_w_dwords(br, static_cast<int>(kw))) * 4,
                 static_cast<size_t>(16 * ct) * (br + 4) * 4);
             if (lds > static_cast<size_t>(kSbLdsBytes)) continue;
+            const int64_t per_cu = std::min<int64_t>(occupancy, std::max<int64_t>(1, kSbLdsBytes / static_cast<int64_t>(lds)));
             const double mfma = rtw * ct * kw * 16.0 * 1.25;
             const double dma = (xcols * 64.0 + br * 4.0) * kw / 32.0;
             const double fin = ks > 1 ? 4000.0 + 2.0 * ks * batch * kpad * 4.0 / (256.0 * 16.0) : 0.0;
-            const double cost = (mfma + dma) * static_cast<double>(ceil_div(blocks, kSbMaxBlocks)) + fin;
+            const double cost = (mfma + dma) * static_cast<double>(ceil_div(blocks, kSbMaxBlocks * per_cu)) + fin;
             if (best < 0 || cost < best) {
                 best = cost;
                 p.rtw = rtw;
