@@ -162,6 +162,55 @@ __global__ __launch_bounds__(kThreads) void pack_marlin_kernel(const int8_t* __r
     dst[t] = word;
 }
 
+// The same words from a 16-byte aligned matrix, one block per 64 outputs x kMarlinTileK k: the
+// block's 64 row segments reach LDS by 16-byte loads (16 lanes over a row's 256 bytes, where one
+// thread per word made 2-byte loads spread over eight rows), then each thread assembles words
+// from LDS and a tile row's 32 words go out as one 128-byte run.
+constexpr int kMarlinTileK = 256;
+constexpr int kMarlinRowStride = kMarlinTileK + 16;  // bytes: rows 4 banks apart, 16-byte aligned
+
+__global__ __launch_bounds__(kThreads) void pack_marlin_tiled_kernel(const int8_t* __restrict__ w,
+                                                                     uint32_t* __restrict__ dst, int64_t O,
+                                                                     int64_t K) {
+    __shared__ __attribute__((aligned(16))) int8_t tile[64 * kMarlinRowStride];
+    const int t = static_cast<int>(threadIdx.x);
+    const int64_t tile_out = blockIdx.y;
+    const int64_t k0 = static_cast<int64_t>(blockIdx.x) * kMarlinTileK;
+    const int kn = static_cast<int>(K - k0 < kMarlinTileK ? K - k0 : kMarlinTileK);  // a multiple of 16
+    constexpr int kChunks = kMarlinTileK / 16;  // 16-byte chunks of a full row segment
+    for (int i = t; i < 64 * kChunks; i += kThreads) {
+        const int r = i / kChunks, c = i - r * kChunks;
+        if (16 * c < kn) {
+            const int8_t* src = w + (tile_out * 64 + r) * K + k0 + 16 * c;
+            *reinterpret_cast<u32x4*>(tile + r * kMarlinRowStride + 16 * c) = *reinterpret_cast<const u32x4*>(src);
+        }
+    }
+    __syncthreads();
+    const int64_t half_o = O / 2;
+    for (int i = t; i < (kn / 16) * 32; i += kThreads) {
+        const int trl = i / 32, cl = i - trl * 32;
+        const int o1 = cl / 4, r2 = cl % 4;
+        uint32_t word = 0;
+#pragma unroll
+        for (int o16 = 0; o16 < 4; ++o16) {
+#pragma unroll
+            for (int o8 = 0; o8 < 2; ++o8) {
+#pragma unroll
+                for (int r8 = 0; r8 < 2; ++r8) {
+                    const int row = o16 * 16 + o8 * 8 + o1;
+                    const int kk = trl * 16 + r8 * 8 + r2 * 2;
+                    const uint16_t pair = *reinterpret_cast<const uint16_t*>(tile + row * kMarlinRowStride + kk);
+                    const uint32_t neg_lo = (pair >> 7) & 1u;   // element k   (r1 = 0)
+                    const uint32_t neg_hi = (pair >> 15) & 1u;  // element k+1 (r1 = 1)
+                    const int bit = 15 - (2 * o8 + r8) - 4 * o16;
+                    word |= (neg_lo << bit) | (neg_hi << (bit + 16));
+                }
+            }
+        }
+        dst[(k0 / 16 + trl) * half_o + tile_out * 32 + cl] = word;
+    }
+}
+
 // Marlin words [K_pad/16, O_pad/2] straight from the sign words of a [O, K] matrix (lsb_first
 // or half2, ceil(K/32) words a row), as a checkpoint stores V [r, n] and U [m, r]; elements past
 // O or K are +1 (bit 0). Each output word's four k lie in one 16-k group, so in one source word
@@ -314,7 +363,11 @@ int nq_pack_marlin(const int8_t* weight, uint32_t* dst, int64_t O, int64_t K, nq
     if (O == 0 || K == 0) return NQ_OK;
     if (!weight || !dst) return fail(NQ_ERR_INVALID_ARGUMENT, "nq_pack_marlin: null pointer");
     if (!aligned(weight, 2)) return fail(NQ_ERR_ALIGNMENT, "nq_pack_marlin: weight must be 2-byte aligned");
-    pack_marlin_kernel<<<grid_for((K / 16) * (O / 2)), kThreads, 0, as_stream(stream)>>>(weight, dst, O, K);
+    if (aligned(weight, 16))
+        pack_marlin_tiled_kernel<<<dim3(static_cast<unsigned>(ceil_div(K, kMarlinTileK)), static_cast<unsigned>(O / 64)),
+                                   kThreads, 0, as_stream(stream)>>>(weight, dst, O, K);
+    else
+        pack_marlin_kernel<<<grid_for((K / 16) * (O / 2)), kThreads, 0, as_stream(stream)>>>(weight, dst, O, K);
     return check_launch("nq_pack_marlin");
 }
 

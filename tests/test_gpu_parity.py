@@ -150,6 +150,30 @@ def test_marlin_pack_large_and_unpack(nq, OK):
     np.testing.assert_array_equal(back.cpu().numpy(), w)
 
 
+def test_marlin_pack_from_unaligned_weights(nq):
+    """Weights 16-byte aligned take the tiled packer (blocks of 64 outputs x 256 k, the last k tile
+    partial here), weights only 2-byte aligned the one-thread-per-word packer: the same words, and
+    the oracle's."""
+    O_, K_ = 1792, 1104  # 1104 = 4 * 256 + 80
+    announce("marlin pack unaligned", O_, K_)
+    rng = np.random.default_rng(77)
+    w = np.where(rng.random((O_, K_)) < 0.5, -1, 1).astype(np.int8)
+    buf = torch.zeros(O_ * K_ + 16, dtype=torch.int8, device="cuda")
+    view = buf[2:2 + O_ * K_].view(O_, K_)
+    view.copy_(dev_t(w))
+    assert view.data_ptr() % 16 == 2
+    ones_k = torch.ones(K_, dtype=torch.float16, device="cuda")
+    ones_o = torch.ones(O_, dtype=torch.float16, device="cuda")
+    words_u, _, _, _ = nq.pack_binary_marlin(view, ones_k, ones_o)
+    aligned_w = dev_t(w)
+    assert aligned_w.data_ptr() % 16 == 0
+    words_a, _, _, _ = nq.pack_binary_marlin(aligned_w, ones_k, ones_o)
+    torch.cuda.synchronize()
+    assert torch.equal(words_u, words_a)
+    exp, _, _, _ = O.pack_binary_marlin(w, np.ones(K_, np.float16), np.ones(O_, np.float16))
+    np.testing.assert_array_equal(as_words(words_a), exp)
+
+
 @pytest.mark.parametrize("shape", [(1, 1), (33, 95), (300, 1000), (1632, 11008)])
 def test_host_and_hip_packers_write_the_same_words(nq, shape):
     """The same signs packed as a CPU tensor (host path) and as a CUDA tensor (HIP kernels): sign
