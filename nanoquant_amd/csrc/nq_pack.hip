@@ -165,7 +165,9 @@ __global__ __launch_bounds__(kThreads) void pack_marlin_kernel(const int8_t* __r
 // The same words from a 16-byte aligned matrix, one block per 64 outputs x kMarlinTileK k: the
 // block's 64 row segments reach LDS by 16-byte loads (16 lanes over a row's 256 bytes, where one
 // thread per word made 2-byte loads spread over eight rows), then each thread assembles words
-// from LDS and a tile row's 32 words go out as one 128-byte run.
+// from LDS and a tile row's 32 words go out as one 128-byte run. V^T [1792, 11008] over 8
+// rotating copies: 25.4 us one thread per word, 6.34 us tiled, 5.77 us with each thread's four
+// loads issued before their LDS stores (a 512-k tile with eight: 6.42).
 constexpr int kMarlinTileK = 256;
 constexpr int kMarlinRowStride = kMarlinTileK + 16;  // bytes: rows 4 banks apart, 16-byte aligned
 
@@ -178,12 +180,19 @@ __global__ __launch_bounds__(kThreads) void pack_marlin_tiled_kernel(const int8_
     const int64_t k0 = static_cast<int64_t>(blockIdx.x) * kMarlinTileK;
     const int kn = static_cast<int>(K - k0 < kMarlinTileK ? K - k0 : kMarlinTileK);  // a multiple of 16
     constexpr int kChunks = kMarlinTileK / 16;  // 16-byte chunks of a full row segment
-    for (int i = t; i < 64 * kChunks; i += kThreads) {
+    constexpr int kPer = 64 * kChunks / kThreads;  // 16-byte loads per thread, all issued before their stores
+    u32x4 v[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int i = t + j * kThreads;
         const int r = i / kChunks, c = i - r * kChunks;
-        if (16 * c < kn) {
-            const int8_t* src = w + (tile_out * 64 + r) * K + k0 + 16 * c;
-            *reinterpret_cast<u32x4*>(tile + r * kMarlinRowStride + 16 * c) = *reinterpret_cast<const u32x4*>(src);
-        }
+        v[j] = 16 * c < kn ? *reinterpret_cast<const u32x4*>(w + (tile_out * 64 + r) * K + k0 + 16 * c) : u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int i = t + j * kThreads;
+        const int r = i / kChunks, c = i - r * kChunks;
+        if (16 * c < kn) *reinterpret_cast<u32x4*>(tile + r * kMarlinRowStride + 16 * c) = v[j];
     }
     __syncthreads();
     const int64_t half_o = O / 2;
