@@ -1,9 +1,10 @@
 // Sign-bit packing kernels: the two 32-column word orders (lsb_first, half2),
 // the reorder between them, and the Marlin GEMM layout.
 //
-// All of them are HBM-bound integer work: one thread owns one output word (or
-// one input word for the unpackers) so every load and store is a plain
-// coalesced vector access and no thread needs another thread's data.
+// All of them are HBM-bound integer work: one thread owns one output word (the
+// unpacker of whole-word rows: two 16-byte halves of int8 output) so every load
+// and store is a plain coalesced vector access and no thread needs another
+// thread's data.
 #include "nq_common.h"
 
 namespace nq {
@@ -60,7 +61,48 @@ __device__ inline uint32_t nibble_to_signs(uint32_t nib) {
 
 // --------------------------------------------------------------------------- 32-column words
 
-template <bool kVec>
+// Whole-word rows (cols = 32 * words) from a 16-byte aligned source: word t's 32 bytes sit at
+// src + 32 t, so no row index is needed; one thread per word, two 16-byte loads.
+__global__ __launch_bounds__(kThreads) void pack_signs_words_kernel(const int8_t* __restrict__ src,
+                                                                    uint32_t* __restrict__ dst, int64_t total,
+                                                                    int method) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (t >= total) return;
+    const u32x4 a = *reinterpret_cast<const u32x4*>(src + t * 32);
+    const u32x4 b = *reinterpret_cast<const u32x4*>(src + t * 32 + 16);
+    const uint32_t L = sign_nibble(a.x) | (sign_nibble(a.y) << 4) | (sign_nibble(a.z) << 8) |
+                       (sign_nibble(a.w) << 12) | (sign_nibble(b.x) << 16) | (sign_nibble(b.y) << 20) |
+                       (sign_nibble(b.z) << 24) | (sign_nibble(b.w) << 28);
+    dst[t] = to_method(L, method);
+}
+
+// The inverse, whole-word rows into a 16-byte aligned destination: a block owns 256 words and
+// thread j writes the 16-byte halves j and j + 256 of their 512, so each store of a wave covers
+// 1 KB contiguously (one thread per word storing both halves left every store 32-byte strided).
+// Over 8 rotating [1632, 11008] copies: 6.8 us before, 5.75 us; packing 4.78 -> 4.58 us without
+// the per-thread 64-bit row division.
+__global__ __launch_bounds__(kThreads) void unpack_signs_words_kernel(const uint32_t* __restrict__ src,
+                                                                      int8_t* __restrict__ dst, int64_t total,
+                                                                      int method) {
+    const int j = static_cast<int>(threadIdx.x);
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kThreads;
+    const int half = j & 1;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        const int64_t w = base + 128 * s + (j >> 1);
+        if (w < total) {
+            const uint32_t L = from_method(src[w], method) >> (16 * half);
+            u32x4 a;
+            a.x = nibble_to_signs(L);
+            a.y = nibble_to_signs(L >> 4);
+            a.z = nibble_to_signs(L >> 8);
+            a.w = nibble_to_signs(L >> 12);
+            *reinterpret_cast<u32x4*>(dst + w * 32 + half * 16) = a;
+        }
+    }
+}
+
+// Any other shape or alignment: one thread per word, bytewise over the row's valid columns.
 __global__ __launch_bounds__(kThreads) void pack_signs_kernel(const int8_t* __restrict__ src,
                                                               uint32_t* __restrict__ dst, int64_t rows,
                                                               int64_t cols, int64_t words, int method) {
@@ -70,20 +112,11 @@ __global__ __launch_bounds__(kThreads) void pack_signs_kernel(const int8_t* __re
     const int64_t w = t - row * words;
     const int8_t* p = src + row * cols + w * 32;
     uint32_t L = 0;
-    if (kVec) {
-        const u32x4 a = *reinterpret_cast<const u32x4*>(p);
-        const u32x4 b = *reinterpret_cast<const u32x4*>(p + 16);
-        L = sign_nibble(a.x) | (sign_nibble(a.y) << 4) | (sign_nibble(a.z) << 8) | (sign_nibble(a.w) << 12) |
-            (sign_nibble(b.x) << 16) | (sign_nibble(b.y) << 20) | (sign_nibble(b.z) << 24) |
-            (sign_nibble(b.w) << 28);
-    } else {
-        const int64_t valid = cols - w * 32 < 32 ? cols - w * 32 : 32;
-        for (int e = 0; e < valid; ++e) L |= static_cast<uint32_t>(p[e] < 0) << e;
-    }
+    const int64_t valid = cols - w * 32 < 32 ? cols - w * 32 : 32;
+    for (int e = 0; e < valid; ++e) L |= static_cast<uint32_t>(p[e] < 0) << e;
     dst[t] = to_method(L, method);
 }
 
-template <bool kVec>
 __global__ __launch_bounds__(kThreads) void unpack_signs_kernel(const uint32_t* __restrict__ src,
                                                                 int8_t* __restrict__ dst, int64_t rows,
                                                                 int64_t cols, int64_t words, int method) {
@@ -93,34 +126,23 @@ __global__ __launch_bounds__(kThreads) void unpack_signs_kernel(const uint32_t* 
     const int64_t w = t - row * words;
     const uint32_t L = from_method(src[t], method);
     int8_t* p = dst + row * cols + w * 32;
-    if (kVec) {
-        u32x4 a, b;
-        a.x = nibble_to_signs(L);
-        a.y = nibble_to_signs(L >> 4);
-        a.z = nibble_to_signs(L >> 8);
-        a.w = nibble_to_signs(L >> 12);
-        b.x = nibble_to_signs(L >> 16);
-        b.y = nibble_to_signs(L >> 20);
-        b.z = nibble_to_signs(L >> 24);
-        b.w = nibble_to_signs(L >> 28);
-        *reinterpret_cast<u32x4*>(p) = a;
-        *reinterpret_cast<u32x4*>(p + 16) = b;
-    } else {
-        const int64_t valid = cols - w * 32 < 32 ? cols - w * 32 : 32;
-        for (int e = 0; e < valid; ++e) p[e] = ((L >> e) & 1u) ? int8_t(-1) : int8_t(1);
-    }
+    const int64_t valid = cols - w * 32 < 32 ? cols - w * 32 : 32;
+    for (int e = 0; e < valid; ++e) p[e] = ((L >> e) & 1u) ? int8_t(-1) : int8_t(1);
 }
 
+template <bool kWhole>
 __global__ __launch_bounds__(kThreads) void repack_signs_kernel(const uint32_t* __restrict__ src,
                                                                  uint32_t* __restrict__ dst, int64_t rows,
                                                                  int64_t cols, int64_t words, int src_method,
                                                                  int dst_method) {
     const int64_t t = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
     if (t >= rows * words) return;
-    const int64_t w = t % words;
     uint32_t L = from_method(src[t], src_method);
-    const int64_t valid = cols - w * 32;
-    if (valid < 32) L &= (1u << valid) - 1u;  // padding columns stay +1
+    if (!kWhole) {  // cols % 32 != 0: the row's last word has padding columns
+        const int64_t w = t % words;
+        const int64_t valid = cols - w * 32;
+        if (valid < 32) L &= (1u << valid) - 1u;  // padding columns stay +1
+    }
     dst[t] = to_method(L, dst_method);
 }
 
@@ -328,11 +350,11 @@ int nq_pack_signs(const int8_t* src, uint32_t* dst, int64_t rows, int64_t cols, 
     if (!src || !dst) return fail(NQ_ERR_INVALID_ARGUMENT, "nq_pack_signs: null pointer");
     const bool vec = (cols % 32 == 0) && aligned(src, 16);
     if (vec)
-        pack_signs_kernel<true><<<grid_for(rows * words), kThreads, 0, as_stream(stream)>>>(src, dst, rows, cols,
-                                                                                             words, method);
+        pack_signs_words_kernel<<<grid_for(rows * words), kThreads, 0, as_stream(stream)>>>(src, dst, rows * words,
+                                                                                             method);
     else
-        pack_signs_kernel<false><<<grid_for(rows * words), kThreads, 0, as_stream(stream)>>>(src, dst, rows, cols,
-                                                                                              words, method);
+        pack_signs_kernel<<<grid_for(rows * words), kThreads, 0, as_stream(stream)>>>(src, dst, rows, cols, words,
+                                                                                      method);
     return check_launch("nq_pack_signs");
 }
 
@@ -344,11 +366,11 @@ int nq_unpack_signs(const uint32_t* src, int8_t* dst, int64_t rows, int64_t cols
     if (!src || !dst) return fail(NQ_ERR_INVALID_ARGUMENT, "nq_unpack_signs: null pointer");
     const bool vec = (cols % 32 == 0) && aligned(dst, 16);
     if (vec)
-        unpack_signs_kernel<true><<<grid_for(rows * words), kThreads, 0, as_stream(stream)>>>(src, dst, rows, cols,
-                                                                                               words, method);
+        unpack_signs_words_kernel<<<grid_for(rows * words), kThreads, 0, as_stream(stream)>>>(src, dst,
+                                                                                               rows * words, method);
     else
-        unpack_signs_kernel<false><<<grid_for(rows * words), kThreads, 0, as_stream(stream)>>>(src, dst, rows,
-                                                                                                cols, words, method);
+        unpack_signs_kernel<<<grid_for(rows * words), kThreads, 0, as_stream(stream)>>>(src, dst, rows, cols, words,
+                                                                                        method);
     return check_launch("nq_unpack_signs");
 }
 
@@ -360,8 +382,12 @@ int nq_repack_signs(const uint32_t* src, uint32_t* dst, int64_t rows, int64_t co
     const int64_t words = ceil_div(cols, 32);
     if (rows == 0 || words == 0) return NQ_OK;
     if (!src || !dst) return fail(NQ_ERR_INVALID_ARGUMENT, "nq_repack_signs: null pointer");
-    repack_signs_kernel<<<grid_for(rows * words), kThreads, 0, as_stream(stream)>>>(src, dst, rows, cols, words,
-                                                                                    src_method, dst_method);
+    if (cols % 32 == 0)
+        repack_signs_kernel<true><<<grid_for(rows * words), kThreads, 0, as_stream(stream)>>>(
+            src, dst, rows, cols, words, src_method, dst_method);
+    else
+        repack_signs_kernel<false><<<grid_for(rows * words), kThreads, 0, as_stream(stream)>>>(
+            src, dst, rows, cols, words, src_method, dst_method);
     return check_launch("nq_repack_signs");
 }
 

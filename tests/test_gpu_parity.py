@@ -78,7 +78,9 @@ def round_bf16(h):
 
 # --------------------------------------------------------------------------- packing
 
-PACK_SHAPES = [(1, 1), (3, 5), (7, 3), (4, 32), (5, 33), (17, 100), (64, 4096), (1632, 4096), (11008, 1632)]
+# (5, 3200): 500 whole words, so the last 256-word block of the word kernels is partly empty
+PACK_SHAPES = [(1, 1), (3, 5), (7, 3), (4, 32), (5, 33), (17, 100), (5, 3200), (64, 4096), (1632, 4096),
+               (11008, 1632)]
 
 
 @pytest.mark.parametrize("method", ["lsb_first", "half2"])
@@ -96,7 +98,7 @@ def test_pack_unpack_bit_exact(nq, shape, method):
     np.testing.assert_array_equal(back.cpu().numpy(), s)
 
 
-@pytest.mark.parametrize("shape", [(3, 5), (17, 100), (1632, 4096), (4096, 1632)])
+@pytest.mark.parametrize("shape", [(3, 5), (17, 100), (5, 3200), (1632, 4096), (4096, 1632)])
 def test_repack_between_orders(nq, shape):
     announce("repack", shape)
     rng = np.random.default_rng(7)
